@@ -1,0 +1,185 @@
+/*
+ * libq8gemv: C ABI of the MI355X (gfx950) decode-GEMV path of Qwen3-0.6B.
+ *
+ * The reference substitutes six IREE dispatch executables with hand-written
+ * kernels at compile time (compile.sh:35-43, --iree-hal-substitute-executable-
+ * source=decode_dispatch_N=FILE).  Each executable's binding ABI is
+ *   (binding0 weights RO, binding1 input buffer RO, binding2 output buffer)
+ *   + i32 push constants (layer as lo/hi, output byte offset)
+ * with the x / y byte offsets baked into each kernel
+ * (kernels/cuda/dispatch_3.cu:8-22, dispatch_4.cu:8-22, dispatch_24.cu:11-20;
+ * layouts in kernels/cuda/dispatch_*.mlir:5).  This library keeps that ABI's
+ * data contract -- GGUF Q8_0 34-byte blocks, [N,K] row-major weights stacked
+ * per layer as [28, BPL] bytes, f16 x, f32 accumulation, f16 y -- and takes
+ * explicit device pointers instead of baked-in offsets.
+ *
+ * Conventions
+ *   - Every pointer argument of a compute entry point is a device pointer the
+ *     caller owns.  Compute entry points only enqueue work on `stream` (a
+ *     hipStream_t; NULL = the null stream) and never allocate.
+ *   - Every function returns Q8_OK (0) or a Q8_ERR_* code; q8gemv_last_error()
+ *     gives the message for the calling thread.  Arguments are validated on
+ *     the host before anything is enqueued; nothing aborts the process.
+ *   - Compute entry points are safe to call from several host threads, each
+ *     with its own stream, once q8gemv_init() has returned.
+ *   - Alignment: weights and x 16 bytes, y / logits 2 bytes, token 4 bytes,
+ *     workspace 16 bytes.
+ */
+#ifndef QWEN3_Q8GEMV_H
+#define QWEN3_Q8GEMV_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ---- */
+#define Q8_OK                  0
+#define Q8_ERR_NOT_INITIALIZED 1  /* q8gemv_init() not called or failed */
+#define Q8_ERR_INVALID_KIND    2  /* kind outside enum q8_kind */
+#define Q8_ERR_NULL_POINTER    3  /* a required pointer is NULL */
+#define Q8_ERR_LAYER_RANGE     4  /* layer outside [0, Q8_NUM_LAYERS) */
+#define Q8_ERR_MISALIGNED      5  /* pointer alignment below the contract */
+#define Q8_ERR_BAD_SHAPE       6  /* unsupported N / K / row count */
+#define Q8_ERR_CODE_OBJECT     7  /* code object missing, unreadable or lacks a kernel */
+#define Q8_ERR_HIP             8  /* a HIP runtime call failed (message has details) */
+#define Q8_ERR_BAD_ARGUMENT    9  /* other invalid argument (tuning values, sizes) */
+
+/* ---- model constants (model/qwen3_full.mlir:29-64; tools/create_q8_irpa.py:16-25) ---- */
+#define Q8_NUM_LAYERS   28
+#define Q8_BLOCK_ELEMS  32
+#define Q8_BLOCK_BYTES  34
+#define Q8_VOCAB_ROWS   151936
+#define Q8_HIDDEN       1024
+
+/* The five Q8_0 GEMV kinds, in the per-layer call order of
+ * model/qwen3_full.mlir:751-864 (q, k, v, o, gate_up, down). */
+enum q8_kind {
+  Q8_ATTN_Q   = 0, /* [2048,1024] decode_dispatch_3,  qwen3_full.mlir:625       */
+  Q8_ATTN_KV  = 1, /* [1024,1024] decode_dispatch_4,  qwen3_full.mlir:630, 635  */
+  Q8_ATTN_O   = 2, /* [1024,2048] decode_dispatch_12, qwen3_full.mlir:739       */
+  Q8_GATE_UP  = 3, /* [6144,1024] decode_dispatch_18, qwen3_full.mlir:820       */
+  Q8_FFN_DN   = 4  /* [1024,3072] decode_dispatch_20, qwen3_full.mlir:852       */
+};
+
+/* ---- lifetime ---- */
+
+/* Loads the gfx950 code object (hipModuleLoad) on the current device and
+ * resolves every kernel.  code_object_path NULL = "q8gemv_gfx950.hsaco" in
+ * the directory holding this library.  Idempotent.  Replaces the compile-time
+ * substitution step of compile.sh:35-43. */
+int q8gemv_init(const char* code_object_path);
+void q8gemv_shutdown(void);
+const char* q8gemv_last_error(void);
+
+/* Shape of a kind: N rows, K columns, bytes per layer N*K/32*34
+ * (create_q8_irpa.py:195-197).  Any output pointer may be NULL. */
+int q8gemv_kind_shape(int kind, int64_t* n, int64_t* k, int64_t* bytes_per_layer);
+
+/* ---- Q8_0 GEMV ---- */
+
+/* y[N] = W[layer] . x[K] for one kind.  w_stacked points at the [28, BPL]
+ * stacked buffer (create_q8_irpa.py:185-224); the layer's rows start at
+ * w_stacked + layer*BPL, row n at + n*K/32*34 (dispatch_3.cu:17-32).
+ * Replaces the body of @q8_fused_gemv (qwen3_full.mlir:536-589) as executed
+ * by decode_dispatch_{3,4,12,18,20}. */
+int q8gemv(int kind, const void* w_stacked, int64_t layer, const void* x_f16,
+           void* y_f16, void* stream);
+
+/* Generic form over one layer's bytes: n_rows >= 1 rows of K = 1024, 2048 or
+ * 3072 columns starting at w_layer. */
+int q8gemv_rows(const void* w_layer, int64_t n_rows, int64_t k, const void* x_f16,
+                void* y_f16, void* stream);
+
+/* The five Q8 dispatches under the reference's executable names.
+ * decode_dispatch_3_matmul_2048x1x1024_f16   kernels/cuda/dispatch_3.cu:8-13
+ * decode_dispatch_4_matmul_1024x1x1024_f16   kernels/cuda/dispatch_4.cu:8-13
+ * decode_dispatch_12_matmul_1024x1x2048_f16  kernels/cuda/dispatch_12.cu
+ * decode_dispatch_18_matmul_6144x1x1024_f16  kernels/cuda/dispatch_18.cu
+ * decode_dispatch_20_matmul_1024x1x3072_f16  kernels/cuda/dispatch_20.cu
+ * The reference's (binding, push-constant) pairs become (w_stacked, layer,
+ * x, y): the layer push constants c0|c1<<32 (dispatch_3.cu:19) are `layer`;
+ * dispatch_4's output byte offset c0 (dispatch_4.cu:19-22) is folded into y. */
+int decode_dispatch_3_matmul_2048x1x1024_f16(const void* q8_stacked, int64_t layer,
+                                             const void* x_f16, void* y_f16, void* stream);
+int decode_dispatch_4_matmul_1024x1x1024_f16(const void* q8_stacked, int64_t layer,
+                                             const void* x_f16, void* y_f16, void* stream);
+int decode_dispatch_12_matmul_1024x1x2048_f16(const void* q8_stacked, int64_t layer,
+                                              const void* x_f16, void* y_f16, void* stream);
+int decode_dispatch_18_matmul_6144x1x1024_f16(const void* q8_stacked, int64_t layer,
+                                              const void* x_f16, void* y_f16, void* stream);
+int decode_dispatch_20_matmul_1024x1x3072_f16(const void* q8_stacked, int64_t layer,
+                                              const void* x_f16, void* y_f16, void* stream);
+
+/* ---- f16 vocab GEMV + fused two-phase argmax ---- */
+
+/* Workspace for the argmax partials: a completion counter plus one 8-byte
+ * partial per workgroup.  The counter must be zero before the first launch
+ * that uses a workspace (vocab_argmax_workspace_reset, or a zero fill); every
+ * launch leaves it zero again.  Two launches must not share a workspace
+ * concurrently. */
+size_t vocab_argmax_workspace_bytes(void);
+int vocab_argmax_workspace_reset(void* workspace, void* stream);
+
+/* logits[151936] = f16(W[151936,1024] . x) and *token = the lowest index of
+ * the maximal f16 logit (-1 if none is > -inf; NaN never wins).
+ * decode_dispatch_24_matmul_151936x1x1024_f16 (kernels/cuda/dispatch_24.cu:11-46)
+ * fused with the tiled argmax of qwen3_full.mlir:1469-1511 (i64 there, int32
+ * here).  logits may be NULL to skip writing them. */
+int vocab_gemv_argmax(const void* w_f16, const void* x_f16, void* logits_f16,
+                      int32_t* token, void* workspace, void* stream);
+int decode_dispatch_24_matmul_151936x1x1024_f16(const void* w_f16, const void* x_f16,
+                                                void* logits_f16, int32_t* token,
+                                                void* workspace, void* stream);
+
+/* Generic form: n_rows in [1, 2^31) rows of K = 1024. */
+int f16_gemv_argmax_rows(const void* w_f16, int64_t n_rows, const void* x_f16,
+                         void* logits_f16, int32_t* token, void* workspace, void* stream);
+
+/* ---- launch-shape tuning (no reference counterpart) ---- */
+
+/* Row quads per wave (1,2,3,4,6 for K=1024; 1,2,4 for K=2048/3072) used for
+ * K = 1024*p.  Applies to later launches. */
+int q8gemv_set_rows_per_wave(int64_t k, int quads_per_wave);
+int q8gemv_get_rows_per_wave(int64_t k, int* quads_per_wave);
+/* Workgroups (256 threads) of the vocab kernel, 1..4096; 0 = default
+ * (4 per compute unit). */
+int vocab_set_workgroups(int workgroups);
+int vocab_get_workgroups(int* workgroups);
+
+/* ---- device runtime helpers (no reference counterpart: the IREE HAL owns
+ * allocation, streams and timing there, benchmark.py:34-49) ---- */
+int q8rt_device_count(int* count);
+int q8rt_set_device(int device);
+int q8rt_device_info(char* name, int name_len, int* compute_units, int64_t* total_mem);
+int q8rt_malloc(void** ptr, size_t bytes);
+int q8rt_free(void* ptr);
+int q8rt_memcpy_htod(void* dst_device, const void* src_host, size_t bytes);
+int q8rt_memcpy_dtoh(void* dst_host, const void* src_device, size_t bytes);
+int q8rt_memcpy_dtod(void* dst_device, const void* src_device, size_t bytes);
+int q8rt_memset(void* ptr, int value, size_t bytes);
+int q8rt_device_synchronize(void);
+int q8rt_stream_create(void** stream);
+int q8rt_stream_destroy(void* stream);
+int q8rt_stream_synchronize(void* stream);
+int q8rt_event_create(void** event);
+int q8rt_event_destroy(void* event);
+int q8rt_event_record(void* event, void* stream);
+int q8rt_event_synchronize(void* event);
+int q8rt_event_elapsed_ms(float* ms, void* start, void* stop);
+/* Stream capture into a hipGraph and replay. */
+int q8rt_graph_begin_capture(void* stream);
+int q8rt_graph_end_capture(void* stream, void** graph_exec);
+int q8rt_graph_launch(void* graph_exec, void* stream);
+int q8rt_graph_destroy(void* graph_exec);
+/* The calling thread's next kernel launch through this library records
+ * `start` / `stop` around that kernel alone (hipExtModuleLaunchKernel
+ * events), for per-kernel timing.  One-shot. */
+int q8rt_time_next_launch(void* start_event, void* stop_event);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

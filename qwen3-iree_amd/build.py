@@ -1,0 +1,73 @@
+"""Build recipe for the gfx950 code object and the C-ABI shim library.
+
+  lib/q8gemv_gfx950.hsaco  hipcc --genco --offload-arch=gfx950 of csrc/q8gemv_kernels.hip
+  lib/libq8gemv.so         g++ of csrc/q8gemv_shim.cpp against libamdhip64
+
+Both cross-compile without a GPU.  Run as `python qwen3-iree_amd/build.py`.
+"""
+from __future__ import annotations
+
+import os
+import subprocess
+import sys
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+REPO = PKG.parent
+CSRC = PKG / "csrc"
+LIB = PKG / "lib"
+ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
+
+CODE_OBJECT = LIB / "q8gemv_gfx950.hsaco"
+SHIM = LIB / "libq8gemv.so"
+
+HIPCC_FLAGS = [
+    "--offload-arch=gfx950",
+    "-O3",
+    "-std=c++17",
+    # no packed-FP32 instructions anywhere in the device code
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "--genco",
+    "--no-gpu-bundle-output",
+]
+
+
+def _run(cmd: list[str]) -> None:
+    proc = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    out = "\n".join(l for l in proc.stdout.splitlines() if "packed-fp32-ops" not in l)
+    if proc.returncode != 0:
+        raise RuntimeError(f"build step failed ({proc.returncode}): {' '.join(cmd)}\n{out}")
+
+
+def build_code_object() -> Path:
+    LIB.mkdir(exist_ok=True)
+    tmp = CODE_OBJECT.with_suffix(".hsaco.tmp")
+    _run([str(ROCM / "bin" / "hipcc"), *HIPCC_FLAGS, str(CSRC / "q8gemv_kernels.hip"), "-o", str(tmp)])
+    os.replace(tmp, CODE_OBJECT)
+    return CODE_OBJECT
+
+
+def build_shim() -> Path:
+    LIB.mkdir(exist_ok=True)
+    tmp = SHIM.with_suffix(".so.tmp")
+    _run([
+        "g++", "-O2", "-std=c++17", "-Wall", "-Wextra", "-fPIC", "-shared",
+        "-D__HIP_PLATFORM_AMD__",
+        f"-I{ROCM / 'include'}", f"-I{REPO / 'include'}",
+        str(CSRC / "q8gemv_shim.cpp"),
+        f"-L{ROCM / 'lib'}", "-lamdhip64", "-ldl", f"-Wl,-rpath,{ROCM / 'lib'}",
+        "-o", str(tmp),
+    ])
+    os.replace(tmp, SHIM)
+    return SHIM
+
+
+def build_all() -> tuple[Path, Path]:
+    return build_code_object(), build_shim()
+
+
+if __name__ == "__main__":
+    co, so = build_all()
+    print(co)
+    print(so)
+    sys.exit(0)

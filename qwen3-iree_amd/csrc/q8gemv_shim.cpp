@@ -1,0 +1,486 @@
+// C-ABI shim over the prebuilt gfx950 code object (q8gemv_kernels.hip).
+//
+// Host side only: hipModuleLoad / hipModuleGetFunction at init, then argument
+// validation and hipModuleLaunchKernel per call.  The ABI is declared in
+// include/q8gemv.h.
+#include "q8gemv.h"
+
+#include <dlfcn.h>
+#include <hip/hip_runtime_api.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+
+// hipExtModuleLaunchKernel lives in hip/hip_ext.h, which pulls in the device
+// headers; its C declaration is all the shim needs.
+extern "C" hipError_t hipExtModuleLaunchKernel(hipFunction_t f, uint32_t globalWorkSizeX,
+                                               uint32_t globalWorkSizeY, uint32_t globalWorkSizeZ,
+                                               uint32_t localWorkSizeX, uint32_t localWorkSizeY,
+                                               uint32_t localWorkSizeZ, size_t sharedMemBytes,
+                                               hipStream_t hStream, void** kernelParams,
+                                               void** extra, hipEvent_t startEvent,
+                                               hipEvent_t stopEvent, uint32_t flags);
+
+namespace {
+
+struct KindInfo {
+  const char* name;
+  int64_t n, k;
+};
+
+// create_q8_irpa.py:185-224 (shapes), qwen3_full.mlir:772-777 (stacked params)
+constexpr KindInfo kKinds[5] = {
+    {"attn_q", 2048, 1024},
+    {"attn_kv", 1024, 1024},
+    {"attn_o", 1024, 2048},
+    {"gate_up", 6144, 1024},
+    {"ffn_dn", 1024, 3072},
+};
+
+constexpr int kMaxQuads = 6;
+constexpr int kVocabMaxWorkgroups = 4096;
+constexpr size_t kWsHeader = 16;
+
+// Row quads per wave compiled for each P = K/1024 (index P-1).
+constexpr int kQuadsAvail[3][kMaxQuads + 1] = {
+    {0, 1, 1, 1, 1, 0, 1},  // P=1: 1,2,3,4,6
+    {0, 1, 1, 0, 1, 0, 0},  // P=2: 1,2,4
+    {0, 1, 1, 0, 1, 0, 0},  // P=3: 1,2,4
+};
+
+struct State {
+  std::mutex mu;
+  bool ready = false;
+  int device = -1;
+  int compute_units = 0;
+  hipModule_t module = nullptr;
+  hipFunction_t q8fn[3][kMaxQuads + 1] = {};
+  hipFunction_t vocab = nullptr;
+  hipFunction_t ws_reset = nullptr;
+  int quads[3] = {1, 1, 1};
+  int vocab_wgs = 0;  // 0 = default
+};
+
+State g;
+
+thread_local std::string t_err;
+thread_local hipEvent_t t_start = nullptr;
+thread_local hipEvent_t t_stop = nullptr;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  t_err = buf;
+  return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+  return fail(Q8_ERR_HIP, "%s failed: %s (%d)", what, hipGetErrorString(e), (int)e);
+}
+
+#define HIP_TRY(expr)                                 \
+  do {                                                \
+    hipError_t _e = (expr);                           \
+    if (_e != hipSuccess) return hip_fail(_e, #expr); \
+  } while (0)
+
+bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+std::string default_code_object() {
+  Dl_info info;
+  if (dladdr(reinterpret_cast<void*>(&q8gemv_init), &info) && info.dli_fname) {
+    std::string p(info.dli_fname);
+    size_t slash = p.rfind('/');
+    std::string dir = slash == std::string::npos ? std::string(".") : p.substr(0, slash);
+    return dir + "/q8gemv_gfx950.hsaco";
+  }
+  return "q8gemv_gfx950.hsaco";
+}
+
+int launch(hipFunction_t fn, uint32_t grid, uint32_t block, void** args, hipStream_t stream) {
+  hipError_t e;
+  if (t_start != nullptr || t_stop != nullptr) {
+    hipEvent_t s = t_start, p = t_stop;
+    t_start = t_stop = nullptr;
+    e = hipExtModuleLaunchKernel(fn, grid * block, 1, 1, block, 1, 1, 0, stream, args, nullptr,
+                                 s, p, 0);
+  } else {
+    e = hipModuleLaunchKernel(fn, grid, 1, 1, block, 1, 1, 0, stream, args, nullptr);
+  }
+  if (e != hipSuccess) return hip_fail(e, "kernel launch");
+  return Q8_OK;
+}
+
+int check_ready() {
+  if (!g.ready) return fail(Q8_ERR_NOT_INITIALIZED, "q8gemv_init() has not succeeded");
+  return Q8_OK;
+}
+
+int q8_launch(const void* w_layer, int64_t n_rows, int64_t k, const void* x, void* y,
+              void* stream) {
+  const int p = (int)(k / 1024);
+  const int quads = g.quads[p - 1];
+  hipFunction_t fn = g.q8fn[p - 1][quads];
+  const int64_t rows_per_wg = 4LL * quads;
+  const int64_t grid = (n_rows + rows_per_wg - 1) / rows_per_wg;
+  const void* w_arg = w_layer;
+  const void* x_arg = x;
+  void* y_arg = y;
+  int n_arg = (int)n_rows;
+  void* args[] = {&w_arg, &x_arg, &y_arg, &n_arg};
+  return launch(fn, (uint32_t)grid, 64, args, static_cast<hipStream_t>(stream));
+}
+
+int vocab_grid() {
+  if (g.vocab_wgs > 0) return g.vocab_wgs;
+  int wgs = 4 * (g.compute_units > 0 ? g.compute_units : 256);
+  return wgs > kVocabMaxWorkgroups ? kVocabMaxWorkgroups : wgs;
+}
+
+}  // namespace
+
+extern "C" {
+
+int q8gemv_init(const char* code_object_path) {
+  std::lock_guard<std::mutex> lock(g.mu);
+  if (g.ready) return Q8_OK;
+  std::string path = code_object_path ? std::string(code_object_path) : default_code_object();
+  FILE* f = std::fopen(path.c_str(), "rb");
+  if (!f) return fail(Q8_ERR_CODE_OBJECT, "cannot open code object %s", path.c_str());
+  std::fclose(f);
+  int dev = 0;
+  HIP_TRY(hipGetDevice(&dev));
+  hipModule_t mod = nullptr;
+  hipError_t e = hipModuleLoad(&mod, path.c_str());
+  if (e != hipSuccess)
+    return fail(Q8_ERR_CODE_OBJECT, "hipModuleLoad(%s): %s", path.c_str(), hipGetErrorString(e));
+  for (int p = 1; p <= 3; ++p) {
+    for (int r = 1; r <= kMaxQuads; ++r) {
+      if (!kQuadsAvail[p - 1][r]) continue;
+      char name[64];
+      std::snprintf(name, sizeof(name), "q8gemv_p%d_r%d", p, r);
+      e = hipModuleGetFunction(&g.q8fn[p - 1][r], mod, name);
+      if (e != hipSuccess) {
+        (void)hipModuleUnload(mod);
+        return fail(Q8_ERR_CODE_OBJECT, "kernel %s missing from %s", name, path.c_str());
+      }
+    }
+  }
+  e = hipModuleGetFunction(&g.vocab, mod, "vocab_gemv_argmax_k1024");
+  if (e == hipSuccess) e = hipModuleGetFunction(&g.ws_reset, mod, "vocab_workspace_reset");
+  if (e != hipSuccess) {
+    (void)hipModuleUnload(mod);
+    return fail(Q8_ERR_CODE_OBJECT, "vocab kernels missing from %s", path.c_str());
+  }
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+    cus = 256;
+  g.module = mod;
+  g.device = dev;
+  g.compute_units = cus;
+  // Launch shapes: one row quad per wave for every K (the widest grids).
+  g.quads[0] = g.quads[1] = g.quads[2] = 1;
+  g.vocab_wgs = 0;
+  g.ready = true;
+  return Q8_OK;
+}
+
+void q8gemv_shutdown(void) {
+  std::lock_guard<std::mutex> lock(g.mu);
+  if (!g.ready) return;
+  (void)hipModuleUnload(g.module);
+  g.module = nullptr;
+  std::memset(g.q8fn, 0, sizeof(g.q8fn));
+  g.vocab = g.ws_reset = nullptr;
+  g.ready = false;
+}
+
+const char* q8gemv_last_error(void) { return t_err.c_str(); }
+
+int q8gemv_kind_shape(int kind, int64_t* n, int64_t* k, int64_t* bytes_per_layer) {
+  if (kind < 0 || kind > 4) return fail(Q8_ERR_INVALID_KIND, "invalid kind %d", kind);
+  const KindInfo& ki = kKinds[kind];
+  if (n) *n = ki.n;
+  if (k) *k = ki.k;
+  if (bytes_per_layer) *bytes_per_layer = ki.n * ki.k / Q8_BLOCK_ELEMS * Q8_BLOCK_BYTES;
+  return Q8_OK;
+}
+
+int q8gemv_rows(const void* w_layer, int64_t n_rows, int64_t k, const void* x_f16, void* y_f16,
+                void* stream) {
+  if (!w_layer || !x_f16 || !y_f16) return fail(Q8_ERR_NULL_POINTER, "null w, x or y");
+  if (k != 1024 && k != 2048 && k != 3072)
+    return fail(Q8_ERR_BAD_SHAPE, "K=%lld not in {1024, 2048, 3072}", (long long)k);
+  if (n_rows < 1 || n_rows > (1LL << 24))
+    return fail(Q8_ERR_BAD_SHAPE, "n_rows=%lld outside [1, 2^24]", (long long)n_rows);
+  if (!aligned(w_layer, 16)) return fail(Q8_ERR_MISALIGNED, "weights not 16-byte aligned");
+  if (!aligned(x_f16, 16)) return fail(Q8_ERR_MISALIGNED, "x not 16-byte aligned");
+  if (!aligned(y_f16, 2)) return fail(Q8_ERR_MISALIGNED, "y not 2-byte aligned");
+  int rc = check_ready();
+  if (rc) return rc;
+  return q8_launch(w_layer, n_rows, k, x_f16, y_f16, stream);
+}
+
+int q8gemv(int kind, const void* w_stacked, int64_t layer, const void* x_f16, void* y_f16,
+           void* stream) {
+  if (kind < 0 || kind > 4) return fail(Q8_ERR_INVALID_KIND, "invalid kind %d", kind);
+  if (!w_stacked || !x_f16 || !y_f16) return fail(Q8_ERR_NULL_POINTER, "null w, x or y");
+  if (layer < 0 || layer >= Q8_NUM_LAYERS)
+    return fail(Q8_ERR_LAYER_RANGE, "layer %lld outside [0, %d)", (long long)layer,
+                Q8_NUM_LAYERS);
+  const KindInfo& ki = kKinds[kind];
+  const int64_t bpl = ki.n * ki.k / Q8_BLOCK_ELEMS * Q8_BLOCK_BYTES;
+  const void* w_layer = static_cast<const uint8_t*>(w_stacked) + layer * bpl;
+  return q8gemv_rows(w_layer, ki.n, ki.k, x_f16, y_f16, stream);
+}
+
+int decode_dispatch_3_matmul_2048x1x1024_f16(const void* q8_stacked, int64_t layer,
+                                             const void* x_f16, void* y_f16, void* stream) {
+  return q8gemv(Q8_ATTN_Q, q8_stacked, layer, x_f16, y_f16, stream);
+}
+int decode_dispatch_4_matmul_1024x1x1024_f16(const void* q8_stacked, int64_t layer,
+                                             const void* x_f16, void* y_f16, void* stream) {
+  return q8gemv(Q8_ATTN_KV, q8_stacked, layer, x_f16, y_f16, stream);
+}
+int decode_dispatch_12_matmul_1024x1x2048_f16(const void* q8_stacked, int64_t layer,
+                                              const void* x_f16, void* y_f16, void* stream) {
+  return q8gemv(Q8_ATTN_O, q8_stacked, layer, x_f16, y_f16, stream);
+}
+int decode_dispatch_18_matmul_6144x1x1024_f16(const void* q8_stacked, int64_t layer,
+                                              const void* x_f16, void* y_f16, void* stream) {
+  return q8gemv(Q8_GATE_UP, q8_stacked, layer, x_f16, y_f16, stream);
+}
+int decode_dispatch_20_matmul_1024x1x3072_f16(const void* q8_stacked, int64_t layer,
+                                              const void* x_f16, void* y_f16, void* stream) {
+  return q8gemv(Q8_FFN_DN, q8_stacked, layer, x_f16, y_f16, stream);
+}
+
+size_t vocab_argmax_workspace_bytes(void) { return kWsHeader + 8u * kVocabMaxWorkgroups; }
+
+int vocab_argmax_workspace_reset(void* workspace, void* stream) {
+  if (!workspace) return fail(Q8_ERR_NULL_POINTER, "null workspace");
+  if (!aligned(workspace, 16)) return fail(Q8_ERR_MISALIGNED, "workspace not 16-byte aligned");
+  int rc = check_ready();
+  if (rc) return rc;
+  void* ws = workspace;
+  void* args[] = {&ws};
+  return launch(g.ws_reset, 1, 64, args, static_cast<hipStream_t>(stream));
+}
+
+int f16_gemv_argmax_rows(const void* w_f16, int64_t n_rows, const void* x_f16, void* logits_f16,
+                         int32_t* token, void* workspace, void* stream) {
+  if (!w_f16 || !x_f16 || !token || !workspace)
+    return fail(Q8_ERR_NULL_POINTER, "null w, x, token or workspace");
+  if (n_rows < 1 || n_rows >= (1LL << 31))
+    return fail(Q8_ERR_BAD_SHAPE, "n_rows=%lld outside [1, 2^31)", (long long)n_rows);
+  if (!aligned(w_f16, 16)) return fail(Q8_ERR_MISALIGNED, "weights not 16-byte aligned");
+  if (!aligned(x_f16, 16)) return fail(Q8_ERR_MISALIGNED, "x not 16-byte aligned");
+  if (logits_f16 && !aligned(logits_f16, 2))
+    return fail(Q8_ERR_MISALIGNED, "logits not 2-byte aligned");
+  if (!aligned(token, 4)) return fail(Q8_ERR_MISALIGNED, "token not 4-byte aligned");
+  if (!aligned(workspace, 16)) return fail(Q8_ERR_MISALIGNED, "workspace not 16-byte aligned");
+  int rc = check_ready();
+  if (rc) return rc;
+  const void* w_arg = w_f16;
+  const void* x_arg = x_f16;
+  void* l_arg = logits_f16;
+  int n_arg = (int)n_rows;
+  int32_t* t_arg = token;
+  void* ws_arg = workspace;
+  void* args[] = {&w_arg, &x_arg, &l_arg, &n_arg, &t_arg, &ws_arg};
+  return launch(g.vocab, (uint32_t)vocab_grid(), 256, args, static_cast<hipStream_t>(stream));
+}
+
+int vocab_gemv_argmax(const void* w_f16, const void* x_f16, void* logits_f16, int32_t* token,
+                      void* workspace, void* stream) {
+  return f16_gemv_argmax_rows(w_f16, Q8_VOCAB_ROWS, x_f16, logits_f16, token, workspace, stream);
+}
+
+int decode_dispatch_24_matmul_151936x1x1024_f16(const void* w_f16, const void* x_f16,
+                                                void* logits_f16, int32_t* token,
+                                                void* workspace, void* stream) {
+  return vocab_gemv_argmax(w_f16, x_f16, logits_f16, token, workspace, stream);
+}
+
+int q8gemv_set_rows_per_wave(int64_t k, int quads_per_wave) {
+  if (k != 1024 && k != 2048 && k != 3072)
+    return fail(Q8_ERR_BAD_SHAPE, "K=%lld not in {1024, 2048, 3072}", (long long)k);
+  const int p = (int)(k / 1024);
+  if (quads_per_wave < 1 || quads_per_wave > kMaxQuads || !kQuadsAvail[p - 1][quads_per_wave])
+    return fail(Q8_ERR_BAD_ARGUMENT, "no kernel with %d row quads per wave for K=%lld",
+                quads_per_wave, (long long)k);
+  g.quads[p - 1] = quads_per_wave;
+  return Q8_OK;
+}
+
+int q8gemv_get_rows_per_wave(int64_t k, int* quads_per_wave) {
+  if (k != 1024 && k != 2048 && k != 3072)
+    return fail(Q8_ERR_BAD_SHAPE, "K=%lld not in {1024, 2048, 3072}", (long long)k);
+  if (!quads_per_wave) return fail(Q8_ERR_NULL_POINTER, "null output");
+  *quads_per_wave = g.quads[k / 1024 - 1];
+  return Q8_OK;
+}
+
+int vocab_set_workgroups(int workgroups) {
+  if (workgroups < 0 || workgroups > kVocabMaxWorkgroups)
+    return fail(Q8_ERR_BAD_ARGUMENT, "workgroups %d outside [0, %d]", workgroups,
+                kVocabMaxWorkgroups);
+  g.vocab_wgs = workgroups;
+  return Q8_OK;
+}
+
+int vocab_get_workgroups(int* workgroups) {
+  if (!workgroups) return fail(Q8_ERR_NULL_POINTER, "null output");
+  *workgroups = vocab_grid();
+  return Q8_OK;
+}
+
+// ---------------------------------------------------------------- runtime
+
+int q8rt_device_count(int* count) {
+  if (!count) return fail(Q8_ERR_NULL_POINTER, "null count");
+  HIP_TRY(hipGetDeviceCount(count));
+  return Q8_OK;
+}
+
+int q8rt_set_device(int device) {
+  HIP_TRY(hipSetDevice(device));
+  return Q8_OK;
+}
+
+int q8rt_device_info(char* name, int name_len, int* compute_units, int64_t* total_mem) {
+  int dev = 0;
+  HIP_TRY(hipGetDevice(&dev));
+  hipDeviceProp_t prop;
+  HIP_TRY(hipGetDeviceProperties(&prop, dev));
+  if (name && name_len > 0) {
+    std::snprintf(name, (size_t)name_len, "%s (%s)", prop.name, prop.gcnArchName);
+  }
+  if (compute_units) *compute_units = prop.multiProcessorCount;
+  if (total_mem) *total_mem = (int64_t)prop.totalGlobalMem;
+  return Q8_OK;
+}
+
+int q8rt_malloc(void** ptr, size_t bytes) {
+  if (!ptr) return fail(Q8_ERR_NULL_POINTER, "null ptr");
+  HIP_TRY(hipMalloc(ptr, bytes));
+  return Q8_OK;
+}
+
+int q8rt_free(void* ptr) {
+  HIP_TRY(hipFree(ptr));
+  return Q8_OK;
+}
+
+int q8rt_memcpy_htod(void* dst, const void* src, size_t bytes) {
+  HIP_TRY(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice));
+  return Q8_OK;
+}
+
+int q8rt_memcpy_dtoh(void* dst, const void* src, size_t bytes) {
+  HIP_TRY(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost));
+  return Q8_OK;
+}
+
+int q8rt_memcpy_dtod(void* dst, const void* src, size_t bytes) {
+  HIP_TRY(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToDevice));
+  return Q8_OK;
+}
+
+int q8rt_memset(void* ptr, int value, size_t bytes) {
+  HIP_TRY(hipMemset(ptr, value, bytes));
+  return Q8_OK;
+}
+
+int q8rt_device_synchronize(void) {
+  HIP_TRY(hipDeviceSynchronize());
+  return Q8_OK;
+}
+
+int q8rt_stream_create(void** stream) {
+  if (!stream) return fail(Q8_ERR_NULL_POINTER, "null stream");
+  hipStream_t s = nullptr;
+  HIP_TRY(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+  *stream = s;
+  return Q8_OK;
+}
+
+int q8rt_stream_destroy(void* stream) {
+  HIP_TRY(hipStreamDestroy(static_cast<hipStream_t>(stream)));
+  return Q8_OK;
+}
+
+int q8rt_stream_synchronize(void* stream) {
+  HIP_TRY(hipStreamSynchronize(static_cast<hipStream_t>(stream)));
+  return Q8_OK;
+}
+
+int q8rt_event_create(void** event) {
+  if (!event) return fail(Q8_ERR_NULL_POINTER, "null event");
+  hipEvent_t e = nullptr;
+  HIP_TRY(hipEventCreate(&e));
+  *event = e;
+  return Q8_OK;
+}
+
+int q8rt_event_destroy(void* event) {
+  HIP_TRY(hipEventDestroy(static_cast<hipEvent_t>(event)));
+  return Q8_OK;
+}
+
+int q8rt_event_record(void* event, void* stream) {
+  HIP_TRY(hipEventRecord(static_cast<hipEvent_t>(event), static_cast<hipStream_t>(stream)));
+  return Q8_OK;
+}
+
+int q8rt_event_synchronize(void* event) {
+  HIP_TRY(hipEventSynchronize(static_cast<hipEvent_t>(event)));
+  return Q8_OK;
+}
+
+int q8rt_event_elapsed_ms(float* ms, void* start, void* stop) {
+  if (!ms) return fail(Q8_ERR_NULL_POINTER, "null ms");
+  HIP_TRY(hipEventElapsedTime(ms, static_cast<hipEvent_t>(start), static_cast<hipEvent_t>(stop)));
+  return Q8_OK;
+}
+
+int q8rt_graph_begin_capture(void* stream) {
+  HIP_TRY(hipStreamBeginCapture(static_cast<hipStream_t>(stream), hipStreamCaptureModeThreadLocal));
+  return Q8_OK;
+}
+
+int q8rt_graph_end_capture(void* stream, void** graph_exec) {
+  if (!graph_exec) return fail(Q8_ERR_NULL_POINTER, "null graph_exec");
+  hipGraph_t graph = nullptr;
+  HIP_TRY(hipStreamEndCapture(static_cast<hipStream_t>(stream), &graph));
+  hipGraphExec_t exec = nullptr;
+  hipError_t e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+  (void)hipGraphDestroy(graph);
+  if (e != hipSuccess) return hip_fail(e, "hipGraphInstantiate");
+  *graph_exec = exec;
+  return Q8_OK;
+}
+
+int q8rt_graph_launch(void* graph_exec, void* stream) {
+  HIP_TRY(hipGraphLaunch(static_cast<hipGraphExec_t>(graph_exec), static_cast<hipStream_t>(stream)));
+  return Q8_OK;
+}
+
+int q8rt_graph_destroy(void* graph_exec) {
+  HIP_TRY(hipGraphExecDestroy(static_cast<hipGraphExec_t>(graph_exec)));
+  return Q8_OK;
+}
+
+int q8rt_time_next_launch(void* start_event, void* stop_event) {
+  t_start = static_cast<hipEvent_t>(start_event);
+  t_stop = static_cast<hipEvent_t>(stop_event);
+  return Q8_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,129 @@
+"""CPU-side checks of the C ABI (no GPU): the library loads, exports every
+symbol include/q8gemv.h declares, and validates arguments before touching
+the device, reporting status codes instead of aborting."""
+from __future__ import annotations
+
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+REPO = Path(__file__).resolve().parent.parent
+HEADER = REPO / "include" / "q8gemv.h"
+
+A16 = 0x10000  # fake, 16-byte aligned "device" addresses: never dereferenced here
+
+
+def declared_functions() -> list[str]:
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return re.findall(r"^(?:int|void|size_t|const char\*)\s+(\w+)\s*\(", text, flags=re.M)
+
+
+def test_header_declares_expected_entry_points():
+    names = set(declared_functions())
+    for required in ("q8gemv_init", "q8gemv", "vocab_gemv_argmax",
+                     "vocab_argmax_workspace_bytes", "q8gemv_shutdown",
+                     "decode_dispatch_3_matmul_2048x1x1024_f16",
+                     "decode_dispatch_24_matmul_151936x1x1024_f16"):
+        assert required in names
+
+
+def test_library_exports_every_declared_symbol(Q):
+    lib = Q.load_library()
+    missing = [n for n in declared_functions() if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_python_binding_covers_header(Q):
+    assert set(declared_functions()) == set(Q._SIGNATURES)
+
+
+def test_kind_shapes_and_bytes_per_layer(Q):
+    want = {0: (2048, 1024, 2228224), 1: (1024, 1024, 1114112), 2: (1024, 2048, 2228224),
+            3: (6144, 1024, 6684672), 4: (1024, 3072, 3342336)}
+    for kind, shape in want.items():
+        assert Q.kind_shape(kind) == shape
+        d = Q.Q8_KINDS[kind]
+        assert (d.n, d.k, d.bytes_per_layer) == shape
+    with pytest.raises(Q.Q8GemvError) as e:
+        Q.kind_shape(5)
+    assert e.value.code == Q.Q8_ERR_INVALID_KIND
+
+
+def test_dispatch_table_mirrors_reference_exports(Q):
+    assert {o: d.export for o, d in Q.DISPATCHES.items()} == {
+        3: "decode_dispatch_3_matmul_2048x1x1024_f16",
+        4: "decode_dispatch_4_matmul_1024x1x1024_f16",
+        12: "decode_dispatch_12_matmul_1024x1x2048_f16",
+        18: "decode_dispatch_18_matmul_6144x1x1024_f16",
+        20: "decode_dispatch_20_matmul_1024x1x3072_f16",
+        24: "decode_dispatch_24_matmul_151936x1x1024_f16",
+    }
+    assert Q.VOCAB.bytes_per_layer == 151936 * 2048
+
+
+@pytest.mark.parametrize("call,code", [
+    (lambda L: L.q8gemv(7, A16, 0, A16, A16, None), 2),
+    (lambda L: L.q8gemv(-1, A16, 0, A16, A16, None), 2),
+    (lambda L: L.q8gemv(0, None, 0, A16, A16, None), 3),
+    (lambda L: L.q8gemv(0, A16, 0, None, A16, None), 3),
+    (lambda L: L.q8gemv(0, A16, 0, A16, None, None), 3),
+    (lambda L: L.q8gemv(0, A16, 28, A16, A16, None), 4),
+    (lambda L: L.q8gemv(0, A16, -1, A16, A16, None), 4),
+    (lambda L: L.q8gemv(0, A16 + 8, 0, A16, A16, None), 5),
+    (lambda L: L.q8gemv(0, A16, 0, A16 + 4, A16, None), 5),
+    (lambda L: L.q8gemv(0, A16, 0, A16, A16 + 1, None), 5),
+    (lambda L: L.q8gemv_rows(A16, 16, 512, A16, A16, None), 6),
+    (lambda L: L.q8gemv_rows(A16, 0, 1024, A16, A16, None), 6),
+    (lambda L: L.f16_gemv_argmax_rows(A16, 0, A16, A16, A16, A16, None), 6),
+    (lambda L: L.f16_gemv_argmax_rows(A16, 10, A16, None, None, A16, None), 3),
+    (lambda L: L.vocab_gemv_argmax(A16, A16, A16, A16 + 2, A16, None), 5),
+    (lambda L: L.vocab_gemv_argmax(A16, A16, A16 + 1, A16, A16, None), 5),
+    (lambda L: L.vocab_gemv_argmax(A16, A16, None, A16, A16 + 8, None), 5),
+    (lambda L: L.q8gemv_set_rows_per_wave(1024, 5), 9),
+    (lambda L: L.q8gemv_set_rows_per_wave(2048, 3), 9),
+    (lambda L: L.q8gemv_set_rows_per_wave(4096, 1), 6),
+    (lambda L: L.vocab_set_workgroups(5000), 9),
+])
+def test_argument_validation_before_any_device_work(Q, call, code):
+    lib = Q.load_library()
+    assert call(lib) == code
+    assert Q.last_error()
+
+
+def test_not_initialized_is_reported(Q):
+    lib = Q.load_library()
+    # valid arguments, but no code object loaded in this process
+    assert lib.q8gemv(0, A16, 0, A16, A16, None) == Q.Q8_ERR_NOT_INITIALIZED
+    assert lib.vocab_gemv_argmax(A16, A16, None, A16, A16, None) == Q.Q8_ERR_NOT_INITIALIZED
+    for ordinal in (3, 4, 12, 18, 20):
+        export = Q.DISPATCHES[ordinal].export
+        assert getattr(lib, export)(A16, 0, A16, A16, None) == Q.Q8_ERR_NOT_INITIALIZED
+
+
+def test_missing_code_object_is_an_error(Q, tmp_path):
+    with pytest.raises(Q.Q8GemvError) as e:
+        Q.init(tmp_path / "absent.hsaco")
+    assert e.value.code == Q.Q8_ERR_CODE_OBJECT
+
+
+def test_workspace_size_and_tuning_roundtrip(Q):
+    assert Q.vocab_workspace_bytes() == 16 + 8 * 4096
+    Q.set_rows_per_wave(1024, 2)
+    assert Q.get_rows_per_wave(1024) == 2
+    Q.set_rows_per_wave(1024, 1)
+    Q.set_vocab_workgroups(512)
+    assert Q.get_vocab_workgroups() == 512
+    Q.set_vocab_workgroups(0)
+
+
+def test_code_object_targets_gfx950_and_has_every_kernel():
+    co = REPO / "qwen3-iree_amd" / "lib" / "q8gemv_gfx950.hsaco"
+    data = co.read_bytes()
+    assert data[:4] == b"\x7fELF"
+    assert b"amdgcn-amd-amdhsa--gfx950" in data
+    for name in ("q8gemv_p1_r1", "q8gemv_p2_r1", "q8gemv_p3_r1", "vocab_gemv_argmax_k1024",
+                 "vocab_workspace_reset"):
+        assert name.encode() in data
