@@ -3,16 +3,20 @@
 
 Workload (the headline metric's configuration): the 28-layer stacked
 cold-cache Q8_0 GEMV sweep -- five stacked weight sets (attn_q, attn_kv, attn_o,
-gate_up, ffn_dn; 436,731,904 bytes, more than the 256 MB MALL), for layer
-0..27 the five GEMVs in that order (140 dispatches per step), each with its own
-f16 x and y.  One step = one sweep, replayed from a hipGraph of the 140
-launches through the C ABI.  Inputs are resident in HBM before timing.
+gate_up, ffn_dn; 436,731,904 bytes, more than the 256 MB MALL); for layer
+0..27 the five GEMVs in that order, 140 GEMVs per step, each with its own f16 x
+and y.  Inputs are resident in HBM before timing.
 
-Also measured in the same run:
-  * per-dispatch kernel durations (HIP events bound to each launch), from
-    which the roofline of the dominant kernel is computed;
+One step = one sweep executed as a single batched launch (q8gemv_batch: the
+140 GEMVs listed in sweep order; waves stream the list in order, so the access
+pattern still rotates through the 28 layers).  Measured in the same run:
+  * the same sweep as 140 stream-ordered dispatches of the per-GEMV entry
+    point (the reference's dispatch granularity), replayed from a hipGraph;
   * the f16 vocab GEMV + fused argmax [151936, 1024];
-  * the GEMV share of a decode step (28 x q,k,v,o,gate_up,down + vocab);
+  * the GEMV share of a decode step: 28 x (one batched q/k/v launch, o,
+    gate_up, down) + vocab, stream-ordered, replayed from a hipGraph;
+  * parity of all 140 sweep outputs and of the vocab logits/token against the
+    CPU oracle;
   * the CPU oracle on a bounded sample of the same sweep (cpu_baseline).
 
 Prints one JSON line.  Only --gpus 1 is supported: this path runs on one GPU.
@@ -41,8 +45,24 @@ def log(msg: str) -> None:
 
 
 def algorithmic_bytes(d) -> int:
-    """Weights + x + y of one dispatch, each byte counted once."""
+    """Weights + x + y of one GEMV, each byte counted once."""
     return d.bytes_per_layer + 2 * d.k + 2 * d.n
+
+
+def timed_ms(Q, stream, fn, reps: int) -> float:
+    """Mean ms per call of fn() over `reps` back-to-back calls on `stream`,
+    bracketed by HIP events on that stream."""
+    e0, e1 = Q.Event(), Q.Event()
+    stream.synchronize()
+    e0.record(stream)
+    for _ in range(reps):
+        fn()
+    e1.record(stream)
+    e1.synchronize()
+    ms = e0.elapsed_ms(e1) / reps
+    e0.destroy()
+    e1.destroy()
+    return ms
 
 
 def main() -> int:
@@ -50,9 +70,10 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--kernel-reps", type=int, default=5, help="timed sweeps for per-kernel events")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline sample budget")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-graph", action="store_true",
+                    help="issue the per-dispatch and decode-step chains eagerly instead of from hipGraphs")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -91,67 +112,51 @@ def main() -> int:
         f"{sweep_bytes} algorithmic bytes per step")
 
     stream = Q.Stream()
+    sweep_order = [(layer, d) for layer in range(layers) for d in kinds]
 
-    def record_sweep():
-        for layer in range(layers):
-            for d in kinds:
-                Q.q8gemv(d.kind, stacks[d.kind][1], layer, xs[(layer, d.kind)][1],
-                         ys[(layer, d.kind)], stream)
-
-    # correctness spot check of the timed configuration (layer 27 gate_up)
-    record_sweep()
-    stream.synchronize()
-
-    graph = Q.Graph(stream, record_sweep)
+    # ------------------------------------------- headline: batched sweep
+    batch = Q.Q8Batch([Q.desc_for_kind(d.kind, stacks[d.kind][1], layer, xs[(layer, d.kind)][1],
+                                       ys[(layer, d.kind)]) for layer, d in sweep_order])
     for _ in range(args.warmup):
-        graph.launch(stream)
-    stream.synchronize()
-
-    ev0, ev1 = Q.Event(), Q.Event()
-    Q.synchronize()
+        batch.launch(stream)
     t_wall = time.perf_counter()
-    ev0.record(stream)
-    for _ in range(args.steps):
-        graph.launch(stream)
-    ev1.record(stream)
-    ev1.synchronize()
-    Q.synchronize()
+    ms_per_step = timed_ms(Q, stream, lambda: batch.launch(stream), args.steps)
     wall_s = time.perf_counter() - t_wall
-    ms_total = ev0.elapsed_ms(ev1)
-    ms_per_step = ms_total / args.steps
     value = sweep_bytes / (ms_per_step * 1e-3) / 1e9
-    log(f"sweep: {ms_per_step * 1e3:.1f} us/step, {value:.1f} GB/s "
+    log(f"batched sweep: {ms_per_step * 1e3:.2f} us/step, {value:.1f} GB/s "
         f"({100 * value / HBM_PEAK_GBS:.1f}% of peak); host wall {wall_s:.3f}s")
 
-    # ------------------------------------------------- per-kernel durations
-    per_kind = {d.kind: [] for d in kinds}
-    starts = [Q.Event() for _ in range(layers * len(kinds))]
-    stops = [Q.Event() for _ in range(layers * len(kinds))]
-    for rep in range(args.kernel_reps):
-        i = 0
-        for layer in range(layers):
-            for d in kinds:
-                Q.time_next_launch(starts[i], stops[i])
-                Q.q8gemv(d.kind, stacks[d.kind][1], layer, xs[(layer, d.kind)][1],
-                         ys[(layer, d.kind)], stream)
-                i += 1
-        stream.synchronize()
-        i = 0
-        for layer in range(layers):
-            for d in kinds:
-                per_kind[d.kind].append(starts[i].elapsed_ms(stops[i]) * 1e3)
-                i += 1
-    kern = {}
-    for d in kinds:
-        us = float(np.mean(per_kind[d.kind]))
-        gbs = algorithmic_bytes(d) / (us * 1e-6) / 1e9
-        kern[d.name] = {"avg_us": round(us, 3), "median_us": round(float(np.median(per_kind[d.kind])), 3),
-                        "GBps": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
-                        "bytes": algorithmic_bytes(d), "launches": len(per_kind[d.kind])}
-    sum_kernel_us = sum(kern[d.name]["avg_us"] for d in kinds) * layers
-    dominant = max(kinds, key=lambda d: kern[d.name]["avg_us"])
-    dk = kern[dominant.name]
-    log("kernels: " + ", ".join(f"{n} {v['avg_us']:.2f}us {v['GBps']:.0f}GB/s" for n, v in kern.items()))
+    # parity of every sweep output (the last timed launch wrote them)
+    sys.path.insert(0, str(REPO / "oracle"))
+    import oracle as O  # the checker; also the CPU baseline below
+
+    fails = floor = 0
+    for layer, d in sweep_order:
+        raw = stacks[d.kind][0][layer]
+        x = xs[(layer, d.kind)][0]
+        rep = O.gemv_tolerance_report(ys[(layer, d.kind)].download(np.float16),
+                                      O.q8_gemv(raw, d.n, d.k, x), O.q8_gemv_f64(raw, d.n, d.k, x)[1])
+        fails += rep["fail"]
+        floor += rep["on_floor"]
+    log(f"parity: {fails} failing outputs of {sum(d.n for _, d in sweep_order)} ({floor} on the noise floor)")
+
+    # ------------------------------- the same sweep as 140 dispatches
+    def record_sweep():
+        for layer, d in sweep_order:
+            Q.q8gemv(d.kind, stacks[d.kind][1], layer, xs[(layer, d.kind)][1], ys[(layer, d.kind)], stream)
+
+    if args.no_graph:
+        chain_fn = record_sweep
+    else:
+        graph = Q.Graph(stream, record_sweep)
+        chain_fn = lambda: graph.launch(stream)  # noqa: E731
+    for _ in range(3):
+        chain_fn()
+    chain_reps = max(10, args.steps // 4)
+    chain_ms = timed_ms(Q, stream, chain_fn, chain_reps)
+    chain_gbs = sweep_bytes / (chain_ms * 1e-3) / 1e9
+    log(f"per-dispatch sweep (140 launches{'' if args.no_graph else ', hipGraph'}): "
+        f"{chain_ms * 1e3:.1f} us, {chain_gbs:.1f} GB/s")
 
     # ------------------------------------------------------------- vocab
     t0 = time.time()
@@ -165,63 +170,47 @@ def main() -> int:
     Q.vocab_workspace_reset(ws, stream)
     log(f"vocab inputs ready in {time.time() - t0:.1f}s")
     vocab_bytes = Q.VOCAB.bytes_per_layer + 2 * Q.HIDDEN + 2 * Q.VOCAB_ROWS + 4
+    vocab_fn = lambda: Q.vocab_gemv_argmax(wv_dev, xv_dev, logits_dev, tok_dev, ws, stream)  # noqa: E731
     for _ in range(5):
-        Q.vocab_gemv_argmax(wv_dev, xv_dev, logits_dev, tok_dev, ws, stream)
-    stream.synchronize()
-    vs, ve = Q.Event(), Q.Event()
-    vocab_us = []
-    for _ in range(20):
-        Q.time_next_launch(vs, ve)
-        Q.vocab_gemv_argmax(wv_dev, xv_dev, logits_dev, tok_dev, ws, stream)
-        ve.synchronize()
-        vocab_us.append(vs.elapsed_ms(ve) * 1e3)
-    v_us = float(np.mean(vocab_us))
-    v_gbs = vocab_bytes / (v_us * 1e-6) / 1e9
+        vocab_fn()
+    v_ms = timed_ms(Q, stream, vocab_fn, 50)
+    v_gbs = vocab_bytes / (v_ms * 1e-3) / 1e9
     token = int(tok_dev.download(np.int32, 1)[0])
     logits = logits_dev.download(np.float16, Q.VOCAB_ROWS)
-    log(f"vocab: {v_us:.2f} us, {v_gbs:.0f} GB/s, token {token}")
+    rep_v = O.gemv_tolerance_report(logits, O.f16_gemv(Wv, xv), O.f16_gemv_f64(Wv, xv)[1])
+    own = O.argmax_tiled(logits)
+    log(f"vocab GEMV + argmax: {v_ms * 1e3:.2f} us/op, {v_gbs:.0f} GB/s, token {token} "
+        f"(argmax of own logits {own}, {rep_v['fail']} failing logits)")
 
     # ---------------------------------------- GEMV share of a decode step
-    # 28 x (q, k, v, o, gate_up, down) + vocab, each dispatch ordered after
-    # the previous one on one stream, replayed from a graph.
-    step_y = [Q.DeviceBuffer(2 * 6144) for _ in range(6)]
+    qkv = []
+    step_y = {name: Q.DeviceBuffer(2 * 6144) for name in ("q", "k", "v", "o", "gu", "dn")}
+    for layer in range(layers):
+        xq = xs[(layer, Q.ATTN_Q.kind)][1]
+        qkv.append(Q.Q8Batch([
+            Q.desc_for_kind(Q.ATTN_Q.kind, stacks[Q.ATTN_Q.kind][1], layer, xq, step_y["q"]),
+            Q.desc_for_kind(Q.ATTN_KV.kind, stacks[Q.ATTN_KV.kind][1], layer, xq, step_y["k"]),
+            Q.desc_for_kind(Q.ATTN_KV.kind, stacks[Q.ATTN_KV.kind][1], layer, xq, step_y["v"]),
+        ]))
 
     def record_decode_gemvs():
         for layer in range(layers):
-            for j, d in enumerate(Q.LAYER_ORDER):
-                Q.q8gemv(d.kind, stacks[d.kind][1], layer, xs[(layer, d.kind)][1], step_y[j], stream)
-        Q.vocab_gemv_argmax(wv_dev, xv_dev, logits_dev, tok_dev, ws, stream)
+            qkv[layer].launch(stream)
+            for d, yname in ((Q.ATTN_O, "o"), (Q.GATE_UP, "gu"), (Q.FFN_DN, "dn")):
+                Q.q8gemv(d.kind, stacks[d.kind][1], layer, xs[(layer, d.kind)][1], step_y[yname], stream)
+        vocab_fn()
 
-    dgraph = Q.Graph(stream, record_decode_gemvs)
-    for _ in range(5):
-        dgraph.launch(stream)
-    stream.synchronize()
-    ev0.record(stream)
-    reps = 50
-    for _ in range(reps):
-        dgraph.launch(stream)
-    ev1.record(stream)
-    ev1.synchronize()
-    decode_gemv_us = ev0.elapsed_ms(ev1) * 1e3 / reps
-    log(f"decode-step GEMVs (168 Q8 + vocab): {decode_gemv_us:.1f} us")
+    if args.no_graph:
+        dstep_fn = record_decode_gemvs
+    else:
+        dgraph = Q.Graph(stream, record_decode_gemvs)
+        dstep_fn = lambda: dgraph.launch(stream)  # noqa: E731
+    for _ in range(3):
+        dstep_fn()
+    decode_gemv_us = timed_ms(Q, stream, dstep_fn, 30) * 1e3
+    log(f"decode-step GEMVs (28 x [qkv batch, o, gate_up, down] + vocab): {decode_gemv_us:.1f} us")
 
-    # ---------------------------------------------------- parity spot check
-    sys.path.insert(0, str(REPO / "oracle"))
-    import oracle as O  # the checker; also the CPU baseline below
-
-    d = Q.GATE_UP
-    y_gpu = ys[(layers - 1, d.kind)].download(np.float16)
-    raw = stacks[d.kind][0][layers - 1]
-    x27 = xs[(layers - 1, d.kind)][0]
-    ref = O.q8_gemv(raw, d.n, d.k, x27)
-    _, mag = O.q8_gemv_f64(raw, d.n, d.k, x27)
-    rep_q8 = O.gemv_tolerance_report(y_gpu, ref, mag)
-    ref_v = O.f16_gemv(Wv, xv)
-    _, mag_v = O.f16_gemv_f64(Wv, xv)
-    rep_v = O.gemv_tolerance_report(logits, ref_v, mag_v)
-    parity_ok = rep_q8["fail"] == 0 and rep_v["fail"] == 0 and token == O.argmax_tiled(logits)
-    log(f"parity: gate_up L27 {rep_q8['fail']} fails, vocab {rep_v['fail']} fails, "
-        f"token {token} vs argmax(own logits) {O.argmax_tiled(logits)}")
+    parity_ok = fails == 0 and rep_v["fail"] == 0 and token == own
 
     # ------------------------------------------------------ CPU baseline
     cpu = None
@@ -232,17 +221,16 @@ def main() -> int:
         sweeps = 0
         t0 = time.perf_counter()
         while True:
-            for layer in range(layers):
-                for d in kinds:
-                    O.q8_gemv(host[d.kind][layer], d.n, d.k, hx[(layer, d.kind)])
+            for layer, d in sweep_order:
+                O.q8_gemv(host[d.kind][layer], d.n, d.k, hx[(layer, d.kind)])
             sweeps += 1
             if time.perf_counter() - t0 >= args.cpu_seconds:
                 break
         cpu_s = time.perf_counter() - t0
         cpu_gbs = sweep_bytes * sweeps / cpu_s / 1e9
         cpu = {"value": round(cpu_gbs, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-               "sample": f"{sweeps} full 28-layer sweeps (140 Q8_0 GEMVs each, same inputs) with the "
-                         f"C oracle in the reference kernels' f32 order, OpenMP {threads} threads, "
+               "sample": f"{sweeps} full 28-layer sweeps (140 Q8_0 GEMVs each, the same inputs) with "
+                         f"the C oracle in the reference kernels' f32 order, OpenMP {threads} threads, "
                          f"{cpu_s:.1f}s", "ms_per_step": round(1e3 * cpu_s / sweeps, 3)}
         log(f"cpu oracle: {cpu_gbs:.2f} GB/s over {sweeps} sweeps ({threads} threads)")
 
@@ -260,10 +248,10 @@ def main() -> int:
         "dtype": "q8_0 x f16 -> f32",
         "data": "synthetic (seeded N(0,0.02) weights quantized to Q8_0, N(0,1) f16 x)",
         "config": {
-            "workload": "28-layer stacked cold-cache Q8_0 GEMV sweep (attn_q, attn_kv, attn_o, "
-                        "gate_up, ffn_dn per layer; 140 dispatches; hipGraph replay)",
+            "workload": "28-layer stacked cold-cache Q8_0 GEMV sweep: per layer attn_q, attn_kv, "
+                        "attn_o, gate_up, ffn_dn (140 GEMVs), one batched launch per step",
             "layers": layers,
-            "dispatches_per_step": layers * len(kinds),
+            "gemvs_per_step": len(sweep_order),
             "weight_bytes": weight_bytes,
             "algorithmic_bytes_per_step": sweep_bytes,
             "device": info["name"],
@@ -272,18 +260,19 @@ def main() -> int:
         "us_per_step": round(ms_per_step * 1e3, 2),
         "roofline": {
             "bound": "hbm",
-            "kernel": f"q8gemv {dominant.name} [{dominant.n},{dominant.k}]",
-            "achieved": dk["GBps"],
+            "kernel": "q8gemv_batch_k (28-layer sweep, 140 GEMVs)",
+            "achieved": round(value, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
-            "frac": dk["frac"],
-            "avg_us": dk["avg_us"],
-            "bytes_per_launch": dk["bytes"],
+            "frac": round(value / HBM_PEAK_GBS, 4),
+            "avg_us": round(ms_per_step * 1e3, 2),
+            "bytes_per_launch": sweep_bytes,
             "traffic": None,
         },
-        "kernels": kern,
-        "sum_kernel_us_per_step": round(sum_kernel_us, 2),
-        "vocab": {"avg_us": round(v_us, 3), "GBps": round(v_gbs, 1),
+        "per_dispatch_sweep": {"us": round(chain_ms * 1e3, 1), "GBps": round(chain_gbs, 1),
+                               "frac": round(chain_gbs / HBM_PEAK_GBS, 4), "dispatches": 140,
+                               "launch": "eager" if args.no_graph else "hipGraph"},
+        "vocab": {"us": round(v_ms * 1e3, 2), "GBps": round(v_gbs, 1),
                   "frac": round(v_gbs / HBM_PEAK_GBS, 4), "bytes": vocab_bytes, "token": token},
         "decode_step_gemv_us": round(decode_gemv_us, 2),
         "parity_ok": bool(parity_ok),

@@ -113,18 +113,54 @@ int decode_dispatch_18_matmul_6144x1x1024_f16(const void* q8_stacked, int64_t la
 int decode_dispatch_20_matmul_1024x1x3072_f16(const void* q8_stacked, int64_t layer,
                                               const void* x_f16, void* y_f16, void* stream);
 
+/* ---- batched Q8_0 GEMVs: several independent GEMVs in one launch (no
+ * reference counterpart; the reference issues one dispatch per GEMV) ----
+ *
+ * For GEMVs that do not depend on each other -- q, k and v of a layer, which
+ * read the same x (qwen3_full.mlir:625-635), or any list of independent calls
+ * -- one launch replaces one dispatch each: the batch's row quads are spread
+ * evenly over the whole GPU, so small GEMVs stop paying a dispatch apiece.
+ * Every row is computed exactly as q8gemv_rows computes it (bit-identical).
+ * The outputs must not overlap each other or any input. */
+typedef struct q8gemv_desc {
+  const void* w_layer; /* first row of the layer's Q8_0 bytes, 16-byte aligned */
+  const void* x_f16;   /* K f16 values, 16-byte aligned */
+  void* y_f16;         /* n_rows f16 outputs, 2-byte aligned */
+  int64_t n_rows;      /* 1 .. 2^24 */
+  int64_t k;           /* 1024, 2048 or 3072 */
+} q8gemv_desc;
+
+/* Fills *out for one kind's layer of a [28, BPL] stacked buffer. */
+int q8gemv_desc_for_kind(int kind, const void* w_stacked, int64_t layer, const void* x_f16,
+                         void* y_f16, q8gemv_desc* out);
+/* Bytes of the device table for `count` descriptors (0 if count is out of
+ * range). */
+size_t q8gemv_batch_table_bytes(int count);
+/* Validates the descriptors (as q8gemv_rows would) and encodes them into a
+ * host buffer of q8gemv_batch_table_bytes(count) bytes; *total_units receives
+ * the work size to pass to q8gemv_batch.  Host-only: copy the table to device
+ * memory (any allocation the caller owns, 16-byte aligned) before launching. */
+int q8gemv_batch_encode(const q8gemv_desc* descs, int count, void* host_table,
+                        size_t table_bytes, int32_t* total_units);
+/* Launches every GEMV of an encoded table that was copied to the device
+ * unchanged.  The table is read by the kernel, so it must stay valid until
+ * the launch completes; it can be reused by any number of launches. */
+int q8gemv_batch(const void* device_table, int count, int32_t total_units, void* stream);
+
 /* ---- f16 vocab GEMV + fused two-phase argmax ---- */
 
-/* Workspace for the argmax partials: a completion counter plus one 8-byte
- * partial per workgroup.  The counter must be zero before the first launch
- * that uses a workspace (vocab_argmax_workspace_reset, or a zero fill); every
- * launch leaves it zero again.  Two launches must not share a workspace
- * concurrently. */
+/* Workspace of the fused argmax: a 64-bit (value, index) key that every
+ * workgroup folds its best candidate into with an atomic max.  It must be
+ * zero before the first launch that uses it (vocab_argmax_workspace_reset, or
+ * a zero fill); every launch leaves it zero again.  Two launches must not
+ * share a workspace concurrently. */
 size_t vocab_argmax_workspace_bytes(void);
 int vocab_argmax_workspace_reset(void* workspace, void* stream);
 
 /* logits[151936] = f16(W[151936,1024] . x) and *token = the lowest index of
- * the maximal f16 logit (-1 if none is > -inf; NaN never wins).
+ * the maximal f16 logit (-1 if none is > -inf; NaN never wins).  Enqueues two
+ * kernels: the GEMV with the per-workgroup argmax phase, then a one-thread
+ * finalize that writes *token.
  * decode_dispatch_24_matmul_151936x1x1024_f16 (kernels/cuda/dispatch_24.cu:11-46)
  * fused with the tiled argmax of qwen3_full.mlir:1469-1511 (i64 there, int32
  * here).  logits may be NULL to skip writing them. */
@@ -140,17 +176,19 @@ int f16_gemv_argmax_rows(const void* w_f16, int64_t n_rows, const void* x_f16,
 
 /* ---- launch-shape tuning (no reference counterpart) ---- */
 
-/* Row quads per wave (1,2,3,4,6 for K=1024; 1,2,4 for K=2048/3072) used for
- * K = 1024*p.  Applies to later launches. */
-int q8gemv_set_rows_per_wave(int64_t k, int quads_per_wave);
-int q8gemv_get_rows_per_wave(int64_t k, int* quads_per_wave);
-/* Workgroups (256 threads) of the vocab kernel, 1..4096; 0 = default
+/* Upper bound on the workgroups (one wave each) of a batched Q8_0 launch;
+ * 0 = default (12 per compute unit).  A launch never uses more workgroups than
+ * it has work units.  (A single GEMV always runs one wave per row quad.) */
+int q8gemv_batch_set_workgroups(int workgroups);
+/* Workgroups (256 threads) of the vocab kernel, 1..8192; 0 = default
  * (4 per compute unit). */
 int vocab_set_workgroups(int workgroups);
 int vocab_get_workgroups(int* workgroups);
 
 /* ---- device runtime helpers (no reference counterpart: the IREE HAL owns
- * allocation, streams and timing there, benchmark.py:34-49) ---- */
+ * allocation, streams and timing there, benchmark.py:34-49).  The copy and
+ * memset helpers are set-up tools, fully synchronous with the device: they
+ * wait for all prior work on every stream and return after completing. ---- */
 int q8rt_device_count(int* count);
 int q8rt_set_device(int device);
 int q8rt_device_info(char* name, int name_len, int* compute_units, int64_t* total_mem);
@@ -174,6 +212,10 @@ int q8rt_graph_begin_capture(void* stream);
 int q8rt_graph_end_capture(void* stream, void** graph_exec);
 int q8rt_graph_launch(void* graph_exec, void* stream);
 int q8rt_graph_destroy(void* graph_exec);
+/* Device-to-device copy by a plain streaming kernel (16-byte aligned pointers,
+ * bytes % 16 == 0; bytes = 0 launches one empty workgroup).  A kernel of known
+ * traffic for calibrating HBM byte counters and dispatch overhead. */
+int q8rt_stream_copy(void* dst, const void* src, size_t bytes, void* stream);
 /* The calling thread's next kernel launch through this library records
  * `start` / `stop` around that kernel alone (hipExtModuleLaunchKernel
  * events), for per-kernel timing.  One-shot. */

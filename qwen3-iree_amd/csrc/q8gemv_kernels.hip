@@ -35,6 +35,37 @@ __device__ __forceinline__ f16x2 q8x2_to_f16x2(uint32_t biased, uint32_t sel) {
 
 __device__ __forceinline__ f16x2 as_f16x2(uint32_t v) { return __builtin_bit_cast(f16x2, v); }
 
+// Load flavour of the weight streams (read once per launch): the Q8_0 kernels
+// use nontemporal loads (global_load ... nt), the vocab kernel plain loads,
+// each the faster of the two on MI355X.
+#ifndef Q8_NT_LOADS
+#define Q8_NT_LOADS 1
+#endif
+#ifndef VOCAB_NT_LOADS
+#define VOCAB_NT_LOADS 0
+#endif
+
+// Pointers read from a batch table are generic; accessing them through the
+// global address space keeps the loads global_load (counted by vmcnt alone)
+// rather than flat_load, whose completion the compiler can only await with a
+// full vmcnt(0) lgkmcnt(0) drain.
+#define GLOBAL_AS __attribute__((address_space(1)))
+
+template <bool NT>
+__device__ __forceinline__ u32x4 load_stream(const u32x4* p) {
+  const GLOBAL_AS u32x4* g = (const GLOBAL_AS u32x4*)p;
+  if constexpr (NT) return __builtin_nontemporal_load(g);
+  else return *g;
+}
+
+__device__ __forceinline__ u32x4 load_global(const u32x4* p) {
+  return *(const GLOBAL_AS u32x4*)p;
+}
+
+__device__ __forceinline__ void store_global_u16(uint16_t* p, uint16_t v) {
+  *(GLOBAL_AS uint16_t*)p = v;
+}
+
 __device__ __forceinline__ float f16_bits_to_f32(uint32_t bits16) {
   return (float)__builtin_bit_cast(_Float16, (uint16_t)bits16);
 }
@@ -56,13 +87,6 @@ __device__ __forceinline__ float reduce_row16(float v) {
   v += dpp<0x4E>(v);   // quad_perm [2,3,0,1]
   v += dpp<0x141>(v);  // row_half_mirror
   v += dpp<0x140>(v);  // row_mirror
-  return v;
-}
-
-__device__ __forceinline__ float reduce_wave64(float v) {
-  v = reduce_row16(v);
-  v += __shfl_xor(v, 16, 64);
-  v += __shfl_xor(v, 32, 64);
   return v;
 }
 
@@ -91,88 +115,247 @@ __device__ __forceinline__ float q8_pair_dot(const uint32_t (&d)[17], const u32x
   return s0 * dot0 + s1 * dot1;
 }
 
-// One wave (64 lanes) per workgroup; the wave owns R quads of 4 consecutive
-// rows.  Lane l works on row (l >> 4) of each quad and on block pairs
-// p, p+16, ..., p+16(P-1) with p = l & 15, i.e. K positions
-// [1024c + 64p, 1024c + 64p + 64) for c < P.
+// ---------------------------------------------------------- Q8_0 GEMV ------
 //
-// The wave's rows are one contiguous byte span (4*R*ROWB bytes).  It is read
-// with fully coalesced 16-byte loads (lane l takes bytes 16l, 16l+1024, ...),
-// staged through LDS, and read back per lane as 68-byte block pairs, so HBM
-// sees whole 1 KiB requests per instruction despite the 34-byte block stride.
-// All of a wave's weight loads are issued before its first x load, so the
-// weight stream and the x fetch overlap.
-template <int P, int R>
-__device__ __forceinline__ void q8gemv_body(const uint8_t* __restrict__ w,
-                                            const uint16_t* __restrict__ x,
-                                            uint16_t* __restrict__ y, int n_rows,
-                                            uint8_t* __restrict__ lds) {
-  constexpr int ROWB = 1088 * P;      // bytes per row (32*P blocks of 34 B)
-  constexpr int SPAN = 4 * R * ROWB;  // bytes per wave
-  constexpr int CHUNKS = SPAN / 16;
-  constexpr int ITERS = (CHUNKS + 63) / 64;
+// Rows are handled in quads of 4 consecutive rows; a quad's bytes are one
+// contiguous span (4 rows x K/32 blocks x 34 B).  A wave reads its span with
+// fully coalesced 16-byte loads (lane l takes pieces l, l+64, ...), stages it
+// in LDS and reads it back as 68-byte block pairs: lane l works on row (l >> 4)
+// of the quad and pair (l & 15) of each 1024-column chunk.  HBM therefore sees
+// whole 1 KiB wave requests despite the 34-byte block stride.  A row's partial
+// sums stay in the lane across its K/1024 chunks and meet in a 16-lane DPP
+// reduction.
+//
+// Batched launches split their work into units of one 1024-column chunk of a
+// quad (32 blocks per row, 4352 bytes, whatever K is); a wave owns a
+// contiguous range of units of a GEMV, quad-major and chunk-minor, so it
+// finishes every row it starts.
+
+constexpr int kChunkBytes = 1088;                    // 32 Q8_0 blocks
+constexpr int kUnitBytes = 4 * kChunkBytes;          // 4352
+constexpr int kUnitPieces = kUnitBytes / 16;         // 272
+constexpr int kUnitLoads = (kUnitPieces + 63) / 64;  // 5 per lane
+constexpr int kMaxP = 3;                             // K <= 3072
+constexpr int kSlotBytes = kUnitLoads * 1024;        // 5120: a unit plus spare tail
+
+struct Q8Seg {
+  const uint8_t* w;  // first row of the layer
+  const uint16_t* x;
+  uint16_t* y;
+  int n_rows;
+  int p;  // K / 1024
+};
+
+// Where lane `lane`'s pieces of a unit sit: row within the quad and byte
+// offset within that row's 1088-byte chunk.  The last load covers pieces
+// 256..319 of which only 272 exist; lanes past the end re-read piece 271 (the
+// same 16 bytes lane 15 reads) so that every load is issued by every lane and
+// no load sits behind a branch, and they park the copy in the slot's spare
+// tail.
+struct PieceMap {
+  int row[kUnitLoads];
+  int off[kUnitLoads];
+};
+
+__device__ __forceinline__ PieceMap piece_map(int lane) {
+  PieceMap pm;
+#pragma unroll
+  for (int i = 0; i < kUnitLoads; ++i) {
+    int j = i * 64 + lane;
+    j = j < kUnitPieces ? j : kUnitPieces - 1;
+    pm.row[i] = j / 68;
+    pm.off[i] = (j - (j / 68) * 68) * 16;
+  }
+  return pm;
+}
+
+__device__ __forceinline__ void unit_load(const Q8Seg& s, int quad, int c, const PieceMap& pm,
+                                          u32x4 (&buf)[kUnitLoads]) {
+  const size_t rowb = (size_t)kChunkBytes * s.p;
+  const uint8_t* base = s.w + (size_t)c * kChunkBytes;
+#pragma unroll
+  for (int i = 0; i < kUnitLoads; ++i) {
+    int row = quad * 4 + pm.row[i];
+    row = row < s.n_rows ? row : s.n_rows - 1;  // ragged last quad: re-read a valid row
+    buf[i] = load_stream<Q8_NT_LOADS>(
+        reinterpret_cast<const u32x4*>(base + (size_t)row * rowb + pm.off[i]));
+  }
+}
+
+// Units [u_begin, u_end) of one GEMV in a batched launch (segment-local
+// numbering: quad = u / p, chunk = u % p; u_begin and u_end are multiples of
+// p).  Two register sets ping-pong so that while one unit is computed the
+// next one is already in flight; every load inside the loop is unconditional,
+// so the wait before staging a set covers only that set.
+__device__ __forceinline__ void q8_segment(const Q8Seg& s, int u_begin, int u_end,
+                                           uint8_t* __restrict__ slot,
+                                           uint16_t* __restrict__ xl) {
+  const int lane = threadIdx.x;
+  const PieceMap pm = piece_map(lane);
+  const int p16 = lane & 15;
+  const int rsub = lane >> 4;
+  u32x4* l4 = reinterpret_cast<u32x4*>(slot);
+
+  int lq = u_begin / s.p, lc = 0;  // next unit to load
+  auto load_next = [&](u32x4 (&dst)[kUnitLoads]) {
+    unit_load(s, lq, lc, pm, dst);
+    if (++lc == s.p) {
+      lc = 0;
+      ++lq;
+    }
+  };
+  int cq = lq, cc = 0;  // next unit to compute
+  float acc = 0.0f;
+  auto compute = [&](const u32x4 (&src)[kUnitLoads]) {
+#pragma unroll
+    for (int i = 0; i < kUnitLoads; ++i) l4[i * 64 + lane] = src[i];
+    __syncthreads();
+    const uint32_t* pp = reinterpret_cast<const uint32_t*>(slot + rsub * kChunkBytes + 68 * p16);
+    uint32_t d[17];
+#pragma unroll
+    for (int m = 0; m < 17; ++m) d[m] = pp[m];
+    const u32x4* xs = reinterpret_cast<const u32x4*>(xl + 1024 * cc + 64 * p16);
+    u32x4 xr[8];
+#pragma unroll
+    for (int m = 0; m < 8; ++m) xr[m] = xs[m];
+    acc += q8_pair_dot(d, xr);
+    if (cc == s.p - 1) {
+      const float tot = reduce_row16(acc);
+      const int row = cq * 4 + rsub;
+      if (p16 == 0 && row < s.n_rows) store_global_u16(s.y + row, f32_to_f16_bits(tot));
+      acc = 0.0f;
+    }
+    if (++cc == s.p) {
+      cc = 0;
+      ++cq;
+    }
+    __syncthreads();
+  };
+
+  const int n = u_end - u_begin;
+  u32x4 A[kUnitLoads], B[kUnitLoads];
+  load_next(A);
+  const u32x4* xg = reinterpret_cast<const u32x4*>(s.x);
+  u32x4* xl4 = reinterpret_cast<u32x4*>(xl);
+  for (int t = lane; t < 128 * s.p; t += 64) xl4[t] = load_global(xg + t);
+  int i = 0;
+  for (; i + 2 < n; i += 2) {
+    load_next(B);
+    compute(A);
+    load_next(A);
+    compute(B);
+  }
+  if (n - i == 2) {
+    load_next(B);
+    compute(A);
+    compute(B);
+  } else {
+    compute(A);
+  }
+}
+
+// Single GEMV: one wave per row quad, the latency-bound shape of a lone
+// decode dispatch.  The wave issues all P*5 of its weight loads at once (the
+// quad's 4 rows x P chunks are one contiguous span of 4*1088*P bytes), then
+// its x loads (64 columns per chunk straight into registers), stages the span
+// in LDS and reads it back as block pairs.
+template <int P>
+__device__ __forceinline__ void q8_quad(const uint8_t* __restrict__ w,
+                                        const uint16_t* __restrict__ x,
+                                        uint16_t* __restrict__ y, int n_rows,
+                                        uint8_t* __restrict__ lds) {
+  constexpr int ROWB = kChunkBytes * P;
+  constexpr int PIECES = 4 * ROWB / 16;  // 272 * P
+  constexpr int LOADS = (PIECES + 63) / 64;
 
   const int lane = threadIdx.x;
-  const int row0 = blockIdx.x * (4 * R);
+  const int row0 = blockIdx.x * 4;
   int rows_here = n_rows - row0;
-  rows_here = rows_here < 4 * R ? rows_here : 4 * R;
-  const int valid = rows_here * (ROWB / 16);
+  rows_here = rows_here < 4 ? rows_here : 4;
+  // Pieces past the quad's valid bytes (ragged last quad, or the last load's
+  // spare lanes) re-read the last valid piece and land in rows or LDS bytes
+  // that are never consumed, so every lane issues every load.
+  const int last = rows_here * (ROWB / 16) - 1;
   const u32x4* src = reinterpret_cast<const u32x4*>(w + (size_t)row0 * ROWB);
 
-  u32x4 buf[ITERS];
+  u32x4 buf[LOADS];
 #pragma unroll
-  for (int i = 0; i < ITERS; ++i) {
+  for (int i = 0; i < LOADS; ++i) {
     const int c = i * 64 + lane;
-    if (c < valid) buf[i] = __builtin_nontemporal_load(src + c);
+    buf[i] = load_stream<Q8_NT_LOADS>(src + (c < last ? c : last));
   }
-
-  const int p = lane & 15;
+  const int p16 = lane & 15;
   const int rsub = lane >> 4;
   u32x4 xr[P][8];
 #pragma unroll
   for (int c = 0; c < P; ++c) {
-    const u32x4* xs = reinterpret_cast<const u32x4*>(x + 1024 * c + 64 * p);
+    const u32x4* xs = reinterpret_cast<const u32x4*>(x + 1024 * c + 64 * p16);
 #pragma unroll
     for (int m = 0; m < 8; ++m) xr[c][m] = xs[m];
   }
-
   u32x4* l4 = reinterpret_cast<u32x4*>(lds);
 #pragma unroll
-  for (int i = 0; i < ITERS; ++i) {
-    const int c = i * 64 + lane;
-    if (c < valid) l4[c] = buf[i];
-  }
+  for (int i = 0; i < LOADS; ++i) l4[i * 64 + lane] = buf[i];
   __syncthreads();
 
+  float acc = 0.0f;
 #pragma unroll
-  for (int i = 0; i < R; ++i) {
-    const int rl = 4 * i + rsub;
-    float acc = 0.0f;
+  for (int c = 0; c < P; ++c) {
+    const uint32_t* pp =
+        reinterpret_cast<const uint32_t*>(lds + rsub * ROWB + kChunkBytes * c + 68 * p16);
+    uint32_t d[17];
 #pragma unroll
-    for (int c = 0; c < P; ++c) {
-      const uint32_t* pp = reinterpret_cast<const uint32_t*>(lds + rl * ROWB + 68 * (p + 16 * c));
-      uint32_t d[17];
-#pragma unroll
-      for (int m = 0; m < 17; ++m) d[m] = pp[m];
-      acc += q8_pair_dot(d, xr[c]);
-    }
-    acc = reduce_row16(acc);
-    const int row = row0 + rl;
-    if (p == 0 && row < n_rows) y[row] = f32_to_f16_bits(acc);
+    for (int m = 0; m < 17; ++m) d[m] = pp[m];
+    acc += q8_pair_dot(d, xr[c]);
   }
+  acc = reduce_row16(acc);
+  const int row = row0 + rsub;
+  if (p16 == 0 && row < n_rows) y[row] = f32_to_f16_bits(acc);
 }
+
+// Device table of a batched launch: a 16-byte header, then one entry per GEMV
+// in the order the caller listed them.  unit_begin is the exclusive prefix sum
+// of ceil(n_rows / 4) * p.
+struct Q8BatchEntry {
+  const uint8_t* w;
+  const uint16_t* x;
+  uint16_t* y;
+  int32_t n_rows;
+  int32_t p;
+  int32_t unit_begin;
+  int32_t reserved;
+};
+static_assert(sizeof(Q8BatchEntry) == 40, "batch entry layout");
+constexpr int kBatchHeaderBytes = 16;
 
 // ------------------------------------------------------------ vocab ------
 
-struct ArgmaxPartial {
-  float value;
-  int32_t index;
-};
+// Workspace: one u64 argmax key (below), zero between launches.  Every
+// workgroup folds its best (value, index) into it with a 64-bit atomic max;
+// vocab_argmax_finalize turns the key into the token and zeroes it again.
+// Atomics on one location need no fences, so no workgroup pays for an L2
+// writeback or invalidate.
 
-// Workspace layout: [0,16) completion counter (u32), then one 8-byte
-// (value, index) partial per workgroup.
-constexpr int kWsHeader = 16;
+// Order-preserving key of a candidate (f16 value v at row i >= 0): the high
+// word maps the f16 bit pattern to an unsigned order (-0 folded onto +0, so
+// the two tie), the low word is ~i so that equal values prefer the lower row.
+// Every candidate key is >= 2^42 (its value is > -inf); 0 means "none".
+__device__ __forceinline__ uint64_t argmax_key(float v, int i) {
+  uint32_t h = f32_to_f16_bits(v);  // exact: v is an f16 value
+  if (h == 0x8000u) h = 0u;
+  const uint32_t ord = (h & 0x8000u) ? (~h & 0xffffu) : (h | 0x8000u);
+  return ((uint64_t)ord << 32) | (uint64_t)(0xffffffffu - (uint32_t)i);
+}
 
+// (v, i) beats (bv, bi): a larger value, or an equal value at a lower index.
+// Ordered compares, so NaN never wins; -0 == +0 ties.  A candidate whose value
+// is -inf always carries index -1 (nothing was selected), so it never beats
+// the initial (-inf, -1).
+__device__ __forceinline__ bool argmax_better(float v, int i, float bv, int bi) {
+  return v > bv || (v == bv && i < bi);
+}
+
+// acc + sum of the 8 products w[j]*xv[j] (4 x v_dot2_f32_f16; products exact in f32).
 __device__ __forceinline__ float f16_row_dot(const u32x4& w, const u32x4& xv, float acc) {
   acc = __builtin_amdgcn_fdot2(as_f16x2(w[0]), as_f16x2(xv[0]), acc, false);
   acc = __builtin_amdgcn_fdot2(as_f16x2(w[1]), as_f16x2(xv[1]), acc, false);
@@ -183,152 +366,115 @@ __device__ __forceinline__ float f16_row_dot(const u32x4& w, const u32x4& xv, fl
 
 // f16 GEMV rows [0, n_rows) x K=1024 with a fused argmax.
 //
-// 256 threads = 4 waves per workgroup; global wave g owns the contiguous rows
-// [g*n/TW, (g+1)*n/TW).  Per row, lane l reads bytes [16l, 16l+16) and
-// [1024+16l, 1024+16l+16) of the 2 KiB row (two fully coalesced 1 KiB wave
-// loads) and keeps its 16 x values in registers for every row.  U rows are in
-// flight per wave (double buffered).
+// Rows are taken in batches of 4.  Within a wave, DPP row g (lanes 16g..16g+15)
+// owns matrix row 4b+g of batch b: lane i of the group reads bytes
+// [256m + 16i, 256m + 16i + 16) of that row for m = 0..7, so each wave load
+// instruction covers four fully used 256-byte row segments, and the group's
+// partial sums meet in a 16-lane DPP reduction (no cross-row exchange).  The
+// lane keeps its 64 x values (positions 128m + 8i .. +8) in registers for all
+// rows.  Global wave w owns the contiguous batches [w*B/TW, (w+1)*B/TW); the
+// next batch's loads are issued unconditionally before the current batch is
+// reduced, so every wave keeps 8 KiB of weights in flight.
 //
 // Argmax: each logit is rounded to f16 first (the reference compares the f16
-// logits tensor); a strictly-greater test in increasing row order keeps the
-// lowest index among equal maxima, NaN never wins and -inf never replaces the
-// initial (-inf, -1).  Waves, then workgroups, are combined in row order with
-// the same rule; the last workgroup to finish (device-scope counter) reduces
-// the per-workgroup partials and resets the counter for the next launch.
-template <int U>
+// logits tensor).  Per group the rows arrive in increasing order, so a
+// strictly-greater update keeps the first maximum; the 16 groups of a
+// workgroup are merged with argmax_better, and workgroups meet in a 64-bit
+// atomic max over argmax_key, whose order is the same rule.
+template <bool NT>
 __device__ __forceinline__ void vocab_body(const uint16_t* __restrict__ W,
                                            const uint16_t* __restrict__ x,
                                            uint16_t* __restrict__ logits, int n_rows,
-                                           int32_t* __restrict__ token,
                                            uint8_t* __restrict__ ws) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int gw = blockIdx.x * 4 + wave;
+  const int grp = lane >> 4;
+  const int li = lane & 15;
+  const int64_t gw = (int64_t)blockIdx.x * 4 + wave;
   const int64_t tw = (int64_t)gridDim.x * 4;
-  const int r_begin = (int)((int64_t)gw * n_rows / tw);
-  const int r_end = (int)((int64_t)(gw + 1) * n_rows / tw);
+  const int64_t nbatch = ((int64_t)n_rows + 3) / 4;
+  const int b_begin = (int)(gw * nbatch / tw);
+  const int b_end = (int)((gw + 1) * nbatch / tw);
 
   const u32x4* xv = reinterpret_cast<const u32x4*>(x);
-  const u32x4 xa = xv[lane];
-  const u32x4 xb = xv[64 + lane];
+  u32x4 xr[8];
+#pragma unroll
+  for (int m = 0; m < 8; ++m) xr[m] = xv[16 * m + li];
+
   const u32x4* Wv = reinterpret_cast<const u32x4*>(W);
+  auto load_batch = [&](int b, u32x4 (&dst)[8]) {
+    int row = 4 * b + grp;
+    row = row < n_rows ? row : n_rows - 1;  // only the grid's last batch can be short
+    const u32x4* p = Wv + (size_t)row * 128 + li;
+#pragma unroll
+    for (int m = 0; m < 8; ++m) dst[m] = load_stream<NT>(p + 16 * m);
+  };
 
   float best_v = -__builtin_inff();
   int best_i = -1;
-
-  auto consume = [&](int row, const u32x4& wa, const u32x4& wb) {
-    float acc = f16_row_dot(wa, xa, 0.0f);
-    acc = f16_row_dot(wb, xb, acc);
-    acc = reduce_wave64(acc);
+  auto consume = [&](int b, const u32x4 (&w)[8]) {
+    float a0 = 0.0f, a1 = 0.0f;
+#pragma unroll
+    for (int m = 0; m < 8; m += 2) {
+      a0 = f16_row_dot(w[m], xr[m], a0);
+      a1 = f16_row_dot(w[m + 1], xr[m + 1], a1);
+    }
+    const float acc = reduce_row16(a0 + a1);
+    const int row = 4 * b + grp;
     const uint16_t hb = f32_to_f16_bits(acc);
-    if (logits != nullptr && lane == 0) logits[row] = hb;
-    const float hv = f16_bits_to_f32(hb);
-    if (hv > best_v) {
-      best_v = hv;
-      best_i = row;
+    if (row < n_rows) {
+      if (logits != nullptr && li == 0) logits[row] = hb;
+      const float hv = f16_bits_to_f32(hb);
+      if (hv > best_v) {
+        best_v = hv;
+        best_i = row;
+      }
     }
   };
 
-  int r = r_begin;
-  if (r + U <= r_end) {
-    u32x4 ca[U], cb[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      ca[u] = __builtin_nontemporal_load(Wv + (size_t)(r + u) * 128 + lane);
-      cb[u] = __builtin_nontemporal_load(Wv + (size_t)(r + u) * 128 + 64 + lane);
+  // Ping-pong between two register sets; every load inside the loop is
+  // unconditional, so the compiler can wait for exactly the older set.
+  const int nb = b_end - b_begin;
+  if (nb > 0) {
+    u32x4 A[8], B[8];
+    load_batch(b_begin, A);
+    int i = 0;
+    for (; i + 2 < nb; i += 2) {
+      load_batch(b_begin + i + 1, B);
+      consume(b_begin + i, A);
+      load_batch(b_begin + i + 2, A);
+      consume(b_begin + i + 1, B);
     }
-    for (;;) {
-      const int nr = r + U;
-      const bool more = nr + U <= r_end;
-      u32x4 na[U], nb[U];
-      if (more) {
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-          na[u] = __builtin_nontemporal_load(Wv + (size_t)(nr + u) * 128 + lane);
-          nb[u] = __builtin_nontemporal_load(Wv + (size_t)(nr + u) * 128 + 64 + lane);
-        }
-      }
-#pragma unroll
-      for (int u = 0; u < U; ++u) consume(r + u, ca[u], cb[u]);
-      r = nr;
-      if (!more) break;
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        ca[u] = na[u];
-        cb[u] = nb[u];
-      }
+    if (nb - i == 2) {
+      load_batch(b_begin + i + 1, B);
+      consume(b_begin + i, A);
+      consume(b_begin + i + 1, B);
+    } else {
+      consume(b_begin + i, A);
     }
-  }
-  for (; r < r_end; ++r) {
-    const u32x4 wa = __builtin_nontemporal_load(Wv + (size_t)r * 128 + lane);
-    const u32x4 wb = __builtin_nontemporal_load(Wv + (size_t)r * 128 + 64 + lane);
-    consume(r, wa, wb);
   }
 
-  // ---- workgroup combine (waves hold increasing row ranges) ----
-  __shared__ float s_val[4];
-  __shared__ int s_idx[4];
-  __shared__ int s_last;
-  if (lane == 0) {
-    s_val[wave] = best_v;
-    s_idx[wave] = best_i;
+  // ---- workgroup combine: 4 waves x 4 row groups, then one atomic ----
+  __shared__ float s_val[16];
+  __shared__ int s_idx[16];
+  if (li == 0) {
+    s_val[wave * 4 + grp] = best_v;
+    s_idx[wave * 4 + grp] = best_i;
   }
   __syncthreads();
-
-  uint32_t* counter = reinterpret_cast<uint32_t*>(ws);
-  uint64_t* partials = reinterpret_cast<uint64_t*>(ws + kWsHeader);
   if (threadIdx.x == 0) {
     float bv = -__builtin_inff();
     int bi = -1;
-#pragma unroll
-    for (int w4 = 0; w4 < 4; ++w4) {
-      if (s_val[w4] > bv) {
-        bv = s_val[w4];
-        bi = s_idx[w4];
+    for (int c = 0; c < 16; ++c) {
+      if (argmax_better(s_val[c], s_idx[c], bv, bi)) {
+        bv = s_val[c];
+        bi = s_idx[c];
       }
     }
-    const uint64_t packed = (uint64_t)__builtin_bit_cast(uint32_t, bv) |
-                            ((uint64_t)(uint32_t)bi << 32);
-    __hip_atomic_store(partials + blockIdx.x, packed, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __threadfence();
-    const uint32_t prev = atomicAdd(counter, 1u);
-    s_last = (prev == gridDim.x - 1) ? 1 : 0;
-  }
-  __syncthreads();
-  if (!s_last) return;
-  __threadfence();
-
-  // ---- last workgroup: reduce the partials in workgroup order ----
-  const int G = gridDim.x;
-  const int t = threadIdx.x;
-  const int p_begin = (int)((int64_t)t * G / 256);
-  const int p_end = (int)((int64_t)(t + 1) * G / 256);
-  float tv = -__builtin_inff();
-  int ti = -1;
-  for (int g = p_begin; g < p_end; ++g) {
-    const uint64_t pk = __hip_atomic_load(partials + g, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const float v = __builtin_bit_cast(float, (uint32_t)(pk & 0xffffffffu));
-    if (v > tv) {
-      tv = v;
-      ti = (int32_t)(uint32_t)(pk >> 32);
+    if (bi >= 0) {
+      __hip_atomic_fetch_max(reinterpret_cast<uint64_t*>(ws), argmax_key(bv, bi), __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
     }
-  }
-  __shared__ float f_val[256];
-  __shared__ int f_idx[256];
-  f_val[t] = tv;
-  f_idx[t] = ti;
-  __syncthreads();
-  if (t == 0) {
-    float bv = -__builtin_inff();
-    int bi = -1;
-    for (int k = 0; k < 256; ++k) {
-      if (f_val[k] > bv) {
-        bv = f_val[k];
-        bi = f_idx[k];
-      }
-    }
-    *token = bi;
-    __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
@@ -336,35 +482,79 @@ __device__ __forceinline__ void vocab_body(const uint16_t* __restrict__ W,
 
 // ------------------------------------------------------------ exports -----
 
-#define Q8GEMV_KERNEL(P, R)                                                              \
-  extern "C" __global__ __launch_bounds__(64) void q8gemv_p##P##_r##R(                   \
-      const uint8_t* __restrict__ w, const uint16_t* __restrict__ x,                     \
-      uint16_t* __restrict__ y, int n_rows) {                                            \
-    __shared__ __attribute__((aligned(16))) uint8_t lds[4 * (R) * 1088 * (P)];           \
-    q8gemv_body<P, R>(w, x, y, n_rows, lds);                                             \
+// One GEMV of K = 1024*P: workgroup (one wave) b computes row quad b.
+#define Q8GEMV_SINGLE(P)                                                                   \
+  extern "C" __global__ __launch_bounds__(64) void q8gemv_p##P(                            \
+      const uint8_t* __restrict__ w, const uint16_t* __restrict__ x,                       \
+      uint16_t* __restrict__ y, int n_rows) {                                              \
+    __shared__ __attribute__((aligned(16))) uint8_t lds[(4 * (P) * 68 + 63) / 64 * 1024];  \
+    q8_quad<P>(w, x, y, n_rows, lds);                                                      \
   }
+Q8GEMV_SINGLE(1)
+Q8GEMV_SINGLE(2)
+Q8GEMV_SINGLE(3)
 
-Q8GEMV_KERNEL(1, 1)
-Q8GEMV_KERNEL(1, 2)
-Q8GEMV_KERNEL(1, 3)
-Q8GEMV_KERNEL(1, 4)
-Q8GEMV_KERNEL(1, 6)
-Q8GEMV_KERNEL(2, 1)
-Q8GEMV_KERNEL(2, 2)
-Q8GEMV_KERNEL(2, 4)
-Q8GEMV_KERNEL(3, 1)
-Q8GEMV_KERNEL(3, 2)
-Q8GEMV_KERNEL(3, 4)
+// Many independent GEMVs in one launch.  The batch's units are split evenly
+// over the waves; a wave owns every quad whose first unit falls in its range
+// and walks the table entries that range touches.
+extern "C" __global__ __launch_bounds__(64) void q8gemv_batch_k(const uint8_t* __restrict__ table,
+                                                               int count, int total_units) {
+  __shared__ __attribute__((aligned(16))) uint8_t slot[kSlotBytes];
+  __shared__ __attribute__((aligned(16))) uint16_t xl[1024 * kMaxP];
+  const Q8BatchEntry* e = reinterpret_cast<const Q8BatchEntry*>(table + kBatchHeaderBytes);
+  const int64_t W = gridDim.x;
+  const int ga = (int)((int64_t)blockIdx.x * total_units / W);
+  const int gb = (int)((int64_t)(blockIdx.x + 1) * total_units / W);
+  if (ga >= gb) return;
+  int lo = 0, hi = count - 1;  // last entry with unit_begin <= ga
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (e[mid].unit_begin <= ga) lo = mid;
+    else hi = mid - 1;
+  }
+  for (int d = lo; d < count && e[d].unit_begin < gb; ++d) {
+    const int p = e[d].p;
+    const int nq = (e[d].n_rows + 3) / 4;
+    const int t0 = ga - e[d].unit_begin;
+    const int t1 = gb - e[d].unit_begin;
+    const int qa = t0 <= 0 ? 0 : min(nq, (t0 + p - 1) / p);
+    const int qb = t1 <= 0 ? 0 : min(nq, (t1 + p - 1) / p);
+    if (qa >= qb) continue;
+    const Q8Seg s{e[d].w, e[d].x, e[d].y, e[d].n_rows, p};
+    q8_segment(s, qa * p, qb * p, slot, xl);
+    __syncthreads();
+  }
+}
 
 extern "C" __global__ __launch_bounds__(256) void vocab_gemv_argmax_k1024(
     const uint16_t* __restrict__ W, const uint16_t* __restrict__ x,
-    uint16_t* __restrict__ logits, int n_rows, int32_t* __restrict__ token,
-    uint8_t* __restrict__ ws) {
-  vocab_body<4>(W, x, logits, n_rows, token, ws);
+    uint16_t* __restrict__ logits, int n_rows, uint8_t* __restrict__ ws) {
+  vocab_body<VOCAB_NT_LOADS != 0>(W, x, logits, n_rows, ws);
 }
 
-// Zeroes the workspace completion counter (graph-capture safe: a kernel, not
-// a memset node).
+// token = row of the winning key (-1 for none); leaves the key zero for the
+// next launch.
+extern "C" __global__ void vocab_argmax_finalize(uint64_t* __restrict__ ws,
+                                                 int32_t* __restrict__ token) {
+  if (threadIdx.x == 0) {
+    const uint64_t key = ws[0];
+    *token = key == 0 ? -1 : (int32_t)(0xffffffffu - (uint32_t)(key & 0xffffffffu));
+    ws[0] = 0;
+  }
+}
+
+// Zeroes the workspace key (graph-capture safe: a kernel, not a memset node).
 extern "C" __global__ void vocab_workspace_reset(uint32_t* __restrict__ ws) {
   if (threadIdx.x < 4) ws[threadIdx.x] = 0u;
+}
+
+// Plain device copy of n16 16-byte words (grid-stride): the reference kernel
+// of known traffic for calibrating HBM byte counters, and (with n16 = 0) an
+// empty launch for measuring dispatch overhead.
+extern "C" __global__ __launch_bounds__(256) void stream_copy_b128(const u32x4* __restrict__ src,
+                                                                   u32x4* __restrict__ dst,
+                                                                   int64_t n16) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += stride)
+    dst[i] = src[i];
 }

@@ -40,16 +40,24 @@ constexpr KindInfo kKinds[5] = {
     {"ffn_dn", 1024, 3072},
 };
 
-constexpr int kMaxQuads = 6;
-constexpr int kVocabMaxWorkgroups = 4096;
-constexpr size_t kWsHeader = 16;
+constexpr int kVocabMaxWorkgroups = 8192;
+constexpr int kQ8MaxWorkgroups = 65536;
+constexpr size_t kVocabWorkspaceBytes = 256;
+constexpr int kBatchMaxCount = 1 << 20;
+constexpr size_t kBatchHeaderBytes = 16;
+constexpr size_t kBatchEntryBytes = 40;
 
-// Row quads per wave compiled for each P = K/1024 (index P-1).
-constexpr int kQuadsAvail[3][kMaxQuads + 1] = {
-    {0, 1, 1, 1, 1, 0, 1},  // P=1: 1,2,3,4,6
-    {0, 1, 1, 0, 1, 0, 0},  // P=2: 1,2,4
-    {0, 1, 1, 0, 1, 0, 0},  // P=3: 1,2,4
+// Device layout of one batch table entry (q8gemv_kernels.hip, Q8BatchEntry).
+struct BatchEntry {
+  const void* w;
+  const void* x;
+  void* y;
+  int32_t n_rows;
+  int32_t p;
+  int32_t unit_begin;
+  int32_t reserved;
 };
+static_assert(sizeof(BatchEntry) == kBatchEntryBytes, "batch entry layout");
 
 struct State {
   std::mutex mu;
@@ -57,11 +65,14 @@ struct State {
   int device = -1;
   int compute_units = 0;
   hipModule_t module = nullptr;
-  hipFunction_t q8fn[3][kMaxQuads + 1] = {};
+  hipFunction_t q8[3] = {};  // K = 1024, 2048, 3072
+  hipFunction_t q8batch = nullptr;
   hipFunction_t vocab = nullptr;
+  hipFunction_t vocab_finalize = nullptr;
   hipFunction_t ws_reset = nullptr;
-  int quads[3] = {1, 1, 1};
-  int vocab_wgs = 0;  // 0 = default
+  hipFunction_t copy = nullptr;
+  int batch_wgs = 0;      // 0 = default
+  int vocab_wgs = 0;      // 0 = default
 };
 
 State g;
@@ -122,24 +133,35 @@ int check_ready() {
   return Q8_OK;
 }
 
+int cu_count() { return g.compute_units > 0 ? g.compute_units : 256; }
+
 int q8_launch(const void* w_layer, int64_t n_rows, int64_t k, const void* x, void* y,
               void* stream) {
-  const int p = (int)(k / 1024);
-  const int quads = g.quads[p - 1];
-  hipFunction_t fn = g.q8fn[p - 1][quads];
-  const int64_t rows_per_wg = 4LL * quads;
-  const int64_t grid = (n_rows + rows_per_wg - 1) / rows_per_wg;
+  const int64_t quads = (n_rows + 3) / 4;  // one wave per row quad
   const void* w_arg = w_layer;
   const void* x_arg = x;
   void* y_arg = y;
   int n_arg = (int)n_rows;
   void* args[] = {&w_arg, &x_arg, &y_arg, &n_arg};
-  return launch(fn, (uint32_t)grid, 64, args, static_cast<hipStream_t>(stream));
+  return launch(g.q8[k / 1024 - 1], (uint32_t)quads, 64, args, static_cast<hipStream_t>(stream));
+}
+
+int validate_gemv(const void* w_layer, int64_t n_rows, int64_t k, const void* x_f16,
+                  const void* y_f16) {
+  if (!w_layer || !x_f16 || !y_f16) return fail(Q8_ERR_NULL_POINTER, "null w, x or y");
+  if (k != 1024 && k != 2048 && k != 3072)
+    return fail(Q8_ERR_BAD_SHAPE, "K=%lld not in {1024, 2048, 3072}", (long long)k);
+  if (n_rows < 1 || n_rows > (1LL << 24))
+    return fail(Q8_ERR_BAD_SHAPE, "n_rows=%lld outside [1, 2^24]", (long long)n_rows);
+  if (!aligned(w_layer, 16)) return fail(Q8_ERR_MISALIGNED, "weights not 16-byte aligned");
+  if (!aligned(x_f16, 16)) return fail(Q8_ERR_MISALIGNED, "x not 16-byte aligned");
+  if (!aligned(y_f16, 2)) return fail(Q8_ERR_MISALIGNED, "y not 2-byte aligned");
+  return Q8_OK;
 }
 
 int vocab_grid() {
   if (g.vocab_wgs > 0) return g.vocab_wgs;
-  int wgs = 4 * (g.compute_units > 0 ? g.compute_units : 256);
+  int wgs = 4 * cu_count();
   return wgs > kVocabMaxWorkgroups ? kVocabMaxWorkgroups : wgs;
 }
 
@@ -160,23 +182,21 @@ int q8gemv_init(const char* code_object_path) {
   hipError_t e = hipModuleLoad(&mod, path.c_str());
   if (e != hipSuccess)
     return fail(Q8_ERR_CODE_OBJECT, "hipModuleLoad(%s): %s", path.c_str(), hipGetErrorString(e));
-  for (int p = 1; p <= 3; ++p) {
-    for (int r = 1; r <= kMaxQuads; ++r) {
-      if (!kQuadsAvail[p - 1][r]) continue;
-      char name[64];
-      std::snprintf(name, sizeof(name), "q8gemv_p%d_r%d", p, r);
-      e = hipModuleGetFunction(&g.q8fn[p - 1][r], mod, name);
-      if (e != hipSuccess) {
-        (void)hipModuleUnload(mod);
-        return fail(Q8_ERR_CODE_OBJECT, "kernel %s missing from %s", name, path.c_str());
-      }
-    }
-  }
-  e = hipModuleGetFunction(&g.vocab, mod, "vocab_gemv_argmax_k1024");
-  if (e == hipSuccess) e = hipModuleGetFunction(&g.ws_reset, mod, "vocab_workspace_reset");
+  e = hipModuleGetFunction(&g.q8[0], mod, "q8gemv_p1");
+  if (e == hipSuccess) e = hipModuleGetFunction(&g.q8[1], mod, "q8gemv_p2");
+  if (e == hipSuccess) e = hipModuleGetFunction(&g.q8[2], mod, "q8gemv_p3");
+  if (e == hipSuccess) e = hipModuleGetFunction(&g.q8batch, mod, "q8gemv_batch_k");
   if (e != hipSuccess) {
     (void)hipModuleUnload(mod);
-    return fail(Q8_ERR_CODE_OBJECT, "vocab kernels missing from %s", path.c_str());
+    return fail(Q8_ERR_CODE_OBJECT, "Q8_0 GEMV kernels missing from %s", path.c_str());
+  }
+  e = hipModuleGetFunction(&g.vocab, mod, "vocab_gemv_argmax_k1024");
+  if (e == hipSuccess) e = hipModuleGetFunction(&g.vocab_finalize, mod, "vocab_argmax_finalize");
+  if (e == hipSuccess) e = hipModuleGetFunction(&g.ws_reset, mod, "vocab_workspace_reset");
+  if (e == hipSuccess) e = hipModuleGetFunction(&g.copy, mod, "stream_copy_b128");
+  if (e != hipSuccess) {
+    (void)hipModuleUnload(mod);
+    return fail(Q8_ERR_CODE_OBJECT, "vocab / copy kernels missing from %s", path.c_str());
   }
   int cus = 0;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
@@ -184,9 +204,7 @@ int q8gemv_init(const char* code_object_path) {
   g.module = mod;
   g.device = dev;
   g.compute_units = cus;
-  // Launch shapes: one row quad per wave for every K (the widest grids).
-  g.quads[0] = g.quads[1] = g.quads[2] = 1;
-  g.vocab_wgs = 0;
+  g.batch_wgs = g.vocab_wgs = 0;
   g.ready = true;
   return Q8_OK;
 }
@@ -196,8 +214,8 @@ void q8gemv_shutdown(void) {
   if (!g.ready) return;
   (void)hipModuleUnload(g.module);
   g.module = nullptr;
-  std::memset(g.q8fn, 0, sizeof(g.q8fn));
-  g.vocab = g.ws_reset = nullptr;
+  g.q8[0] = g.q8[1] = g.q8[2] = g.q8batch = nullptr;
+  g.vocab = g.vocab_finalize = g.ws_reset = g.copy = nullptr;
   g.ready = false;
 }
 
@@ -214,15 +232,9 @@ int q8gemv_kind_shape(int kind, int64_t* n, int64_t* k, int64_t* bytes_per_layer
 
 int q8gemv_rows(const void* w_layer, int64_t n_rows, int64_t k, const void* x_f16, void* y_f16,
                 void* stream) {
-  if (!w_layer || !x_f16 || !y_f16) return fail(Q8_ERR_NULL_POINTER, "null w, x or y");
-  if (k != 1024 && k != 2048 && k != 3072)
-    return fail(Q8_ERR_BAD_SHAPE, "K=%lld not in {1024, 2048, 3072}", (long long)k);
-  if (n_rows < 1 || n_rows > (1LL << 24))
-    return fail(Q8_ERR_BAD_SHAPE, "n_rows=%lld outside [1, 2^24]", (long long)n_rows);
-  if (!aligned(w_layer, 16)) return fail(Q8_ERR_MISALIGNED, "weights not 16-byte aligned");
-  if (!aligned(x_f16, 16)) return fail(Q8_ERR_MISALIGNED, "x not 16-byte aligned");
-  if (!aligned(y_f16, 2)) return fail(Q8_ERR_MISALIGNED, "y not 2-byte aligned");
-  int rc = check_ready();
+  int rc = validate_gemv(w_layer, n_rows, k, x_f16, y_f16);
+  if (rc) return rc;
+  rc = check_ready();
   if (rc) return rc;
   return q8_launch(w_layer, n_rows, k, x_f16, y_f16, stream);
 }
@@ -261,7 +273,81 @@ int decode_dispatch_20_matmul_1024x1x3072_f16(const void* q8_stacked, int64_t la
   return q8gemv(Q8_FFN_DN, q8_stacked, layer, x_f16, y_f16, stream);
 }
 
-size_t vocab_argmax_workspace_bytes(void) { return kWsHeader + 8u * kVocabMaxWorkgroups; }
+int q8gemv_desc_for_kind(int kind, const void* w_stacked, int64_t layer, const void* x_f16,
+                         void* y_f16, q8gemv_desc* out) {
+  if (kind < 0 || kind > 4) return fail(Q8_ERR_INVALID_KIND, "invalid kind %d", kind);
+  if (!w_stacked || !out) return fail(Q8_ERR_NULL_POINTER, "null w_stacked or out");
+  if (layer < 0 || layer >= Q8_NUM_LAYERS)
+    return fail(Q8_ERR_LAYER_RANGE, "layer %lld outside [0, %d)", (long long)layer,
+                Q8_NUM_LAYERS);
+  const KindInfo& ki = kKinds[kind];
+  const int64_t bpl = ki.n * ki.k / Q8_BLOCK_ELEMS * Q8_BLOCK_BYTES;
+  out->w_layer = static_cast<const uint8_t*>(w_stacked) + layer * bpl;
+  out->x_f16 = x_f16;
+  out->y_f16 = y_f16;
+  out->n_rows = ki.n;
+  out->k = ki.k;
+  return Q8_OK;
+}
+
+size_t q8gemv_batch_table_bytes(int count) {
+  if (count < 1 || count > kBatchMaxCount) return 0;
+  return kBatchHeaderBytes + kBatchEntryBytes * (size_t)count;
+}
+
+int q8gemv_batch_encode(const q8gemv_desc* descs, int count, void* host_table,
+                        size_t table_bytes, int32_t* total_units) {
+  if (!descs || !host_table || !total_units) return fail(Q8_ERR_NULL_POINTER, "null argument");
+  if (count < 1 || count > kBatchMaxCount)
+    return fail(Q8_ERR_BAD_ARGUMENT, "count %d outside [1, %d]", count, kBatchMaxCount);
+  if (table_bytes < q8gemv_batch_table_bytes(count))
+    return fail(Q8_ERR_BAD_ARGUMENT, "table needs %zu bytes, got %zu",
+                q8gemv_batch_table_bytes(count), table_bytes);
+  uint8_t* t = static_cast<uint8_t*>(host_table);
+  int64_t units = 0;
+  for (int i = 0; i < count; ++i) {
+    const q8gemv_desc& d = descs[i];
+    int rc = validate_gemv(d.w_layer, d.n_rows, d.k, d.x_f16, d.y_f16);
+    if (rc) {
+      std::string msg = t_err;
+      return fail(rc, "descriptor %d: %s", i, msg.c_str());
+    }
+    BatchEntry be;
+    be.w = d.w_layer;
+    be.x = d.x_f16;
+    be.y = d.y_f16;
+    be.n_rows = (int32_t)d.n_rows;
+    be.p = (int32_t)(d.k / 1024);
+    be.unit_begin = (int32_t)units;
+    be.reserved = 0;
+    std::memcpy(t + kBatchHeaderBytes + kBatchEntryBytes * (size_t)i, &be, sizeof(be));
+    units += (d.n_rows + 3) / 4 * (d.k / 1024);
+    if (units >= (1LL << 31)) return fail(Q8_ERR_BAD_SHAPE, "batch too large");
+  }
+  int32_t header[4] = {count, (int32_t)units, 0, 0};
+  std::memcpy(t, header, sizeof(header));
+  *total_units = (int32_t)units;
+  return Q8_OK;
+}
+
+int q8gemv_batch(const void* device_table, int count, int32_t total_units, void* stream) {
+  if (!device_table) return fail(Q8_ERR_NULL_POINTER, "null table");
+  if (!aligned(device_table, 16)) return fail(Q8_ERR_MISALIGNED, "table not 16-byte aligned");
+  if (count < 1 || count > kBatchMaxCount)
+    return fail(Q8_ERR_BAD_ARGUMENT, "count %d outside [1, %d]", count, kBatchMaxCount);
+  if (total_units < count) return fail(Q8_ERR_BAD_ARGUMENT, "total_units %d < count", total_units);
+  int rc = check_ready();
+  if (rc) return rc;
+  const int64_t cap = g.batch_wgs > 0 ? g.batch_wgs : 12LL * cu_count();
+  const int64_t grid = total_units < cap ? total_units : cap;
+  const void* t_arg = device_table;
+  int c_arg = count;
+  int u_arg = total_units;
+  void* args[] = {&t_arg, &c_arg, &u_arg};
+  return launch(g.q8batch, (uint32_t)grid, 64, args, static_cast<hipStream_t>(stream));
+}
+
+size_t vocab_argmax_workspace_bytes(void) { return kVocabWorkspaceBytes; }
 
 int vocab_argmax_workspace_reset(void* workspace, void* stream) {
   if (!workspace) return fail(Q8_ERR_NULL_POINTER, "null workspace");
@@ -293,8 +379,12 @@ int f16_gemv_argmax_rows(const void* w_f16, int64_t n_rows, const void* x_f16, v
   int n_arg = (int)n_rows;
   int32_t* t_arg = token;
   void* ws_arg = workspace;
-  void* args[] = {&w_arg, &x_arg, &l_arg, &n_arg, &t_arg, &ws_arg};
-  return launch(g.vocab, (uint32_t)vocab_grid(), 256, args, static_cast<hipStream_t>(stream));
+  void* args[] = {&w_arg, &x_arg, &l_arg, &n_arg, &ws_arg};
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  rc = launch(g.vocab, (uint32_t)vocab_grid(), 256, args, s);
+  if (rc) return rc;
+  void* fargs[] = {&ws_arg, &t_arg};
+  return launch(g.vocab_finalize, 1, 64, fargs, s);
 }
 
 int vocab_gemv_argmax(const void* w_f16, const void* x_f16, void* logits_f16, int32_t* token,
@@ -308,22 +398,10 @@ int decode_dispatch_24_matmul_151936x1x1024_f16(const void* w_f16, const void* x
   return vocab_gemv_argmax(w_f16, x_f16, logits_f16, token, workspace, stream);
 }
 
-int q8gemv_set_rows_per_wave(int64_t k, int quads_per_wave) {
-  if (k != 1024 && k != 2048 && k != 3072)
-    return fail(Q8_ERR_BAD_SHAPE, "K=%lld not in {1024, 2048, 3072}", (long long)k);
-  const int p = (int)(k / 1024);
-  if (quads_per_wave < 1 || quads_per_wave > kMaxQuads || !kQuadsAvail[p - 1][quads_per_wave])
-    return fail(Q8_ERR_BAD_ARGUMENT, "no kernel with %d row quads per wave for K=%lld",
-                quads_per_wave, (long long)k);
-  g.quads[p - 1] = quads_per_wave;
-  return Q8_OK;
-}
-
-int q8gemv_get_rows_per_wave(int64_t k, int* quads_per_wave) {
-  if (k != 1024 && k != 2048 && k != 3072)
-    return fail(Q8_ERR_BAD_SHAPE, "K=%lld not in {1024, 2048, 3072}", (long long)k);
-  if (!quads_per_wave) return fail(Q8_ERR_NULL_POINTER, "null output");
-  *quads_per_wave = g.quads[k / 1024 - 1];
+int q8gemv_batch_set_workgroups(int workgroups) {
+  if (workgroups < 0 || workgroups > kQ8MaxWorkgroups)
+    return fail(Q8_ERR_BAD_ARGUMENT, "workgroups %d outside [0, %d]", workgroups, kQ8MaxWorkgroups);
+  g.batch_wgs = workgroups;
   return Q8_OK;
 }
 
@@ -380,21 +458,27 @@ int q8rt_free(void* ptr) {
 
 int q8rt_memcpy_htod(void* dst, const void* src, size_t bytes) {
   HIP_TRY(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice));
+  HIP_TRY(hipDeviceSynchronize());
   return Q8_OK;
 }
 
 int q8rt_memcpy_dtoh(void* dst, const void* src, size_t bytes) {
+  HIP_TRY(hipDeviceSynchronize());
   HIP_TRY(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost));
   return Q8_OK;
 }
 
 int q8rt_memcpy_dtod(void* dst, const void* src, size_t bytes) {
+  HIP_TRY(hipDeviceSynchronize());
   HIP_TRY(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToDevice));
+  HIP_TRY(hipDeviceSynchronize());
   return Q8_OK;
 }
 
 int q8rt_memset(void* ptr, int value, size_t bytes) {
+  HIP_TRY(hipDeviceSynchronize());
   HIP_TRY(hipMemset(ptr, value, bytes));
+  HIP_TRY(hipDeviceSynchronize());
   return Q8_OK;
 }
 
@@ -475,6 +559,22 @@ int q8rt_graph_launch(void* graph_exec, void* stream) {
 int q8rt_graph_destroy(void* graph_exec) {
   HIP_TRY(hipGraphExecDestroy(static_cast<hipGraphExec_t>(graph_exec)));
   return Q8_OK;
+}
+
+int q8rt_stream_copy(void* dst, const void* src, size_t bytes, void* stream) {
+  if ((!dst || !src) && bytes) return fail(Q8_ERR_NULL_POINTER, "null dst or src");
+  if (bytes % 16 || !aligned(dst, 16) || !aligned(src, 16))
+    return fail(Q8_ERR_MISALIGNED, "copy needs 16-byte aligned pointers and sizes");
+  int rc = check_ready();
+  if (rc) return rc;
+  int64_t n16 = (int64_t)(bytes / 16);
+  int64_t grid = (n16 + 255) / 256;
+  if (grid > 8192) grid = 8192;
+  if (grid < 1) grid = 1;
+  const void* s_arg = src;
+  void* d_arg = dst;
+  void* args[] = {&s_arg, &d_arg, &n16};
+  return launch(g.copy, (uint32_t)grid, 256, args, static_cast<hipStream_t>(stream));
 }
 
 int q8rt_time_next_launch(void* start_event, void* stop_event) {

@@ -110,8 +110,11 @@ _SIGNATURES = {
     "vocab_gemv_argmax": [_P, _P, _P, _P, _P, _P],
     "decode_dispatch_24_matmul_151936x1x1024_f16": [_P, _P, _P, _P, _P, _P],
     "f16_gemv_argmax_rows": [_P, _I64, _P, _P, _P, _P, _P],
-    "q8gemv_set_rows_per_wave": [_I64, _I],
-    "q8gemv_get_rows_per_wave": [_I64, _P],
+    "q8gemv_desc_for_kind": [_I, _P, _I64, _P, _P, _P],
+    "q8gemv_batch_table_bytes": [_I],
+    "q8gemv_batch_encode": [_P, _I, _P, _SZ, _P],
+    "q8gemv_batch": [_P, _I, ctypes.c_int32, _P],
+    "q8gemv_batch_set_workgroups": [_I],
     "vocab_set_workgroups": [_I],
     "vocab_get_workgroups": [_P],
     "q8rt_device_count": [_P],
@@ -137,11 +140,13 @@ _SIGNATURES = {
     "q8rt_graph_launch": [_P, _P],
     "q8rt_graph_destroy": [_P],
     "q8rt_time_next_launch": [_P, _P],
+    "q8rt_stream_copy": [_P, _P, _SZ, _P],
 }
 _RESTYPES = {
     "q8gemv_shutdown": None,
     "q8gemv_last_error": ctypes.c_char_p,
     "vocab_argmax_workspace_bytes": _SZ,
+    "q8gemv_batch_table_bytes": _SZ,
 }
 
 _lib: ctypes.CDLL | None = None
@@ -320,6 +325,10 @@ class Graph:
             self.exec = None
 
 
+def stream_copy(dst, src, nbytes: int, stream=None) -> None:
+    _call("q8rt_stream_copy", _ptr(dst), _ptr(src), int(nbytes), _stream(stream))
+
+
 def time_next_launch(start: Event, stop: Event) -> None:
     _call("q8rt_time_next_launch", start.handle, stop.handle)
 
@@ -388,14 +397,51 @@ def f16_gemv_argmax_rows(w, n_rows: int, x, logits, token, workspace, stream=Non
           _ptr(workspace), _stream(stream))
 
 
-def set_rows_per_wave(k: int, quads: int) -> None:
-    _call("q8gemv_set_rows_per_wave", int(k), int(quads))
+def set_batch_workgroups(n: int) -> None:
+    """Cap on workgroups of a batched Q8_0 launch (0 = default)."""
+    _call("q8gemv_batch_set_workgroups", int(n))
 
 
-def get_rows_per_wave(k: int) -> int:
-    q = ctypes.c_int(0)
-    _call("q8gemv_get_rows_per_wave", int(k), ctypes.byref(q))
-    return q.value
+class Q8Desc(ctypes.Structure):
+    """struct q8gemv_desc (include/q8gemv.h)."""
+    _fields_ = [("w_layer", ctypes.c_void_p), ("x_f16", ctypes.c_void_p),
+                ("y_f16", ctypes.c_void_p), ("n_rows", ctypes.c_int64), ("k", ctypes.c_int64)]
+
+
+def desc(w_layer, n_rows: int, k: int, x, y) -> Q8Desc:
+    return Q8Desc(_ptr(w_layer), _ptr(x), _ptr(y), int(n_rows), int(k))
+
+
+def desc_for_kind(kind: int, w_stacked, layer: int, x, y) -> Q8Desc:
+    d = Q8Desc()
+    _call("q8gemv_desc_for_kind", int(kind), _ptr(w_stacked), int(layer), _ptr(x), _ptr(y),
+          ctypes.byref(d))
+    return d
+
+
+class Q8Batch:
+    """An encoded list of independent Q8_0 GEMVs resident on the device; each
+    launch() runs all of them in one kernel launch."""
+
+    def __init__(self, descs: list[Q8Desc]):
+        n = len(descs)
+        arr = (Q8Desc * n)(*descs)
+        nbytes = int(load_library().q8gemv_batch_table_bytes(n))
+        if nbytes == 0:
+            raise Q8GemvError(Q8_ERR_BAD_ARGUMENT, f"bad batch size {n}")
+        host = (ctypes.c_uint8 * nbytes)()
+        units = ctypes.c_int32(0)
+        _call("q8gemv_batch_encode", arr, n, host, nbytes, ctypes.byref(units))
+        self.count = n
+        self.total_units = units.value
+        self.table = DeviceBuffer(nbytes)
+        self.table.upload(np.frombuffer(host, dtype=np.uint8))
+
+    def launch(self, stream=None) -> None:
+        _call("q8gemv_batch", self.table.ptr, self.count, self.total_units, _stream(stream))
+
+    def free(self) -> None:
+        self.table.free()
 
 
 def set_vocab_workgroups(n: int) -> None:

@@ -82,10 +82,15 @@ def test_dispatch_table_mirrors_reference_exports(Q):
     (lambda L: L.vocab_gemv_argmax(A16, A16, A16, A16 + 2, A16, None), 5),
     (lambda L: L.vocab_gemv_argmax(A16, A16, A16 + 1, A16, A16, None), 5),
     (lambda L: L.vocab_gemv_argmax(A16, A16, None, A16, A16 + 8, None), 5),
-    (lambda L: L.q8gemv_set_rows_per_wave(1024, 5), 9),
-    (lambda L: L.q8gemv_set_rows_per_wave(2048, 3), 9),
-    (lambda L: L.q8gemv_set_rows_per_wave(4096, 1), 6),
-    (lambda L: L.vocab_set_workgroups(5000), 9),
+    (lambda L: L.q8gemv_batch_set_workgroups(70000), 9),
+    (lambda L: L.q8gemv_batch_set_workgroups(-2), 9),
+    (lambda L: L.vocab_set_workgroups(9000), 9),
+    (lambda L: L.q8gemv_batch(A16, 0, 10, None), 9),
+    (lambda L: L.q8gemv_batch(A16, 4, 2, None), 9),
+    (lambda L: L.q8gemv_batch(None, 4, 8, None), 3),
+    (lambda L: L.q8gemv_batch(A16 + 8, 4, 8, None), 5),
+    (lambda L: L.q8gemv_desc_for_kind(9, A16, 0, A16, A16, A16), 2),
+    (lambda L: L.q8gemv_desc_for_kind(0, A16, 28, A16, A16, A16), 4),
 ])
 def test_argument_validation_before_any_device_work(Q, call, code):
     lib = Q.load_library()
@@ -110,10 +115,9 @@ def test_missing_code_object_is_an_error(Q, tmp_path):
 
 
 def test_workspace_size_and_tuning_roundtrip(Q):
-    assert Q.vocab_workspace_bytes() == 16 + 8 * 4096
-    Q.set_rows_per_wave(1024, 2)
-    assert Q.get_rows_per_wave(1024) == 2
-    Q.set_rows_per_wave(1024, 1)
+    assert Q.vocab_workspace_bytes() == 256
+    Q.set_batch_workgroups(64)
+    Q.set_batch_workgroups(0)
     Q.set_vocab_workgroups(512)
     assert Q.get_vocab_workgroups() == 512
     Q.set_vocab_workgroups(0)
@@ -124,6 +128,60 @@ def test_code_object_targets_gfx950_and_has_every_kernel():
     data = co.read_bytes()
     assert data[:4] == b"\x7fELF"
     assert b"amdgcn-amd-amdhsa--gfx950" in data
-    for name in ("q8gemv_p1_r1", "q8gemv_p2_r1", "q8gemv_p3_r1", "vocab_gemv_argmax_k1024",
-                 "vocab_workspace_reset"):
+    for name in ("q8gemv_p1", "q8gemv_p2", "q8gemv_p3", "q8gemv_batch_k", "vocab_gemv_argmax_k1024",
+                 "vocab_argmax_finalize", "vocab_workspace_reset", "stream_copy_b128"):
         assert name.encode() in data
+
+
+def test_desc_for_kind_addresses_the_layer(Q):
+    base = 0x100000
+    for d in Q.Q8_KINDS:
+        desc = Q.desc_for_kind(d.kind, base, 5, A16, A16)
+        assert desc.w_layer == base + 5 * d.bytes_per_layer
+        assert (desc.n_rows, desc.k) == (d.n, d.k)
+
+
+def _encode(Q, descs):
+    import ctypes
+
+    lib = Q.load_library()
+    n = len(descs)
+    arr = (Q.Q8Desc * n)(*descs)
+    nbytes = lib.q8gemv_batch_table_bytes(n)
+    host = (ctypes.c_uint8 * nbytes)()
+    units = ctypes.c_int32(0)
+    rc = lib.q8gemv_batch_encode(arr, n, host, nbytes, ctypes.byref(units))
+    return rc, bytes(host), units.value
+
+
+def test_batch_encode_layout(Q):
+    descs = [Q.desc(0x20000, 2048, 1024, 0x30000, 0x40000),
+             Q.desc(0x50000, 1023, 3072, 0x60000, 0x70002),
+             Q.desc(0x80000, 1, 2048, 0x90000, 0xA0000)]
+    rc, table, units = _encode(Q, descs)
+    assert rc == 0
+    assert units == 512 * 1 + 256 * 3 + 1 * 2
+    assert len(table) == 16 + 40 * 3
+    hdr = np.frombuffer(table[:16], np.int32)
+    assert hdr.tolist() == [3, units, 0, 0]
+    ent = np.frombuffer(table[16:], dtype=np.dtype([("w", "<u8"), ("x", "<u8"), ("y", "<u8"),
+                                                     ("n", "<i4"), ("p", "<i4"),
+                                                     ("ub", "<i4"), ("r", "<i4")]))
+    assert ent["w"].tolist() == [0x20000, 0x50000, 0x80000]
+    assert ent["y"].tolist() == [0x40000, 0x70002, 0xA0000]
+    assert ent["n"].tolist() == [2048, 1023, 1]
+    assert ent["p"].tolist() == [1, 3, 2]
+    assert ent["ub"].tolist() == [0, 512, 512 + 768]
+
+
+@pytest.mark.parametrize("bad,code", [
+    (dict(w=0x20008), 5), (dict(x=0x30004), 5), (dict(y=0x40001), 5),
+    (dict(k=4096), 6), (dict(n=0), 6), (dict(w=0), 3),
+])
+def test_batch_encode_rejects_bad_descriptors(Q, bad, code):
+    f = dict(w=0x20000, n=64, k=1024, x=0x30000, y=0x40000)
+    f.update(bad)
+    good = Q.desc(0x20000, 64, 1024, 0x30000, 0x40000)
+    rc, _, _ = _encode(Q, [good, Q.desc(f["w"], f["n"], f["k"], f["x"], f["y"])])
+    assert rc == code
+    assert "descriptor 1" in Q.last_error()

@@ -124,29 +124,70 @@ def test_ragged_row_counts(gpu, O, Wt, k, n_rows):
     assert np.all(out[2 * n_rows:] == 0x7B)
 
 
-@pytest.mark.parametrize("k,quads", [(1024, 1), (1024, 2), (1024, 3), (1024, 4), (1024, 6),
-                                     (2048, 1), (2048, 2), (2048, 4),
-                                     (3072, 1), (3072, 2), (3072, 4)])
-def test_every_launch_shape_is_bit_identical(gpu, O, Wt, k, quads):
+def _batch_case(Q, Wt, stacks):
+    """15 full-shape GEMVs (5 kinds x 3 layers) plus ragged ones, each with
+    its own x and y."""
+    items = []
+    for d in Q.Q8_KINDS:
+        for layer in range(3):
+            items.append((d.n, d.k, stacks[d.kind][layer]))
+    for n, k in ((1, 1024), (5, 3072), (1023, 2048), (17, 1024)):
+        items.append((n, k, Wt.synthetic_q8_layer(n, k, SEED, n, 90 + k // 1024)))
+    bufs = []
+    for i, (n, k, raw) in enumerate(items):
+        x = Wt.synthetic_x(k, SEED, 300 + i)
+        bufs.append((Q.DeviceBuffer.from_array(raw), Q.DeviceBuffer.from_array(x),
+                     Q.DeviceBuffer(2 * n + 64), x))
+    return items, bufs
+
+
+@pytest.mark.parametrize("wgs", [0, 1, 7, 300])
+def test_batched_launch_matches_single_launches(gpu, O, Wt, stacks, wgs):
     Q = gpu
-    n = 6144 if k == 1024 else 1024
-    n = n - 4  # not a multiple of any quad count
-    raw = Wt.synthetic_q8_layer(n, k, SEED, 0, 50)
-    x = Wt.synthetic_x(k, SEED, 9)
-    base_q = Q.get_rows_per_wave(k)
+    items, bufs = _batch_case(Q, Wt, stacks)
     try:
-        with Q.DeviceBuffer.from_array(raw) as w_dev, Q.DeviceBuffer.from_array(x) as x_dev, \
-                Q.DeviceBuffer(2 * n) as y1, Q.DeviceBuffer(2 * n) as y2:
-            Q.set_rows_per_wave(k, 1)
-            Q.q8gemv_rows(w_dev, n, k, x_dev, y1)
-            Q.set_rows_per_wave(k, quads)
-            Q.q8gemv_rows(w_dev, n, k, x_dev, y2)
-            Q.synchronize()
-            a, b = y1.download(np.uint16), y2.download(np.uint16)
+        singles = []
+        for (n, k, raw), (w, xb, y, x) in zip(items, bufs):
+            Q.q8gemv_rows(w, n, k, xb, y)
+        Q.synchronize()
+        for (n, k, raw), (w, xb, y, x) in zip(items, bufs):
+            singles.append(y.download(np.uint16, n))
+            y.fill(0x7B)
+        batch = Q.Q8Batch([Q.desc(w, n, k, xb, y) for (n, k, raw), (w, xb, y, x) in zip(items, bufs)])
+        Q.set_batch_workgroups(wgs)
+        batch.launch()
+        Q.synchronize()
+        for i, ((n, k, raw), (w, xb, y, x)) in enumerate(zip(items, bufs)):
+            out = y.download(np.uint8)
+            assert np.array_equal(out[: 2 * n].view(np.uint16), singles[i]), i
+            assert np.all(out[2 * n:] == 0x7B), i
+            _check(O, singles[i].view(np.float16), raw, n, k, x)
+        batch.free()
     finally:
-        Q.set_rows_per_wave(k, base_q)
-    assert np.array_equal(a, b)
-    _check(O, b.view(np.float16), raw, n, k, x)
+        Q.set_batch_workgroups(0)
+        for b in bufs:
+            for buf in b[:3]:
+                buf.free()
+
+
+def test_batched_qkv_of_one_layer_share_x(gpu, O, Wt, stacks):
+    """q, k and v of a layer read the same x: one batched launch of the three."""
+    Q = gpu
+    x = Wt.synthetic_x(1024, SEED, 77)
+    kv = stacks[Q.ATTN_KV.kind]
+    with Q.DeviceBuffer.from_array(stacks[Q.ATTN_Q.kind]) as wq, Q.DeviceBuffer.from_array(kv) as wkv, \
+            Q.DeviceBuffer.from_array(x) as xb, Q.DeviceBuffer(2 * 4096) as y:
+        descs = [Q.desc_for_kind(Q.ATTN_Q.kind, wq, 1, xb, y.ptr),
+                 Q.desc_for_kind(Q.ATTN_KV.kind, wkv, 1, xb, y.ptr + 4096),
+                 Q.desc_for_kind(Q.ATTN_KV.kind, wkv, 2, xb, y.ptr + 6144)]
+        b = Q.Q8Batch(descs)
+        b.launch()
+        Q.synchronize()
+        out = y.download(np.float16)
+        b.free()
+    _check(O, out[:2048], stacks[Q.ATTN_Q.kind][1], 2048, 1024, x)
+    _check(O, out[2048:3072], kv[1], 1024, 1024, x)
+    _check(O, out[3072:], kv[2], 1024, 1024, x)
 
 
 def test_zero_x_and_power_of_two_linearity(gpu, O, Wt):
