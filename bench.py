@@ -13,7 +13,7 @@ pattern still rotates through the 28 layers).  Measured in the same run:
   * the same sweep as 140 stream-ordered dispatches of the per-GEMV entry
     point (the reference's dispatch granularity), replayed from a hipGraph;
   * the f16 vocab GEMV + fused argmax [151936, 1024];
-  * the GEMV share of a decode step: 28 x (one batched q/k/v launch, o,
+  * the GEMV share of a decode step: 28 x (one fused q/k/v launch, o,
     gate_up, down) + vocab, stream-ordered, replayed from a hipGraph;
   * parity of all 140 sweep outputs and of the vocab logits/token against the
     CPU oracle;
@@ -49,6 +49,19 @@ def algorithmic_bytes(d) -> int:
     return d.bytes_per_layer + 2 * d.k + 2 * d.n
 
 
+def profiled_traffic(name: str, grid_threads: int):
+    """HBM bytes per dispatch of kernel `name` at this grid, from the committed
+    rocprofv3 counter summary (FETCH_SIZE + WRITE_SIZE, each scaled by what it
+    reads for a copy kernel of known size); None if not profiled."""
+    path = REPO / "profiles" / "traffic.json"
+    if not path.exists():
+        return None
+    for k in json.loads(path.read_text()).get("kernels", []):
+        if k.get("name") == name and k.get("grid") == grid_threads and k.get("hbm_bytes"):
+            return int(k["hbm_bytes"])
+    return None
+
+
 def timed_ms(Q, stream, fn, reps: int) -> float:
     """Mean ms per call of fn() over `reps` back-to-back calls on `stream`,
     bracketed by HIP events on that stream."""
@@ -74,6 +87,9 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-graph", action="store_true",
                     help="issue the per-dispatch and decode-step chains eagerly instead of from hipGraphs")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="first run the plain copy kernel over MIB MiB five times (a kernel of known "
+                         "traffic for scaling HBM byte counters)")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -113,6 +129,17 @@ def main() -> int:
 
     stream = Q.Stream()
     sweep_order = [(layer, d) for layer in range(layers) for d in kinds]
+
+    copy_cal = None
+    if args.copy_calibration > 0:
+        nbytes = args.copy_calibration << 20
+        src, dst = Q.DeviceBuffer(nbytes), Q.DeviceBuffer(nbytes)
+        copy_ms = timed_ms(Q, stream, lambda: Q.stream_copy(dst, src, nbytes, stream), 5)
+        copy_cal = {"bytes_read": nbytes, "bytes_written": nbytes, "us": round(copy_ms * 1e3, 2),
+                    "GBps_read_plus_write": round(2 * nbytes / (copy_ms * 1e-3) / 1e9, 1)}
+        log(f"copy calibration: {nbytes} B read + written in {copy_ms * 1e3:.1f} us")
+        src.free()
+        dst.free()
 
     # ------------------------------------------- headline: batched sweep
     batch = Q.Q8Batch([Q.desc_for_kind(d.kind, stacks[d.kind][1], layer, xs[(layer, d.kind)][1],
@@ -183,19 +210,15 @@ def main() -> int:
         f"(argmax of own logits {own}, {rep_v['fail']} failing logits)")
 
     # ---------------------------------------- GEMV share of a decode step
-    qkv = []
+    # Separate K and V weights (the attn_kv stack above serves as K).
+    v_host = Wt.synthetic_q8_stack(1024, 1024, layers, seed=SEED, tensor=7, workers=16)
+    v_dev = Q.DeviceBuffer.from_array(v_host)
     step_y = {name: Q.DeviceBuffer(2 * 6144) for name in ("q", "k", "v", "o", "gu", "dn")}
-    for layer in range(layers):
-        xq = xs[(layer, Q.ATTN_Q.kind)][1]
-        qkv.append(Q.Q8Batch([
-            Q.desc_for_kind(Q.ATTN_Q.kind, stacks[Q.ATTN_Q.kind][1], layer, xq, step_y["q"]),
-            Q.desc_for_kind(Q.ATTN_KV.kind, stacks[Q.ATTN_KV.kind][1], layer, xq, step_y["k"]),
-            Q.desc_for_kind(Q.ATTN_KV.kind, stacks[Q.ATTN_KV.kind][1], layer, xq, step_y["v"]),
-        ]))
 
     def record_decode_gemvs():
         for layer in range(layers):
-            qkv[layer].launch(stream)
+            Q.q8gemv_qkv(stacks[Q.ATTN_Q.kind][1], stacks[Q.ATTN_KV.kind][1], v_dev, layer,
+                         xs[(layer, Q.ATTN_Q.kind)][1], step_y["q"], step_y["k"], step_y["v"], stream)
             for d, yname in ((Q.ATTN_O, "o"), (Q.GATE_UP, "gu"), (Q.FFN_DN, "dn")):
                 Q.q8gemv(d.kind, stacks[d.kind][1], layer, xs[(layer, d.kind)][1], step_y[yname], stream)
         vocab_fn()
@@ -208,9 +231,13 @@ def main() -> int:
     for _ in range(3):
         dstep_fn()
     decode_gemv_us = timed_ms(Q, stream, dstep_fn, 30) * 1e3
-    log(f"decode-step GEMVs (28 x [qkv batch, o, gate_up, down] + vocab): {decode_gemv_us:.1f} us")
+    decode_bytes = (sum(algorithmic_bytes(d) for d in Q.LAYER_ORDER) * layers + vocab_bytes)
+    log(f"decode-step GEMVs (28 x [q8gemv_qkv, o, gate_up, down] + vocab, 114 dispatches): "
+        f"{decode_gemv_us:.1f} us, {decode_bytes / decode_gemv_us / 1e3:.0f} GB/s")
 
     parity_ok = fails == 0 and rep_v["fail"] == 0 and token == own
+    batch_grid = min(batch.total_units, 12 * info["compute_units"]) * 64
+    traffic = profiled_traffic("q8gemv_batch_k", batch_grid)
 
     # ------------------------------------------------------ CPU baseline
     cpu = None
@@ -267,15 +294,21 @@ def main() -> int:
             "frac": round(value / HBM_PEAK_GBS, 4),
             "avg_us": round(ms_per_step * 1e3, 2),
             "bytes_per_launch": sweep_bytes,
-            "traffic": None,
+            "traffic": traffic,
+            "traffic_source": "profiles/traffic.json: rocprofv3 FETCH_SIZE + WRITE_SIZE per dispatch, "
+                              "each scaled by its reading for the plain copy kernel of known size",
         },
         "per_dispatch_sweep": {"us": round(chain_ms * 1e3, 1), "GBps": round(chain_gbs, 1),
                                "frac": round(chain_gbs / HBM_PEAK_GBS, 4), "dispatches": 140,
                                "launch": "eager" if args.no_graph else "hipGraph"},
         "vocab": {"us": round(v_ms * 1e3, 2), "GBps": round(v_gbs, 1),
                   "frac": round(v_gbs / HBM_PEAK_GBS, 4), "bytes": vocab_bytes, "token": token},
-        "decode_step_gemv_us": round(decode_gemv_us, 2),
+        "decode_step_gemv": {"us": round(decode_gemv_us, 2), "bytes": decode_bytes,
+                             "GBps": round(decode_bytes / decode_gemv_us / 1e3, 1),
+                             "dispatches": 4 * layers + 2,
+                             "launch": "eager" if args.no_graph else "hipGraph"},
         "parity_ok": bool(parity_ok),
+        "copy_calibration": copy_cal,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)

@@ -113,6 +113,16 @@ int decode_dispatch_18_matmul_6144x1x1024_f16(const void* q8_stacked, int64_t la
 int decode_dispatch_20_matmul_1024x1x3072_f16(const void* q8_stacked, int64_t layer,
                                               const void* x_f16, void* y_f16, void* stream);
 
+/* q, k and v of one layer in one launch (no reference counterpart: the
+ * reference runs decode_dispatch_3 once and decode_dispatch_4 twice on the
+ * same normed input, model/qwen3_full.mlir:625-635).  wq_stacked is the
+ * [28, 2228224] attn_q buffer, wk_stacked / wv_stacked the [28, 1114112]
+ * attn_k / attn_v buffers; yq receives 2048 values, yk and yv 1024 each.
+ * Each output is bit-identical to the corresponding q8gemv call. */
+int q8gemv_qkv(const void* wq_stacked, const void* wk_stacked, const void* wv_stacked,
+               int64_t layer, const void* x_f16, void* yq_f16, void* yk_f16, void* yv_f16,
+               void* stream);
+
 /* ---- batched Q8_0 GEMVs: several independent GEMVs in one launch (no
  * reference counterpart; the reference issues one dispatch per GEMV) ----
  *

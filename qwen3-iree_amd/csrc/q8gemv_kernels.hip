@@ -16,6 +16,11 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+// Every multiply-add below is written out; the compiler may not contract on
+// its own, so the same row computes to the same bits in every kernel that
+// inlines the shared helpers (single, fused q/k/v and batched launches).
+#pragma clang fp contract(off)
+
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
@@ -40,6 +45,9 @@ __device__ __forceinline__ f16x2 as_f16x2(uint32_t v) { return __builtin_bit_cas
 // each the faster of the two on MI355X.
 #ifndef Q8_NT_LOADS
 #define Q8_NT_LOADS 1
+#endif
+#ifndef Q8_X_REUSE
+#define Q8_X_REUSE 1
 #endif
 #ifndef VOCAB_NT_LOADS
 #define VOCAB_NT_LOADS 0
@@ -94,8 +102,8 @@ __device__ __forceinline__ float reduce_row16(float v) {
 //   d[0..16]: the pair's 17 dwords (pair start is 4-byte aligned)
 //     byte 0-1 scale0, 2-33 q0[0..31], 34-35 scale1, 36-67 q1[0..31]
 //   xr[0..7]: x for the pair's 64 K positions, 8 f16 per u32x4
-// Returns f32(scale0)*dot0 + f32(scale1)*dot1 with each dot an f32 sum of
-// exact int8*f16 products.
+// Returns fma(f32(scale1), dot1, f32(scale0)*dot0) with each dot an f32 sum
+// of exact int8*f16 products.
 __device__ __forceinline__ float q8_pair_dot(const uint32_t (&d)[17], const u32x4 (&xr)[8]) {
   uint32_t e[17];
 #pragma unroll
@@ -112,7 +120,7 @@ __device__ __forceinline__ float q8_pair_dot(const uint32_t (&d)[17], const u32x
   }
   const float s0 = f16_bits_to_f32(d[0] & 0xffffu);
   const float s1 = f16_bits_to_f32(d[8] >> 16);
-  return s0 * dot0 + s1 * dot1;
+  return __builtin_fmaf(s1, dot1, s0 * dot0);
 }
 
 // ---------------------------------------------------------- Q8_0 GEMV ------
@@ -206,6 +214,8 @@ __device__ __forceinline__ void q8_segment(const Q8Seg& s, int u_begin, int u_en
   };
   int cq = lq, cc = 0;  // next unit to compute
   float acc = 0.0f;
+  u32x4 xr[8];   // x of chunk xr_c for this lane's 64 columns; for K = 1024
+  int xr_c = -1;  // every unit of the GEMV reuses it
   auto compute = [&](const u32x4 (&src)[kUnitLoads]) {
 #pragma unroll
     for (int i = 0; i < kUnitLoads; ++i) l4[i * 64 + lane] = src[i];
@@ -214,10 +224,12 @@ __device__ __forceinline__ void q8_segment(const Q8Seg& s, int u_begin, int u_en
     uint32_t d[17];
 #pragma unroll
     for (int m = 0; m < 17; ++m) d[m] = pp[m];
-    const u32x4* xs = reinterpret_cast<const u32x4*>(xl + 1024 * cc + 64 * p16);
-    u32x4 xr[8];
+    if (cc != xr_c || !Q8_X_REUSE) {
+      const u32x4* xs = reinterpret_cast<const u32x4*>(xl + 1024 * cc + 64 * p16);
 #pragma unroll
-    for (int m = 0; m < 8; ++m) xr[m] = xs[m];
+      for (int m = 0; m < 8; ++m) xr[m] = xs[m];
+      xr_c = cc;
+    }
     acc += q8_pair_dot(d, xr);
     if (cc == s.p - 1) {
       const float tot = reduce_row16(acc);
@@ -262,14 +274,14 @@ __device__ __forceinline__ void q8_segment(const Q8Seg& s, int u_begin, int u_en
 template <int P>
 __device__ __forceinline__ void q8_quad(const uint8_t* __restrict__ w,
                                         const uint16_t* __restrict__ x,
-                                        uint16_t* __restrict__ y, int n_rows,
+                                        uint16_t* __restrict__ y, int n_rows, int quad,
                                         uint8_t* __restrict__ lds) {
   constexpr int ROWB = kChunkBytes * P;
   constexpr int PIECES = 4 * ROWB / 16;  // 272 * P
   constexpr int LOADS = (PIECES + 63) / 64;
 
   const int lane = threadIdx.x;
-  const int row0 = blockIdx.x * 4;
+  const int row0 = quad * 4;
   int rows_here = n_rows - row0;
   rows_here = rows_here < 4 ? rows_here : 4;
   // Pieces past the quad's valid bytes (ragged last quad, or the last load's
@@ -488,11 +500,25 @@ __device__ __forceinline__ void vocab_body(const uint16_t* __restrict__ W,
       const uint8_t* __restrict__ w, const uint16_t* __restrict__ x,                       \
       uint16_t* __restrict__ y, int n_rows) {                                              \
     __shared__ __attribute__((aligned(16))) uint8_t lds[(4 * (P) * 68 + 63) / 64 * 1024];  \
-    q8_quad<P>(w, x, y, n_rows, lds);                                                      \
+    q8_quad<P>(w, x, y, n_rows, blockIdx.x, lds);                                          \
   }
 Q8GEMV_SINGLE(1)
 Q8GEMV_SINGLE(2)
 Q8GEMV_SINGLE(3)
+
+// q, k and v of one layer in one launch: the three GEMVs read the same x
+// (model/qwen3_full.mlir:625-635).  Workgroups 0..511 take the 512 row quads
+// of q [2048,1024], 512..767 those of k [1024,1024], 768..1023 those of v.
+extern "C" __global__ __launch_bounds__(64) void q8gemv_qkv_k(
+    const uint8_t* __restrict__ wq, const uint8_t* __restrict__ wk,
+    const uint8_t* __restrict__ wv, const uint16_t* __restrict__ x, uint16_t* __restrict__ yq,
+    uint16_t* __restrict__ yk, uint16_t* __restrict__ yv) {
+  __shared__ __attribute__((aligned(16))) uint8_t lds[5 * 1024];
+  const int b = blockIdx.x;
+  if (b < 512) q8_quad<1>(wq, x, yq, 2048, b, lds);
+  else if (b < 768) q8_quad<1>(wk, x, yk, 1024, b - 512, lds);
+  else q8_quad<1>(wv, x, yv, 1024, b - 768, lds);
+}
 
 // Many independent GEMVs in one launch.  The batch's units are split evenly
 // over the waves; a wave owns every quad whose first unit falls in its range

@@ -67,6 +67,7 @@ struct State {
   hipModule_t module = nullptr;
   hipFunction_t q8[3] = {};  // K = 1024, 2048, 3072
   hipFunction_t q8batch = nullptr;
+  hipFunction_t q8qkv = nullptr;
   hipFunction_t vocab = nullptr;
   hipFunction_t vocab_finalize = nullptr;
   hipFunction_t ws_reset = nullptr;
@@ -186,6 +187,7 @@ int q8gemv_init(const char* code_object_path) {
   if (e == hipSuccess) e = hipModuleGetFunction(&g.q8[1], mod, "q8gemv_p2");
   if (e == hipSuccess) e = hipModuleGetFunction(&g.q8[2], mod, "q8gemv_p3");
   if (e == hipSuccess) e = hipModuleGetFunction(&g.q8batch, mod, "q8gemv_batch_k");
+  if (e == hipSuccess) e = hipModuleGetFunction(&g.q8qkv, mod, "q8gemv_qkv_k");
   if (e != hipSuccess) {
     (void)hipModuleUnload(mod);
     return fail(Q8_ERR_CODE_OBJECT, "Q8_0 GEMV kernels missing from %s", path.c_str());
@@ -214,7 +216,7 @@ void q8gemv_shutdown(void) {
   if (!g.ready) return;
   (void)hipModuleUnload(g.module);
   g.module = nullptr;
-  g.q8[0] = g.q8[1] = g.q8[2] = g.q8batch = nullptr;
+  g.q8[0] = g.q8[1] = g.q8[2] = g.q8batch = g.q8qkv = nullptr;
   g.vocab = g.vocab_finalize = g.ws_reset = g.copy = nullptr;
   g.ready = false;
 }
@@ -288,6 +290,34 @@ int q8gemv_desc_for_kind(int kind, const void* w_stacked, int64_t layer, const v
   out->n_rows = ki.n;
   out->k = ki.k;
   return Q8_OK;
+}
+
+int q8gemv_qkv(const void* wq_stacked, const void* wk_stacked, const void* wv_stacked,
+               int64_t layer, const void* x_f16, void* yq_f16, void* yk_f16, void* yv_f16,
+               void* stream) {
+  if (!wq_stacked || !wk_stacked || !wv_stacked || !x_f16 || !yq_f16 || !yk_f16 || !yv_f16)
+    return fail(Q8_ERR_NULL_POINTER, "null weight, x or y pointer");
+  if (layer < 0 || layer >= Q8_NUM_LAYERS)
+    return fail(Q8_ERR_LAYER_RANGE, "layer %lld outside [0, %d)", (long long)layer,
+                Q8_NUM_LAYERS);
+  if (!aligned(wq_stacked, 16) || !aligned(wk_stacked, 16) || !aligned(wv_stacked, 16))
+    return fail(Q8_ERR_MISALIGNED, "weights not 16-byte aligned");
+  if (!aligned(x_f16, 16)) return fail(Q8_ERR_MISALIGNED, "x not 16-byte aligned");
+  if (!aligned(yq_f16, 2) || !aligned(yk_f16, 2) || !aligned(yv_f16, 2))
+    return fail(Q8_ERR_MISALIGNED, "y not 2-byte aligned");
+  int rc = check_ready();
+  if (rc) return rc;
+  const int64_t bpl_q = 2048LL * 1024 / Q8_BLOCK_ELEMS * Q8_BLOCK_BYTES;
+  const int64_t bpl_kv = 1024LL * 1024 / Q8_BLOCK_ELEMS * Q8_BLOCK_BYTES;
+  const void* wq = static_cast<const uint8_t*>(wq_stacked) + layer * bpl_q;
+  const void* wk = static_cast<const uint8_t*>(wk_stacked) + layer * bpl_kv;
+  const void* wv = static_cast<const uint8_t*>(wv_stacked) + layer * bpl_kv;
+  const void* x = x_f16;
+  void* yq = yq_f16;
+  void* yk = yk_f16;
+  void* yv = yv_f16;
+  void* args[] = {&wq, &wk, &wv, &x, &yq, &yk, &yv};
+  return launch(g.q8qkv, 1024, 64, args, static_cast<hipStream_t>(stream));
 }
 
 size_t q8gemv_batch_table_bytes(int count) {

@@ -110,6 +110,7 @@ _SIGNATURES = {
     "vocab_gemv_argmax": [_P, _P, _P, _P, _P, _P],
     "decode_dispatch_24_matmul_151936x1x1024_f16": [_P, _P, _P, _P, _P, _P],
     "f16_gemv_argmax_rows": [_P, _I64, _P, _P, _P, _P, _P],
+    "q8gemv_qkv": [_P, _P, _P, _I64, _P, _P, _P, _P, _P],
     "q8gemv_desc_for_kind": [_I, _P, _I64, _P, _P, _P],
     "q8gemv_batch_table_bytes": [_I],
     "q8gemv_batch_encode": [_P, _I, _P, _SZ, _P],
@@ -358,6 +359,12 @@ def kind_shape(kind: int) -> tuple[int, int, int]:
 def q8gemv(kind: int, w_stacked, layer: int, x, y, stream=None) -> None:
     """y = W[layer] . x for one Q8_0 kind (decode_dispatch_{3,4,12,18,20})."""
     _call("q8gemv", int(kind), _ptr(w_stacked), int(layer), _ptr(x), _ptr(y), _stream(stream))
+
+
+def q8gemv_qkv(wq_stacked, wk_stacked, wv_stacked, layer: int, x, yq, yk, yv, stream=None) -> None:
+    """q, k and v of one layer in one launch (all three read x)."""
+    _call("q8gemv_qkv", _ptr(wq_stacked), _ptr(wk_stacked), _ptr(wv_stacked), int(layer), _ptr(x),
+          _ptr(yq), _ptr(yk), _ptr(yv), _stream(stream))
 
 
 def q8gemv_rows(w_layer, n_rows: int, k: int, x, y, stream=None) -> None:

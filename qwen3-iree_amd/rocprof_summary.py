@@ -1,0 +1,101 @@
+#!/usr/bin/env python3
+"""Summarise rocprofv3 CSV output of bench.py into a short markdown report.
+
+Inputs (directories written by `rocprofv3 -f csv -d DIR -o bench ...`):
+  --trace DIR   a --kernel-trace --stats run  (bench_kernel_stats.csv,
+                bench_kernel_trace.csv)
+  --fetch DIR   a --pmc FETCH_SIZE run         (bench_counter_collection.csv)
+  --write DIR   a --pmc WRITE_SIZE run         (bench_counter_collection.csv)
+  --copy-bytes N  bytes the calibration copy kernel (stream_copy_b128) read
+                and wrote in those runs (bench.py --copy-calibration MIB)
+
+HBM traffic per dispatch = FETCH_SIZE * (N / FETCH_SIZE of the copy kernel)
++ WRITE_SIZE * (N / WRITE_SIZE of the copy kernel): each counter is scaled by
+what it reads for a copy of known size.  Kernels are grouped by name and grid
+size (one launch shape = one row).
+
+Writes the markdown report to stdout and, with --json PATH, the per-kernel
+traffic figures as JSON.
+"""
+from __future__ import annotations
+
+import argparse
+import csv
+import json
+import statistics
+from collections import defaultdict
+from pathlib import Path
+
+
+def _rows(path: Path):
+    with open(path, newline="") as f:
+        yield from csv.DictReader(f)
+
+
+def kernel_durations(trace_dir: Path) -> dict:
+    out = defaultdict(list)
+    for r in _rows(trace_dir / "bench_kernel_trace.csv"):
+        key = (r["Kernel_Name"], int(r["Grid_Size_X"]))
+        out[key].append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    return out
+
+
+def counter_values(pmc_dir: Path, counter: str) -> dict:
+    out = defaultdict(list)
+    for r in _rows(pmc_dir / "bench_counter_collection.csv"):
+        if r["Counter_Name"] != counter:
+            continue
+        out[(r["Kernel_Name"], int(r["Grid_Size"]))].append(float(r["Counter_Value"]))
+    return out
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--trace", type=Path, required=True)
+    ap.add_argument("--fetch", type=Path)
+    ap.add_argument("--write", type=Path)
+    ap.add_argument("--copy-bytes", type=int, default=0)
+    ap.add_argument("--kernels", nargs="*", default=None, help="only these kernel names")
+    ap.add_argument("--json", type=Path)
+    args = ap.parse_args()
+
+    durs = kernel_durations(args.trace)
+    fetch = counter_values(args.fetch, "FETCH_SIZE") if args.fetch else {}
+    write = counter_values(args.write, "WRITE_SIZE") if args.write else {}
+
+    def scale(values: dict) -> float | None:
+        copy = [v for (name, _), vs in values.items() if name == "stream_copy_b128" for v in vs]
+        if not copy or not args.copy_bytes:
+            return None
+        return args.copy_bytes / 1024.0 / statistics.mean(copy)
+
+    fs, ws = scale(fetch), scale(write)
+    print("| kernel | grid (threads) | dispatches | mean us | median us | min us |"
+          " FETCH_SIZE KiB | WRITE_SIZE KiB | HBM bytes / dispatch |")
+    print("|---|---|---|---|---|---|---|---|---|")
+    report = {"fetch_scale": fs, "write_scale": ws, "kernels": []}
+    for key in sorted(durs, key=lambda k: -sum(durs[k])):
+        name, grid = key
+        if args.kernels and name not in args.kernels:
+            continue
+        d = durs[key]
+        f = statistics.mean(fetch[key]) if fetch.get(key) else None
+        w = statistics.mean(write[key]) if write.get(key) else None
+        traffic = None
+        if f is not None and w is not None and fs and ws:
+            traffic = round(f * 1024 * fs + w * 1024 * ws)
+        print(f"| {name} | {grid} | {len(d)} | {statistics.mean(d):.3f} | {statistics.median(d):.3f} |"
+              f" {min(d):.3f} | {'' if f is None else f'{f:.1f}'} | {'' if w is None else f'{w:.1f}'} |"
+              f" {'' if traffic is None else traffic} |")
+        report["kernels"].append({"name": name, "grid": grid, "dispatches": len(d),
+                                  "mean_us": statistics.mean(d), "fetch_kib": f, "write_kib": w,
+                                  "hbm_bytes": traffic})
+    print()
+    print(f"FETCH_SIZE scale (copy kernel): {fs}; WRITE_SIZE scale: {ws}")
+    if args.json:
+        args.json.write_text(json.dumps(report, indent=1) + "\n")
+    return 0
+
+
+if __name__ == "__main__":
+    raise SystemExit(main())

@@ -90,6 +90,10 @@ def test_dispatch_table_mirrors_reference_exports(Q):
     (lambda L: L.q8gemv_batch(None, 4, 8, None), 3),
     (lambda L: L.q8gemv_batch(A16 + 8, 4, 8, None), 5),
     (lambda L: L.q8gemv_desc_for_kind(9, A16, 0, A16, A16, A16), 2),
+    (lambda L: L.q8gemv_qkv(A16, A16, A16, 28, A16, A16, A16, A16, None), 4),
+    (lambda L: L.q8gemv_qkv(A16, None, A16, 0, A16, A16, A16, A16, None), 3),
+    (lambda L: L.q8gemv_qkv(A16, A16, A16 + 4, 0, A16, A16, A16, A16, None), 5),
+    (lambda L: L.q8gemv_qkv(A16, A16, A16, 0, A16, A16, A16 + 1, A16, None), 5),
     (lambda L: L.q8gemv_desc_for_kind(0, A16, 28, A16, A16, A16), 4),
 ])
 def test_argument_validation_before_any_device_work(Q, call, code):
@@ -128,7 +132,7 @@ def test_code_object_targets_gfx950_and_has_every_kernel():
     data = co.read_bytes()
     assert data[:4] == b"\x7fELF"
     assert b"amdgcn-amd-amdhsa--gfx950" in data
-    for name in ("q8gemv_p1", "q8gemv_p2", "q8gemv_p3", "q8gemv_batch_k", "vocab_gemv_argmax_k1024",
+    for name in ("q8gemv_p1", "q8gemv_p2", "q8gemv_p3", "q8gemv_batch_k", "q8gemv_qkv_k", "vocab_gemv_argmax_k1024",
                  "vocab_argmax_finalize", "vocab_workspace_reset", "stream_copy_b128"):
         assert name.encode() in data
 

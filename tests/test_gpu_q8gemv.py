@@ -190,6 +190,30 @@ def test_batched_qkv_of_one_layer_share_x(gpu, O, Wt, stacks):
     _check(O, out[3072:], kv[2], 1024, 1024, x)
 
 
+@pytest.mark.parametrize("layer", [0, 2])
+def test_fused_qkv_matches_three_dispatches(gpu, O, Wt, stacks, layer):
+    """q8gemv_qkv gives exactly the bits of decode_dispatch_3 + 2 x decode_dispatch_4."""
+    Q = gpu
+    x = Wt.synthetic_x(1024, SEED, 78 + layer)
+    wq_h = stacks[Q.ATTN_Q.kind]
+    wk_h = stacks[Q.ATTN_KV.kind]
+    wv_h = Wt.synthetic_q8_stack(1024, 1024, 3, seed=SEED, tensor=99)
+    with Q.DeviceBuffer.from_array(wq_h) as wq, Q.DeviceBuffer.from_array(wk_h) as wk, \
+            Q.DeviceBuffer.from_array(wv_h) as wv, Q.DeviceBuffer.from_array(x) as xb, \
+            Q.DeviceBuffer(2 * 4096) as y1, Q.DeviceBuffer(2 * 4096) as y2:
+        Q.decode_dispatch(3, wq, layer, xb, y1.ptr)
+        Q.decode_dispatch(4, wk, layer, xb, y1.ptr + 4096)
+        Q.decode_dispatch(4, wv, layer, xb, y1.ptr + 6144)
+        y2.fill(0x7B)
+        Q.q8gemv_qkv(wq, wk, wv, layer, xb, y2.ptr, y2.ptr + 4096, y2.ptr + 6144)
+        Q.synchronize()
+        a, b = y1.download(np.uint16), y2.download(np.uint16)
+    assert np.array_equal(a, b)
+    _check(O, b[:2048].view(np.float16), wq_h[layer], 2048, 1024, x)
+    _check(O, b[2048:3072].view(np.float16), wk_h[layer], 1024, 1024, x)
+    _check(O, b[3072:].view(np.float16), wv_h[layer], 1024, 1024, x)
+
+
 def test_zero_x_and_power_of_two_linearity(gpu, O, Wt):
     Q = gpu
     d = Q.ATTN_O
