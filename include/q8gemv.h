@@ -184,6 +184,21 @@ int decode_dispatch_24_matmul_151936x1x1024_f16(const void* w_f16, const void* x
 int f16_gemv_argmax_rows(const void* w_f16, int64_t n_rows, const void* x_f16,
                          void* logits_f16, int32_t* token, void* workspace, void* stream);
 
+/* ---- the reference's own binding ABI ----
+ *
+ * The code object also exports the six kernels under the reference's
+ * executable names with IREE's HAL binding ABI (binding base pointers, then
+ * i32 push constants; x / y at the byte offsets the reference bakes in:
+ * kernels/cuda/dispatch_3.cu:19-21, dispatch_4.cu:19-22, dispatch_12.cu:19-21,
+ * dispatch_18.cu:19-21, dispatch_20.cu:19-21, dispatch_24.cu:19-20), so an
+ * IREE ROCm build can substitute them (compile.sh:35-43; stubs in
+ * INTEGRATION.md).  This launches one of them exactly as such a stub would:
+ * ordinal 3, 4, 12, 18, 20 or 24; push constants as the reference defines them
+ * (layer = c0 | c1 << 32; dispatch 4: c0 = output byte offset, layer =
+ * c1 | c2 << 32; dispatch 24: c0 = output byte offset, logits only). */
+int q8gemv_hal_dispatch(int ordinal, const void* binding0, const void* binding1, void* binding2,
+                        const uint32_t* push_constants, int n_constants, void* stream);
+
 /* ---- launch-shape tuning (no reference counterpart) ---- */
 
 /* Upper bound on the workgroups (one wave each) of a batched Q8_0 launch;

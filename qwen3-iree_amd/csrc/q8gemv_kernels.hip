@@ -393,7 +393,7 @@ __device__ __forceinline__ float f16_row_dot(const u32x4& w, const u32x4& xv, fl
 // strictly-greater update keeps the first maximum; the 16 groups of a
 // workgroup are merged with argmax_better, and workgroups meet in a 64-bit
 // atomic max over argmax_key, whose order is the same rule.
-template <bool NT>
+template <bool NT, bool ARGMAX>
 __device__ __forceinline__ void vocab_body(const uint16_t* __restrict__ W,
                                            const uint16_t* __restrict__ x,
                                            uint16_t* __restrict__ logits, int n_rows,
@@ -436,10 +436,12 @@ __device__ __forceinline__ void vocab_body(const uint16_t* __restrict__ W,
     const uint16_t hb = f32_to_f16_bits(acc);
     if (row < n_rows) {
       if (logits != nullptr && li == 0) logits[row] = hb;
-      const float hv = f16_bits_to_f32(hb);
-      if (hv > best_v) {
-        best_v = hv;
-        best_i = row;
+      if constexpr (ARGMAX) {
+        const float hv = f16_bits_to_f32(hb);
+        if (hv > best_v) {
+          best_v = hv;
+          best_i = row;
+        }
       }
     }
   };
@@ -465,6 +467,8 @@ __device__ __forceinline__ void vocab_body(const uint16_t* __restrict__ W,
       consume(b_begin + i, A);
     }
   }
+
+  if constexpr (!ARGMAX) return;
 
   // ---- workgroup combine: 4 waves x 4 row groups, then one atomic ----
   __shared__ float s_val[16];
@@ -555,7 +559,7 @@ extern "C" __global__ __launch_bounds__(64) void q8gemv_batch_k(const uint8_t* _
 extern "C" __global__ __launch_bounds__(256) void vocab_gemv_argmax_k1024(
     const uint16_t* __restrict__ W, const uint16_t* __restrict__ x,
     uint16_t* __restrict__ logits, int n_rows, uint8_t* __restrict__ ws) {
-  vocab_body<VOCAB_NT_LOADS != 0>(W, x, logits, n_rows, ws);
+  vocab_body<VOCAB_NT_LOADS != 0, true>(W, x, logits, n_rows, ws);
 }
 
 // token = row of the winning key (-1 for none); leaves the key zero for the
@@ -583,4 +587,49 @@ extern "C" __global__ __launch_bounds__(256) void stream_copy_b128(const u32x4* 
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += stride)
     dst[i] = src[i];
+}
+
+// ------------------------------------------------ IREE HAL binding ABI ----
+//
+// The same kernels under the reference's executable export names and binding
+// ABI, for IREE's executable substitution (compile.sh:35-43) with a ROCm HSACO
+// object: binding base pointers, then the i32 push constants, with x and y at
+// the byte offsets the reference bakes in (kernels/cuda/dispatch_3.cu:8-22,
+// dispatch_4.cu:8-22, dispatch_12.cu:19-21, dispatch_18.cu:19-21,
+// dispatch_20.cu:19-21, dispatch_24.cu:11-20).  Launch shape (the stub's
+// workgroup count): Q8_0 dispatches 64-thread workgroups, N/4 of them; the
+// vocab dispatch 1024 workgroups of 256 threads, logits only (the reference
+// runs its argmax as separate dispatches).
+#define HAL_Q8_DISPATCH(NAME, P, N, BPL, X_OFF, Y_OFF)                                      \
+  extern "C" __global__ __launch_bounds__(64) void NAME(                                      \
+      const uint8_t* __restrict__ q8_stacked, const char* __restrict__ b1,                    \
+      char* __restrict__ b2, uint32_t c0, uint32_t c1) {                                      \
+    __shared__ __attribute__((aligned(16))) uint8_t lds[(4 * (P) * 68 + 63) / 64 * 1024];    \
+    const uint64_t layer = (uint64_t)c0 | ((uint64_t)c1 << 32);                               \
+    q8_quad<P>(q8_stacked + layer * (BPL), reinterpret_cast<const uint16_t*>(b1 + (X_OFF)),  \
+               reinterpret_cast<uint16_t*>(b2 + (Y_OFF)), N, blockIdx.x, lds);                \
+  }
+
+HAL_Q8_DISPATCH(decode_dispatch_3_matmul_2048x1x1024_f16, 1, 2048, 2228224ULL, 2112, 4160)
+HAL_Q8_DISPATCH(decode_dispatch_12_matmul_1024x1x2048_f16, 2, 1024, 2228224ULL, 12352, 2048)
+HAL_Q8_DISPATCH(decode_dispatch_18_matmul_6144x1x1024_f16, 1, 6144, 6684672ULL, 64, 6144)
+HAL_Q8_DISPATCH(decode_dispatch_20_matmul_1024x1x3072_f16, 3, 1024, 3342336ULL, 18432, 0)
+
+// dispatch_4 takes the output byte offset as c0 and the layer as c1 | c2 << 32.
+extern "C" __global__ __launch_bounds__(64) void decode_dispatch_4_matmul_1024x1x1024_f16(
+    const uint8_t* __restrict__ q8_stacked, const char* __restrict__ b1, char* __restrict__ b2,
+    uint32_t c0, uint32_t c1, uint32_t c2) {
+  __shared__ __attribute__((aligned(16))) uint8_t lds[5 * 1024];
+  const uint64_t layer = (uint64_t)c1 | ((uint64_t)c2 << 32);
+  q8_quad<1>(q8_stacked + layer * 1114112ULL, reinterpret_cast<const uint16_t*>(b1 + 2112),
+             reinterpret_cast<uint16_t*>(b2 + (int)c0), 1024, blockIdx.x, lds);
+}
+
+// dispatch_24 takes the output byte offset as c0.
+extern "C" __global__ __launch_bounds__(256) void decode_dispatch_24_matmul_151936x1x1024_f16(
+    const uint16_t* __restrict__ weight, const char* __restrict__ b1, char* __restrict__ b2,
+    uint32_t c0) {
+  vocab_body<VOCAB_NT_LOADS != 0, false>(weight, reinterpret_cast<const uint16_t*>(b1 + 64),
+                                         reinterpret_cast<uint16_t*>(b2 + (int)c0), 151936,
+                                         nullptr);
 }

@@ -59,6 +59,25 @@ struct BatchEntry {
 };
 static_assert(sizeof(BatchEntry) == kBatchEntryBytes, "batch entry layout");
 
+// The six reference executables (kernels/cuda/dispatch_*.mlir:5-9): ordinal,
+// export name, push-constant count, workgroup size and count of this build's
+// substitution stubs.
+struct HalDispatch {
+  int ordinal;
+  const char* name;
+  int constants;
+  uint32_t block;
+  uint32_t grid;
+};
+constexpr HalDispatch kHalDispatches[6] = {
+    {3, "decode_dispatch_3_matmul_2048x1x1024_f16", 2, 64, 512},
+    {4, "decode_dispatch_4_matmul_1024x1x1024_f16", 3, 64, 256},
+    {12, "decode_dispatch_12_matmul_1024x1x2048_f16", 2, 64, 256},
+    {18, "decode_dispatch_18_matmul_6144x1x1024_f16", 2, 64, 1536},
+    {20, "decode_dispatch_20_matmul_1024x1x3072_f16", 2, 64, 256},
+    {24, "decode_dispatch_24_matmul_151936x1x1024_f16", 1, 256, 1024},
+};
+
 struct State {
   std::mutex mu;
   bool ready = false;
@@ -68,6 +87,7 @@ struct State {
   hipFunction_t q8[3] = {};  // K = 1024, 2048, 3072
   hipFunction_t q8batch = nullptr;
   hipFunction_t q8qkv = nullptr;
+  hipFunction_t hal[6] = {};  // IREE HAL-ABI kernels, in kHalDispatches order
   hipFunction_t vocab = nullptr;
   hipFunction_t vocab_finalize = nullptr;
   hipFunction_t ws_reset = nullptr;
@@ -188,6 +208,8 @@ int q8gemv_init(const char* code_object_path) {
   if (e == hipSuccess) e = hipModuleGetFunction(&g.q8[2], mod, "q8gemv_p3");
   if (e == hipSuccess) e = hipModuleGetFunction(&g.q8batch, mod, "q8gemv_batch_k");
   if (e == hipSuccess) e = hipModuleGetFunction(&g.q8qkv, mod, "q8gemv_qkv_k");
+  for (int i = 0; i < 6 && e == hipSuccess; ++i)
+    e = hipModuleGetFunction(&g.hal[i], mod, kHalDispatches[i].name);
   if (e != hipSuccess) {
     (void)hipModuleUnload(mod);
     return fail(Q8_ERR_CODE_OBJECT, "Q8_0 GEMV kernels missing from %s", path.c_str());
@@ -217,6 +239,7 @@ void q8gemv_shutdown(void) {
   (void)hipModuleUnload(g.module);
   g.module = nullptr;
   g.q8[0] = g.q8[1] = g.q8[2] = g.q8batch = g.q8qkv = nullptr;
+  std::memset(g.hal, 0, sizeof(g.hal));
   g.vocab = g.vocab_finalize = g.ws_reset = g.copy = nullptr;
   g.ready = false;
 }
@@ -318,6 +341,43 @@ int q8gemv_qkv(const void* wq_stacked, const void* wk_stacked, const void* wv_st
   void* yv = yv_f16;
   void* args[] = {&wq, &wk, &wv, &x, &yq, &yk, &yv};
   return launch(g.q8qkv, 1024, 64, args, static_cast<hipStream_t>(stream));
+}
+
+int q8gemv_hal_dispatch(int ordinal, const void* binding0, const void* binding1, void* binding2,
+                        const uint32_t* push_constants, int n_constants, void* stream) {
+  int idx = -1;
+  for (int i = 0; i < 6; ++i)
+    if (kHalDispatches[i].ordinal == ordinal) idx = i;
+  if (idx < 0) return fail(Q8_ERR_INVALID_KIND, "no substituted dispatch with ordinal %d", ordinal);
+  const HalDispatch& hd = kHalDispatches[idx];
+  if (!binding0 || !binding1 || !binding2 || !push_constants)
+    return fail(Q8_ERR_NULL_POINTER, "null binding or push-constant pointer");
+  if (n_constants != hd.constants)
+    return fail(Q8_ERR_BAD_ARGUMENT, "%s takes %d push constants, got %d", hd.name, hd.constants,
+                n_constants);
+  if (!aligned(binding0, 16) || !aligned(binding1, 16) || !aligned(binding2, 2))
+    return fail(Q8_ERR_MISALIGNED, "bindings 0/1 need 16-byte, binding 2 2-byte alignment");
+  if (ordinal != 24) {
+    const int lo = ordinal == 4 ? 1 : 0;
+    const uint64_t layer = (uint64_t)push_constants[lo] | ((uint64_t)push_constants[lo + 1] << 32);
+    if (layer >= (uint64_t)Q8_NUM_LAYERS)
+      return fail(Q8_ERR_LAYER_RANGE, "layer %llu outside [0, %d)", (unsigned long long)layer,
+                  Q8_NUM_LAYERS);
+  }
+  if ((ordinal == 4 || ordinal == 24) && (push_constants[0] & 1u))
+    return fail(Q8_ERR_MISALIGNED, "output byte offset %u is odd", push_constants[0]);
+  int rc = check_ready();
+  if (rc) return rc;
+  const void* b0 = binding0;
+  const void* b1 = binding1;
+  void* b2 = binding2;
+  uint32_t c[3] = {push_constants[0], hd.constants > 1 ? push_constants[1] : 0u,
+                   hd.constants > 2 ? push_constants[2] : 0u};
+  void* args3[] = {&b0, &b1, &b2, &c[0]};
+  void* args5[] = {&b0, &b1, &b2, &c[0], &c[1]};
+  void* args6[] = {&b0, &b1, &b2, &c[0], &c[1], &c[2]};
+  void** args = hd.constants == 1 ? args3 : hd.constants == 2 ? args5 : args6;
+  return launch(g.hal[idx], hd.grid, hd.block, args, static_cast<hipStream_t>(stream));
 }
 
 size_t q8gemv_batch_table_bytes(int count) {

@@ -111,6 +111,7 @@ _SIGNATURES = {
     "decode_dispatch_24_matmul_151936x1x1024_f16": [_P, _P, _P, _P, _P, _P],
     "f16_gemv_argmax_rows": [_P, _I64, _P, _P, _P, _P, _P],
     "q8gemv_qkv": [_P, _P, _P, _I64, _P, _P, _P, _P, _P],
+    "q8gemv_hal_dispatch": [_I, _P, _P, _P, _P, _I, _P],
     "q8gemv_desc_for_kind": [_I, _P, _I64, _P, _P, _P],
     "q8gemv_batch_table_bytes": [_I],
     "q8gemv_batch_encode": [_P, _I, _P, _SZ, _P],
@@ -384,6 +385,13 @@ def decode_dispatch(ordinal: int, *args, stream=None) -> None:
     else:
         w, x, logits, token, ws = args
         _call(d.export, _ptr(w), _ptr(x), _ptr(logits), _ptr(token), _ptr(ws), _stream(stream))
+
+
+def hal_dispatch(ordinal: int, binding0, binding1, binding2, constants, stream=None) -> None:
+    """Launch a reference executable through its IREE HAL binding ABI."""
+    c = (ctypes.c_uint32 * max(1, len(constants)))(*[int(v) & 0xffffffff for v in constants])
+    _call("q8gemv_hal_dispatch", int(ordinal), _ptr(binding0), _ptr(binding1), _ptr(binding2), c,
+          len(constants), _stream(stream))
 
 
 def vocab_workspace_bytes() -> int:

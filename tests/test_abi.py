@@ -189,3 +189,22 @@ def test_batch_encode_rejects_bad_descriptors(Q, bad, code):
     rc, _, _ = _encode(Q, [good, Q.desc(f["w"], f["n"], f["k"], f["x"], f["y"])])
     assert rc == code
     assert "descriptor 1" in Q.last_error()
+
+
+@pytest.mark.parametrize("ordinal,consts,code", [
+    (5, [0, 0], 2),
+    (3, [0], 9),
+    (4, [0, 0], 9),
+    (24, [0, 0], 9),
+    (3, [28, 0], 4),
+    (3, [0, 1], 4),
+    (4, [0, 28, 0], 4),
+    (4, [3, 0, 0], 5),
+    (24, [7], 5),
+])
+def test_hal_dispatch_validation(Q, ordinal, consts, code):
+    import ctypes
+
+    lib = Q.load_library()
+    c = (ctypes.c_uint32 * len(consts))(*consts)
+    assert lib.q8gemv_hal_dispatch(ordinal, A16, A16, A16, c, len(consts), None) == code
