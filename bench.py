@@ -15,6 +15,10 @@ pattern still rotates through the 28 layers).  Measured in the same run:
   * the f16 vocab GEMV + fused argmax [151936, 1024];
   * the GEMV share of a decode step: 28 x (one fused q/k/v launch, o,
     gate_up, down) + vocab, stream-ordered, replayed from a hipGraph;
+  * the full decode step (qwen3_decode_step: embedding, 28 layers with
+    attention over a 1024-position KV cache, final norm, vocab, argmax) on
+    random-init Qwen3-0.6B weights, replayed from a hipGraph with the token
+    fed back on the device, checked against the oracle's step;
   * parity of all 140 sweep outputs and of the vocab logits/token against the
     CPU oracle;
   * the CPU oracle on a bounded sample of the same sweep (cpu_baseline).
@@ -85,6 +89,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=1000,
                     help="untimed steps before timing (the GPU clock ramps up over the first "
                          "~100 ms of sustained work)")
+    ap.add_argument("--context", type=int, default=1024,
+                    help="positions attended by the timed decode step")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline sample budget")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-graph", action="store_true",
@@ -237,7 +243,57 @@ def main() -> int:
     log(f"decode-step GEMVs (28 x [q8gemv_qkv, o, gate_up, down] + vocab, 114 dispatches): "
         f"{decode_gemv_us:.1f} us, {decode_bytes / decode_gemv_us / 1e3:.0f} GB/s")
 
-    parity_ok = fails == 0 and rep_v["fail"] == 0 and token == own
+    # ------------------------------------------- full decode step (C5)
+    from qwen3_iree_amd import decode as D
+
+    t0 = time.time()
+    mhost = D.synthetic_weights(seed=SEED, workers=16)
+    model = D.DeviceWeights(mhost)
+    ctx = args.context
+    max_seq = ctx
+    sess = D.DecodeSession(model, max_seq, stream)
+    rng = np.random.default_rng(SEED + 5)
+    kc = rng.standard_normal((D.LAYERS * max_seq, D.KV_DIM), dtype=np.float32).astype(np.float16)
+    vc = (np.float32(0.6) * rng.standard_normal((D.LAYERS * max_seq, D.KV_DIM),
+                                                dtype=np.float32)).astype(np.float16)
+    sess.k_cache.upload(kc)
+    sess.v_cache.upload(vc)
+    first_token = 1234
+    sess.set_state(first_token, ctx - 1)
+    log(f"decode model ready in {time.time() - t0:.1f}s ({model.nbytes} parameter bytes), "
+        f"context {ctx}")
+    # one checked step: attention over slots 0..ctx-1, position kept (advance = 0)
+    sess.step(advance=False, logits=True)
+    step_tok, step_pos = sess.get_state()
+    step_logits = sess.read_logits()
+    ref_tok, ref_logits, _ = O.decode_step(mhost, kc, vc, max_seq, first_token, ctx - 1, True)
+    dl = np.abs(step_logits.astype(np.float64) - ref_logits.astype(np.float64))
+    srt = np.sort(ref_logits.astype(np.float64))
+    margin = float(srt[-1] - srt[-2])
+    step_ok = (step_tok == O.argmax_tiled(step_logits) and step_pos == ctx - 1
+               and (step_tok == ref_tok or margin <= 2 * dl.max()))
+    log(f"decode step parity: token {step_tok} (oracle {ref_tok}, margin {margin:.4f}, "
+        f"max |dlogit| {dl.max():.4f})")
+    # timed: replays of the captured step, each consuming the previous token
+    sess.set_state(first_token, ctx - 1)
+    if args.no_graph:
+        dec_fn = lambda: sess.step(advance=False, logits=False)  # noqa: E731
+    else:
+        sess.capture(advance=False, logits=False)
+        dec_fn = lambda: sess.replay(advance=False, logits=False)  # noqa: E731
+    for _ in range(20):
+        dec_fn()
+    dec_us = timed_ms(Q, stream, dec_fn, max(50, args.steps // 4)) * 1e3
+    norm_bytes = 2 * (D.LAYERS * (2 * D.HIDDEN + 2 * D.HEAD_DIM) + D.HIDDEN)
+    kv_bytes = D.LAYERS * ctx * 2 * D.KV_DIM * 2
+    dec_bytes = (sum(algorithmic_bytes(d) for d in Q.LAYER_ORDER) * layers + vocab_bytes
+                 + kv_bytes + norm_bytes + 2 * D.HIDDEN)
+    dec_gbs = dec_bytes / dec_us / 1e3
+    log(f"decode step (context {ctx}, {3 + 6 * layers} launches"
+        f"{'' if args.no_graph else ', hipGraph'}): {dec_us:.1f} us/token, "
+        f"{1e6 / dec_us:.0f} tok/s, {dec_gbs:.0f} GB/s")
+
+    parity_ok = fails == 0 and rep_v["fail"] == 0 and token == own and step_ok
     batch_grid = min(batch.total_units, 12 * info["compute_units"]) * 64
     traffic = profiled_traffic("q8gemv_batch_k", batch_grid)
 
@@ -309,6 +365,11 @@ def main() -> int:
                              "GBps": round(decode_bytes / decode_gemv_us / 1e3, 1),
                              "dispatches": 4 * layers + 2,
                              "launch": "eager" if args.no_graph else "hipGraph"},
+        "decode_step": {"us": round(dec_us, 2), "tok_per_s": round(1e6 / dec_us, 1),
+                        "context": ctx, "bytes": dec_bytes, "GBps": round(dec_gbs, 1),
+                        "frac": round(dec_gbs / HBM_PEAK_GBS, 4), "launches": 3 + 6 * layers,
+                        "launch": "eager" if args.no_graph else "hipGraph",
+                        "token": step_tok, "oracle_token": ref_tok, "parity_ok": bool(step_ok)},
         "parity_ok": bool(parity_ok),
         "copy_calibration": copy_cal,
         "cpu_baseline": cpu,

@@ -1,0 +1,95 @@
+/*
+ * Qwen3-0.6B decode step on MI355X (gfx950): the glue around the Q8_0 GEMVs of
+ * q8gemv.h, as one C ABI.  Implemented by libq8gemv.so (kernels in the code
+ * object decode_gfx950.hsaco, loaded by q8gemv_init).
+ *
+ * The reference runs this step inside IREE: @generate's inner loop
+ * (model/qwen3_full.mlir:1431-1526) = embedding gather, 28 x
+ * @transformer_layer_decode_static (:751-864), final rms_norm, vocab matmul and
+ * the tiled argmax.  Here a step is a sequence of kernel launches on one
+ * stream that reads the input token and the position from device memory and
+ * writes the next token back, so a step captured once in a hipGraph can be
+ * replayed token after token (the reference feeds the token back on device
+ * and increments the position on device, :1512-1523).
+ *
+ * Conventions as in q8gemv.h: device pointers owned by the caller, status
+ * codes, nothing allocates, arguments validated before anything is enqueued.
+ */
+#ifndef QWEN3_DECODE_H
+#define QWEN3_DECODE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Device pointers to the model's parameters, in the reference's layout
+ * (create_q8_irpa.py:149-224; qwen3_full.mlir:66-79, 772-777): all 16-byte
+ * aligned. */
+typedef struct qwen3_weights {
+  const void* token_embd;  /* f16 [151936, 1024] */
+  const void* attn_norm;   /* f16 [28, 1024] */
+  const void* ffn_norm;    /* f16 [28, 1024] */
+  const void* q_norm;      /* f16 [28, 128] */
+  const void* k_norm;      /* f16 [28, 128] */
+  const void* wq;          /* Q8_0 [28, 2228224] */
+  const void* wk;          /* Q8_0 [28, 1114112] */
+  const void* wv;          /* Q8_0 [28, 1114112] */
+  const void* wo;          /* Q8_0 [28, 2228224] */
+  const void* wgu;         /* Q8_0 [28, 6684672] gate rows then up rows */
+  const void* wdn;         /* Q8_0 [28, 3342336] */
+  const void* output_norm; /* f16 [1024] */
+  const void* output_w;    /* f16 [151936, 1024] (output_T.weight) */
+} qwen3_weights;
+
+/* KV cache: two f16 buffers [28 * max_seq, 8, 128] each (K, V), the flat
+ * layout of qwen3_full.mlir:213-230: the entry of layer l, position p is slot
+ * l * max_seq + p (:782, 795). */
+
+/* Scratch (activations, attention partials, argmax key, status word):
+ * qwen3_scratch_bytes() bytes, 256-byte aligned.  Zero it once with
+ * qwen3_scratch_reset before the first step; steps keep it consistent.  One
+ * scratch serves one stream: concurrent steps need their own. */
+size_t qwen3_scratch_bytes(void);
+int qwen3_scratch_reset(void* scratch, void* stream);
+/* Byte offset in the scratch of the u32 status word: bit 0 = a step asked to
+ * advance past the last cache slot (the position then stays). */
+size_t qwen3_scratch_status_offset(void);
+
+/* One token: h = token_embd[*token]; 28 layers at position *pos (attention
+ * over slots 0..*pos of each layer, the new k/v written to slot *pos); final
+ * rms_norm; logits (f16 [151936], may be NULL); *token = argmax (lowest index
+ * of the maximal f16 logit, -1 if none).  With advance != 0, *pos then moves
+ * to *pos + 1 (not past max_seq - 1; see the status word).  A *pos outside
+ * [0, max_seq) is clamped into it.  token and pos are device int32. */
+int qwen3_decode_step(const qwen3_weights* w, void* k_cache, void* v_cache, int64_t max_seq,
+                      int32_t* token, int32_t* pos, void* logits, int advance, void* scratch,
+                      void* stream);
+
+/* The same step in parts, for tests and for callers that interleave work:
+ * embed: h_out = token_embd[*token];
+ * layer: h_out = layer `layer` of h_in at position *pos (h_in, h_out f16[1024],
+ *        distinct; uses and overwrites the scratch activations);
+ * head:  logits / *token / *pos as in qwen3_decode_step from the final h. */
+int qwen3_decode_embed(const qwen3_weights* w, const int32_t* token, void* h_out, void* stream);
+int qwen3_decode_layer(const qwen3_weights* w, int layer, void* k_cache, void* v_cache,
+                       int64_t max_seq, const int32_t* pos, const void* h_in, void* h_out,
+                       void* scratch, void* stream);
+int qwen3_decode_head(const qwen3_weights* w, const void* h, void* logits, int32_t* token,
+                      int32_t* pos, int advance, int64_t max_seq, void* scratch, void* stream);
+
+/* Scratch offsets of the intermediates the last qwen3_decode_layer (or head)
+ * left behind, all f16: "xn" [1024] rms_norm(h_in, attn_norm); "q" [2048],
+ * "k" [1024], "v" [1024] the projections before head norm and RoPE;
+ * "q_roped" [2048] q after head norm and RoPE; "attn" [2048] attention
+ * output; "res" [1024] residual after attention; "fn" [1024]
+ * rms_norm(res, ffn_norm); "act" [3072] SwiGLU output; "on" [1024] the final
+ * rms_norm(h, output_norm) of the head.  -1 for an unknown name. */
+int64_t qwen3_scratch_offset(const char* name);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -55,6 +55,17 @@ def lib() -> ctypes.CDLL:
         L.oracle_argmax_tiled.argtypes = [_P, _I64, _I64]
         L.oracle_argmax_tiled.restype = ctypes.c_int64
         L.oracle_num_threads.restype = ctypes.c_int
+        # decode_oracle.c
+        L.oracle_rmsnorm.argtypes = [_P, _P, ctypes.c_int, ctypes.c_float, _P]
+        L.oracle_head_rmsnorm.argtypes = [_P, ctypes.c_int, _P, ctypes.c_float, _P]
+        L.oracle_rope.argtypes = [_P, ctypes.c_int, ctypes.c_int32, _P]
+        L.oracle_attention.argtypes = [_P, _P, _P, ctypes.c_int, ctypes.c_float, _P]
+        L.oracle_swiglu.argtypes = [_P, _P, ctypes.c_int, _P]
+        L.oracle_add_f16.argtypes = [_P, _P, ctypes.c_int, _P]
+        L.oracle_decode_layer.argtypes = [_P, ctypes.c_int, _P, _P, _I64, ctypes.c_int32, _P, _P,
+                                          _P]
+        L.oracle_decode_step.argtypes = [_P, _P, _P, _I64, ctypes.c_int32, ctypes.c_int32, _P, _P]
+        L.oracle_decode_step.restype = ctypes.c_int64
         _lib = L
     return _lib
 
@@ -145,6 +156,123 @@ def argmax_tiled(v: np.ndarray, tile: int = 256) -> int:
 
 def num_threads() -> int:
     return int(lib().oracle_num_threads())
+
+
+# ---------------------------------------------------------- decode step ----
+# Qwen3-0.6B shapes (model/qwen3_full.mlir:29-64).
+LAYERS, HIDDEN, Q_HEADS, KV_HEADS, HEAD_DIM, FFN, VOCAB = 28, 1024, 16, 8, 128, 3072, 151936
+Q_DIM, KV_DIM = Q_HEADS * HEAD_DIM, KV_HEADS * HEAD_DIM
+EPS = float(np.float32(9.99999997e-7))
+ATTN_SCALE = float(np.float32(1.0 / 11.313708498984761))
+WEIGHT_FIELDS = ("token_embd", "attn_norm", "ffn_norm", "q_norm", "k_norm", "wq", "wk", "wv",
+                 "wo", "wgu", "wdn", "output_norm", "output_w")
+
+
+class _Weights(ctypes.Structure):
+    _fields_ = [(f, _P) for f in WEIGHT_FIELDS]
+
+
+class _Trace(ctypes.Structure):
+    _fields_ = [("q_roped", ctypes.c_uint16 * Q_DIM), ("k_roped", ctypes.c_uint16 * KV_DIM),
+                ("v", ctypes.c_uint16 * KV_DIM), ("attn", ctypes.c_uint16 * Q_DIM),
+                ("res1", ctypes.c_uint16 * HIDDEN), ("act", ctypes.c_uint16 * FFN)]
+
+
+def _f16(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float16)
+
+
+def rmsnorm(x: np.ndarray, w: np.ndarray, eps: float = EPS) -> np.ndarray:
+    x, w = _f16(x).reshape(-1), _f16(w).reshape(-1)
+    assert x.size == w.size
+    out = np.empty_like(x)
+    lib().oracle_rmsnorm(_ptr(x), _ptr(w), x.size, eps, _ptr(out))
+    return out
+
+
+def head_rmsnorm(x: np.ndarray, w: np.ndarray, eps: float = EPS) -> np.ndarray:
+    x, w = _f16(x).reshape(-1), _f16(w).reshape(-1)
+    assert w.size == HEAD_DIM and x.size % HEAD_DIM == 0
+    out = np.empty_like(x)
+    lib().oracle_head_rmsnorm(_ptr(x), x.size // HEAD_DIM, _ptr(w), eps, _ptr(out))
+    return out
+
+
+def rope(x: np.ndarray, pos: int) -> np.ndarray:
+    x = _f16(x).reshape(-1)
+    assert x.size % HEAD_DIM == 0
+    out = np.empty_like(x)
+    lib().oracle_rope(_ptr(x), x.size // HEAD_DIM, int(pos), _ptr(out))
+    return out
+
+
+def attention(q: np.ndarray, k_rows: np.ndarray, v_rows: np.ndarray,
+              scale: float = ATTN_SCALE) -> np.ndarray:
+    """q f16[2048]; k_rows, v_rows f16[ctx, 8, 128] -> f16[2048]."""
+    q = _f16(q).reshape(-1)
+    k_rows, v_rows = _f16(k_rows).reshape(-1, KV_DIM), _f16(v_rows).reshape(-1, KV_DIM)
+    assert q.size == Q_DIM and k_rows.shape == v_rows.shape
+    out = np.empty(Q_DIM, np.float16)
+    lib().oracle_attention(_ptr(q), _ptr(k_rows), _ptr(v_rows), k_rows.shape[0], scale, _ptr(out))
+    return out
+
+
+def swiglu(gate: np.ndarray, up: np.ndarray) -> np.ndarray:
+    gate, up = _f16(gate).reshape(-1), _f16(up).reshape(-1)
+    assert gate.size == up.size
+    out = np.empty_like(gate)
+    lib().oracle_swiglu(_ptr(gate), _ptr(up), gate.size, _ptr(out))
+    return out
+
+
+def add_f16(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    a, b = _f16(a).reshape(-1), _f16(b).reshape(-1)
+    out = np.empty_like(a)
+    lib().oracle_add_f16(_ptr(a), _ptr(b), a.size, _ptr(out))
+    return out
+
+
+def _weights_struct(w) -> _Weights:
+    """w: an object with the WEIGHT_FIELDS attributes as contiguous numpy arrays."""
+    ptrs = []
+    for f in WEIGHT_FIELDS:
+        a = getattr(w, f)
+        assert a.flags["C_CONTIGUOUS"], f
+        ptrs.append(a.ctypes.data)
+    return _Weights(*ptrs)
+
+
+def decode_layer(w, layer: int, k_cache: np.ndarray, v_cache: np.ndarray, max_seq: int,
+                 pos: int, h_in: np.ndarray) -> tuple[np.ndarray, dict]:
+    """One layer at position pos; updates k_cache / v_cache ([28*max_seq, 1024]
+    f16) in place.  Returns (h_out, trace dict of intermediates)."""
+    assert k_cache.dtype == np.float16 and k_cache.flags["C_CONTIGUOUS"]
+    assert v_cache.dtype == np.float16 and v_cache.flags["C_CONTIGUOUS"]
+    assert k_cache.size == LAYERS * max_seq * KV_DIM == v_cache.size
+    h_in = _f16(h_in).reshape(-1)
+    h_out = np.empty(HIDDEN, np.float16)
+    tr = _Trace()
+    ws = _weights_struct(w)
+    lib().oracle_decode_layer(ctypes.byref(ws), int(layer), _ptr(k_cache), _ptr(v_cache),
+                              int(max_seq), int(pos), _ptr(h_in), _ptr(h_out), ctypes.byref(tr))
+    trace = {name: np.frombuffer(bytes(getattr(tr, name)), np.float16).copy()
+             for name, _ in _Trace._fields_}
+    return h_out, trace
+
+
+def decode_step(w, k_cache: np.ndarray, v_cache: np.ndarray, max_seq: int, token: int,
+                pos: int, want_logits: bool = True, want_hidden: bool = False):
+    """One token; updates the caches in place.  Returns (token, logits | None,
+    h_layers [29, 1024] | None)."""
+    assert k_cache.size == LAYERS * max_seq * KV_DIM == v_cache.size
+    logits = np.empty(VOCAB, np.float16) if want_logits else None
+    hl = np.empty((LAYERS + 1, HIDDEN), np.float16) if want_hidden else None
+    ws = _weights_struct(w)
+    tok = lib().oracle_decode_step(ctypes.byref(ws), _ptr(k_cache), _ptr(v_cache), int(max_seq),
+                                   int(token), int(pos),
+                                   _ptr(logits) if logits is not None else None,
+                                   _ptr(hl) if hl is not None else None)
+    return int(tok), logits, hl
 
 
 # ------------------------------------------------------------ tolerance ----

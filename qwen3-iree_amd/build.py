@@ -1,6 +1,7 @@
 """Build recipe for the gfx950 code object and the C-ABI shim library.
 
   lib/q8gemv_gfx950.hsaco  hipcc --genco --offload-arch=gfx950 of csrc/q8gemv_kernels.hip
+  lib/decode_gfx950.hsaco  the same for csrc/decode_kernels.hip (decode-step kernels)
   lib/libq8gemv.so         g++ of csrc/q8gemv_shim.cpp against libamdhip64
 
 Both cross-compile without a GPU.  Run as `python qwen3-iree_amd/build.py`.
@@ -19,6 +20,7 @@ LIB = PKG / "lib"
 ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
 
 CODE_OBJECT = LIB / "q8gemv_gfx950.hsaco"
+DECODE_OBJECT = LIB / "decode_gfx950.hsaco"
 SHIM = LIB / "libq8gemv.so"
 
 HIPCC_FLAGS = [
@@ -39,12 +41,20 @@ def _run(cmd: list[str]) -> None:
         raise RuntimeError(f"build step failed ({proc.returncode}): {' '.join(cmd)}\n{out}")
 
 
-def build_code_object() -> Path:
+def _hsaco(src: Path, out: Path) -> Path:
     LIB.mkdir(exist_ok=True)
-    tmp = CODE_OBJECT.with_suffix(".hsaco.tmp")
-    _run([str(ROCM / "bin" / "hipcc"), *HIPCC_FLAGS, str(CSRC / "q8gemv_kernels.hip"), "-o", str(tmp)])
-    os.replace(tmp, CODE_OBJECT)
-    return CODE_OBJECT
+    tmp = out.with_suffix(".hsaco.tmp")
+    _run([str(ROCM / "bin" / "hipcc"), *HIPCC_FLAGS, f"-I{CSRC}", str(src), "-o", str(tmp)])
+    os.replace(tmp, out)
+    return out
+
+
+def build_code_object() -> Path:
+    return _hsaco(CSRC / "q8gemv_kernels.hip", CODE_OBJECT)
+
+
+def build_decode_object() -> Path:
+    return _hsaco(CSRC / "decode_kernels.hip", DECODE_OBJECT)
 
 
 def build_shim() -> Path:
@@ -62,12 +72,11 @@ def build_shim() -> Path:
     return SHIM
 
 
-def build_all() -> tuple[Path, Path]:
-    return build_code_object(), build_shim()
+def build_all() -> tuple[Path, Path, Path]:
+    return build_code_object(), build_decode_object(), build_shim()
 
 
 if __name__ == "__main__":
-    co, so = build_all()
-    print(co)
-    print(so)
+    for path in build_all():
+        print(path)
     sys.exit(0)

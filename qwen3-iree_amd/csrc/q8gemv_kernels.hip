@@ -3,9 +3,11 @@
 // Built ahead of time into a code object (hipcc --genco) and launched through
 // hipModuleLaunchKernel by the C-ABI shim in q8gemv_shim.cpp.
 //
-//  * q8gemv_p{P}_r{R}: Q8_0 dequant + GEMV, y[N] = W[N,K] . x[K] for
-//    K = 1024*P, one layer of a stacked [L, N*K/32*34] byte buffer.  Replaces
-//    kernels/mlir/dispatch_{3,4,12,18,20}_gpu.mlir (model/qwen3_full.mlir:536-589).
+//  * q8gemv_p{1,2,3}, q8gemv_qkv_k, q8gemv_batch_k: Q8_0 dequant + GEMV,
+//    y[N] = W[N,K] . x[K] for K = 1024*P over one layer of a stacked
+//    [L, N*K/32*34] byte buffer -- one GEMV, q/k/v of a layer, or a list of
+//    GEMVs per launch.  Replace kernels/mlir/dispatch_{3,4,12,18,20}_gpu.mlir
+//    (model/qwen3_full.mlir:536-589).
 //  * vocab_gemv_argmax: f16 GEMV over [n_rows, 1024] with the two-phase argmax
 //    fused in.  Replaces kernels/mlir/dispatch_24_gpu.mlir plus the tiled argmax
 //    at model/qwen3_full.mlir:1469-1511.
@@ -13,488 +15,7 @@
 // Numerics: f16 x, f32 accumulation, round-to-nearest-even f16 outputs.
 // int8 -> f16 conversion is exact (0x6400|u encodes 1024+u; u = q+128), so
 // every int8 x f16 product formed by v_dot2_f32_f16 is exact in f32.
-#include <hip/hip_runtime.h>
-#include <stdint.h>
-
-// Every multiply-add below is written out; the compiler may not contract on
-// its own, so the same row computes to the same bits in every kernel that
-// inlines the shared helpers (single, fused q/k/v and batched launches).
-#pragma clang fp contract(off)
-
-typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-
-namespace {
-
-// v_perm_b32 selectors: output bytes (b_lo, 0x64, b_hi, 0x64) taking b from
-// bytes 0,1 (SEL_LO) or 2,3 (SEL_HI) of the second operand; selector 4 picks
-// byte 0 of the first operand, the 0x64646464 constant.
-constexpr uint32_t kSelLo = 0x04010400u;
-constexpr uint32_t kSelHi = 0x04030402u;
-
-__device__ __forceinline__ f16x2 q8x2_to_f16x2(uint32_t biased, uint32_t sel) {
-  const uint32_t v = __builtin_amdgcn_perm(0x64646464u, biased, sel);
-  // (1024 + u) - 1152 = u - 128 = q, exact in f16.
-  return __builtin_bit_cast(f16x2, v) - (f16x2){(_Float16)1152.0f, (_Float16)1152.0f};
-}
-
-__device__ __forceinline__ f16x2 as_f16x2(uint32_t v) { return __builtin_bit_cast(f16x2, v); }
-
-// Load flavour of the weight streams (read once per launch): the Q8_0 kernels
-// use nontemporal loads (global_load ... nt), the vocab kernel plain loads,
-// each the faster of the two on MI355X.
-#ifndef Q8_NT_LOADS
-#define Q8_NT_LOADS 1
-#endif
-#ifndef Q8_X_REUSE
-#define Q8_X_REUSE 1
-#endif
-#ifndef VOCAB_NT_LOADS
-#define VOCAB_NT_LOADS 0
-#endif
-
-// Pointers read from a batch table are generic; accessing them through the
-// global address space keeps the loads global_load (counted by vmcnt alone)
-// rather than flat_load, whose completion the compiler can only await with a
-// full vmcnt(0) lgkmcnt(0) drain.
-#define GLOBAL_AS __attribute__((address_space(1)))
-
-template <bool NT>
-__device__ __forceinline__ u32x4 load_stream(const u32x4* p) {
-  const GLOBAL_AS u32x4* g = (const GLOBAL_AS u32x4*)p;
-  if constexpr (NT) return __builtin_nontemporal_load(g);
-  else return *g;
-}
-
-__device__ __forceinline__ u32x4 load_global(const u32x4* p) {
-  return *(const GLOBAL_AS u32x4*)p;
-}
-
-__device__ __forceinline__ void store_global_u16(uint16_t* p, uint16_t v) {
-  *(GLOBAL_AS uint16_t*)p = v;
-}
-
-__device__ __forceinline__ float f16_bits_to_f32(uint32_t bits16) {
-  return (float)__builtin_bit_cast(_Float16, (uint16_t)bits16);
-}
-
-__device__ __forceinline__ uint16_t f32_to_f16_bits(float v) {
-  return __builtin_bit_cast(uint16_t, (_Float16)v);  // v_cvt_f16_f32, RNE
-}
-
-template <int CTRL>
-__device__ __forceinline__ float dpp(float v) {
-  return __builtin_bit_cast(
-      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
-}
-
-// Sum over the 16 lanes of a DPP row; every lane of the row ends with the same
-// value (each step adds a lane and its mirror partner, a symmetric pairing).
-__device__ __forceinline__ float reduce_row16(float v) {
-  v += dpp<0xB1>(v);   // quad_perm [1,0,3,2]
-  v += dpp<0x4E>(v);   // quad_perm [2,3,0,1]
-  v += dpp<0x141>(v);  // row_half_mirror
-  v += dpp<0x140>(v);  // row_mirror
-  return v;
-}
-
-// Dot product of one 68-byte Q8_0 block pair with 64 x values.
-//   d[0..16]: the pair's 17 dwords (pair start is 4-byte aligned)
-//     byte 0-1 scale0, 2-33 q0[0..31], 34-35 scale1, 36-67 q1[0..31]
-//   xr[0..7]: x for the pair's 64 K positions, 8 f16 per u32x4
-// Returns fma(f32(scale1), dot1, f32(scale0)*dot0) with each dot an f32 sum
-// of exact int8*f16 products.
-__device__ __forceinline__ float q8_pair_dot(const uint32_t (&d)[17], const u32x4 (&xr)[8]) {
-  uint32_t e[17];
-#pragma unroll
-  for (int m = 0; m < 17; ++m) e[m] = d[m] ^ 0x80808080u;  // q -> q+128 per byte
-  float dot0 = 0.0f, dot1 = 0.0f;
-#pragma unroll
-  for (int t = 0; t < 16; ++t) {
-    const int b0 = 2 + 2 * t;   // byte of q0[2t] in the pair
-    const int b1 = 36 + 2 * t;  // byte of q1[2t]
-    const f16x2 q0 = q8x2_to_f16x2(e[b0 >> 2], (b0 & 2) ? kSelHi : kSelLo);
-    const f16x2 q1 = q8x2_to_f16x2(e[b1 >> 2], (b1 & 2) ? kSelHi : kSelLo);
-    dot0 = __builtin_amdgcn_fdot2(q0, as_f16x2(xr[t >> 2][t & 3]), dot0, false);
-    dot1 = __builtin_amdgcn_fdot2(q1, as_f16x2(xr[4 + (t >> 2)][t & 3]), dot1, false);
-  }
-  const float s0 = f16_bits_to_f32(d[0] & 0xffffu);
-  const float s1 = f16_bits_to_f32(d[8] >> 16);
-  return __builtin_fmaf(s1, dot1, s0 * dot0);
-}
-
-// ---------------------------------------------------------- Q8_0 GEMV ------
-//
-// Rows are handled in quads of 4 consecutive rows; a quad's bytes are one
-// contiguous span (4 rows x K/32 blocks x 34 B).  A wave reads its span with
-// fully coalesced 16-byte loads (lane l takes pieces l, l+64, ...), stages it
-// in LDS and reads it back as 68-byte block pairs: lane l works on row (l >> 4)
-// of the quad and pair (l & 15) of each 1024-column chunk.  HBM therefore sees
-// whole 1 KiB wave requests despite the 34-byte block stride.  A row's partial
-// sums stay in the lane across its K/1024 chunks and meet in a 16-lane DPP
-// reduction.
-//
-// Batched launches split their work into units of one 1024-column chunk of a
-// quad (32 blocks per row, 4352 bytes, whatever K is); a wave owns a
-// contiguous range of units of a GEMV, quad-major and chunk-minor, so it
-// finishes every row it starts.
-
-constexpr int kChunkBytes = 1088;                    // 32 Q8_0 blocks
-constexpr int kUnitBytes = 4 * kChunkBytes;          // 4352
-constexpr int kUnitPieces = kUnitBytes / 16;         // 272
-constexpr int kUnitLoads = (kUnitPieces + 63) / 64;  // 5 per lane
-constexpr int kMaxP = 3;                             // K <= 3072
-constexpr int kSlotBytes = kUnitLoads * 1024;        // 5120: a unit plus spare tail
-
-struct Q8Seg {
-  const uint8_t* w;  // first row of the layer
-  const uint16_t* x;
-  uint16_t* y;
-  int n_rows;
-  int p;  // K / 1024
-};
-
-// Where lane `lane`'s pieces of a unit sit: row within the quad and byte
-// offset within that row's 1088-byte chunk.  The last load covers pieces
-// 256..319 of which only 272 exist; lanes past the end re-read piece 271 (the
-// same 16 bytes lane 15 reads) so that every load is issued by every lane and
-// no load sits behind a branch, and they park the copy in the slot's spare
-// tail.
-struct PieceMap {
-  int row[kUnitLoads];
-  int off[kUnitLoads];
-};
-
-__device__ __forceinline__ PieceMap piece_map(int lane) {
-  PieceMap pm;
-#pragma unroll
-  for (int i = 0; i < kUnitLoads; ++i) {
-    int j = i * 64 + lane;
-    j = j < kUnitPieces ? j : kUnitPieces - 1;
-    pm.row[i] = j / 68;
-    pm.off[i] = (j - (j / 68) * 68) * 16;
-  }
-  return pm;
-}
-
-__device__ __forceinline__ void unit_load(const Q8Seg& s, int quad, int c, const PieceMap& pm,
-                                          u32x4 (&buf)[kUnitLoads]) {
-  const size_t rowb = (size_t)kChunkBytes * s.p;
-  const uint8_t* base = s.w + (size_t)c * kChunkBytes;
-#pragma unroll
-  for (int i = 0; i < kUnitLoads; ++i) {
-    int row = quad * 4 + pm.row[i];
-    row = row < s.n_rows ? row : s.n_rows - 1;  // ragged last quad: re-read a valid row
-    buf[i] = load_stream<Q8_NT_LOADS>(
-        reinterpret_cast<const u32x4*>(base + (size_t)row * rowb + pm.off[i]));
-  }
-}
-
-// Units [u_begin, u_end) of one GEMV in a batched launch (segment-local
-// numbering: quad = u / p, chunk = u % p; u_begin and u_end are multiples of
-// p).  Two register sets ping-pong so that while one unit is computed the
-// next one is already in flight; every load inside the loop is unconditional,
-// so the wait before staging a set covers only that set.
-__device__ __forceinline__ void q8_segment(const Q8Seg& s, int u_begin, int u_end,
-                                           uint8_t* __restrict__ slot,
-                                           uint16_t* __restrict__ xl) {
-  const int lane = threadIdx.x;
-  const PieceMap pm = piece_map(lane);
-  const int p16 = lane & 15;
-  const int rsub = lane >> 4;
-  u32x4* l4 = reinterpret_cast<u32x4*>(slot);
-
-  int lq = u_begin / s.p, lc = 0;  // next unit to load
-  auto load_next = [&](u32x4 (&dst)[kUnitLoads]) {
-    unit_load(s, lq, lc, pm, dst);
-    if (++lc == s.p) {
-      lc = 0;
-      ++lq;
-    }
-  };
-  int cq = lq, cc = 0;  // next unit to compute
-  float acc = 0.0f;
-  u32x4 xr[8];   // x of chunk xr_c for this lane's 64 columns; for K = 1024
-  int xr_c = -1;  // every unit of the GEMV reuses it
-  auto compute = [&](const u32x4 (&src)[kUnitLoads]) {
-#pragma unroll
-    for (int i = 0; i < kUnitLoads; ++i) l4[i * 64 + lane] = src[i];
-    __syncthreads();
-    const uint32_t* pp = reinterpret_cast<const uint32_t*>(slot + rsub * kChunkBytes + 68 * p16);
-    uint32_t d[17];
-#pragma unroll
-    for (int m = 0; m < 17; ++m) d[m] = pp[m];
-    if (cc != xr_c || !Q8_X_REUSE) {
-      const u32x4* xs = reinterpret_cast<const u32x4*>(xl + 1024 * cc + 64 * p16);
-#pragma unroll
-      for (int m = 0; m < 8; ++m) xr[m] = xs[m];
-      xr_c = cc;
-    }
-    acc += q8_pair_dot(d, xr);
-    if (cc == s.p - 1) {
-      const float tot = reduce_row16(acc);
-      const int row = cq * 4 + rsub;
-      if (p16 == 0 && row < s.n_rows) store_global_u16(s.y + row, f32_to_f16_bits(tot));
-      acc = 0.0f;
-    }
-    if (++cc == s.p) {
-      cc = 0;
-      ++cq;
-    }
-    __syncthreads();
-  };
-
-  const int n = u_end - u_begin;
-  u32x4 A[kUnitLoads], B[kUnitLoads];
-  load_next(A);
-  const u32x4* xg = reinterpret_cast<const u32x4*>(s.x);
-  u32x4* xl4 = reinterpret_cast<u32x4*>(xl);
-  for (int t = lane; t < 128 * s.p; t += 64) xl4[t] = load_global(xg + t);
-  int i = 0;
-  for (; i + 2 < n; i += 2) {
-    load_next(B);
-    compute(A);
-    load_next(A);
-    compute(B);
-  }
-  if (n - i == 2) {
-    load_next(B);
-    compute(A);
-    compute(B);
-  } else {
-    compute(A);
-  }
-}
-
-// Single GEMV: one wave per row quad, the latency-bound shape of a lone
-// decode dispatch.  The wave issues all P*5 of its weight loads at once (the
-// quad's 4 rows x P chunks are one contiguous span of 4*1088*P bytes), then
-// its x loads (64 columns per chunk straight into registers), stages the span
-// in LDS and reads it back as block pairs.
-template <int P>
-__device__ __forceinline__ void q8_quad(const uint8_t* __restrict__ w,
-                                        const uint16_t* __restrict__ x,
-                                        uint16_t* __restrict__ y, int n_rows, int quad,
-                                        uint8_t* __restrict__ lds) {
-  constexpr int ROWB = kChunkBytes * P;
-  constexpr int PIECES = 4 * ROWB / 16;  // 272 * P
-  constexpr int LOADS = (PIECES + 63) / 64;
-
-  const int lane = threadIdx.x;
-  const int row0 = quad * 4;
-  int rows_here = n_rows - row0;
-  rows_here = rows_here < 4 ? rows_here : 4;
-  // Pieces past the quad's valid bytes (ragged last quad, or the last load's
-  // spare lanes) re-read the last valid piece and land in rows or LDS bytes
-  // that are never consumed, so every lane issues every load.
-  const int last = rows_here * (ROWB / 16) - 1;
-  const u32x4* src = reinterpret_cast<const u32x4*>(w + (size_t)row0 * ROWB);
-
-  u32x4 buf[LOADS];
-#pragma unroll
-  for (int i = 0; i < LOADS; ++i) {
-    const int c = i * 64 + lane;
-    buf[i] = load_stream<Q8_NT_LOADS>(src + (c < last ? c : last));
-  }
-  const int p16 = lane & 15;
-  const int rsub = lane >> 4;
-  u32x4 xr[P][8];
-#pragma unroll
-  for (int c = 0; c < P; ++c) {
-    const u32x4* xs = reinterpret_cast<const u32x4*>(x + 1024 * c + 64 * p16);
-#pragma unroll
-    for (int m = 0; m < 8; ++m) xr[c][m] = xs[m];
-  }
-  u32x4* l4 = reinterpret_cast<u32x4*>(lds);
-#pragma unroll
-  for (int i = 0; i < LOADS; ++i) l4[i * 64 + lane] = buf[i];
-  __syncthreads();
-
-  float acc = 0.0f;
-#pragma unroll
-  for (int c = 0; c < P; ++c) {
-    const uint32_t* pp =
-        reinterpret_cast<const uint32_t*>(lds + rsub * ROWB + kChunkBytes * c + 68 * p16);
-    uint32_t d[17];
-#pragma unroll
-    for (int m = 0; m < 17; ++m) d[m] = pp[m];
-    acc += q8_pair_dot(d, xr[c]);
-  }
-  acc = reduce_row16(acc);
-  const int row = row0 + rsub;
-  if (p16 == 0 && row < n_rows) y[row] = f32_to_f16_bits(acc);
-}
-
-// Device table of a batched launch: a 16-byte header, then one entry per GEMV
-// in the order the caller listed them.  unit_begin is the exclusive prefix sum
-// of ceil(n_rows / 4) * p.
-struct Q8BatchEntry {
-  const uint8_t* w;
-  const uint16_t* x;
-  uint16_t* y;
-  int32_t n_rows;
-  int32_t p;
-  int32_t unit_begin;
-  int32_t reserved;
-};
-static_assert(sizeof(Q8BatchEntry) == 40, "batch entry layout");
-constexpr int kBatchHeaderBytes = 16;
-
-// ------------------------------------------------------------ vocab ------
-
-// Workspace: one u64 argmax key (below), zero between launches.  Every
-// workgroup folds its best (value, index) into it with a 64-bit atomic max;
-// vocab_argmax_finalize turns the key into the token and zeroes it again.
-// Atomics on one location need no fences, so no workgroup pays for an L2
-// writeback or invalidate.
-
-// Order-preserving key of a candidate (f16 value v at row i >= 0): the high
-// word maps the f16 bit pattern to an unsigned order (-0 folded onto +0, so
-// the two tie), the low word is ~i so that equal values prefer the lower row.
-// Every candidate key is >= 2^42 (its value is > -inf); 0 means "none".
-__device__ __forceinline__ uint64_t argmax_key(float v, int i) {
-  uint32_t h = f32_to_f16_bits(v);  // exact: v is an f16 value
-  if (h == 0x8000u) h = 0u;
-  const uint32_t ord = (h & 0x8000u) ? (~h & 0xffffu) : (h | 0x8000u);
-  return ((uint64_t)ord << 32) | (uint64_t)(0xffffffffu - (uint32_t)i);
-}
-
-// (v, i) beats (bv, bi): a larger value, or an equal value at a lower index.
-// Ordered compares, so NaN never wins; -0 == +0 ties.  A candidate whose value
-// is -inf always carries index -1 (nothing was selected), so it never beats
-// the initial (-inf, -1).
-__device__ __forceinline__ bool argmax_better(float v, int i, float bv, int bi) {
-  return v > bv || (v == bv && i < bi);
-}
-
-// acc + sum of the 8 products w[j]*xv[j] (4 x v_dot2_f32_f16; products exact in f32).
-__device__ __forceinline__ float f16_row_dot(const u32x4& w, const u32x4& xv, float acc) {
-  acc = __builtin_amdgcn_fdot2(as_f16x2(w[0]), as_f16x2(xv[0]), acc, false);
-  acc = __builtin_amdgcn_fdot2(as_f16x2(w[1]), as_f16x2(xv[1]), acc, false);
-  acc = __builtin_amdgcn_fdot2(as_f16x2(w[2]), as_f16x2(xv[2]), acc, false);
-  acc = __builtin_amdgcn_fdot2(as_f16x2(w[3]), as_f16x2(xv[3]), acc, false);
-  return acc;
-}
-
-// f16 GEMV rows [0, n_rows) x K=1024 with a fused argmax.
-//
-// Rows are taken in batches of 4.  Within a wave, DPP row g (lanes 16g..16g+15)
-// owns matrix row 4b+g of batch b: lane i of the group reads bytes
-// [256m + 16i, 256m + 16i + 16) of that row for m = 0..7, so each wave load
-// instruction covers four fully used 256-byte row segments, and the group's
-// partial sums meet in a 16-lane DPP reduction (no cross-row exchange).  The
-// lane keeps its 64 x values (positions 128m + 8i .. +8) in registers for all
-// rows.  Global wave w owns the contiguous batches [w*B/TW, (w+1)*B/TW); the
-// next batch's loads are issued unconditionally before the current batch is
-// reduced, so every wave keeps 8 KiB of weights in flight.
-//
-// Argmax: each logit is rounded to f16 first (the reference compares the f16
-// logits tensor).  Per group the rows arrive in increasing order, so a
-// strictly-greater update keeps the first maximum; the 16 groups of a
-// workgroup are merged with argmax_better, and workgroups meet in a 64-bit
-// atomic max over argmax_key, whose order is the same rule.
-template <bool NT, bool ARGMAX>
-__device__ __forceinline__ void vocab_body(const uint16_t* __restrict__ W,
-                                           const uint16_t* __restrict__ x,
-                                           uint16_t* __restrict__ logits, int n_rows,
-                                           uint8_t* __restrict__ ws) {
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int grp = lane >> 4;
-  const int li = lane & 15;
-  const int64_t gw = (int64_t)blockIdx.x * 4 + wave;
-  const int64_t tw = (int64_t)gridDim.x * 4;
-  const int64_t nbatch = ((int64_t)n_rows + 3) / 4;
-  const int b_begin = (int)(gw * nbatch / tw);
-  const int b_end = (int)((gw + 1) * nbatch / tw);
-
-  const u32x4* xv = reinterpret_cast<const u32x4*>(x);
-  u32x4 xr[8];
-#pragma unroll
-  for (int m = 0; m < 8; ++m) xr[m] = xv[16 * m + li];
-
-  const u32x4* Wv = reinterpret_cast<const u32x4*>(W);
-  auto load_batch = [&](int b, u32x4 (&dst)[8]) {
-    int row = 4 * b + grp;
-    row = row < n_rows ? row : n_rows - 1;  // only the grid's last batch can be short
-    const u32x4* p = Wv + (size_t)row * 128 + li;
-#pragma unroll
-    for (int m = 0; m < 8; ++m) dst[m] = load_stream<NT>(p + 16 * m);
-  };
-
-  float best_v = -__builtin_inff();
-  int best_i = -1;
-  auto consume = [&](int b, const u32x4 (&w)[8]) {
-    float a0 = 0.0f, a1 = 0.0f;
-#pragma unroll
-    for (int m = 0; m < 8; m += 2) {
-      a0 = f16_row_dot(w[m], xr[m], a0);
-      a1 = f16_row_dot(w[m + 1], xr[m + 1], a1);
-    }
-    const float acc = reduce_row16(a0 + a1);
-    const int row = 4 * b + grp;
-    const uint16_t hb = f32_to_f16_bits(acc);
-    if (row < n_rows) {
-      if (logits != nullptr && li == 0) logits[row] = hb;
-      if constexpr (ARGMAX) {
-        const float hv = f16_bits_to_f32(hb);
-        if (hv > best_v) {
-          best_v = hv;
-          best_i = row;
-        }
-      }
-    }
-  };
-
-  // Ping-pong between two register sets; every load inside the loop is
-  // unconditional, so the compiler can wait for exactly the older set.
-  const int nb = b_end - b_begin;
-  if (nb > 0) {
-    u32x4 A[8], B[8];
-    load_batch(b_begin, A);
-    int i = 0;
-    for (; i + 2 < nb; i += 2) {
-      load_batch(b_begin + i + 1, B);
-      consume(b_begin + i, A);
-      load_batch(b_begin + i + 2, A);
-      consume(b_begin + i + 1, B);
-    }
-    if (nb - i == 2) {
-      load_batch(b_begin + i + 1, B);
-      consume(b_begin + i, A);
-      consume(b_begin + i + 1, B);
-    } else {
-      consume(b_begin + i, A);
-    }
-  }
-
-  if constexpr (!ARGMAX) return;
-
-  // ---- workgroup combine: 4 waves x 4 row groups, then one atomic ----
-  __shared__ float s_val[16];
-  __shared__ int s_idx[16];
-  if (li == 0) {
-    s_val[wave * 4 + grp] = best_v;
-    s_idx[wave * 4 + grp] = best_i;
-  }
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    float bv = -__builtin_inff();
-    int bi = -1;
-    for (int c = 0; c < 16; ++c) {
-      if (argmax_better(s_val[c], s_idx[c], bv, bi)) {
-        bv = s_val[c];
-        bi = s_idx[c];
-      }
-    }
-    if (bi >= 0) {
-      __hip_atomic_fetch_max(reinterpret_cast<uint64_t*>(ws), argmax_key(bv, bi), __ATOMIC_RELAXED,
-                             __HIP_MEMORY_SCOPE_AGENT);
-    }
-  }
-}
-
-}  // namespace
+#include "q8_device.h"
 
 // ------------------------------------------------------------ exports -----
 
@@ -503,7 +24,7 @@ __device__ __forceinline__ void vocab_body(const uint16_t* __restrict__ W,
   extern "C" __global__ __launch_bounds__(64) void q8gemv_p##P(                            \
       const uint8_t* __restrict__ w, const uint16_t* __restrict__ x,                       \
       uint16_t* __restrict__ y, int n_rows) {                                              \
-    __shared__ __attribute__((aligned(16))) uint8_t lds[(4 * (P) * 68 + 63) / 64 * 1024];  \
+    __shared__ __attribute__((aligned(16))) uint8_t lds[QuadShape<P>::LDS_BYTES];           \
     q8_quad<P>(w, x, y, n_rows, blockIdx.x, lds);                                          \
   }
 Q8GEMV_SINGLE(1)
@@ -604,7 +125,7 @@ extern "C" __global__ __launch_bounds__(256) void stream_copy_b128(const u32x4* 
   extern "C" __global__ __launch_bounds__(64) void NAME(                                      \
       const uint8_t* __restrict__ q8_stacked, const char* __restrict__ b1,                    \
       char* __restrict__ b2, uint32_t c0, uint32_t c1) {                                      \
-    __shared__ __attribute__((aligned(16))) uint8_t lds[(4 * (P) * 68 + 63) / 64 * 1024];    \
+    __shared__ __attribute__((aligned(16))) uint8_t lds[QuadShape<P>::LDS_BYTES];             \
     const uint64_t layer = (uint64_t)c0 | ((uint64_t)c1 << 32);                               \
     q8_quad<P>(q8_stacked + layer * (BPL), reinterpret_cast<const uint16_t*>(b1 + (X_OFF)),  \
                reinterpret_cast<uint16_t*>(b2 + (Y_OFF)), N, blockIdx.x, lds);                \

@@ -4,6 +4,7 @@
 // validation and hipModuleLaunchKernel per call.  The ABI is declared in
 // include/q8gemv.h.
 #include "q8gemv.h"
+#include "qwen3_decode.h"
 
 #include <dlfcn.h>
 #include <hip/hip_runtime_api.h>
@@ -13,6 +14,7 @@
 #include <cstring>
 #include <mutex>
 #include <string>
+#include <utility>
 
 // hipExtModuleLaunchKernel lives in hip/hip_ext.h, which pulls in the device
 // headers; its C declaration is all the shim needs.
@@ -93,6 +95,10 @@ struct State {
   hipFunction_t ws_reset = nullptr;
   hipFunction_t copy = nullptr;
   int batch_wgs = 0;      // 0 = default
+  hipModule_t dec_module = nullptr;  // decode_gfx950.hsaco (optional)
+  hipFunction_t dec_embed = nullptr, dec_qkv = nullptr, dec_attn = nullptr, dec_combine = nullptr,
+                dec_o = nullptr, dec_gu = nullptr, dec_dn = nullptr, dec_vocab = nullptr,
+                dec_final = nullptr;
   int vocab_wgs = 0;      // 0 = default
 };
 
@@ -222,6 +228,42 @@ int q8gemv_init(const char* code_object_path) {
     (void)hipModuleUnload(mod);
     return fail(Q8_ERR_CODE_OBJECT, "vocab / copy kernels missing from %s", path.c_str());
   }
+  // The decode-step kernels live in a second code object next to the first
+  // (or next to this library); without it the qwen3_decode_* calls report
+  // Q8_ERR_CODE_OBJECT.
+  {
+    const size_t slash = path.rfind('/');
+    std::string dir = slash == std::string::npos ? std::string(".") : path.substr(0, slash);
+    std::string dpath = dir + "/decode_gfx950.hsaco";
+    FILE* df = std::fopen(dpath.c_str(), "rb");
+    if (!df) {
+      std::string lib = default_code_object();
+      dpath = lib.substr(0, lib.rfind('/')) + "/decode_gfx950.hsaco";
+      df = std::fopen(dpath.c_str(), "rb");
+    }
+    if (df) {
+      std::fclose(df);
+      hipModule_t dm = nullptr;
+      if (hipModuleLoad(&dm, dpath.c_str()) == hipSuccess) {
+        struct {
+          hipFunction_t* fn;
+          const char* name;
+        } names[] = {{&g.dec_embed, "dec_embed"},     {&g.dec_qkv, "dec_qkv"},
+                     {&g.dec_attn, "dec_attn_split"}, {&g.dec_combine, "dec_attn_combine"},
+                     {&g.dec_o, "dec_o_res"},         {&g.dec_gu, "dec_gu_swiglu"},
+                     {&g.dec_dn, "dec_down_res"},     {&g.dec_vocab, "dec_vocab_argmax"},
+                     {&g.dec_final, "dec_finalize"}};
+        bool ok = true;
+        for (auto& n : names) ok = ok && hipModuleGetFunction(n.fn, dm, n.name) == hipSuccess;
+        if (ok) {
+          g.dec_module = dm;
+        } else {
+          (void)hipModuleUnload(dm);
+          for (auto& n : names) *n.fn = nullptr;
+        }
+      }
+    }
+  }
   int cus = 0;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
     cus = 256;
@@ -240,6 +282,10 @@ void q8gemv_shutdown(void) {
   g.module = nullptr;
   g.q8[0] = g.q8[1] = g.q8[2] = g.q8batch = g.q8qkv = nullptr;
   std::memset(g.hal, 0, sizeof(g.hal));
+  if (g.dec_module) (void)hipModuleUnload(g.dec_module);
+  g.dec_module = nullptr;
+  g.dec_embed = g.dec_qkv = g.dec_attn = g.dec_combine = g.dec_o = g.dec_gu = g.dec_dn =
+      g.dec_vocab = g.dec_final = nullptr;
   g.vocab = g.vocab_finalize = g.ws_reset = g.copy = nullptr;
   g.ready = false;
 }
@@ -671,6 +717,248 @@ int q8rt_time_next_launch(void* start_event, void* stop_event) {
   t_start = static_cast<hipEvent_t>(start_event);
   t_stop = static_cast<hipEvent_t>(stop_event);
   return Q8_OK;
+}
+
+}  // extern "C"
+
+// ------------------------------------------------------------ decode step
+
+namespace {
+
+constexpr int kLayers = 28;
+constexpr int kVocabRows = 151936;
+constexpr int64_t kKvRow = 8 * 128;  // f16 elements per cache slot
+constexpr int kAttnSplitsHost = 32;
+
+// Scratch layout (bytes).  Key + status first; every region 256-byte aligned.
+constexpr size_t kScrKey = 0;        // u64 argmax key
+constexpr size_t kScrStatus = 8;     // u32 status
+constexpr size_t kScrHA = 256;       // f16[1024]
+constexpr size_t kScrHB = kScrHA + 2048;
+constexpr size_t kScrRes = kScrHB + 2048;
+constexpr size_t kScrQ = kScrRes + 2048;     // f16[2048]
+constexpr size_t kScrK = kScrQ + 4096;       // f16[1024]
+constexpr size_t kScrV = kScrK + 2048;       // f16[1024]
+constexpr size_t kScrAttn = kScrV + 2048;    // f16[2048]
+constexpr size_t kScrAct = kScrAttn + 4096;  // f16[3072]
+constexpr size_t kScrXn = kScrAct + 6144;    // f16[1024] rms_norm(h, attn_norm)
+constexpr size_t kScrQr = kScrXn + 2048;     // f16[2048] q after head norm + RoPE
+constexpr size_t kScrFn = kScrQr + 4096;     // f16[1024] rms_norm(res, ffn_norm)
+constexpr size_t kScrOn = kScrFn + 2048;     // f16[1024] rms_norm(h, output_norm)
+constexpr size_t kScrPart = kScrOn + 2048;   // f32[16][32][130]
+constexpr size_t kScrBytes = kScrPart + 16 * kAttnSplitsHost * 130 * 4;
+
+const uint8_t* cb(const void* p) { return static_cast<const uint8_t*>(p); }
+uint8_t* mb(void* p) { return static_cast<uint8_t*>(p); }
+
+int check_decode_ready() {
+  int rc = check_ready();
+  if (rc) return rc;
+  if (!g.dec_module)
+    return fail(Q8_ERR_CODE_OBJECT, "decode_gfx950.hsaco was not found or lacks a kernel");
+  return Q8_OK;
+}
+
+int validate_weights(const qwen3_weights* w) {
+  if (!w) return fail(Q8_ERR_NULL_POINTER, "null weights struct");
+  const void* ptrs[] = {w->token_embd, w->attn_norm, w->ffn_norm, w->q_norm, w->k_norm,
+                        w->wq,         w->wk,        w->wv,       w->wo,     w->wgu,
+                        w->wdn,        w->output_norm, w->output_w};
+  for (const void* p : ptrs) {
+    if (!p) return fail(Q8_ERR_NULL_POINTER, "null weight pointer");
+    if (!aligned(p, 16)) return fail(Q8_ERR_MISALIGNED, "weights must be 16-byte aligned");
+  }
+  return Q8_OK;
+}
+
+int validate_cache(void* k_cache, void* v_cache, int64_t max_seq) {
+  if (!k_cache || !v_cache) return fail(Q8_ERR_NULL_POINTER, "null KV cache");
+  if (!aligned(k_cache, 16) || !aligned(v_cache, 16))
+    return fail(Q8_ERR_MISALIGNED, "KV cache must be 16-byte aligned");
+  if (max_seq < 1 || max_seq > (1LL << 24))
+    return fail(Q8_ERR_BAD_SHAPE, "max_seq %lld outside [1, 2^24]", (long long)max_seq);
+  return Q8_OK;
+}
+
+int launch_layer(const qwen3_weights* w, int layer, void* k_cache, void* v_cache, int64_t max_seq,
+                 const int32_t* pos, const void* h_in, void* h_out, void* scratch,
+                 hipStream_t st) {
+  const int64_t bpl_q = 2048LL * 1024 / 32 * 34, bpl_kv = 1024LL * 1024 / 32 * 34;
+  const int64_t bpl_o = 1024LL * 2048 / 32 * 34, bpl_gu = 6144LL * 1024 / 32 * 34;
+  const int64_t bpl_dn = 1024LL * 3072 / 32 * 34;
+  const void* wq = cb(w->wq) + layer * bpl_q;
+  const void* wk = cb(w->wk) + layer * bpl_kv;
+  const void* wv = cb(w->wv) + layer * bpl_kv;
+  const void* wo = cb(w->wo) + layer * bpl_o;
+  const void* wgu = cb(w->wgu) + layer * bpl_gu;
+  const void* wdn = cb(w->wdn) + layer * bpl_dn;
+  const void* an = cb(w->attn_norm) + layer * 2048;
+  const void* fn = cb(w->ffn_norm) + layer * 2048;
+  const void* qn = cb(w->q_norm) + layer * 256;
+  const void* kn = cb(w->k_norm) + layer * 256;
+  void* kc = mb(k_cache) + (int64_t)layer * max_seq * kKvRow * 2;
+  void* vc = mb(v_cache) + (int64_t)layer * max_seq * kKvRow * 2;
+  void* q = mb(scratch) + kScrQ;
+  void* k = mb(scratch) + kScrK;
+  void* v = mb(scratch) + kScrV;
+  void* attn = mb(scratch) + kScrAttn;
+  void* res = mb(scratch) + kScrRes;
+  void* act = mb(scratch) + kScrAct;
+  void* part = mb(scratch) + kScrPart;
+  void* xn = mb(scratch) + kScrXn;
+  void* qr = mb(scratch) + kScrQr;
+  void* fnx = mb(scratch) + kScrFn;
+  const void* hin = h_in;
+  int ms = (int)max_seq;
+  int rc;
+  {
+    void* args[] = {&wq, &wk, &wv, &hin, &an, &q, &k, &v, &xn};
+    if ((rc = launch(g.dec_qkv, 1024, 64, args, st))) return rc;
+  }
+  {
+    const void* pp = pos;
+    void* args[] = {&q, &k, &v, &qn, &kn, &pp, &ms, &kc, &vc, &part, &qr};
+    if ((rc = launch(g.dec_attn, 8 * kAttnSplitsHost, 64, args, st))) return rc;
+  }
+  {
+    void* args[] = {&part, &attn};
+    if ((rc = launch(g.dec_combine, 16, 128, args, st))) return rc;
+  }
+  {
+    void* args[] = {&wo, &attn, &hin, &res};
+    if ((rc = launch(g.dec_o, 256, 64, args, st))) return rc;
+  }
+  {
+    void* args[] = {&wgu, &res, &fn, &act, &fnx};
+    if ((rc = launch(g.dec_gu, 768, 64, args, st))) return rc;
+  }
+  {
+    void* args[] = {&wdn, &act, &res, &h_out};
+    if ((rc = launch(g.dec_dn, 256, 64, args, st))) return rc;
+  }
+  return Q8_OK;
+}
+
+int launch_head(const qwen3_weights* w, const void* h, void* logits, int32_t* token,
+                int32_t* pos, int advance, int64_t max_seq, void* scratch, hipStream_t st) {
+  const void* W = w->output_w;
+  const void* on = w->output_norm;
+  void* ws = mb(scratch) + kScrKey;
+  void* status = mb(scratch) + kScrStatus;
+  void* xn = mb(scratch) + kScrOn;
+  int rc;
+  {
+    void* args[] = {&W, &h, &on, &logits, &ws, &xn};
+    if ((rc = launch(g.dec_vocab, (uint32_t)vocab_grid(), 256, args, st))) return rc;
+  }
+  int adv = advance ? 1 : 0;
+  int ms = (int)max_seq;
+  void* args[] = {&ws, &token, &pos, &adv, &ms, &status};
+  return launch(g.dec_final, 1, 64, args, st);
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t qwen3_scratch_bytes(void) { return kScrBytes; }
+size_t qwen3_scratch_status_offset(void) { return kScrStatus; }
+
+int64_t qwen3_scratch_offset(const char* name) {
+  if (!name) return -1;
+  const std::string n(name);
+  if (n == "q") return (int64_t)kScrQ;
+  if (n == "k") return (int64_t)kScrK;
+  if (n == "v") return (int64_t)kScrV;
+  if (n == "attn") return (int64_t)kScrAttn;
+  if (n == "res") return (int64_t)kScrRes;
+  if (n == "act") return (int64_t)kScrAct;
+  if (n == "xn") return (int64_t)kScrXn;
+  if (n == "q_roped") return (int64_t)kScrQr;
+  if (n == "fn") return (int64_t)kScrFn;
+  if (n == "on") return (int64_t)kScrOn;
+  return -1;
+}
+
+int qwen3_scratch_reset(void* scratch, void* stream) {
+  if (!scratch) return fail(Q8_ERR_NULL_POINTER, "null scratch");
+  if (!aligned(scratch, 256)) return fail(Q8_ERR_MISALIGNED, "scratch must be 256-byte aligned");
+  int rc = check_ready();
+  if (rc) return rc;
+  void* ws = scratch;
+  void* args[] = {&ws};
+  return launch(g.ws_reset, 1, 64, args, static_cast<hipStream_t>(stream));
+}
+
+int qwen3_decode_embed(const qwen3_weights* w, const int32_t* token, void* h_out, void* stream) {
+  int rc = validate_weights(w);
+  if (rc) return rc;
+  if (!token || !h_out) return fail(Q8_ERR_NULL_POINTER, "null token or h_out");
+  if (!aligned(token, 4) || !aligned(h_out, 16))
+    return fail(Q8_ERR_MISALIGNED, "token needs 4-byte, h_out 16-byte alignment");
+  if ((rc = check_decode_ready())) return rc;
+  const void* t = token;
+  const void* e = w->token_embd;
+  void* args[] = {&t, &e, &h_out};
+  return launch(g.dec_embed, 1, 128, args, static_cast<hipStream_t>(stream));
+}
+
+int qwen3_decode_layer(const qwen3_weights* w, int layer, void* k_cache, void* v_cache,
+                       int64_t max_seq, const int32_t* pos, const void* h_in, void* h_out,
+                       void* scratch, void* stream) {
+  int rc = validate_weights(w);
+  if (rc) return rc;
+  if (layer < 0 || layer >= kLayers)
+    return fail(Q8_ERR_LAYER_RANGE, "layer %d outside [0, %d)", layer, kLayers);
+  if ((rc = validate_cache(k_cache, v_cache, max_seq))) return rc;
+  if (!pos || !h_in || !h_out || !scratch) return fail(Q8_ERR_NULL_POINTER, "null argument");
+  if (!aligned(pos, 4) || !aligned(h_in, 16) || !aligned(h_out, 16) || !aligned(scratch, 256))
+    return fail(Q8_ERR_MISALIGNED, "pos 4, h 16, scratch 256-byte alignment required");
+  if (h_in == h_out) return fail(Q8_ERR_BAD_ARGUMENT, "h_in and h_out must differ");
+  if ((rc = check_decode_ready())) return rc;
+  return launch_layer(w, layer, k_cache, v_cache, max_seq, pos, h_in, h_out, scratch,
+                      static_cast<hipStream_t>(stream));
+}
+
+int qwen3_decode_head(const qwen3_weights* w, const void* h, void* logits, int32_t* token,
+                      int32_t* pos, int advance, int64_t max_seq, void* scratch, void* stream) {
+  int rc = validate_weights(w);
+  if (rc) return rc;
+  if (!h || !token || !pos || !scratch) return fail(Q8_ERR_NULL_POINTER, "null argument");
+  if (!aligned(h, 16) || !aligned(token, 4) || !aligned(pos, 4) || !aligned(scratch, 256) ||
+      (logits && !aligned(logits, 2)))
+    return fail(Q8_ERR_MISALIGNED, "h 16, token/pos 4, scratch 256, logits 2-byte alignment");
+  if (max_seq < 1) return fail(Q8_ERR_BAD_SHAPE, "max_seq must be >= 1");
+  if ((rc = check_decode_ready())) return rc;
+  return launch_head(w, h, logits, token, pos, advance, max_seq, scratch,
+                     static_cast<hipStream_t>(stream));
+}
+
+int qwen3_decode_step(const qwen3_weights* w, void* k_cache, void* v_cache, int64_t max_seq,
+                      int32_t* token, int32_t* pos, void* logits, int advance, void* scratch,
+                      void* stream) {
+  int rc = validate_weights(w);
+  if (rc) return rc;
+  if ((rc = validate_cache(k_cache, v_cache, max_seq))) return rc;
+  if (!token || !pos || !scratch) return fail(Q8_ERR_NULL_POINTER, "null token, pos or scratch");
+  if (!aligned(token, 4) || !aligned(pos, 4) || !aligned(scratch, 256) ||
+      (logits && !aligned(logits, 2)))
+    return fail(Q8_ERR_MISALIGNED, "token/pos 4, scratch 256, logits 2-byte alignment");
+  if ((rc = check_decode_ready())) return rc;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  void* ha = mb(scratch) + kScrHA;
+  void* hb = mb(scratch) + kScrHB;
+  {
+    const void* t = token;
+    const void* e = w->token_embd;
+    void* args[] = {&t, &e, &ha};
+    if ((rc = launch(g.dec_embed, 1, 128, args, st))) return rc;
+  }
+  for (int l = 0; l < kLayers; ++l) {
+    if ((rc = launch_layer(w, l, k_cache, v_cache, max_seq, pos, ha, hb, scratch, st))) return rc;
+    std::swap(ha, hb);
+  }
+  return launch_head(w, ha, logits, token, pos, advance, max_seq, scratch, st);
 }
 
 }  // extern "C"

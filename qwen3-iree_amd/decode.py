@@ -1,0 +1,245 @@
+"""Host side of the Qwen3-0.6B decode step (include/qwen3_decode.h).
+
+The reference runs a token as @generate's inner loop inside IREE
+(model/qwen3_full.mlir:1431-1526): embedding gather, 28 x
+@transformer_layer_decode_static, final rms_norm, the vocab GEMV and the tiled
+argmax, with the token fed back and the position incremented on the device.
+Here the same step is one C call that enqueues 171 gfx950 kernel launches on a
+stream (libq8gemv.so); this module owns the device buffers it needs (weights,
+the flat KV cache, scratch, token and position words), captures the step in a
+hipGraph and replays it.
+
+Weights come in the reference's parameter layout (create_q8_irpa.py:149-224):
+Q8_0 stacks [28, BPL] bytes, gate and up concatenated by rows, f16 norms and
+f16 embedding / output matrices.  No checkpoint is available offline, so
+`synthetic_weights` draws them from seeded normal distributions.
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass, fields
+
+import numpy as np
+
+from . import q8gemv as Q
+from . import weights as Wt
+
+LAYERS = 28
+HIDDEN = 1024
+Q_HEADS, KV_HEADS, HEAD_DIM = 16, 8, 128
+Q_DIM, KV_DIM = Q_HEADS * HEAD_DIM, KV_HEADS * HEAD_DIM
+FFN = 3072
+VOCAB = 151936
+WEIGHT_FIELDS = ("token_embd", "attn_norm", "ffn_norm", "q_norm", "k_norm", "wq", "wk", "wv",
+                 "wo", "wgu", "wdn", "output_norm", "output_w")
+# (rows, cols) of each Q8_0 matrix per layer (qwen3_full.mlir:772-777)
+Q8_SHAPES = {"wq": (Q_DIM, HIDDEN), "wk": (KV_DIM, HIDDEN), "wv": (KV_DIM, HIDDEN),
+             "wo": (HIDDEN, Q_DIM), "wgu": (2 * FFN, HIDDEN), "wdn": (HIDDEN, FFN)}
+NORM_STD = 0.1
+
+
+@dataclass
+class HostWeights:
+    """numpy copies of every parameter, in the device layout."""
+    token_embd: np.ndarray   # f16 [151936, 1024]
+    attn_norm: np.ndarray    # f16 [28, 1024]
+    ffn_norm: np.ndarray     # f16 [28, 1024]
+    q_norm: np.ndarray       # f16 [28, 128]
+    k_norm: np.ndarray       # f16 [28, 128]
+    wq: np.ndarray           # u8 [28, 2228224]
+    wk: np.ndarray           # u8 [28, 1114112]
+    wv: np.ndarray           # u8 [28, 1114112]
+    wo: np.ndarray           # u8 [28, 2228224]
+    wgu: np.ndarray          # u8 [28, 6684672]
+    wdn: np.ndarray          # u8 [28, 3342336]
+    output_norm: np.ndarray  # f16 [1024]
+    output_w: np.ndarray     # f16 [151936, 1024]
+
+    def validate(self) -> None:
+        want = {"token_embd": ((VOCAB, HIDDEN), np.float16),
+                "attn_norm": ((LAYERS, HIDDEN), np.float16),
+                "ffn_norm": ((LAYERS, HIDDEN), np.float16),
+                "q_norm": ((LAYERS, HEAD_DIM), np.float16),
+                "k_norm": ((LAYERS, HEAD_DIM), np.float16),
+                "output_norm": ((HIDDEN,), np.float16),
+                "output_w": ((VOCAB, HIDDEN), np.float16)}
+        for name, (n, k) in Q8_SHAPES.items():
+            want[name] = ((LAYERS, n * k // 32 * 34), np.uint8)
+        for name, (shape, dtype) in want.items():
+            a = getattr(self, name)
+            if a.shape != shape or a.dtype != dtype or not a.flags["C_CONTIGUOUS"]:
+                raise ValueError(f"{name}: expected contiguous {np.dtype(dtype)}{shape}, "
+                                 f"got {a.dtype}{a.shape}")
+
+
+def _norm_weights(shape, seed: int, tensor: int) -> np.ndarray:
+    r = Wt._rng(seed, tensor, 0).standard_normal(shape, dtype=np.float32)
+    return (np.float32(1.0) + np.float32(NORM_STD) * r).astype(np.float16)
+
+
+def synthetic_weights(seed: int = 0, workers: int = 8) -> HostWeights:
+    """Random-init Qwen3-0.6B parameters: matrices N(0, 0.02) (Q8_0 through
+    the reference quantizer), norm weights 1 + N(0, 0.1), embedding and output
+    matrices f16(N(0, 0.02)).  One PCG64 stream per (seed, tensor, layer)."""
+    q8 = {name: Wt.synthetic_q8_stack(n, k, LAYERS, seed, 10 + i, workers)
+          for i, (name, (n, k)) in enumerate(Q8_SHAPES.items())}
+    hw = HostWeights(
+        token_embd=Wt.synthetic_f16_matrix(VOCAB, HIDDEN, seed, 100, workers),
+        attn_norm=_norm_weights((LAYERS, HIDDEN), seed, 101),
+        ffn_norm=_norm_weights((LAYERS, HIDDEN), seed, 102),
+        q_norm=_norm_weights((LAYERS, HEAD_DIM), seed, 103),
+        k_norm=_norm_weights((LAYERS, HEAD_DIM), seed, 104),
+        output_norm=_norm_weights((HIDDEN,), seed, 105),
+        output_w=Wt.synthetic_f16_matrix(VOCAB, HIDDEN, seed, 106, workers),
+        **q8)
+    hw.validate()
+    return hw
+
+
+class WeightsC(ctypes.Structure):
+    """struct qwen3_weights (include/qwen3_decode.h)."""
+    _fields_ = [(f, ctypes.c_void_p) for f in WEIGHT_FIELDS]
+
+
+class DeviceWeights:
+    """The parameters resident in device memory, one allocation each."""
+
+    def __init__(self, host: HostWeights):
+        host.validate()
+        self.buffers = {f.name: Q.DeviceBuffer.from_array(getattr(host, f.name))
+                        for f in fields(HostWeights)}
+        self.struct = WeightsC(*(self.buffers[f].ptr for f in WEIGHT_FIELDS))
+
+    @property
+    def nbytes(self) -> int:
+        return sum(b.nbytes for b in self.buffers.values())
+
+    def ref(self):
+        return ctypes.byref(self.struct)
+
+    def free(self) -> None:
+        for b in self.buffers.values():
+            b.free()
+
+
+def scratch_bytes() -> int:
+    return int(Q.load_library().qwen3_scratch_bytes())
+
+
+def scratch_offset(name: str) -> int:
+    off = int(Q.load_library().qwen3_scratch_offset(name.encode()))
+    if off < 0:
+        raise KeyError(name)
+    return off
+
+
+class DecodeSession:
+    """One sequence: KV cache for max_seq positions, scratch, and the device
+    words holding the current token and position.
+
+    step() enqueues one token; capture() records a step in a hipGraph that
+    replays with whatever token / position the device words hold, so the
+    argmax of one replay is the input of the next (qwen3_full.mlir:1512-1523).
+    """
+
+    def __init__(self, model: DeviceWeights, max_seq: int, stream: Q.Stream | None = None):
+        if max_seq < 1:
+            raise ValueError("max_seq must be >= 1")
+        self.model = model
+        self.max_seq = int(max_seq)
+        self.stream = stream
+        cache_bytes = LAYERS * self.max_seq * KV_DIM * 2
+        self.k_cache = Q.DeviceBuffer(cache_bytes)
+        self.v_cache = Q.DeviceBuffer(cache_bytes)
+        self.k_cache.fill(0)
+        self.v_cache.fill(0)
+        self.scratch = Q.DeviceBuffer(scratch_bytes())
+        self.scratch.fill(0)
+        self.state = Q.DeviceBuffer(256)  # int32 token at 0, int32 pos at 4
+        self.state.fill(0)
+        self.logits = Q.DeviceBuffer(VOCAB * 2)
+        Q._call("qwen3_scratch_reset", self.scratch.ptr, Q._stream(stream))
+        self._graphs: dict[tuple[bool, bool], Q.Graph] = {}
+
+    # device words
+    @property
+    def token_ptr(self) -> int:
+        return self.state.ptr
+
+    @property
+    def pos_ptr(self) -> int:
+        return self.state.ptr + 4
+
+    def set_state(self, token: int, pos: int) -> None:
+        self.state.upload(np.array([token, pos], np.int32))
+
+    def get_state(self) -> tuple[int, int]:
+        t, p = self.state.download(np.int32, 2)
+        return int(t), int(p)
+
+    def status(self) -> int:
+        off = int(Q.load_library().qwen3_scratch_status_offset())
+        return int(self.scratch.download(np.uint32, 1, off)[0])
+
+    def step(self, advance: bool = True, logits: bool = True) -> None:
+        Q._call("qwen3_decode_step", self.model.ref(), self.k_cache.ptr, self.v_cache.ptr,
+                self.max_seq, self.token_ptr, self.pos_ptr,
+                self.logits.ptr if logits else None, int(bool(advance)), self.scratch.ptr,
+                Q._stream(self.stream))
+
+    def capture(self, advance: bool = True, logits: bool = False) -> Q.Graph:
+        """hipGraph of one step (needs a non-null stream)."""
+        if self.stream is None:
+            raise ValueError("graph capture needs an explicit stream")
+        key = (bool(advance), bool(logits))
+        if key not in self._graphs:
+            self._graphs[key] = Q.Graph(self.stream, lambda: self.step(advance, logits))
+        return self._graphs[key]
+
+    def replay(self, advance: bool = True, logits: bool = False) -> None:
+        self.capture(advance, logits).launch(self.stream)
+
+    def synchronize(self) -> None:
+        if self.stream is not None:
+            self.stream.synchronize()
+        else:
+            Q.synchronize()
+
+    def read_logits(self) -> np.ndarray:
+        self.synchronize()
+        return self.logits.download(np.float16, VOCAB)
+
+    # the step in parts
+    def embed(self, h_out: Q.DeviceBuffer) -> None:
+        Q._call("qwen3_decode_embed", self.model.ref(), self.token_ptr, h_out.ptr,
+                Q._stream(self.stream))
+
+    def layer(self, layer: int, h_in: Q.DeviceBuffer, h_out: Q.DeviceBuffer) -> None:
+        Q._call("qwen3_decode_layer", self.model.ref(), int(layer), self.k_cache.ptr,
+                self.v_cache.ptr, self.max_seq, self.pos_ptr, h_in.ptr, h_out.ptr,
+                self.scratch.ptr, Q._stream(self.stream))
+
+    def head(self, h: Q.DeviceBuffer, advance: bool = False, logits: bool = True) -> None:
+        Q._call("qwen3_decode_head", self.model.ref(), h.ptr, self.logits.ptr if logits else None,
+                self.token_ptr, self.pos_ptr, int(bool(advance)), self.max_seq,
+                self.scratch.ptr, Q._stream(self.stream))
+
+    def scratch_f16(self, name: str, count: int) -> np.ndarray:
+        self.synchronize()
+        return self.scratch.download(np.float16, count, scratch_offset(name))
+
+    def cache_rows(self, layer: int, start: int, stop: int) -> tuple[np.ndarray, np.ndarray]:
+        """(K, V) f16 [stop-start, 1024] of one layer's slots."""
+        self.synchronize()
+        off = (layer * self.max_seq + start) * KV_DIM * 2
+        n = (stop - start) * KV_DIM
+        k = self.k_cache.download(np.float16, n, off).reshape(-1, KV_DIM)
+        v = self.v_cache.download(np.float16, n, off).reshape(-1, KV_DIM)
+        return k, v
+
+    def free(self) -> None:
+        for g in self._graphs.values():
+            g.destroy()
+        self._graphs.clear()
+        for b in (self.k_cache, self.v_cache, self.scratch, self.state, self.logits):
+            b.free()

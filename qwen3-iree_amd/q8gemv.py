@@ -143,12 +143,24 @@ _SIGNATURES = {
     "q8rt_graph_destroy": [_P],
     "q8rt_time_next_launch": [_P, _P],
     "q8rt_stream_copy": [_P, _P, _SZ, _P],
+    # include/qwen3_decode.h
+    "qwen3_scratch_bytes": [],
+    "qwen3_scratch_reset": [_P, _P],
+    "qwen3_scratch_status_offset": [],
+    "qwen3_scratch_offset": [ctypes.c_char_p],
+    "qwen3_decode_step": [_P, _P, _P, _I64, _P, _P, _P, _I, _P, _P],
+    "qwen3_decode_embed": [_P, _P, _P, _P],
+    "qwen3_decode_layer": [_P, _I, _P, _P, _I64, _P, _P, _P, _P, _P],
+    "qwen3_decode_head": [_P, _P, _P, _P, _P, _I, _I64, _P, _P],
 }
 _RESTYPES = {
     "q8gemv_shutdown": None,
     "q8gemv_last_error": ctypes.c_char_p,
     "vocab_argmax_workspace_bytes": _SZ,
     "q8gemv_batch_table_bytes": _SZ,
+    "qwen3_scratch_bytes": _SZ,
+    "qwen3_scratch_status_offset": _SZ,
+    "qwen3_scratch_offset": _I64,
 }
 
 _lib: ctypes.CDLL | None = None

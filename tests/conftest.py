@@ -62,3 +62,11 @@ def gpu(Q):
     object cannot be loaded: GPU tests must run the HIP path."""
     Q.init()
     return Q
+
+
+@pytest.fixture(scope="session")
+def model_host():
+    """Seeded random-init Qwen3-0.6B parameters in the device layout (~1.1 GB)."""
+    from qwen3_iree_amd import decode
+
+    return decode.synthetic_weights(seed=0)

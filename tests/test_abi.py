@@ -1,8 +1,10 @@
 """CPU-side checks of the C ABI (no GPU): the library loads, exports every
-symbol include/q8gemv.h declares, and validates arguments before touching
-the device, reporting status codes instead of aborting."""
+symbol include/q8gemv.h and include/qwen3_decode.h declare, and validates
+arguments before touching the device, reporting status codes instead of
+aborting."""
 from __future__ import annotations
 
+import ctypes
 import re
 from pathlib import Path
 
@@ -10,15 +12,18 @@ import numpy as np
 import pytest
 
 REPO = Path(__file__).resolve().parent.parent
-HEADER = REPO / "include" / "q8gemv.h"
+HEADERS = (REPO / "include" / "q8gemv.h", REPO / "include" / "qwen3_decode.h")
 
 A16 = 0x10000  # fake, 16-byte aligned "device" addresses: never dereferenced here
 
 
 def declared_functions() -> list[str]:
-    text = HEADER.read_text()
-    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return re.findall(r"^(?:int|void|size_t|const char\*)\s+(\w+)\s*\(", text, flags=re.M)
+    names = []
+    for header in HEADERS:
+        text = re.sub(r"/\*.*?\*/", "", header.read_text(), flags=re.S)
+        names += re.findall(r"^(?:int|int64_t|void|size_t|const char\*)\s+(\w+)\s*\(", text,
+                            flags=re.M)
+    return names
 
 
 def test_header_declares_expected_entry_points():
@@ -26,7 +31,8 @@ def test_header_declares_expected_entry_points():
     for required in ("q8gemv_init", "q8gemv", "vocab_gemv_argmax",
                      "vocab_argmax_workspace_bytes", "q8gemv_shutdown",
                      "decode_dispatch_3_matmul_2048x1x1024_f16",
-                     "decode_dispatch_24_matmul_151936x1x1024_f16"):
+                     "decode_dispatch_24_matmul_151936x1x1024_f16",
+                     "qwen3_decode_step", "qwen3_decode_layer", "qwen3_scratch_bytes"):
         assert required in names
 
 
@@ -208,3 +214,69 @@ def test_hal_dispatch_validation(Q, ordinal, consts, code):
     lib = Q.load_library()
     c = (ctypes.c_uint32 * len(consts))(*consts)
     assert lib.q8gemv_hal_dispatch(ordinal, A16, A16, A16, c, len(consts), None) == code
+
+
+# ------------------------------------------------------------ decode step ----
+
+def _fake_weights(Q, **override):
+    from qwen3_iree_amd import decode
+
+    vals = {f: A16 + 0x100000 * i for i, f in enumerate(decode.WEIGHT_FIELDS)}
+    vals.update(override)
+    return decode.WeightsC(*(vals[f] for f in decode.WEIGHT_FIELDS))
+
+
+def test_decode_scratch_layout(Q):
+    from qwen3_iree_amd import decode
+
+    L = Q.load_library()
+    total = decode.scratch_bytes()
+    assert total % 256 == 0 and 0 < total < 1 << 20
+    assert L.qwen3_scratch_status_offset() < 256
+    names = {"xn": 1024, "q": 2048, "k": 1024, "v": 1024, "q_roped": 2048, "attn": 2048,
+             "res": 1024, "fn": 1024, "act": 3072, "on": 1024}
+    spans = sorted((decode.scratch_offset(n), decode.scratch_offset(n) + 2 * c) for n, c in
+                   names.items())
+    assert spans[0][0] >= 256 and spans[-1][1] <= total
+    for (a0, a1), (b0, _) in zip(spans, spans[1:]):
+        assert a0 % 256 == 0 and a1 <= b0
+    assert L.qwen3_scratch_offset(b"nope") == -1
+
+
+@pytest.mark.parametrize("call,code", [
+    # layer outside [0, 28)
+    (lambda L, w: L.qwen3_decode_layer(w, 28, A16, A16, 8, A16, A16, A16 + 4096, A16, None), 4),
+    (lambda L, w: L.qwen3_decode_layer(w, -1, A16, A16, 8, A16, A16, A16 + 4096, A16, None), 4),
+    # h_in == h_out
+    (lambda L, w: L.qwen3_decode_layer(w, 0, A16, A16, 8, A16, A16, A16, A16, None), 9),
+    # max_seq
+    (lambda L, w: L.qwen3_decode_step(w, A16, A16, 0, A16, A16, None, 1, A16, None), 6),
+    (lambda L, w: L.qwen3_decode_step(w, A16, A16, 1 << 25, A16, A16, None, 1, A16, None), 6),
+    # null / misaligned buffers
+    (lambda L, w: L.qwen3_decode_step(w, None, A16, 8, A16, A16, None, 1, A16, None), 3),
+    (lambda L, w: L.qwen3_decode_step(w, A16, A16, 8, None, A16, None, 1, A16, None), 3),
+    (lambda L, w: L.qwen3_decode_step(w, A16, A16, 8, A16, A16, None, 1, A16 + 16, None), 5),
+    (lambda L, w: L.qwen3_decode_step(w, A16 + 8, A16, 8, A16, A16, None, 1, A16, None), 5),
+    (lambda L, w: L.qwen3_decode_step(w, A16, A16, 8, A16 + 2, A16, None, 1, A16, None), 5),
+    (lambda L, w: L.qwen3_decode_head(w, A16, A16 + 1, A16, A16, 1, 8, A16, None), 5),
+    (lambda L, w: L.qwen3_decode_embed(w, None, A16, None), 3),
+    (lambda L, w: L.qwen3_scratch_reset(A16 + 16, None), 5),
+])
+def test_decode_validation_before_device(Q, call, code):
+    L = Q.load_library()
+    w = _fake_weights(Q)
+    assert call(L, ctypes.byref(w)) == code
+    assert Q.last_error()
+
+
+@pytest.mark.parametrize("field,value,code", [("wq", None, 3), ("output_w", A16 + 4, 5),
+                                              ("token_embd", None, 3)])
+def test_decode_validates_weight_pointers(Q, field, value, code):
+    L = Q.load_library()
+    w = _fake_weights(Q, **{field: value})
+    assert L.qwen3_decode_step(ctypes.byref(w), A16, A16, 8, A16, A16, None, 1, A16, None) == code
+
+
+def test_decode_null_weights_struct(Q):
+    L = Q.load_library()
+    assert L.qwen3_decode_step(None, A16, A16, 8, A16, A16, None, 1, A16, None) == 3
