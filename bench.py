@@ -82,6 +82,67 @@ def timed_ms(Q, stream, fn, reps: int) -> float:
     return ms
 
 
+def bench_decode(Q, O, stream, args) -> dict:
+    """The full decode step at context args.context: one step checked against
+    the oracle's, then replays of the captured step timed with HIP events."""
+    from qwen3_iree_amd import decode as D
+
+    layers = D.LAYERS
+    vocab_bytes = Q.VOCAB.bytes_per_layer + 2 * Q.HIDDEN + 2 * Q.VOCAB_ROWS + 4
+    t0 = time.time()
+    mhost = D.synthetic_weights(seed=SEED, workers=16)
+    model = D.DeviceWeights(mhost)
+    ctx = args.context
+    max_seq = ctx
+    sess = D.DecodeSession(model, max_seq, stream)
+    rng = np.random.default_rng(SEED + 5)
+    kc = rng.standard_normal((D.LAYERS * max_seq, D.KV_DIM), dtype=np.float32).astype(np.float16)
+    vc = (np.float32(0.6) * rng.standard_normal((D.LAYERS * max_seq, D.KV_DIM),
+                                                dtype=np.float32)).astype(np.float16)
+    sess.k_cache.upload(kc)
+    sess.v_cache.upload(vc)
+    first_token = 1234
+    sess.set_state(first_token, ctx - 1)
+    log(f"decode model ready in {time.time() - t0:.1f}s ({model.nbytes} parameter bytes), "
+        f"context {ctx}")
+    # one checked step: attention over slots 0..ctx-1, position kept (advance = 0)
+    sess.step(advance=False, logits=True)
+    step_tok, step_pos = sess.get_state()
+    step_logits = sess.read_logits()
+    ref_tok, ref_logits, _ = O.decode_step(mhost, kc, vc, max_seq, first_token, ctx - 1, True)
+    dl = np.abs(step_logits.astype(np.float64) - ref_logits.astype(np.float64))
+    srt = np.sort(ref_logits.astype(np.float64))
+    margin = float(srt[-1] - srt[-2])
+    step_ok = (step_tok == O.argmax_tiled(step_logits) and step_pos == ctx - 1
+               and (step_tok == ref_tok or margin <= 2 * dl.max()))
+    log(f"decode step parity: token {step_tok} (oracle {ref_tok}, margin {margin:.4f}, "
+        f"max |dlogit| {dl.max():.4f})")
+    # timed: replays of the captured step, each consuming the previous token
+    sess.set_state(first_token, ctx - 1)
+    if args.no_graph:
+        dec_fn = lambda: sess.step(advance=False, logits=False)  # noqa: E731
+    else:
+        sess.capture(advance=False, logits=False)
+        dec_fn = lambda: sess.replay(advance=False, logits=False)  # noqa: E731
+    for _ in range(20):
+        dec_fn()
+    dec_us = timed_ms(Q, stream, dec_fn, max(50, args.steps // 4)) * 1e3
+    norm_bytes = 2 * (D.LAYERS * (2 * D.HIDDEN + 2 * D.HEAD_DIM) + D.HIDDEN)
+    kv_bytes = D.LAYERS * ctx * 2 * D.KV_DIM * 2
+    dec_bytes = (sum(algorithmic_bytes(d) for d in Q.LAYER_ORDER) * layers + vocab_bytes
+                 + kv_bytes + norm_bytes + 2 * D.HIDDEN)
+    dec_gbs = dec_bytes / dec_us / 1e3
+    log(f"decode step (context {ctx}, {3 + 5 * layers} launches"
+        f"{'' if args.no_graph else ', hipGraph'}): {dec_us:.1f} us/token, "
+        f"{1e6 / dec_us:.0f} tok/s, {dec_gbs:.0f} GB/s")
+    sess.free()
+    model.free()
+    return {"us": round(dec_us, 2), "tok_per_s": round(1e6 / dec_us, 1), "context": ctx,
+            "bytes": dec_bytes, "GBps": round(dec_gbs, 1), "frac": round(dec_gbs / HBM_PEAK_GBS, 4),
+            "launches": 3 + 5 * layers, "launch": "eager" if args.no_graph else "hipGraph",
+            "token": step_tok, "oracle_token": ref_tok, "parity_ok": bool(step_ok)}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -91,6 +152,8 @@ def main() -> int:
                          "~100 ms of sustained work)")
     ap.add_argument("--context", type=int, default=1024,
                     help="positions attended by the timed decode step")
+    ap.add_argument("--decode-only", action="store_true",
+                    help="run only the full decode step and print its JSON line")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline sample budget")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-graph", action="store_true",
@@ -115,6 +178,12 @@ def main() -> int:
     Q.init()
     info = Q.device_info()
     log(f"device {info['name']}, {info['compute_units']} CUs")
+    sys.path.insert(0, str(REPO / "oracle"))
+    import oracle as O  # the checker; also the CPU baseline below
+
+    if args.decode_only:
+        print(json.dumps({"decode_step": bench_decode(Q, O, Q.Stream(), args)}), flush=True)
+        return 0
 
     # ---------------------------------------------------------------- inputs
     t0 = time.time()
@@ -162,9 +231,6 @@ def main() -> int:
         f"({100 * value / HBM_PEAK_GBS:.1f}% of peak); host wall {wall_s:.3f}s")
 
     # parity of every sweep output (the last timed launch wrote them)
-    sys.path.insert(0, str(REPO / "oracle"))
-    import oracle as O  # the checker; also the CPU baseline below
-
     fails = floor = 0
     for layer, d in sweep_order:
         raw = stacks[d.kind][0][layer]
@@ -244,54 +310,8 @@ def main() -> int:
         f"{decode_gemv_us:.1f} us, {decode_bytes / decode_gemv_us / 1e3:.0f} GB/s")
 
     # ------------------------------------------- full decode step (C5)
-    from qwen3_iree_amd import decode as D
-
-    t0 = time.time()
-    mhost = D.synthetic_weights(seed=SEED, workers=16)
-    model = D.DeviceWeights(mhost)
-    ctx = args.context
-    max_seq = ctx
-    sess = D.DecodeSession(model, max_seq, stream)
-    rng = np.random.default_rng(SEED + 5)
-    kc = rng.standard_normal((D.LAYERS * max_seq, D.KV_DIM), dtype=np.float32).astype(np.float16)
-    vc = (np.float32(0.6) * rng.standard_normal((D.LAYERS * max_seq, D.KV_DIM),
-                                                dtype=np.float32)).astype(np.float16)
-    sess.k_cache.upload(kc)
-    sess.v_cache.upload(vc)
-    first_token = 1234
-    sess.set_state(first_token, ctx - 1)
-    log(f"decode model ready in {time.time() - t0:.1f}s ({model.nbytes} parameter bytes), "
-        f"context {ctx}")
-    # one checked step: attention over slots 0..ctx-1, position kept (advance = 0)
-    sess.step(advance=False, logits=True)
-    step_tok, step_pos = sess.get_state()
-    step_logits = sess.read_logits()
-    ref_tok, ref_logits, _ = O.decode_step(mhost, kc, vc, max_seq, first_token, ctx - 1, True)
-    dl = np.abs(step_logits.astype(np.float64) - ref_logits.astype(np.float64))
-    srt = np.sort(ref_logits.astype(np.float64))
-    margin = float(srt[-1] - srt[-2])
-    step_ok = (step_tok == O.argmax_tiled(step_logits) and step_pos == ctx - 1
-               and (step_tok == ref_tok or margin <= 2 * dl.max()))
-    log(f"decode step parity: token {step_tok} (oracle {ref_tok}, margin {margin:.4f}, "
-        f"max |dlogit| {dl.max():.4f})")
-    # timed: replays of the captured step, each consuming the previous token
-    sess.set_state(first_token, ctx - 1)
-    if args.no_graph:
-        dec_fn = lambda: sess.step(advance=False, logits=False)  # noqa: E731
-    else:
-        sess.capture(advance=False, logits=False)
-        dec_fn = lambda: sess.replay(advance=False, logits=False)  # noqa: E731
-    for _ in range(20):
-        dec_fn()
-    dec_us = timed_ms(Q, stream, dec_fn, max(50, args.steps // 4)) * 1e3
-    norm_bytes = 2 * (D.LAYERS * (2 * D.HIDDEN + 2 * D.HEAD_DIM) + D.HIDDEN)
-    kv_bytes = D.LAYERS * ctx * 2 * D.KV_DIM * 2
-    dec_bytes = (sum(algorithmic_bytes(d) for d in Q.LAYER_ORDER) * layers + vocab_bytes
-                 + kv_bytes + norm_bytes + 2 * D.HIDDEN)
-    dec_gbs = dec_bytes / dec_us / 1e3
-    log(f"decode step (context {ctx}, {3 + 6 * layers} launches"
-        f"{'' if args.no_graph else ', hipGraph'}): {dec_us:.1f} us/token, "
-        f"{1e6 / dec_us:.0f} tok/s, {dec_gbs:.0f} GB/s")
+    dec = bench_decode(Q, O, stream, args)
+    step_ok = dec["parity_ok"]
 
     parity_ok = fails == 0 and rep_v["fail"] == 0 and token == own and step_ok
     batch_grid = min(batch.total_units, 12 * info["compute_units"]) * 64
@@ -365,11 +385,7 @@ def main() -> int:
                              "GBps": round(decode_bytes / decode_gemv_us / 1e3, 1),
                              "dispatches": 4 * layers + 2,
                              "launch": "eager" if args.no_graph else "hipGraph"},
-        "decode_step": {"us": round(dec_us, 2), "tok_per_s": round(1e6 / dec_us, 1),
-                        "context": ctx, "bytes": dec_bytes, "GBps": round(dec_gbs, 1),
-                        "frac": round(dec_gbs / HBM_PEAK_GBS, 4), "launches": 3 + 6 * layers,
-                        "launch": "eager" if args.no_graph else "hipGraph",
-                        "token": step_tok, "oracle_token": ref_tok, "parity_ok": bool(step_ok)},
+        "decode_step": dec,
         "parity_ok": bool(parity_ok),
         "copy_calibration": copy_cal,
         "cpu_baseline": cpu,

@@ -80,6 +80,27 @@ int qwen3_decode_layer(const qwen3_weights* w, int layer, void* k_cache, void* v
 int qwen3_decode_head(const qwen3_weights* w, const void* h, void* logits, int32_t* token,
                       int32_t* pos, int advance, int64_t max_seq, void* scratch, void* stream);
 
+/* Prompt ingestion as decode steps, the reference's @prefill_all
+ * (qwen3_full.mlir:1541-1561): for i in [0, n_prompt) one step at position
+ * *pos with input token prompt[i] (device int32 [n_prompt]); logits are only
+ * formed after the last prompt token, whose argmax goes to *token.  *pos ends
+ * n_prompt slots further (not past max_seq - 1; see the status word). */
+int qwen3_prefill(const qwen3_weights* w, void* k_cache, void* v_cache, int64_t max_seq,
+                  const int32_t* prompt, int32_t n_prompt, int32_t* token, int32_t* pos,
+                  void* scratch, void* stream);
+
+/* The token loop of @generate (qwen3_full.mlir:1396-1534): starting from
+ * *token at *pos, steps run in batches of 4 (fewer for the last) with the
+ * token fed back and the position advanced on the device; step i's token goes
+ * to out_tokens[i] (device int32 [max_new]).  After each batch the host reads
+ * the last token and stops if it equals eos_id, so up to 3 tokens past an EOS
+ * are produced, as in the reference.  The input token itself is not output.
+ * *n_generated (host) = tokens produced.  Blocks until the loop ends; fails
+ * with Q8_ERR_BAD_SHAPE unless *pos + max_new <= max_seq. */
+int qwen3_generate(const qwen3_weights* w, void* k_cache, void* v_cache, int64_t max_seq,
+                   int32_t* token, int32_t* pos, int32_t max_new, int32_t eos_id,
+                   int32_t* out_tokens, int32_t* n_generated, void* scratch, void* stream);
+
 /* Scratch offsets of the intermediates the last qwen3_decode_layer (or head)
  * left behind, all f16: "xn" [1024] rms_norm(h_in, attn_norm); "q" [2048],
  * "k" [1024], "v" [1024] the projections before head norm and RoPE;

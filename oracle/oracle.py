@@ -275,6 +275,43 @@ def decode_step(w, k_cache: np.ndarray, v_cache: np.ndarray, max_seq: int, token
     return int(tok), logits, hl
 
 
+# ------------------------------------------------------ generation loop ----
+
+def generate_control(step, first_token: int, start_pos: int, max_new: int, eos_id: int,
+                     batch: int = 4):
+    """@generate's control flow (qwen3_full.mlir:1396-1534) around
+    step(token, pos) -> next token.
+
+    out = zeros(max_new); batches of min(4, remaining) steps (:1412, 1419-1420),
+    each writing its token to out[idx] and advancing pos (:1512-1523); after a
+    batch the last token is compared with eos (:1528-1531).  The first token
+    is an input only (:1427).  Returns (out int64 [max_new], count).
+    """
+    out = np.zeros(max_new, np.int64)
+    tok, pos, idx, not_eos = int(first_token), int(start_pos), 0, True
+    while idx < max_new and not_eos:
+        for _ in range(min(batch, max_new - idx)):
+            tok = int(step(tok, pos))
+            out[idx] = tok
+            idx += 1
+            pos += 1
+        not_eos = tok != eos_id
+    return out, idx
+
+
+def run_control(step_logits, step, prompt, max_gen: int, eos_id: int):
+    """@run (qwen3_full.mlir:2113-2167) with prompt ingestion as per-token
+    decode steps (@prefill_all, :1541-1561): step_logits(token, pos) -> f16
+    logits for each prompt token at positions 0..n-1; the first token is the
+    lowest-index argmax of the last logits; then @generate from position n."""
+    prompt = [int(t) for t in prompt]
+    logits = None
+    for i, t in enumerate(prompt):
+        logits = step_logits(t, i)
+    first = argmax_tiled(logits)
+    return generate_control(step, first, len(prompt), max_gen, eos_id)
+
+
 # ------------------------------------------------------------ tolerance ----
 
 def ulp_f16(v: np.ndarray) -> np.ndarray:

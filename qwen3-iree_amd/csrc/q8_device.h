@@ -63,6 +63,14 @@ __device__ __forceinline__ u32x4 load_global(const u32x4* p) {
   return *(const GLOBAL_AS u32x4*)p;
 }
 
+__device__ __forceinline__ uint32_t load_global(const uint32_t* p) {
+  return *(const GLOBAL_AS uint32_t*)p;
+}
+
+__device__ __forceinline__ uint16_t load_global_u16(const uint16_t* p) {
+  return *(const GLOBAL_AS uint16_t*)p;
+}
+
 __device__ __forceinline__ void store_global_u16(uint16_t* p, uint16_t v) {
   *(GLOBAL_AS uint16_t*)p = v;
 }
@@ -339,17 +347,26 @@ __device__ __forceinline__ void load_x_cols(const uint16_t* __restrict__ x, u32x
 // Single GEMV, one wave per row quad: all of the quad's weight loads are in
 // flight before XLoad fetches x (xr[c] = this lane's 64 columns of chunk c);
 // Epi(row, acc) runs on one lane per valid row.
-template <int P, class XLoad, class Epi>
-__device__ __forceinline__ void q8_quad_core(const uint8_t* __restrict__ w, int n_rows, int quad,
-                                             uint8_t* __restrict__ lds, XLoad&& xload,
-                                             Epi&& epi) {
+// Returns the row sum of this lane's row (row quad*4 + lane/16) in all 16
+// lanes of its row group.
+template <int P, class XLoad>
+__device__ __forceinline__ float q8_quad_core_acc(const uint8_t* __restrict__ w, int n_rows,
+                                                  int quad, uint8_t* __restrict__ lds,
+                                                  XLoad&& xload) {
   u32x4 buf[QuadShape<P>::LOADS];
   q8_quad_load<P>(w, n_rows, quad, buf);
   u32x4 xr[P][8];
   xload(xr);
   q8_quad_stage<P>(buf, lds);
   __syncthreads();
-  const float acc = q8_quad_dot<P>(lds, xr);
+  return q8_quad_dot<P>(lds, xr);
+}
+
+template <int P, class XLoad, class Epi>
+__device__ __forceinline__ void q8_quad_core(const uint8_t* __restrict__ w, int n_rows, int quad,
+                                             uint8_t* __restrict__ lds, XLoad&& xload,
+                                             Epi&& epi) {
+  const float acc = q8_quad_core_acc<P>(w, n_rows, quad, lds, xload);
   const int lane = threadIdx.x & 63;
   const int row = quad * 4 + (lane >> 4);
   if ((lane & 15) == 0 && row < n_rows) epi(row, acc);

@@ -94,9 +94,11 @@ extern "C" __global__ void vocab_argmax_finalize(uint64_t* __restrict__ ws,
   }
 }
 
-// Zeroes the workspace key (graph-capture safe: a kernel, not a memset node).
+// Zeroes the 256-byte workspace (graph-capture safe: a kernel, not a memset
+// node): the argmax key and, in a decode scratch, the status word and the
+// attention merge counters.
 extern "C" __global__ void vocab_workspace_reset(uint32_t* __restrict__ ws) {
-  if (threadIdx.x < 4) ws[threadIdx.x] = 0u;
+  if (threadIdx.x < 64) ws[threadIdx.x] = 0u;
 }
 
 // Plain device copy of n16 16-byte words (grid-stride): the reference kernel

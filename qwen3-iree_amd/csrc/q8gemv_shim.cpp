@@ -96,9 +96,9 @@ struct State {
   hipFunction_t copy = nullptr;
   int batch_wgs = 0;      // 0 = default
   hipModule_t dec_module = nullptr;  // decode_gfx950.hsaco (optional)
-  hipFunction_t dec_embed = nullptr, dec_qkv = nullptr, dec_attn = nullptr, dec_combine = nullptr,
+  hipFunction_t dec_embed = nullptr, dec_qkv = nullptr, dec_attn = nullptr,
                 dec_o = nullptr, dec_gu = nullptr, dec_dn = nullptr, dec_vocab = nullptr,
-                dec_final = nullptr;
+                dec_final = nullptr, dec_adv = nullptr;
   int vocab_wgs = 0;      // 0 = default
 };
 
@@ -249,10 +249,10 @@ int q8gemv_init(const char* code_object_path) {
           hipFunction_t* fn;
           const char* name;
         } names[] = {{&g.dec_embed, "dec_embed"},     {&g.dec_qkv, "dec_qkv"},
-                     {&g.dec_attn, "dec_attn_split"}, {&g.dec_combine, "dec_attn_combine"},
+                     {&g.dec_attn, "dec_attention"},
                      {&g.dec_o, "dec_o_res"},         {&g.dec_gu, "dec_gu_swiglu"},
                      {&g.dec_dn, "dec_down_res"},     {&g.dec_vocab, "dec_vocab_argmax"},
-                     {&g.dec_final, "dec_finalize"}};
+                     {&g.dec_final, "dec_finalize"},  {&g.dec_adv, "dec_advance"}};
         bool ok = true;
         for (auto& n : names) ok = ok && hipModuleGetFunction(n.fn, dm, n.name) == hipSuccess;
         if (ok) {
@@ -284,8 +284,8 @@ void q8gemv_shutdown(void) {
   std::memset(g.hal, 0, sizeof(g.hal));
   if (g.dec_module) (void)hipModuleUnload(g.dec_module);
   g.dec_module = nullptr;
-  g.dec_embed = g.dec_qkv = g.dec_attn = g.dec_combine = g.dec_o = g.dec_gu = g.dec_dn =
-      g.dec_vocab = g.dec_final = nullptr;
+  g.dec_embed = g.dec_qkv = g.dec_attn = g.dec_o = g.dec_gu = g.dec_dn =
+      g.dec_vocab = g.dec_final = g.dec_adv = nullptr;
   g.vocab = g.vocab_finalize = g.ws_reset = g.copy = nullptr;
   g.ready = false;
 }
@@ -728,7 +728,8 @@ namespace {
 constexpr int kLayers = 28;
 constexpr int kVocabRows = 151936;
 constexpr int64_t kKvRow = 8 * 128;  // f16 elements per cache slot
-constexpr int kAttnSplitsHost = 32;
+constexpr int kAttnGroupsHost = 8;  // attention workgroups (partials) per kv head
+constexpr int32_t kGenerateBatch = 4;  // tokens between EOS checks (qwen3_full.mlir:1412)
 
 // Scratch layout (bytes).  Key + status first; every region 256-byte aligned.
 constexpr size_t kScrKey = 0;        // u64 argmax key
@@ -745,8 +746,8 @@ constexpr size_t kScrXn = kScrAct + 6144;    // f16[1024] rms_norm(h, attn_norm)
 constexpr size_t kScrQr = kScrXn + 2048;     // f16[2048] q after head norm + RoPE
 constexpr size_t kScrFn = kScrQr + 4096;     // f16[1024] rms_norm(res, ffn_norm)
 constexpr size_t kScrOn = kScrFn + 2048;     // f16[1024] rms_norm(h, output_norm)
-constexpr size_t kScrPart = kScrOn + 2048;   // f32[16][32][130]
-constexpr size_t kScrBytes = kScrPart + 16 * kAttnSplitsHost * 130 * 4;
+constexpr size_t kScrPart = kScrOn + 2048;   // f32[16][8][132] attention partials
+constexpr size_t kScrBytes = kScrPart + 16 * kAttnGroupsHost * 132 * 4;
 
 const uint8_t* cb(const void* p) { return static_cast<const uint8_t*>(p); }
 uint8_t* mb(void* p) { return static_cast<uint8_t*>(p); }
@@ -818,15 +819,11 @@ int launch_layer(const qwen3_weights* w, int layer, void* k_cache, void* v_cache
   {
     const void* pp = pos;
     void* args[] = {&q, &k, &v, &qn, &kn, &pp, &ms, &kc, &vc, &part, &qr};
-    if ((rc = launch(g.dec_attn, 8 * kAttnSplitsHost, 64, args, st))) return rc;
+    if ((rc = launch(g.dec_attn, 8 * kAttnGroupsHost, 256, args, st))) return rc;
   }
   {
-    void* args[] = {&part, &attn};
-    if ((rc = launch(g.dec_combine, 16, 128, args, st))) return rc;
-  }
-  {
-    void* args[] = {&wo, &attn, &hin, &res};
-    if ((rc = launch(g.dec_o, 256, 64, args, st))) return rc;
+    void* args[] = {&wo, &part, &hin, &res, &attn};
+    if ((rc = launch(g.dec_o, 64, 256, args, st))) return rc;
   }
   {
     void* args[] = {&wgu, &res, &fn, &act, &fnx};
@@ -840,7 +837,8 @@ int launch_layer(const qwen3_weights* w, int layer, void* k_cache, void* v_cache
 }
 
 int launch_head(const qwen3_weights* w, const void* h, void* logits, int32_t* token,
-                int32_t* pos, int advance, int64_t max_seq, void* scratch, hipStream_t st) {
+                int32_t* pos, int advance, int64_t max_seq, void* scratch, hipStream_t st,
+                int32_t* out = nullptr) {
   const void* W = w->output_w;
   const void* on = w->output_norm;
   void* ws = mb(scratch) + kScrKey;
@@ -853,8 +851,43 @@ int launch_head(const qwen3_weights* w, const void* h, void* logits, int32_t* to
   }
   int adv = advance ? 1 : 0;
   int ms = (int)max_seq;
-  void* args[] = {&ws, &token, &pos, &adv, &ms, &status};
+  void* args[] = {&ws, &token, &pos, &adv, &ms, &status, &out};
   return launch(g.dec_final, 1, 64, args, st);
+}
+
+int launch_embed(const qwen3_weights* w, const int32_t* token, void* h, hipStream_t st) {
+  const void* t = token;
+  const void* e = w->token_embd;
+  void* args[] = {&t, &e, &h};
+  return launch(g.dec_embed, 1, 128, args, st);
+}
+
+// Embedding of *token_in, the 28 layers at *pos; the final hidden state is
+// left in the scratch's h_a.
+int launch_body(const qwen3_weights* w, void* k_cache, void* v_cache, int64_t max_seq,
+                const int32_t* token_in, const int32_t* pos, void* scratch, hipStream_t st,
+                void** h_final) {
+  void* ha = mb(scratch) + kScrHA;
+  void* hb = mb(scratch) + kScrHB;
+  int rc = launch_embed(w, token_in, ha, st);
+  if (rc) return rc;
+  for (int l = 0; l < kLayers; ++l) {
+    if ((rc = launch_layer(w, l, k_cache, v_cache, max_seq, pos, ha, hb, scratch, st))) return rc;
+    std::swap(ha, hb);
+  }
+  *h_final = ha;
+  return Q8_OK;
+}
+
+int validate_step_args(const qwen3_weights* w, void* k_cache, void* v_cache, int64_t max_seq,
+                       const int32_t* token, const int32_t* pos, const void* scratch) {
+  int rc = validate_weights(w);
+  if (rc) return rc;
+  if ((rc = validate_cache(k_cache, v_cache, max_seq))) return rc;
+  if (!token || !pos || !scratch) return fail(Q8_ERR_NULL_POINTER, "null token, pos or scratch");
+  if (!aligned(token, 4) || !aligned(pos, 4) || !aligned(scratch, 256))
+    return fail(Q8_ERR_MISALIGNED, "token/pos 4, scratch 256-byte alignment");
+  return Q8_OK;
 }
 
 }  // namespace
@@ -897,10 +930,7 @@ int qwen3_decode_embed(const qwen3_weights* w, const int32_t* token, void* h_out
   if (!aligned(token, 4) || !aligned(h_out, 16))
     return fail(Q8_ERR_MISALIGNED, "token needs 4-byte, h_out 16-byte alignment");
   if ((rc = check_decode_ready())) return rc;
-  const void* t = token;
-  const void* e = w->token_embd;
-  void* args[] = {&t, &e, &h_out};
-  return launch(g.dec_embed, 1, 128, args, static_cast<hipStream_t>(stream));
+  return launch_embed(w, token, h_out, static_cast<hipStream_t>(stream));
 }
 
 int qwen3_decode_layer(const qwen3_weights* w, int layer, void* k_cache, void* v_cache,
@@ -937,28 +967,78 @@ int qwen3_decode_head(const qwen3_weights* w, const void* h, void* logits, int32
 int qwen3_decode_step(const qwen3_weights* w, void* k_cache, void* v_cache, int64_t max_seq,
                       int32_t* token, int32_t* pos, void* logits, int advance, void* scratch,
                       void* stream) {
-  int rc = validate_weights(w);
+  int rc = validate_step_args(w, k_cache, v_cache, max_seq, token, pos, scratch);
   if (rc) return rc;
-  if ((rc = validate_cache(k_cache, v_cache, max_seq))) return rc;
-  if (!token || !pos || !scratch) return fail(Q8_ERR_NULL_POINTER, "null token, pos or scratch");
-  if (!aligned(token, 4) || !aligned(pos, 4) || !aligned(scratch, 256) ||
-      (logits && !aligned(logits, 2)))
-    return fail(Q8_ERR_MISALIGNED, "token/pos 4, scratch 256, logits 2-byte alignment");
+  if (logits && !aligned(logits, 2)) return fail(Q8_ERR_MISALIGNED, "logits 2-byte alignment");
   if ((rc = check_decode_ready())) return rc;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  void* ha = mb(scratch) + kScrHA;
-  void* hb = mb(scratch) + kScrHB;
-  {
-    const void* t = token;
-    const void* e = w->token_embd;
-    void* args[] = {&t, &e, &ha};
-    if ((rc = launch(g.dec_embed, 1, 128, args, st))) return rc;
+  void* h = nullptr;
+  if ((rc = launch_body(w, k_cache, v_cache, max_seq, token, pos, scratch, st, &h))) return rc;
+  return launch_head(w, h, logits, token, pos, advance, max_seq, scratch, st);
+}
+
+int qwen3_prefill(const qwen3_weights* w, void* k_cache, void* v_cache, int64_t max_seq,
+                  const int32_t* prompt, int32_t n_prompt, int32_t* token, int32_t* pos,
+                  void* scratch, void* stream) {
+  int rc = validate_step_args(w, k_cache, v_cache, max_seq, token, pos, scratch);
+  if (rc) return rc;
+  if (!prompt) return fail(Q8_ERR_NULL_POINTER, "null prompt");
+  if (!aligned(prompt, 4)) return fail(Q8_ERR_MISALIGNED, "prompt 4-byte alignment");
+  if (n_prompt < 1 || n_prompt > max_seq)
+    return fail(Q8_ERR_BAD_SHAPE, "n_prompt %d outside [1, max_seq]", n_prompt);
+  if ((rc = check_decode_ready())) return rc;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  void* status = mb(scratch) + kScrStatus;
+  int ms = (int)max_seq;
+  for (int32_t i = 0; i < n_prompt; ++i) {
+    void* h = nullptr;
+    if ((rc = launch_body(w, k_cache, v_cache, max_seq, prompt + i, pos, scratch, st, &h)))
+      return rc;
+    if (i + 1 < n_prompt) {
+      void* args[] = {&pos, &ms, &status};
+      if ((rc = launch(g.dec_adv, 1, 64, args, st))) return rc;
+    } else {
+      if ((rc = launch_head(w, h, nullptr, token, pos, 1, max_seq, scratch, st))) return rc;
+    }
   }
-  for (int l = 0; l < kLayers; ++l) {
-    if ((rc = launch_layer(w, l, k_cache, v_cache, max_seq, pos, ha, hb, scratch, st))) return rc;
-    std::swap(ha, hb);
+  return Q8_OK;
+}
+
+int qwen3_generate(const qwen3_weights* w, void* k_cache, void* v_cache, int64_t max_seq,
+                   int32_t* token, int32_t* pos, int32_t max_new, int32_t eos_id,
+                   int32_t* out_tokens, int32_t* n_generated, void* scratch, void* stream) {
+  int rc = validate_step_args(w, k_cache, v_cache, max_seq, token, pos, scratch);
+  if (rc) return rc;
+  if (!out_tokens || !n_generated) return fail(Q8_ERR_NULL_POINTER, "null out_tokens or n_generated");
+  if (!aligned(out_tokens, 4)) return fail(Q8_ERR_MISALIGNED, "out_tokens 4-byte alignment");
+  if (max_new < 0) return fail(Q8_ERR_BAD_SHAPE, "max_new %d < 0", max_new);
+  if ((rc = check_decode_ready())) return rc;
+  *n_generated = 0;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  int32_t p0 = 0;
+  HIP_TRY(hipMemcpyAsync(&p0, pos, sizeof(p0), hipMemcpyDeviceToHost, st));
+  HIP_TRY(hipStreamSynchronize(st));
+  if (p0 < 0 || (int64_t)p0 + max_new > max_seq)
+    return fail(Q8_ERR_BAD_SHAPE, "positions %d + %d new tokens exceed max_seq %lld", p0, max_new,
+                (long long)max_seq);
+  int32_t idx = 0;
+  while (idx < max_new) {
+    const int32_t batch = max_new - idx < kGenerateBatch ? max_new - idx : kGenerateBatch;
+    for (int32_t b = 0; b < batch; ++b) {
+      void* h = nullptr;
+      if ((rc = launch_body(w, k_cache, v_cache, max_seq, token, pos, scratch, st, &h))) return rc;
+      if ((rc = launch_head(w, h, nullptr, token, pos, 1, max_seq, scratch, st,
+                            out_tokens + idx + b)))
+        return rc;
+    }
+    idx += batch;
+    int32_t last = 0;
+    HIP_TRY(hipMemcpyAsync(&last, token, sizeof(last), hipMemcpyDeviceToHost, st));
+    HIP_TRY(hipStreamSynchronize(st));
+    *n_generated = idx;
+    if (last == eos_id) break;
   }
-  return launch_head(w, ha, logits, token, pos, advance, max_seq, scratch, st);
+  return Q8_OK;
 }
 
 }  // extern "C"

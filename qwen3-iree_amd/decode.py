@@ -4,7 +4,7 @@ The reference runs a token as @generate's inner loop inside IREE
 (model/qwen3_full.mlir:1431-1526): embedding gather, 28 x
 @transformer_layer_decode_static, final rms_norm, the vocab GEMV and the tiled
 argmax, with the token fed back and the position incremented on the device.
-Here the same step is one C call that enqueues 171 gfx950 kernel launches on a
+Here the same step is one C call that enqueues 143 gfx950 kernel launches on a
 stream (libq8gemv.so); this module owns the device buffers it needs (weights,
 the flat KV cache, scratch, token and position words), captures the step in a
 hipGraph and replays it.
@@ -209,6 +209,35 @@ class DecodeSession:
         self.synchronize()
         return self.logits.download(np.float16, VOCAB)
 
+    # prompt ingestion and the generation loop
+    def prefill(self, prompt) -> None:
+        """Decode steps over the prompt tokens from the current position; the
+        token word then holds the argmax after the last prompt token."""
+        prompt = np.ascontiguousarray(prompt, dtype=np.int32).reshape(-1)
+        if prompt.size == 0:
+            raise ValueError("empty prompt")
+        buf = Q.DeviceBuffer.from_array(prompt)
+        try:
+            Q._call("qwen3_prefill", self.model.ref(), self.k_cache.ptr, self.v_cache.ptr,
+                    self.max_seq, buf.ptr, int(prompt.size), self.token_ptr, self.pos_ptr,
+                    self.scratch.ptr, Q._stream(self.stream))
+            self.synchronize()
+        finally:
+            buf.free()
+
+    def generate(self, max_new: int, eos_id: int) -> np.ndarray:
+        """@generate's loop from the current token / position: returns the
+        produced tokens (int32; the EOS check runs after every 4 tokens)."""
+        out = Q.DeviceBuffer(4 * max(int(max_new), 1))
+        n = ctypes.c_int32(0)
+        try:
+            Q._call("qwen3_generate", self.model.ref(), self.k_cache.ptr, self.v_cache.ptr,
+                    self.max_seq, self.token_ptr, self.pos_ptr, int(max_new), int(eos_id),
+                    out.ptr, ctypes.byref(n), self.scratch.ptr, Q._stream(self.stream))
+            return out.download(np.int32, n.value) if n.value else np.zeros(0, np.int32)
+        finally:
+            out.free()
+
     # the step in parts
     def embed(self, h_out: Q.DeviceBuffer) -> None:
         Q._call("qwen3_decode_embed", self.model.ref(), self.token_ptr, h_out.ptr,
@@ -243,3 +272,19 @@ class DecodeSession:
         self._graphs.clear()
         for b in (self.k_cache, self.v_cache, self.scratch, self.state, self.logits):
             b.free()
+
+
+def run(model: DeviceWeights, prompt, max_gen: int, eos_id: int,
+        stream: Q.Stream | None = None) -> np.ndarray:
+    """The reference's @run (qwen3_full.mlir:2113-2167): a KV cache of
+    len(prompt) + max_gen positions, the prompt ingested from position 0, its
+    argmax as the first token, then @generate with max_gen tokens.  Returns the
+    generated tokens (the first token itself is not among them, as there)."""
+    prompt = np.asarray(prompt, dtype=np.int32).reshape(-1)
+    sess = DecodeSession(model, int(prompt.size) + int(max_gen), stream)
+    try:
+        sess.set_state(0, 0)
+        sess.prefill(prompt)
+        return sess.generate(max_gen, eos_id)
+    finally:
+        sess.free()

@@ -261,6 +261,15 @@ def test_decode_scratch_layout(Q):
     (lambda L, w: L.qwen3_decode_head(w, A16, A16 + 1, A16, A16, 1, 8, A16, None), 5),
     (lambda L, w: L.qwen3_decode_embed(w, None, A16, None), 3),
     (lambda L, w: L.qwen3_scratch_reset(A16 + 16, None), 5),
+    # prompt ingestion and the generation loop
+    (lambda L, w: L.qwen3_prefill(w, A16, A16, 8, None, 3, A16, A16, A16, None), 3),
+    (lambda L, w: L.qwen3_prefill(w, A16, A16, 8, A16, 0, A16, A16, A16, None), 6),
+    (lambda L, w: L.qwen3_prefill(w, A16, A16, 8, A16, 9, A16, A16, A16, None), 6),
+    (lambda L, w: L.qwen3_prefill(w, A16, A16, 8, A16 + 2, 3, A16, A16, A16, None), 5),
+    (lambda L, w: L.qwen3_generate(w, A16, A16, 8, A16, A16, 4, 0, None, A16, A16, None), 3),
+    (lambda L, w: L.qwen3_generate(w, A16, A16, 8, A16, A16, 4, 0, A16, None, A16, None), 3),
+    (lambda L, w: L.qwen3_generate(w, A16, A16, 8, A16, A16, -1, 0, A16, A16, A16, None), 6),
+    (lambda L, w: L.qwen3_generate(w, A16, A16, 8, A16, A16, 4, 0, A16 + 1, A16, A16, None), 5),
 ])
 def test_decode_validation_before_device(Q, call, code):
     L = Q.load_library()
