@@ -463,10 +463,8 @@ __device__ __forceinline__ void vocab_body_x(const uint16_t* __restrict__ W, XLo
   const int b_begin = (int)(gw * nbatch / tw);
   const int b_end = (int)((gw + 1) * nbatch / tw);
 
-  u32x4 xr[8];
-  xload(li, xr);
-
   const u32x4* Wv = reinterpret_cast<const u32x4*>(W);
+  u32x4 xr[8];  // this lane's x columns, formed by xload below
   auto load_batch = [&](int b, u32x4 (&dst)[8]) {
     int row = 4 * b + grp;
     row = row < n_rows ? row : n_rows - 1;  // only the grid's last batch can be short
@@ -499,12 +497,17 @@ __device__ __forceinline__ void vocab_body_x(const uint16_t* __restrict__ W, XLo
     }
   };
 
-  // Ping-pong between two register sets; every load inside the loop is
-  // unconditional, so the compiler can wait for exactly the older set.
+  // The first batch is requested before x is formed (x may need loads and
+  // a reduction of its own); rows are clamped, so this is safe even for a
+  // wave with no batch.  Then ping-pong between two register sets; every
+  // load inside the loop is unconditional, so the compiler can wait for
+  // exactly the older set.
+  u32x4 A[8], B[8];
+  load_batch(b_begin, A);
+  __builtin_amdgcn_sched_barrier(0);
+  xload(li, xr);
   const int nb = b_end - b_begin;
   if (nb > 0) {
-    u32x4 A[8], B[8];
-    load_batch(b_begin, A);
     int i = 0;
     for (; i + 2 < nb; i += 2) {
       load_batch(b_begin + i + 1, B);
