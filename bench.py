@@ -143,6 +143,43 @@ def bench_decode(Q, O, stream, args) -> dict:
             "token": step_tok, "oracle_token": ref_tok, "parity_ok": bool(step_ok)}
 
 
+def bench_gguf(Q, tmpdir: Path) -> dict:
+    """GGUF -> HostWeights -> device: throughput of each stage on the full-size
+    synthetic checkpoint (1.09 GB of parameters)."""
+    from qwen3_iree_amd import decode as D
+    from qwen3_iree_amd import gguf as G
+
+    hw = D.synthetic_weights(seed=SEED, workers=16)
+    tmpdir.mkdir(parents=True, exist_ok=True)
+    path = tmpdir / "qwen3-0.6b-synthetic-q8_0.gguf"
+    t0 = time.perf_counter()
+    G.write_qwen3_gguf(hw, path)
+    write_s = time.perf_counter() - t0
+    size = path.stat().st_size
+    reads = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        got = G.qwen3_host_weights(path, workers=16)
+        reads.append(time.perf_counter() - t0)
+    same = all(np.array_equal(getattr(got, f).view(np.uint8), getattr(hw, f).view(np.uint8))
+               for f in D.WEIGHT_FIELDS)
+    t0 = time.perf_counter()
+    model = D.DeviceWeights(got)
+    Q.synchronize()
+    upload_s = time.perf_counter() - t0
+    nbytes = model.nbytes
+    model.free()
+    path.unlink()
+    log(f"gguf: {size} B file written in {write_s:.2f}s; read into the device layout in "
+        f"{reads[0]:.2f}s (first), {min(reads[1:]):.3f}s (warm cache); upload {upload_s:.2f}s; "
+        f"identical={same}")
+    return {"file_bytes": size, "param_bytes": nbytes, "write_s": round(write_s, 3),
+            "read_first_s": round(reads[0], 3), "read_warm_s": round(min(reads[1:]), 3),
+            "read_warm_GBps": round(nbytes / min(reads[1:]) / 1e9, 2),
+            "upload_s": round(upload_s, 3), "upload_GBps": round(nbytes / upload_s / 1e9, 2),
+            "bit_identical": bool(same)}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -154,6 +191,10 @@ def main() -> int:
                     help="positions attended by the timed decode step")
     ap.add_argument("--decode-only", action="store_true",
                     help="run only the full decode step and print its JSON line")
+    ap.add_argument("--gguf-ingest", metavar="DIR", default=None,
+                    help="only measure GGUF ingestion: write the synthetic model as a Q8_0 GGUF "
+                         "under DIR, read it back into the device layout (cold, then warm page "
+                         "cache), upload it, check it bit for bit, print one JSON line")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline sample budget")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-graph", action="store_true",
@@ -181,6 +222,9 @@ def main() -> int:
     sys.path.insert(0, str(REPO / "oracle"))
     import oracle as O  # the checker; also the CPU baseline below
 
+    if args.gguf_ingest:
+        print(json.dumps({"gguf_ingest": bench_gguf(Q, Path(args.gguf_ingest))}), flush=True)
+        return 0
     if args.decode_only:
         print(json.dumps({"decode_step": bench_decode(Q, O, Q.Stream(), args)}), flush=True)
         return 0

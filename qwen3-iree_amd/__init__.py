@@ -3,9 +3,14 @@
 Modules
   q8gemv   ctypes binding of libq8gemv (the C ABI in include/q8gemv.h): the six
            substituted decode dispatches plus a small device runtime.
+  decode   the whole decode step (include/qwen3_decode.h): device weights,
+           sessions with a KV cache, prompt ingestion, the generation loop, run.
+  gguf     GGUF v2/v3 reader / writer and Qwen3-0.6B checkpoint ingestion into
+           the device layout (no IREE).
   weights  Q8_0 quantisation / stacking (the reference's offline weight prep)
            and seeded synthetic inputs.
-  build    hipcc / g++ recipe for lib/q8gemv_gfx950.hsaco and lib/libq8gemv.so.
+  build    hipcc / g++ recipe for lib/q8gemv_gfx950.hsaco, lib/decode_gfx950.hsaco
+           and lib/libq8gemv.so.
 
 The directory name is not a Python identifier; load it as a package with
 load_package() below (or put this directory on sys.path and import the
