@@ -135,9 +135,25 @@ def bench_decode(Q, O, stream, args) -> dict:
     log(f"decode step (context {ctx}, {3 + 5 * layers} launches"
         f"{'' if args.no_graph else ', hipGraph'}): {dec_us:.1f} us/token, "
         f"{1e6 / dec_us:.0f} tok/s, {dec_gbs:.0f} GB/s")
+    # the same step as one cooperative launch (qwen3_set_step_mode(1)), eager
+    single_us = None
+    try:
+        D.set_step_mode(1)
+    except Q.Q8GemvError as e:
+        log(f"single-launch step unavailable: {e}")
+    else:
+        sess.set_state(first_token, ctx - 1)
+        one = lambda: sess.step(advance=False, logits=False)  # noqa: E731
+        for _ in range(20):
+            one()
+        single_us = timed_ms(Q, stream, one, max(50, args.steps // 4)) * 1e3
+        ok1 = sess.get_state()[1] == ctx - 1 and sess.status() == 0
+        D.set_step_mode(0)
+        log(f"decode step as one cooperative launch: {single_us:.1f} us/token (status ok={ok1})")
     sess.free()
     model.free()
-    return {"us": round(dec_us, 2), "tok_per_s": round(1e6 / dec_us, 1), "context": ctx,
+    return {"single_launch_us": None if single_us is None else round(single_us, 2),
+            "us": round(dec_us, 2), "tok_per_s": round(1e6 / dec_us, 1), "context": ctx,
             "bytes": dec_bytes, "GBps": round(dec_gbs, 1), "frac": round(dec_gbs / HBM_PEAK_GBS, 4),
             "launches": 3 + 5 * layers, "launch": "eager" if args.no_graph else "hipGraph",
             "token": step_tok, "oracle_token": ref_tok, "parity_ok": bool(step_ok)}

@@ -48,14 +48,17 @@ typedef struct qwen3_weights {
  * layout of qwen3_full.mlir:213-230: the entry of layer l, position p is slot
  * l * max_seq + p (:782, 795). */
 
-/* Scratch (activations, attention partials, argmax key, status word):
- * qwen3_scratch_bytes() bytes, 256-byte aligned.  Zero it once with
- * qwen3_scratch_reset before the first step; steps keep it consistent.  One
- * scratch serves one stream: concurrent steps need their own. */
+/* Scratch (activations, attention partials, argmax key, status word, the
+ * single-launch step's hand-off words): qwen3_scratch_bytes() bytes, 256-byte
+ * aligned.  Clear it once with qwen3_scratch_reset (a kernel on `stream`)
+ * before the first step; steps keep it consistent.  One scratch serves one
+ * stream: concurrent steps need their own. */
 size_t qwen3_scratch_bytes(void);
 int qwen3_scratch_reset(void* scratch, void* stream);
 /* Byte offset in the scratch of the u32 status word: bit 0 = a step asked to
- * advance past the last cache slot (the position then stays). */
+ * advance past the last cache slot (the position then stays); bit 1 = a
+ * single-launch step gave up waiting for a hand-off (its results are not
+ * valid; never expected on a working device). */
 size_t qwen3_scratch_status_offset(void);
 
 /* One token: h = token_embd[*token]; 28 layers at position *pos (attention
@@ -67,6 +70,17 @@ size_t qwen3_scratch_status_offset(void);
 int qwen3_decode_step(const qwen3_weights* w, void* k_cache, void* v_cache, int64_t max_seq,
                       int32_t* token, int32_t* pos, void* logits, int advance, void* scratch,
                       void* stream);
+
+/* How qwen3_decode_step, qwen3_prefill and qwen3_generate run a step:
+ * mode 0 = one launch per phase (143 per step), the default; mode 1 = one
+ * cooperative launch per step (dec_step: all phases in one kernel, 256
+ * resident workgroups handing activations over through tagged words).  Both
+ * compute every value with the same operations in the same order (tested bit
+ * for bit).  Setting mode 1 on a device that cannot run it fails with
+ * Q8_ERR_BAD_ARGUMENT.  No counterpart in the reference (IREE schedules its
+ * dispatches itself). */
+int qwen3_set_step_mode(int mode);
+int qwen3_get_step_mode(int* mode);
 
 /* The same step in parts, for tests and for callers that interleave work:
  * embed: h_out = token_embd[*token];

@@ -1,0 +1,403 @@
+// Device code shared by the decode-step kernels (decode_kernels.hip): the
+// launch-per-phase kernels and the single-launch (persistent) step call the
+// same functions, so both paths compute every value with the same operations
+// in the same order.  Header-only, internal to the including translation unit.
+#ifndef QWEN3_DECODE_DEVICE_H
+#define QWEN3_DECODE_DEVICE_H
+
+#include "q8_device.h"
+
+namespace {
+
+constexpr int kLayers = 28;
+constexpr int kHidden = 1024;
+constexpr int kHeadDim = 128;
+constexpr int kKvHeads = 8;
+constexpr int kQHeads = 16;
+constexpr int kFfn = 3072;
+constexpr int kVocab = 151936;
+constexpr int kAttnSplits = 32;      // position splits per kv head (one wave each)
+constexpr int kAttnWaves = 4;        // splits per workgroup, merged in LDS
+constexpr int kAttnGroups = kAttnSplits / kAttnWaves;  // partials per query head
+constexpr int kPartStride = 4 + kHeadDim;  // m, l, 2 pad, acc[128] (16-byte aligned acc)
+constexpr float kEps = 9.99999997e-7f;    // qwen3_full.mlir:63
+constexpr float kRopeBase = 1.0e6f;       // qwen3_full.mlir:59
+// rsqrt(128) of qwen3_full.mlir:721-723, the f32 nearest 2^-3.5 (0x3DB504F3)
+constexpr float kAttnScale = 0.0883883461356163f;
+
+__device__ __forceinline__ float wave_sum(float v) {
+  v = reduce_row16(v);
+  v += __shfl_xor(v, 16, 64);
+  v += __shfl_xor(v, 32, 64);
+  return v;
+}
+
+__device__ __forceinline__ float max32(float v) {  // over the 32 lanes of a wave half
+  v = fmaxf(v, dpp<0xB1>(v));
+  v = fmaxf(v, dpp<0x4E>(v));
+  v = fmaxf(v, dpp<0x141>(v));
+  v = fmaxf(v, dpp<0x140>(v));
+  return fmaxf(v, __shfl_xor(v, 16, 64));
+}
+
+__device__ __forceinline__ float sum32(float v) {
+  v = reduce_row16(v);
+  return v + __shfl_xor(v, 16, 64);
+}
+
+__device__ __forceinline__ uint32_t pack_f16x2(float a, float b) {
+  return (uint32_t)f32_to_f16_bits(a) | ((uint32_t)f32_to_f16_bits(b) << 16);
+}
+
+__device__ __forceinline__ _Float16 as_half(uint16_t b) { return __builtin_bit_cast(_Float16, b); }
+
+// rms_norm (qwen3_full.mlir:134-165) of a 1024-vector for the 64 columns this
+// lane holds (hv: the values, wv: the norm weights, 8 per u32x4): the 16
+// lanes of a DPP row together hold all 1024 columns, so their partial sums of
+// squares meet in a row reduction.
+__device__ __forceinline__ void rmsnorm_apply(const u32x4 (&hv)[8], const u32x4 (&wv)[8],
+                                              u32x4 (&xr)[8]) {
+  float ss = 0.0f;
+#pragma unroll
+  for (int m = 0; m < 8; ++m) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const f16x2 hp = as_f16x2(hv[m][j]);
+      const float a = (float)hp.x, b = (float)hp.y;
+      ss = ss + a * a;
+      ss = ss + b * b;
+    }
+  }
+  ss = reduce_row16(ss);
+  const float inv = 1.0f / sqrtf(ss / 1024.0f + kEps);
+#pragma unroll
+  for (int m = 0; m < 8; ++m) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const f16x2 hp = as_f16x2(hv[m][j]), wp = as_f16x2(wv[m][j]);
+      const float a = ((float)hp.x * inv) * (float)wp.x;
+      const float b = ((float)hp.y * inv) * (float)wp.y;
+      xr[m][j] = pack_f16x2(a, b);
+    }
+  }
+}
+
+// h from global memory (H_LDS = false) or from LDS (true); columns col(m).
+template <bool H_LDS, class ColOf>
+__device__ __forceinline__ void rmsnorm_cols(const uint16_t* __restrict__ h,
+                                             const uint16_t* __restrict__ w, ColOf col,
+                                             u32x4 (&xr)[8]) {
+  u32x4 hv[8], wv[8];
+#pragma unroll
+  for (int m = 0; m < 8; ++m) {
+    if constexpr (H_LDS) hv[m] = *reinterpret_cast<const u32x4*>(h + col(m));
+    else hv[m] = load_global(reinterpret_cast<const u32x4*>(h + col(m)));
+    wv[m] = load_global(reinterpret_cast<const u32x4*>(w + col(m)));
+  }
+  rmsnorm_apply(hv, wv, xr);
+}
+
+// The Q8_0 GEMV lane layout: columns [64 p16, 64 p16 + 64) in 8 pieces of 8.
+template <bool H_LDS>
+__device__ __forceinline__ void rmsnorm_gemv_x(const uint16_t* __restrict__ h,
+                                               const uint16_t* __restrict__ w, u32x4 (&xr)[8]) {
+  const int p16 = threadIdx.x & 15;
+  rmsnorm_cols<H_LDS>(h, w, [=](int m) { return 64 * p16 + 8 * m; }, xr);
+}
+
+// x for this lane's GEMV columns of chunk c, from an f16 vector in LDS.
+template <int P>
+__device__ __forceinline__ void lds_x_cols(const uint16_t* __restrict__ x, u32x4 (&xr)[P][8]) {
+  const int p16 = threadIdx.x & 15;
+#pragma unroll
+  for (int c = 0; c < P; ++c) {
+    const u32x4* xs4 = reinterpret_cast<const u32x4*>(x + 1024 * c + 64 * p16);
+#pragma unroll
+    for (int m = 0; m < 8; ++m) xr[c][m] = xs4[m];
+  }
+}
+
+// SwiGLU of qwen3_full.mlir:829-839, every op in f16: e = exp(-g),
+// den = 1 + e, sig = 1 / den, silu = g * sig, out = silu * up (exp and the
+// reciprocal evaluated in f32 and rounded once).
+__device__ __forceinline__ uint16_t swiglu_f16(float gate_acc, float up_acc) {
+  const _Float16 g = to_f16(gate_acc);
+  const _Float16 u = to_f16(up_acc);
+  const _Float16 e = to_f16(expf(-(float)g));
+  const _Float16 den = (_Float16)1.0f + e;
+  const _Float16 sig = to_f16(1.0f / (float)den);
+  const _Float16 silu = g * sig;
+  return __builtin_bit_cast(uint16_t, (_Float16)(silu * u));
+}
+
+// f16(base + f16(acc)): the residual adds of qwen3_full.mlir:801-805, 858-862.
+__device__ __forceinline__ uint16_t residual_f16(_Float16 base, float acc) {
+  return __builtin_bit_cast(uint16_t, (_Float16)(base + to_f16(acc)));
+}
+
+// Weights of the 8 split-group partials of one query head: w_g = exp(m_g -
+// max m) (0 for an empty group), L = sum_g l_g w_g, summed in group order.
+__device__ __forceinline__ void merge_weights(const float (&m)[kAttnGroups],
+                                              const float (&l)[kAttnGroups],
+                                              float (&w)[kAttnGroups], float& L) {
+  float M = -__builtin_inff();
+#pragma unroll
+  for (int g = 0; g < kAttnGroups; ++g) M = fmaxf(M, m[g]);
+  L = 0.0f;
+#pragma unroll
+  for (int g = 0; g < kAttnGroups; ++g) {
+    w[g] = m[g] == -__builtin_inff() ? 0.0f : expf(m[g] - M);
+    L = L + l[g] * w[g];
+  }
+}
+
+// One merged output dim: sum_g acc_g w_g in group order.
+__device__ __forceinline__ float merge_dim(const float (&acc)[kAttnGroups],
+                                           const float (&w)[kAttnGroups]) {
+  float a = 0.0f;
+#pragma unroll
+  for (int g = 0; g < kAttnGroups; ++g) a = a + acc[g] * w[g];
+  return a;
+}
+
+// LDS of one attention workgroup.
+struct AttnLds {
+  float xs[kAttnWaves][3][kHeadDim];  // normed q_A, q_B, k (f16 values)
+  uint32_t qh[kAttnWaves][2][64];     // roped q_A, q_B as f16 pairs
+  uint32_t kh[kAttnWaves][64];        // roped new k as f16 pairs
+  float pbuf[kAttnWaves][2][32];
+  float mrg[kAttnWaves][2][2 + kHeadDim];
+};
+
+// Attention for kv head g and split group sg: four waves, wave w taking
+// position split s = 4 sg + w of the 32 equal splits of ctx = pos + 1; the
+// four results merge in LDS into one partial per query head and group.  Per
+// wave:
+//  0. the split's first 32 cache rows (K: half a row per lane, V: the lane's
+//     two dims for each of the 32 positions) are requested before q/k/v are
+//     fetched (get_qkv), so their latency overlaps that wait and steps 1-2;
+//  1. q heads 2g, 2g+1 and k head g: per-head rms_norm with q_norm / k_norm
+//     (qwen3_full.mlir:648-702), then RoPE (:324-454) at position pos;
+//  2. the wave owning position pos writes the roped k and the raw v to cache
+//     slot pos (k_cache / v_cache: the layer's base; slot layout [max_seq, 8,
+//     128]); split 0 stores the roped q heads to q_roped when it is not null;
+//  3. chunks of 32 positions: lane (j, half) scores position j of the chunk
+//     on dims [64*half, 64*half + 64) for both q heads, the halves meet in one
+//     cross-half add; s_j = (q . k_j) * rsqrt(128); online softmax; the
+//     weighted sum of v (each lane owns dims 2*lane, 2*lane+1 of both heads).
+//     The chunk count is uniform over the workgroup (splits differ by at most
+//     one position), so every wave meets every barrier;
+//  4. publish(hh, m, l, a0, a1) on waves 0 and 1 (query head 2g + hh): m =
+//     max over the 4 waves, l and this lane's two dims rescaled by
+//     exp(m_w - m).  An empty split (ctx < 32) contributes m = -inf, l = 0.
+// get_qkv(xw, v_new) fills this lane's words (dims 2*lane, 2*lane+1) of q
+// head 2g, q head 2g+1, k head g (xw[0..2]) and v head g; every thread of the
+// workgroup calls it once.
+template <class GetQKV, class Publish>
+__device__ __forceinline__ void attention_group(AttnLds& L, int g, int sg, int pos_raw,
+                                                int max_seq, const uint16_t* __restrict__ qn_w,
+                                                const uint16_t* __restrict__ kn_w,
+                                                uint16_t* __restrict__ k_cache,
+                                                uint16_t* __restrict__ v_cache,
+                                                uint16_t* __restrict__ q_roped, GetQKV&& get_qkv,
+                                                Publish&& publish) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int s = sg * kAttnWaves + wave;
+  const int half = lane >> 5;
+  const int pl = lane & 31;
+
+  uint32_t nwv[3];
+  nwv[0] = load_global(reinterpret_cast<const uint32_t*>(qn_w) + lane);
+  nwv[2] = load_global(reinterpret_cast<const uint32_t*>(kn_w) + lane);
+  nwv[1] = nwv[0];
+
+  const int pos = pos_raw < 0 ? 0 : (pos_raw >= max_seq ? max_seq - 1 : pos_raw);
+  const int ctx = pos + 1;
+  const int start = (int)((int64_t)s * ctx / kAttnSplits);
+  const int end = (int)((int64_t)(s + 1) * ctx / kAttnSplits);
+  const int n_chunks = ((ctx + kAttnSplits - 1) / kAttnSplits + 31) / 32;  // workgroup-uniform
+
+  // ---- 0. first chunk of the cache ----
+  // Every lane issues every load (rows clamped into [start, end - 1], row 0
+  // for an empty split) so the compiler's waits stay exact.
+  const int last = end - 1 > 0 ? end - 1 : 0;
+  u32x4 kreg[8];
+  uint32_t vreg[32];
+  auto load_chunk = [&](int c0) {
+    const int p = c0 + pl < last ? c0 + pl : last;
+    const u32x4* krow = reinterpret_cast<const u32x4*>(
+        k_cache + ((size_t)p * kKvHeads + g) * kHeadDim + 64 * half);
+#pragma unroll
+    for (int m = 0; m < 8; ++m) kreg[m] = load_global(krow + m);
+#pragma unroll
+    for (int j = 0; j < 32; ++j) {
+      const int pj = c0 + j < last ? c0 + j : last;
+      vreg[j] = load_global(
+          reinterpret_cast<const uint32_t*>(v_cache + ((size_t)pj * kKvHeads + g) * kHeadDim) + lane);
+    }
+  };
+  load_chunk(start);
+  __builtin_amdgcn_sched_barrier(0);
+
+  uint32_t xw[3], v_new;
+  get_qkv(xw, v_new);
+
+  // ---- 1. head norms: lane owns dims 2*lane, 2*lane+1 ----
+#pragma unroll
+  for (int t = 0; t < 3; ++t) {
+    const f16x2 xv = as_f16x2(xw[t]);
+    const f16x2 wv = as_f16x2(nwv[t]);
+    const float a = (float)xv.x, b = (float)xv.y;
+    float ss = a * a;
+    ss = ss + b * b;
+    ss = wave_sum(ss);
+    const float r = sqrtf(ss / 128.0f + kEps);
+    L.xs[wave][t][2 * lane] = (float)to_f16((a / r) * (float)wv.x);
+    L.xs[wave][t][2 * lane + 1] = (float)to_f16((b / r) * (float)wv.y);
+  }
+  __syncthreads();
+
+  // ---- 1b. RoPE (rotate-half) ----
+  const float posf = (float)pos;
+  float cs[2], sn[2];
+#pragma unroll
+  for (int dd = 0; dd < 2; ++dd) {
+    const int d = 2 * lane + dd;
+    const int i = d < 64 ? d : d - 64;
+    const float e = -((2.0f * (float)i) / 128.0f);
+    const float th = posf * (powf(kRopeBase, e) * 1.0f);
+    cs[dd] = cosf(th);
+    sn[dd] = sinf(th);
+  }
+  uint32_t roped[3];
+#pragma unroll
+  for (int t = 0; t < 3; ++t) {
+    float r2[2];
+#pragma unroll
+    for (int dd = 0; dd < 2; ++dd) {
+      const int d = 2 * lane + dd;
+      if (d < 64) {
+        const float a = L.xs[wave][t][d] * cs[dd];
+        const float b = L.xs[wave][t][d + 64] * sn[dd];
+        r2[dd] = a - b;
+      } else {
+        const float a = L.xs[wave][t][d - 64] * sn[dd];
+        const float b = L.xs[wave][t][d] * cs[dd];
+        r2[dd] = a + b;
+      }
+    }
+    roped[t] = pack_f16x2(r2[0], r2[1]);
+  }
+  L.qh[wave][0][lane] = roped[0];
+  L.qh[wave][1][lane] = roped[1];
+  L.kh[wave][lane] = roped[2];
+
+  // ---- 2. the new position into the cache, the roped q heads once ----
+  if (q_roped != nullptr && s == 0) {
+    reinterpret_cast<uint32_t*>(q_roped + (2 * g) * kHeadDim)[lane] = roped[0];
+    reinterpret_cast<uint32_t*>(q_roped + (2 * g + 1) * kHeadDim)[lane] = roped[1];
+  }
+  if (start <= pos && pos < end) {
+    reinterpret_cast<uint32_t*>(k_cache + ((size_t)pos * kKvHeads + g) * kHeadDim)[lane] = roped[2];
+    reinterpret_cast<uint32_t*>(v_cache + ((size_t)pos * kKvHeads + g) * kHeadDim)[lane] = v_new;
+  }
+  __syncthreads();
+
+  // ---- 3. scores, online softmax, weighted v ----
+  float m = -__builtin_inff(), l = 0.0f;  // per q head; identical in all lanes
+  float mB = -__builtin_inff(), lB = 0.0f;
+  float accA0 = 0.0f, accA1 = 0.0f, accB0 = 0.0f, accB1 = 0.0f;
+  for (int c = 0; c < n_chunks; ++c) {
+    const int c0 = start + 32 * c;
+    const int p = c0 + pl;
+    const bool valid = p < end;
+    // the row of position pos is this step's k (in LDS; the cache slot was
+    // requested before it was written)
+    const bool is_new = p == pos;
+    float dA = 0.0f, dB = 0.0f;
+#pragma unroll
+    for (int mm = 0; mm < 8; ++mm) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int i = 32 * half + 4 * mm + j;
+        const f16x2 kv = as_f16x2(is_new ? L.kh[wave][i] : kreg[mm][j]);
+        dA = __builtin_amdgcn_fdot2(as_f16x2(L.qh[wave][0][i]), kv, dA, false);
+        dB = __builtin_amdgcn_fdot2(as_f16x2(L.qh[wave][1][i]), kv, dB, false);
+      }
+    }
+    dA = dA + __shfl_xor(dA, 32, 64);
+    dB = dB + __shfl_xor(dB, 32, 64);
+    const float sA = valid ? dA * kAttnScale : -__builtin_inff();
+    const float sB = valid ? dB * kAttnScale : -__builtin_inff();
+    const float mnA = fmaxf(m, max32(sA));
+    const float mnB = fmaxf(mB, max32(sB));
+    // mn = -inf only while the split has seen no valid position (acc, l = 0)
+    const float cA = mnA == -__builtin_inff() ? 1.0f : expf(m - mnA);
+    const float cB = mnB == -__builtin_inff() ? 1.0f : expf(mB - mnB);
+    const float pA = valid ? expf(sA - mnA) : 0.0f;
+    const float pB = valid ? expf(sB - mnB) : 0.0f;
+    l = l * cA + sum32(pA);
+    lB = lB * cB + sum32(pB);
+    m = mnA;
+    mB = mnB;
+    if (half == 0) {
+      L.pbuf[wave][0][pl] = pA;
+      L.pbuf[wave][1][pl] = pB;
+    }
+    __syncthreads();
+    accA0 *= cA;
+    accA1 *= cA;
+    accB0 *= cB;
+    accB1 *= cB;
+    const int n = end - c0 < 32 ? end - c0 : 32;
+#pragma unroll
+    for (int j = 0; j < 32; ++j) {
+      // positions past the split hold weight 0 and a clamped (valid) row,
+      // selected to 0 so a non-finite value there cannot leak in
+      const uint32_t vw = c0 + j == pos ? v_new : (j < n ? vreg[j] : 0u);
+      const f16x2 vv = as_f16x2(vw);
+      const float v0 = (float)vv.x, v1 = (float)vv.y;
+      const float wa = L.pbuf[wave][0][j], wb = L.pbuf[wave][1][j];
+      accA0 = accA0 + wa * v0;
+      accA1 = accA1 + wa * v1;
+      accB0 = accB0 + wb * v0;
+      accB1 = accB1 + wb * v1;
+    }
+    __syncthreads();
+    if (c + 1 < n_chunks) load_chunk(c0 + 32);
+  }
+
+  // ---- 4. the four waves' results -> one partial per query head ----
+  if (lane == 0) {
+    L.mrg[wave][0][0] = m;
+    L.mrg[wave][0][1] = l;
+    L.mrg[wave][1][0] = mB;
+    L.mrg[wave][1][1] = lB;
+  }
+  L.mrg[wave][0][2 + 2 * lane] = accA0;
+  L.mrg[wave][0][3 + 2 * lane] = accA1;
+  L.mrg[wave][1][2 + 2 * lane] = accB0;
+  L.mrg[wave][1][3 + 2 * lane] = accB1;
+  __syncthreads();
+  if (wave < 2) {  // wave hh merges query head 2g + hh
+    const int hh = wave;
+    float M = -__builtin_inff();
+#pragma unroll
+    for (int w = 0; w < kAttnWaves; ++w) M = fmaxf(M, L.mrg[w][hh][0]);
+    float Ls = 0.0f, a0 = 0.0f, a1 = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kAttnWaves; ++w) {
+      const float mw = L.mrg[w][hh][0];
+      const float ww = mw == -__builtin_inff() ? 0.0f : expf(mw - M);
+      Ls = Ls + L.mrg[w][hh][1] * ww;
+      a0 = a0 + L.mrg[w][hh][2 + 2 * lane] * ww;
+      a1 = a1 + L.mrg[w][hh][3 + 2 * lane] * ww;
+    }
+    publish(hh, M, Ls, a0, a1);
+  }
+}
+
+}  // namespace
+
+#endif

@@ -1,128 +1,29 @@
 // gfx950 kernels for the rest of the Qwen3-0.6B decode step, built around the
-// Q8_0 GEMV engine of q8_device.h.  One layer
-// (model/qwen3_full.mlir:751-864 with @attention_block_decode_static 591-748)
-// is five launches:
+// Q8_0 GEMV engine of q8_device.h, in two forms that compute the same values
+// with the same operations (shared code in decode_device.h):
 //
+// Launch per phase: one layer (model/qwen3_full.mlir:751-864 with
+// @attention_block_decode_static 591-748) is five launches,
 //   dec_qkv          rms_norm(h, attn_norm) fused into the q/k/v GEMVs
 //   dec_attention    q/k head norms + RoPE, the new k/v written to the flat
-//                    KV cache, split-K GQA attention partials (8 kv heads x 32
-//                    position splits), merged by the last split of each kv
-//                    head
-//   dec_o_res        attn_o GEMV + residual add
+//                    KV cache, split-K GQA attention (8 kv heads x 32
+//                    position splits, 4 splits merged per workgroup)
+//   dec_o_res        the 8 partials per head merged, attn_o GEMV + residual
 //   dec_gu_swiglu    rms_norm(res, ffn_norm) fused into gate_up; each wave
 //                    computes a gate quad and the matching up quad and applies
 //                    SwiGLU in its epilogue
 //   dec_down_res     ffn_down GEMV + residual add
-//
 // plus dec_embed (token row gather), dec_vocab_argmax (final rms_norm fused
 // into the vocab GEMV + argmax) and dec_finalize (token, position).
+//
+// Single launch: dec_step runs the whole step in one cooperative launch of
+// one workgroup per CU, phases handing activations over through tagged
+// 8-byte words instead of kernel boundaries (see its comment).
 //
 // Numerics follow the reference op by op: f16 tensors between ops, f32 in
 // reductions and transcendental math, RNE to f16.  Normalisation multiplies by
 // 1/rms where the reference divides by rms (one f32 rounding apart).
-#include "q8_device.h"
-
-namespace {
-
-constexpr int kHidden = 1024;
-constexpr int kHeadDim = 128;
-constexpr int kKvHeads = 8;
-constexpr int kFfn = 3072;
-constexpr int kVocab = 151936;
-constexpr int kAttnSplits = 32;      // position splits per kv head (one wave each)
-constexpr int kAttnWaves = 4;        // splits per workgroup, merged in LDS
-constexpr int kAttnGroups = kAttnSplits / kAttnWaves;  // partials per query head
-constexpr int kPartStride = 4 + kHeadDim;  // m, l, 2 pad, acc[128] (16-byte aligned acc)
-constexpr float kEps = 9.99999997e-7f;    // qwen3_full.mlir:63
-constexpr float kRopeBase = 1.0e6f;       // qwen3_full.mlir:59
-// rsqrt(128) of qwen3_full.mlir:721-723, the f32 nearest 2^-3.5 (0x3DB504F3)
-constexpr float kAttnScale = 0.0883883461356163f;
-
-__device__ __forceinline__ float wave_sum(float v) {
-  v = reduce_row16(v);
-  v += __shfl_xor(v, 16, 64);
-  v += __shfl_xor(v, 32, 64);
-  return v;
-}
-
-__device__ __forceinline__ float max32(float v) {  // over the 32 lanes of a wave half
-  v = fmaxf(v, dpp<0xB1>(v));
-  v = fmaxf(v, dpp<0x4E>(v));
-  v = fmaxf(v, dpp<0x141>(v));
-  v = fmaxf(v, dpp<0x140>(v));
-  return fmaxf(v, __shfl_xor(v, 16, 64));
-}
-
-__device__ __forceinline__ float sum32(float v) {
-  v = reduce_row16(v);
-  return v + __shfl_xor(v, 16, 64);
-}
-
-__device__ __forceinline__ uint32_t pack_f16x2(float a, float b) {
-  return (uint32_t)f32_to_f16_bits(a) | ((uint32_t)f32_to_f16_bits(b) << 16);
-}
-
-__device__ __forceinline__ _Float16 as_half(uint16_t b) { return __builtin_bit_cast(_Float16, b); }
-
-// rms_norm of a 1024-vector (qwen3_full.mlir:134-165) for the 64 columns
-// col(m, j) of this lane: the 16 lanes of a DPP row together hold all 1024
-// columns, so their partial sums of squares meet in a row reduction.
-template <class ColOf>
-__device__ __forceinline__ void rmsnorm_cols(const uint16_t* __restrict__ h,
-                                             const uint16_t* __restrict__ w, ColOf col,
-                                             u32x4 (&xr)[8]) {
-  u32x4 hv[8], wv[8];
-#pragma unroll
-  for (int m = 0; m < 8; ++m) {
-    hv[m] = load_global(reinterpret_cast<const u32x4*>(h + col(m)));
-    wv[m] = load_global(reinterpret_cast<const u32x4*>(w + col(m)));
-  }
-  float ss = 0.0f;
-#pragma unroll
-  for (int m = 0; m < 8; ++m) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const f16x2 hp = as_f16x2(hv[m][j]);
-      const float a = (float)hp.x, b = (float)hp.y;
-      ss = ss + a * a;
-      ss = ss + b * b;
-    }
-  }
-  ss = reduce_row16(ss);
-  const float inv = 1.0f / sqrtf(ss / 1024.0f + kEps);
-#pragma unroll
-  for (int m = 0; m < 8; ++m) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const f16x2 hp = as_f16x2(hv[m][j]), wp = as_f16x2(wv[m][j]);
-      const float a = ((float)hp.x * inv) * (float)wp.x;
-      const float b = ((float)hp.y * inv) * (float)wp.y;
-      xr[m][j] = pack_f16x2(a, b);
-    }
-  }
-}
-
-// The Q8_0 GEMV lane layout: columns [64 p16, 64 p16 + 64) in 8 pieces of 8.
-__device__ __forceinline__ void rmsnorm_gemv_x(const uint16_t* __restrict__ h,
-                                               const uint16_t* __restrict__ w, u32x4 (&xr)[8]) {
-  const int p16 = threadIdx.x & 15;
-  rmsnorm_cols(h, w, [=](int m) { return 64 * p16 + 8 * m; }, xr);
-}
-
-// SwiGLU of qwen3_full.mlir:829-839, every op in f16: e = exp(-g),
-// den = 1 + e, sig = 1 / den, silu = g * sig, out = silu * up (exp and the
-// reciprocal evaluated in f32 and rounded once).
-__device__ __forceinline__ uint16_t swiglu_f16(float gate_acc, float up_acc) {
-  const _Float16 g = (_Float16)gate_acc;
-  const _Float16 u = (_Float16)up_acc;
-  const _Float16 e = (_Float16)expf(-(float)g);
-  const _Float16 den = (_Float16)1.0f + e;
-  const _Float16 sig = (_Float16)(1.0f / (float)den);
-  const _Float16 silu = g * sig;
-  return __builtin_bit_cast(uint16_t, (_Float16)(silu * u));
-}
-
-}  // namespace
+#include "decode_device.h"
 
 // ------------------------------------------------------------- kernels ----
 
@@ -165,252 +66,41 @@ extern "C" __global__ __launch_bounds__(64) void dec_qkv(
   q8_quad_core<1>(
       w, n, quad, lds,
       [&](u32x4 (&xr)[1][8]) {
-        rmsnorm_gemv_x(h, norm_w, xr[0]);
+        rmsnorm_gemv_x<false>(h, norm_w, xr[0]);
         store_gemv_x(xr[0], xn);
       },
       [&](int row, float acc) { y[row] = f32_to_f16_bits(acc); });
 }
 
-// Attention for kv head g = block / 8 and split group sg = block % 8: four
-// waves, wave w taking position split s = 4 sg + w of the 32 equal splits of
-// ctx = pos + 1; the four results merge in LDS into one partial per query
-// head and group (the attn_o kernel merges the 8 groups).  Per wave:
-//  0. the split's first 32 cache rows (K: half a row per lane, V: the lane's
-//     two dims for each of the 32 positions) are requested before anything
-//     else, so their latency overlaps steps 1-2;
-//  1. q heads 2g, 2g+1 and k head g: per-head rms_norm with q_norm / k_norm
-//     (qwen3_full.mlir:648-702), then RoPE (:324-454) at position pos;
-//  2. the wave owning position pos writes the roped k and the raw v to cache
-//     slot pos (layer base passed in; slot layout [max_seq, 8, 128]); split 0
-//     stores the roped q heads (f16) to q_roped;
-//  3. chunks of 32 positions: lane (j, half) scores position j of the chunk
-//     on dims [64*half, 64*half + 64) for both q heads, the halves meet in one
-//     cross-half add; s_j = (q . k_j) * rsqrt(128); online softmax; the
-//     weighted sum of v (each lane owns dims 2*lane, 2*lane+1 of both heads).
-//     The chunk count is uniform over the workgroup (splits differ by at most
-//     one position), so every wave meets every barrier;
-//  4. partial (m, l, acc[128]) per query head -> part[head][sg]: m = max over
-//     the 4 waves, l and acc rescaled by exp(m_w - m).  An empty split (ctx <
-//     32) contributes m = -inf, l = 0, acc = 0.
+// Attention for kv head g = block / 8 and split group sg = block % 8 (see
+// attention_group): q/k/v from global memory, the partial (m, l, acc[128]) of
+// each query head to part[head][sg] (the attn_o kernel merges the 8 groups).
 extern "C" __global__ __launch_bounds__(256) void dec_attention(
     const uint16_t* __restrict__ q_raw, const uint16_t* __restrict__ k_raw,
     const uint16_t* __restrict__ v_raw, const uint16_t* __restrict__ qn_w,
     const uint16_t* __restrict__ kn_w, const int32_t* __restrict__ pos_ptr, int max_seq,
     uint16_t* __restrict__ k_cache, uint16_t* __restrict__ v_cache, float* __restrict__ part,
     uint16_t* __restrict__ q_roped) {
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  __shared__ AttnLds lds;
   const int g = blockIdx.x / kAttnGroups;
   const int sg = blockIdx.x % kAttnGroups;
-  const int s = sg * kAttnWaves + wave;
-  const int half = lane >> 5;
-  const int pl = lane & 31;
-
-  // ---- inputs that do not depend on the position ----
-  const uint16_t* src[3] = {q_raw + (2 * g) * kHeadDim, q_raw + (2 * g + 1) * kHeadDim,
-                            k_raw + g * kHeadDim};
-  uint32_t xw[3], nwv[3];
-#pragma unroll
-  for (int t = 0; t < 3; ++t) xw[t] = load_global(reinterpret_cast<const uint32_t*>(src[t]) + lane);
-  nwv[0] = load_global(reinterpret_cast<const uint32_t*>(qn_w) + lane);
-  nwv[2] = load_global(reinterpret_cast<const uint32_t*>(kn_w) + lane);
-  nwv[1] = nwv[0];
-  const uint32_t v_new = load_global(reinterpret_cast<const uint32_t*>(v_raw + g * kHeadDim) + lane);
-  __builtin_amdgcn_sched_barrier(0);  // keep these loads ahead of the position-dependent ones
-
-  int pos = *pos_ptr;
-  pos = pos < 0 ? 0 : (pos >= max_seq ? max_seq - 1 : pos);
-  const int ctx = pos + 1;
-  const int start = (int)((int64_t)s * ctx / kAttnSplits);
-  const int end = (int)((int64_t)(s + 1) * ctx / kAttnSplits);
-  const int n_chunks = ((ctx + kAttnSplits - 1) / kAttnSplits + 31) / 32;  // workgroup-uniform
-
-  // ---- 0. first chunk of the cache ----
-  // Every lane issues every load (rows clamped into [start, end - 1], row 0
-  // for an empty split) so the compiler's waits stay exact.
-  const int last = end - 1 > 0 ? end - 1 : 0;
-  u32x4 kreg[8];
-  uint32_t vreg[32];
-  auto load_chunk = [&](int c0) {
-    const int p = c0 + pl < last ? c0 + pl : last;
-    const u32x4* krow = reinterpret_cast<const u32x4*>(
-        k_cache + ((size_t)p * kKvHeads + g) * kHeadDim + 64 * half);
-#pragma unroll
-    for (int m = 0; m < 8; ++m) kreg[m] = load_global(krow + m);
-#pragma unroll
-    for (int j = 0; j < 32; ++j) {
-      const int pj = c0 + j < last ? c0 + j : last;
-      vreg[j] = load_global(
-          reinterpret_cast<const uint32_t*>(v_cache + ((size_t)pj * kKvHeads + g) * kHeadDim) + lane);
-    }
-  };
-  load_chunk(start);
-  __builtin_amdgcn_sched_barrier(0);
-
-  __shared__ float xs[kAttnWaves][3][kHeadDim];  // normed q_A, q_B, k (f16 values)
-  __shared__ uint32_t qh[kAttnWaves][2][64];     // roped q_A, q_B as f16 pairs
-  __shared__ uint32_t kh[kAttnWaves][64];        // roped new k as f16 pairs
-  __shared__ float pbuf[kAttnWaves][2][32];
-  __shared__ float mrg[kAttnWaves][2][2 + kHeadDim];
-
-  // ---- 1. head norms: lane owns dims 2*lane, 2*lane+1 ----
-#pragma unroll
-  for (int t = 0; t < 3; ++t) {
-    const f16x2 xv = as_f16x2(xw[t]);
-    const f16x2 wv = as_f16x2(nwv[t]);
-    const float a = (float)xv.x, b = (float)xv.y;
-    float ss = a * a;
-    ss = ss + b * b;
-    ss = wave_sum(ss);
-    const float r = sqrtf(ss / 128.0f + kEps);
-    xs[wave][t][2 * lane] = (float)(_Float16)((a / r) * (float)wv.x);
-    xs[wave][t][2 * lane + 1] = (float)(_Float16)((b / r) * (float)wv.y);
-  }
-  __syncthreads();
-
-  // ---- 1b. RoPE (rotate-half) ----
-  const float posf = (float)pos;
-  float cs[2], sn[2];
-#pragma unroll
-  for (int dd = 0; dd < 2; ++dd) {
-    const int d = 2 * lane + dd;
-    const int i = d < 64 ? d : d - 64;
-    const float e = -((2.0f * (float)i) / 128.0f);
-    const float th = posf * (powf(kRopeBase, e) * 1.0f);
-    cs[dd] = cosf(th);
-    sn[dd] = sinf(th);
-  }
-  uint32_t roped[3];
-#pragma unroll
-  for (int t = 0; t < 3; ++t) {
-    float r2[2];
-#pragma unroll
-    for (int dd = 0; dd < 2; ++dd) {
-      const int d = 2 * lane + dd;
-      if (d < 64) {
-        const float a = xs[wave][t][d] * cs[dd];
-        const float b = xs[wave][t][d + 64] * sn[dd];
-        r2[dd] = a - b;
-      } else {
-        const float a = xs[wave][t][d - 64] * sn[dd];
-        const float b = xs[wave][t][d] * cs[dd];
-        r2[dd] = a + b;
-      }
-    }
-    roped[t] = pack_f16x2(r2[0], r2[1]);
-  }
-  qh[wave][0][lane] = roped[0];
-  qh[wave][1][lane] = roped[1];
-  kh[wave][lane] = roped[2];
-
-  // ---- 2. the new position into the cache, the roped q heads once ----
-  if (s == 0) {
-    reinterpret_cast<uint32_t*>(q_roped + (2 * g) * kHeadDim)[lane] = roped[0];
-    reinterpret_cast<uint32_t*>(q_roped + (2 * g + 1) * kHeadDim)[lane] = roped[1];
-  }
-  if (start <= pos && pos < end) {
-    reinterpret_cast<uint32_t*>(k_cache + ((size_t)pos * kKvHeads + g) * kHeadDim)[lane] = roped[2];
-    reinterpret_cast<uint32_t*>(v_cache + ((size_t)pos * kKvHeads + g) * kHeadDim)[lane] = v_new;
-  }
-  __syncthreads();
-
-  // ---- 3. scores, online softmax, weighted v ----
-  float m = -__builtin_inff(), l = 0.0f;  // per q head; identical in all lanes
-  float mB = -__builtin_inff(), lB = 0.0f;
-  float accA0 = 0.0f, accA1 = 0.0f, accB0 = 0.0f, accB1 = 0.0f;
-  for (int c = 0; c < n_chunks; ++c) {
-    const int c0 = start + 32 * c;
-    const int p = c0 + pl;
-    const bool valid = p < end;
-    // the row of position pos is this step's k (in LDS; the cache slot was
-    // requested before it was written)
-    const bool is_new = p == pos;
-    float dA = 0.0f, dB = 0.0f;
-#pragma unroll
-    for (int mm = 0; mm < 8; ++mm) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int i = 32 * half + 4 * mm + j;
-        const f16x2 kv = as_f16x2(is_new ? kh[wave][i] : kreg[mm][j]);
-        dA = __builtin_amdgcn_fdot2(as_f16x2(qh[wave][0][i]), kv, dA, false);
-        dB = __builtin_amdgcn_fdot2(as_f16x2(qh[wave][1][i]), kv, dB, false);
-      }
-    }
-    dA = dA + __shfl_xor(dA, 32, 64);
-    dB = dB + __shfl_xor(dB, 32, 64);
-    const float sA = valid ? dA * kAttnScale : -__builtin_inff();
-    const float sB = valid ? dB * kAttnScale : -__builtin_inff();
-    const float mnA = fmaxf(m, max32(sA));
-    const float mnB = fmaxf(mB, max32(sB));
-    // mn = -inf only while the split has seen no valid position (acc, l = 0)
-    const float cA = mnA == -__builtin_inff() ? 1.0f : expf(m - mnA);
-    const float cB = mnB == -__builtin_inff() ? 1.0f : expf(mB - mnB);
-    const float pA = valid ? expf(sA - mnA) : 0.0f;
-    const float pB = valid ? expf(sB - mnB) : 0.0f;
-    l = l * cA + sum32(pA);
-    lB = lB * cB + sum32(pB);
-    m = mnA;
-    mB = mnB;
-    if (half == 0) {
-      pbuf[wave][0][pl] = pA;
-      pbuf[wave][1][pl] = pB;
-    }
-    __syncthreads();
-    accA0 *= cA;
-    accA1 *= cA;
-    accB0 *= cB;
-    accB1 *= cB;
-    const int n = end - c0 < 32 ? end - c0 : 32;
-#pragma unroll
-    for (int j = 0; j < 32; ++j) {
-      // positions past the split hold weight 0 and a clamped (valid) row,
-      // selected to 0 so a non-finite value there cannot leak in
-      const uint32_t vw = c0 + j == pos ? v_new : (j < n ? vreg[j] : 0u);
-      const f16x2 vv = as_f16x2(vw);
-      const float v0 = (float)vv.x, v1 = (float)vv.y;
-      const float wa = pbuf[wave][0][j], wb = pbuf[wave][1][j];
-      accA0 = accA0 + wa * v0;
-      accA1 = accA1 + wa * v1;
-      accB0 = accB0 + wb * v0;
-      accB1 = accB1 + wb * v1;
-    }
-    __syncthreads();
-    if (c + 1 < n_chunks) load_chunk(c0 + 32);
-  }
-
-  // ---- 4. the four waves' results -> one partial per query head ----
-  if (lane == 0) {
-    mrg[wave][0][0] = m;
-    mrg[wave][0][1] = l;
-    mrg[wave][1][0] = mB;
-    mrg[wave][1][1] = lB;
-  }
-  mrg[wave][0][2 + 2 * lane] = accA0;
-  mrg[wave][0][3 + 2 * lane] = accA1;
-  mrg[wave][1][2 + 2 * lane] = accB0;
-  mrg[wave][1][3 + 2 * lane] = accB1;
-  __syncthreads();
-  if (wave < 2) {  // wave hh merges query head 2g + hh
-    const int hh = wave;
-    float M = -__builtin_inff();
-#pragma unroll
-    for (int w = 0; w < kAttnWaves; ++w) M = fmaxf(M, mrg[w][hh][0]);
-    float L = 0.0f, a0 = 0.0f, a1 = 0.0f;
-#pragma unroll
-    for (int w = 0; w < kAttnWaves; ++w) {
-      const float mw = mrg[w][hh][0];
-      const float ww = mw == -__builtin_inff() ? 0.0f : expf(mw - M);
-      L = L + mrg[w][hh][1] * ww;
-      a0 = a0 + mrg[w][hh][2 + 2 * lane] * ww;
-      a1 = a1 + mrg[w][hh][3 + 2 * lane] * ww;
-    }
-    float* dst = part + ((size_t)(2 * g + hh) * kAttnGroups + sg) * kPartStride;
-    if (lane == 0) {
-      dst[0] = M;
-      dst[1] = L;
-    }
-    reinterpret_cast<float2*>(dst + 4)[lane] = float2{a0, a1};
-  }
+  const int lane = threadIdx.x & 63;
+  attention_group(
+      lds, g, sg, *pos_ptr, max_seq, qn_w, kn_w, k_cache, v_cache, q_roped,
+      [&](uint32_t (&xw)[3], uint32_t& v_new) {
+        xw[0] = load_global(reinterpret_cast<const uint32_t*>(q_raw + (2 * g) * kHeadDim) + lane);
+        xw[1] = load_global(reinterpret_cast<const uint32_t*>(q_raw + (2 * g + 1) * kHeadDim) + lane);
+        xw[2] = load_global(reinterpret_cast<const uint32_t*>(k_raw + g * kHeadDim) + lane);
+        v_new = load_global(reinterpret_cast<const uint32_t*>(v_raw + g * kHeadDim) + lane);
+      },
+      [&](int hh, float M, float L, float a0, float a1) {
+        float* dst = part + ((size_t)(2 * g + hh) * kAttnGroups + sg) * kPartStride;
+        if (lane == 0) {
+          dst[0] = M;
+          dst[1] = L;
+        }
+        reinterpret_cast<float2*>(dst + 4)[lane] = float2{a0, a1};
+      });
 }
 
 // attn = the merged attention output: head h, dim d =
@@ -449,41 +139,34 @@ extern "C" __global__ __launch_bounds__(256) void dec_o_res(const uint8_t* __res
           av[gi][0] = load_global(reinterpret_cast<const u32x4*>(pg + 4 + d0));
           av[gi][1] = load_global(reinterpret_cast<const u32x4*>(pg + 4 + d0) + 1);
         }
-        float M = -__builtin_inff();
-#pragma unroll
-        for (int gi = 0; gi < kAttnGroups; ++gi) M = fmaxf(M, ml[gi].x);
-        float wg[kAttnGroups], L = 0.0f;
+        float mg[kAttnGroups], lg[kAttnGroups], wg[kAttnGroups], L;
 #pragma unroll
         for (int gi = 0; gi < kAttnGroups; ++gi) {
-          wg[gi] = ml[gi].x == -__builtin_inff() ? 0.0f : expf(ml[gi].x - M);
-          L = L + ml[gi].y * wg[gi];
+          mg[gi] = ml[gi].x;
+          lg[gi] = ml[gi].y;
         }
-        float a[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+        merge_weights(mg, lg, wg, L);
+        float a[8];
 #pragma unroll
-        for (int gi = 0; gi < kAttnGroups; ++gi) {
+        for (int e = 0; e < 8; ++e) {
+          // copy the elements out first: __builtin_bit_cast of a vector
+          // element lvalue reads element 0 with this compiler
+          float accg[kAttnGroups];
 #pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            // copy the element out first: __builtin_bit_cast of a vector
-            // element lvalue reads element 0 with this compiler
+          for (int gi = 0; gi < kAttnGroups; ++gi) {
             const uint32_t bits = av[gi][e >> 2][e & 3];
-            a[e] = a[e] + __builtin_bit_cast(float, bits) * wg[gi];
+            accg[gi] = __builtin_bit_cast(float, bits);
           }
+          a[e] = merge_dim(accg, wg);
         }
         const u32x4 packed = {pack_f16x2(a[0] / L, a[1] / L), pack_f16x2(a[2] / L, a[3] / L),
                               pack_f16x2(a[4] / L, a[5] / L), pack_f16x2(a[6] / L, a[7] / L)};
         reinterpret_cast<u32x4*>(attn)[t] = packed;
         if (blockIdx.x == 0) reinterpret_cast<u32x4*>(attn_out)[t] = packed;
         __syncthreads();
-        // x for this lane's GEMV columns, from the merged vector in LDS
-        const int p16 = t & 15;
-#pragma unroll
-        for (int c = 0; c < 2; ++c) {
-          const u32x4* xs4 = reinterpret_cast<const u32x4*>(attn + 1024 * c + 64 * p16);
-#pragma unroll
-          for (int m8 = 0; m8 < 8; ++m8) xr[c][m8] = xs4[m8];
-        }
+        lds_x_cols<2>(attn, xr);  // x from the merged vector in LDS
       });
-  res[row] = __builtin_bit_cast(uint16_t, (_Float16)(h_row + (_Float16)acc));
+  res[row] = residual_f16(h_row, acc);
 }
 
 // act[i] = swiglu(gate_i, up_i) with [gate; up] = W_gu[layer] . rms_norm(res,
@@ -502,7 +185,7 @@ extern "C" __global__ __launch_bounds__(64) void dec_gu_swiglu(const uint8_t* __
   q8_quad_load<1>(wgu, 2 * kFfn, b, bg);
   q8_quad_load<1>(wgu, 2 * kFfn, kFfn / 4 + b, bu);
   u32x4 xr[1][8];
-  rmsnorm_gemv_x(res, norm_w, xr[0]);
+  rmsnorm_gemv_x<false>(res, norm_w, xr[0]);
   store_gemv_x(xr[0], xn);
   q8_quad_stage<1>(bg, lds);
   q8_quad_stage<1>(bu, lds + LDSB);
@@ -524,7 +207,7 @@ extern "C" __global__ __launch_bounds__(64) void dec_down_res(const uint8_t* __r
   const _Float16 r_row = as_half(load_global_u16(res + row));
   const float acc = q8_quad_core_acc<3>(
       wdn, kHidden, blockIdx.x, lds, [&](u32x4 (&xr)[3][8]) { load_x_cols<3>(act, xr); });
-  h_out[row] = __builtin_bit_cast(uint16_t, (_Float16)(r_row + (_Float16)acc));
+  h_out[row] = residual_f16(r_row, acc);
 }
 
 // logits = W_out . rms_norm(h, output_norm) (qwen3_full.mlir:1456-1467) with
@@ -536,7 +219,7 @@ extern "C" __global__ __launch_bounds__(256) void dec_vocab_argmax(
   vocab_body_x<VOCAB_NT_LOADS != 0, true>(
       W,
       [&](int li, u32x4 (&xr)[8]) {
-        rmsnorm_cols(h, norm_w, [=](int m) { return 128 * m + 8 * li; }, xr);
+        rmsnorm_cols<false>(h, norm_w, [=](int m) { return 128 * m + 8 * li; }, xr);
         if (blockIdx.x == 0 && threadIdx.x < 16) {
 #pragma unroll
           for (int m = 0; m < 8; ++m)
@@ -575,5 +258,413 @@ extern "C" __global__ void dec_advance(int32_t* __restrict__ pos, int max_seq,
     const int p = *pos;
     if (p + 1 < max_seq) *pos = p + 1;
     else *status |= 1u;
+  }
+}
+
+// Zeroes n words of a decode scratch (graph-capture safe: a kernel).
+extern "C" __global__ __launch_bounds__(256) void dec_scratch_clear(uint32_t* __restrict__ p,
+                                                                   uint32_t n) {
+  for (uint32_t i = blockIdx.x * 256u + threadIdx.x; i < n; i += gridDim.x * 256u) p[i] = 0u;
+}
+
+// ======================================================= single launch ====
+//
+// dec_step: the whole decode step in one launch of kStepWgs workgroups x 256
+// threads, all resident at once (cooperative launch).  Work moves between
+// workgroups as tagged words: a 64-bit word holds 32 bits of data (an f16 pair
+// or an f32) and a 32-bit tag naming (step, layer, phase); a producer stores
+// the word with one agent-scope atomic store, a consumer polls it with
+// agent-scope atomic loads until the tag matches.  A word is its own flag, so
+// no fence, counter or barrier is needed between workgroups, and a consumer
+// requests the weights of its next phase before it starts waiting.
+//
+// Per layer (workgroup ranges; 4 waves each):
+//   A  all 256        qkv quads 4 wg + w: rms_norm(h) (h = the embedding row
+//                     for layer 0, else the previous layer's H words), GEMV,
+//                     rows published in pairs -> Q, K, V words
+//   B  0..63          attention for kv head wg / 8, split group wg % 8
+//                     (attention_group, q/k/v from the tagged words) -> PART
+//   B' 0,8,..,56      the split-group-0 workgroup of each kv head merges the
+//                     8 partials of its 2 query heads -> ATT words
+//   C  64..127        attn_o quads + residual -> RES words
+//   D  0..63,128..255 gate/up quad pairs + SwiGLU -> ACT words
+//   E  64..127        ffn_down quads + residual -> H words
+// then the vocab GEMV over all workgroups (each publishes its best key as two
+// words), and workgroup 0 reduces the 256 keys: token, optional output slot,
+// position advance, sequence number.  Layer-indexed words alternate between
+// two buffers by layer parity.  Every wait is bounded: on timeout a workgroup
+// sets status bit 1 and an abort word, and every waiting workgroup gives up.
+namespace {
+
+constexpr int kStepWgs = 256;
+// tagged-word map (u64 words) per layer parity
+constexpr int kWH = 0;                                     // 512: h (E output)
+constexpr int kWQ = kWH + 512;                             // 1024: q row pairs
+constexpr int kWK = kWQ + 1024;                            // 512
+constexpr int kWV = kWK + 512;                             // 512
+constexpr int kWPart = kWV + 512;                          // 16 x 8 x 130
+constexpr int kWAtt = kWPart + kQHeads * kAttnGroups * 130;  // 1024
+constexpr int kWRes = kWAtt + 1024;                        // 512
+constexpr int kWAct = kWRes + 512;                         // 1536
+constexpr int kWParity = kWAct + 1536;
+constexpr int kWArg = 2 * kWParity;                        // 2 per workgroup
+constexpr int kWTotal = kWArg + 2 * kStepWgs;
+// phases in a tag
+constexpr int kPhQKV = 0, kPhPart = 1, kPhAtt = 2, kPhRes = 3, kPhAct = 4, kPhH = 5, kPhArg = 6;
+constexpr uint32_t kSpinLimit = 1u << 20;
+
+struct StepParams {
+  const uint16_t* token_embd;
+  const uint16_t* attn_norm;
+  const uint16_t* ffn_norm;
+  const uint16_t* q_norm;
+  const uint16_t* k_norm;
+  const uint8_t* wq;
+  const uint8_t* wk;
+  const uint8_t* wv;
+  const uint8_t* wo;
+  const uint8_t* wgu;
+  const uint8_t* wdn;
+  const uint16_t* output_norm;
+  const uint16_t* output_w;
+  uint16_t* k_cache;
+  uint16_t* v_cache;
+  const int32_t* token_in;  // input token (device)
+  int32_t* token_out;       // argmax written here (head only)
+  int32_t* pos;
+  uint16_t* logits;         // may be null
+  int32_t* out;             // extra copy of the token, may be null
+  uint64_t* words;          // kWTotal tagged words
+  uint32_t* seq;            // step sequence number (persists across launches)
+  uint32_t* abort_word;
+  uint32_t* status;
+  uint16_t* on_out;         // the final rms_norm(h, output_norm) (f16[1024])
+  int max_seq;
+  int advance;
+  int head;                 // 0: no vocab / argmax (a prompt step); pos still advances
+  int pad;
+};
+
+__device__ __forceinline__ uint32_t step_tag(uint32_t seq, int layer, int phase) {
+  return (seq << 8) | (uint32_t)(1 + (layer + 1) * 8 + phase);
+}
+
+__device__ __forceinline__ void put_word(uint64_t* p, uint32_t data, uint32_t tag) {
+  __hip_atomic_store(p, ((uint64_t)tag << 32) | data, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ uint64_t get_word(const uint64_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+struct Waiter {
+  uint32_t* abort_word;
+  uint32_t* status;
+  uint32_t seq;
+  int* s_abort;  // LDS flag of the workgroup
+
+  // Every thread of the workgroup calls this with the same arguments: words
+  // [0, n) of src with tag `tag` land (their data halves) in dst[0, n).
+  // Returns false (in every thread) when the step was aborted.
+  __device__ __forceinline__ bool wait(const uint64_t* __restrict__ src, int n, uint32_t tag,
+                                       uint32_t* __restrict__ dst) const {
+    bool ok = true;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+      uint64_t w = get_word(src + i);
+      uint32_t spins = 0;
+      while ((uint32_t)(w >> 32) != tag) {
+        ++spins;
+        if ((spins & 31u) == 0u &&
+            __hip_atomic_load(abort_word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == seq) {
+          ok = false;
+          break;
+        }
+        if (spins > kSpinLimit) {
+          __hip_atomic_fetch_or(status, 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          __hip_atomic_store(abort_word, seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          ok = false;
+          break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+        w = get_word(src + i);
+      }
+      if (!ok) break;
+      dst[i] = (uint32_t)w;
+    }
+    if (!ok) *s_abort = 1;
+    __syncthreads();
+    return *s_abort == 0;
+  }
+};
+
+// Row sums of a quad (rows q4, q4+1, q4+2, q4+3; row r's sum in lanes
+// 16(r - q4)..) published as two f16-pair words: word q4/2 by lane 0, q4/2 + 1
+// by lane 32.  f(acc) maps a row sum to its f16 bits.
+template <class F>
+__device__ __forceinline__ void put_quad(uint64_t* __restrict__ words, int quad, float acc,
+                                         uint32_t tag, F f) {
+  const int lane = threadIdx.x & 63;
+  const uint32_t mine = f(acc, 4 * quad + (lane >> 4));
+  const uint32_t next = __shfl(mine, (lane + 16) & 63, 64);
+  if (lane == 0 || lane == 32)
+    put_word(words + 2 * quad + (lane >> 5), mine | (next << 16), tag);
+}
+
+// u64 max over the 64 lanes of a wave.
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const uint32_t lo = __shfl_xor((uint32_t)v, d, 64);
+    const uint32_t hi = __shfl_xor((uint32_t)(v >> 32), d, 64);
+    const uint64_t o = ((uint64_t)hi << 32) | lo;
+    v = o > v ? o : v;
+  }
+  return v;
+}
+
+constexpr int kGemvLds = QuadShape<3>::LDS_BYTES;  // the largest per-wave staging
+constexpr int kVecWords = 2 * kAttnGroups * 130;     // 2080: the largest polled vector
+constexpr int kStepLds = 4 * kVecWords + 4 * kGemvLds;
+
+}  // namespace
+
+extern "C" __global__ __launch_bounds__(256) void dec_step(StepParams P) {
+  __shared__ __attribute__((aligned(16))) uint8_t smem[kStepLds];
+  __shared__ int s_abort;
+  uint32_t* vec = reinterpret_cast<uint32_t*>(smem);               // polled words' data
+  uint8_t* stage = smem + 4 * kVecWords;                            // GEMV staging / attention
+  const int wg = blockIdx.x;
+  const int t = threadIdx.x;
+  const int wave = t >> 6;
+  const int lane = t & 63;
+  if (t == 0) s_abort = 0;
+
+  const uint32_t seq = __hip_atomic_load(P.seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
+  const int pos_raw = *P.pos;
+  int tok = *P.token_in;
+  tok = (tok < 0 || tok >= kVocab) ? 0 : tok;
+  const uint16_t* emb = P.token_embd + (size_t)tok * kHidden;
+  const Waiter W{P.abort_word, P.status, seq, &s_abort};
+  __syncthreads();
+
+  for (int layer = 0; layer < kLayers; ++layer) {
+    uint64_t* cur = P.words + (layer & 1) * kWParity;
+    const uint64_t* prev = P.words + ((layer & 1) ^ 1) * kWParity;
+    const uint32_t tag_prev_h = step_tag(seq, layer - 1, kPhH);
+
+    // ---- A: q/k/v ----
+    {
+      const int quad = 4 * wg + wave;  // 0..1023
+      const uint8_t* w = quad < 512 ? P.wq : (quad < 768 ? P.wk : P.wv);
+      const int n = quad < 512 ? 2048 : 1024;
+      const int qd = quad < 512 ? quad : (quad < 768 ? quad - 512 : quad - 768);
+      const int64_t bpl = (int64_t)n * (kHidden / 32 * 34);
+      u32x4 buf[QuadShape<1>::LOADS];
+      q8_quad_load<1>(w + layer * bpl, n, qd, buf);
+      u32x4 xr[1][8];
+      const uint16_t* an = P.attn_norm + layer * kHidden;
+      if (layer == 0) {
+        rmsnorm_gemv_x<false>(emb, an, xr[0]);
+      } else {
+        if (!W.wait(prev + kWH, 512, tag_prev_h, vec)) return;
+        rmsnorm_gemv_x<true>(reinterpret_cast<const uint16_t*>(vec), an, xr[0]);
+      }
+      uint8_t* lds = stage + wave * kGemvLds;
+      q8_quad_stage<1>(buf, lds);
+      __syncthreads();
+      const float acc = q8_quad_dot<1>(lds, xr);
+      uint64_t* dst = quad < 512 ? cur + kWQ : (quad < 768 ? cur + kWK : cur + kWV);
+      put_quad(dst, qd, acc, step_tag(seq, layer, kPhQKV),
+               [](float a, int) { return (uint32_t)f32_to_f16_bits(a); });
+    }
+
+    // ---- B: attention, B': merge ----
+    if (wg < 64) {
+      const int g = wg / kAttnGroups;
+      const int sg = wg % kAttnGroups;
+      const int64_t cache_layer = (int64_t)layer * P.max_seq * (kKvHeads * kHeadDim);
+      AttnLds& L = *reinterpret_cast<AttnLds*>(stage);
+      bool ok = true;
+      const uint32_t tq = step_tag(seq, layer, kPhQKV);
+      attention_group(
+          L, g, sg, pos_raw, P.max_seq, P.q_norm + layer * kHeadDim, P.k_norm + layer * kHeadDim,
+          P.k_cache + cache_layer, P.v_cache + cache_layer, nullptr,
+          [&](uint32_t (&xw)[3], uint32_t& v_new) {
+            // q heads 2g, 2g+1 (words 128g..), k head g, v head g (words 64g..)
+            ok = W.wait(cur + kWQ + 128 * g, 128, tq, vec) &&
+                 W.wait(cur + kWK + 64 * g, 64, tq, vec + 128) &&
+                 W.wait(cur + kWV + 64 * g, 64, tq, vec + 192);
+            xw[0] = vec[lane];
+            xw[1] = vec[64 + lane];
+            xw[2] = vec[128 + lane];
+            v_new = vec[192 + lane];
+          },
+          [&](int hh, float M, float Ls, float a0, float a1) {
+            uint64_t* dst = cur + kWPart + ((2 * g + hh) * kAttnGroups + sg) * 130;
+            const uint32_t tp = step_tag(seq, layer, kPhPart);
+            if (lane == 0) {
+              put_word(dst, __builtin_bit_cast(uint32_t, M), tp);
+              put_word(dst + 1, __builtin_bit_cast(uint32_t, Ls), tp);
+            }
+            put_word(dst + 2 + 2 * lane, __builtin_bit_cast(uint32_t, a0), tp);
+            put_word(dst + 3 + 2 * lane, __builtin_bit_cast(uint32_t, a1), tp);
+          });
+      if (!ok) return;
+      if (sg == 0) {
+        // the 8 groups' partials of query heads 2g, 2g+1 (contiguous words)
+        if (!W.wait(cur + kWPart + 2 * g * kAttnGroups * 130, 2 * kAttnGroups * 130,
+                    step_tag(seq, layer, kPhPart), vec))
+          return;
+        if (wave < 2) {
+          const int hh = wave;
+          const float* pv = reinterpret_cast<const float*>(vec) + hh * kAttnGroups * 130;
+          float mg[kAttnGroups], lg[kAttnGroups], wgt[kAttnGroups], Ls;
+#pragma unroll
+          for (int gi = 0; gi < kAttnGroups; ++gi) {
+            mg[gi] = pv[gi * 130];
+            lg[gi] = pv[gi * 130 + 1];
+          }
+          merge_weights(mg, lg, wgt, Ls);
+          float a[2];
+#pragma unroll
+          for (int e = 0; e < 2; ++e) {
+            float accg[kAttnGroups];
+#pragma unroll
+            for (int gi = 0; gi < kAttnGroups; ++gi) accg[gi] = pv[gi * 130 + 2 + 2 * lane + e];
+            a[e] = merge_dim(accg, wgt);
+          }
+          put_word(cur + kWAtt + (2 * g + hh) * 64 + lane, pack_f16x2(a[0] / Ls, a[1] / Ls),
+                   step_tag(seq, layer, kPhAtt));
+        }
+        __syncthreads();  // vec is reused by the next wait
+      }
+    }
+
+    // ---- C: attn_o + residual ----
+    if (wg >= 64 && wg < 128) {
+      const int quad = 4 * (wg - 64) + wave;  // 0..255
+      constexpr int64_t bpl = (int64_t)kHidden * (2 * kHidden / 32 * 34);
+      u32x4 buf[QuadShape<2>::LOADS];
+      q8_quad_load<2>(P.wo + layer * bpl, kHidden, quad, buf);
+      const int row = 4 * quad + (lane >> 4);
+      _Float16 h_row;
+      if (layer == 0) {
+        h_row = as_half(load_global_u16(emb + row));
+      } else {
+        // this workgroup's 16 residual rows = h words [8 (wg - 64), +8)
+        if (!W.wait(prev + kWH + 8 * (wg - 64), 8, tag_prev_h, vec + 1024)) return;
+        h_row = as_half(reinterpret_cast<const uint16_t*>(vec + 1024)[row - 16 * (wg - 64)]);
+      }
+      if (!W.wait(cur + kWAtt, 1024, step_tag(seq, layer, kPhAtt), vec)) return;
+      u32x4 xr[2][8];
+      lds_x_cols<2>(reinterpret_cast<const uint16_t*>(vec), xr);
+      uint8_t* lds = stage + wave * kGemvLds;
+      q8_quad_stage<2>(buf, lds);
+      __syncthreads();
+      const float acc = q8_quad_dot<2>(lds, xr);
+      put_quad(cur + kWRes, quad, acc, step_tag(seq, layer, kPhRes),
+               [&](float a, int) { return (uint32_t)residual_f16(h_row, a); });
+    }
+
+    // ---- D: gate/up + SwiGLU ----
+    if (wg < 64 || wg >= 128) {
+      const int b = 4 * (wg < 64 ? wg : wg - 64) + wave;  // 0..767
+      constexpr int64_t bpl = (int64_t)(2 * kFfn) * (kHidden / 32 * 34);
+      const uint8_t* wl = P.wgu + layer * bpl;
+      u32x4 bg[QuadShape<1>::LOADS], bu[QuadShape<1>::LOADS];
+      q8_quad_load<1>(wl, 2 * kFfn, b, bg);
+      q8_quad_load<1>(wl, 2 * kFfn, kFfn / 4 + b, bu);
+      if (!W.wait(cur + kWRes, 512, step_tag(seq, layer, kPhRes), vec)) return;
+      u32x4 xr[1][8];
+      rmsnorm_gemv_x<true>(reinterpret_cast<const uint16_t*>(vec), P.ffn_norm + layer * kHidden,
+                           xr[0]);
+      uint8_t* lds = stage + wave * kGemvLds;
+      constexpr int LDSB = QuadShape<1>::LDS_BYTES;
+      q8_quad_stage<1>(bg, lds);
+      q8_quad_stage<1>(bu, lds + LDSB);
+      __syncthreads();
+      const float ag = q8_quad_dot<1>(lds, xr);
+      const float au = q8_quad_dot<1>(lds + LDSB, xr);
+      const uint32_t act = swiglu_f16(ag, au);
+      const uint32_t next = __shfl(act, (lane + 16) & 63, 64);
+      if (lane == 0 || lane == 32)
+        put_word(cur + kWAct + 2 * b + (lane >> 5), act | (next << 16),
+                 step_tag(seq, layer, kPhAct));
+    }
+
+    // ---- E: ffn_down + residual ----
+    if (wg >= 64 && wg < 128) {
+      const int quad = 4 * (wg - 64) + wave;
+      constexpr int64_t bpl = (int64_t)kHidden * (kFfn / 32 * 34);
+      u32x4 buf[QuadShape<3>::LOADS];
+      q8_quad_load<3>(P.wdn + layer * bpl, kHidden, quad, buf);
+      if (!W.wait(cur + kWRes + 8 * (wg - 64), 8, step_tag(seq, layer, kPhRes), vec + 1536))
+        return;
+      const int row = 4 * quad + (lane >> 4);
+      const _Float16 r_row =
+          as_half(reinterpret_cast<const uint16_t*>(vec + 1536)[row - 16 * (wg - 64)]);
+      if (!W.wait(cur + kWAct, 1536, step_tag(seq, layer, kPhAct), vec)) return;
+      u32x4 xr[3][8];
+      lds_x_cols<3>(reinterpret_cast<const uint16_t*>(vec), xr);
+      uint8_t* lds = stage + wave * kGemvLds;
+      q8_quad_stage<3>(buf, lds);
+      __syncthreads();
+      const float acc = q8_quad_dot<3>(lds, xr);
+      put_quad(cur + kWH, quad, acc, step_tag(seq, layer, kPhH),
+               [&](float a, int) { return (uint32_t)residual_f16(r_row, a); });
+    }
+  }
+
+  // ---- vocab GEMV + argmax ----
+  const uint64_t* hfin = P.words + ((kLayers - 1) & 1) * kWParity + kWH;
+  const uint32_t tag_h = step_tag(seq, kLayers - 1, kPhH);
+  const uint32_t tag_arg = step_tag(seq, kLayers, kPhArg);
+  if (P.head) {
+    bool ok = true;
+    vocab_body_xp<VOCAB_NT_LOADS != 0, true>(
+        P.output_w,
+        [&](int li, u32x4 (&xr)[8]) {
+          ok = W.wait(hfin, 512, tag_h, vec);
+          if (ok)
+            rmsnorm_cols<true>(reinterpret_cast<const uint16_t*>(vec), P.output_norm,
+                               [=](int m) { return 128 * m + 8 * li; }, xr);
+          if (wg == 0 && t < 16) {
+#pragma unroll
+            for (int m = 0; m < 8; ++m)
+              reinterpret_cast<u32x4*>(P.on_out + 128 * m + 8 * li)[0] = xr[m];
+          }
+        },
+        P.logits, kVocab, [&](uint64_t key) {
+          put_word(P.words + kWArg + 2 * wg, (uint32_t)(key >> 32), tag_arg);
+          put_word(P.words + kWArg + 2 * wg + 1, (uint32_t)key, tag_arg);
+        });
+    if (!ok) return;
+  }
+
+  // ---- workgroup 0: token, position, sequence number ----
+  if (wg != 0) return;
+  if (P.head) {
+    if (!W.wait(P.words + kWArg, 2 * kStepWgs, tag_arg, vec)) return;
+    uint64_t key = ((uint64_t)vec[2 * t] << 32) | vec[2 * t + 1];
+    key = wave_max_u64(key);
+    __shared__ uint64_t s_key[4];
+    if (lane == 0) s_key[wave] = key;
+    __syncthreads();
+    if (t == 0) {
+      uint64_t k = s_key[0];
+      for (int i = 1; i < 4; ++i) k = s_key[i] > k ? s_key[i] : k;
+      const int32_t token = k == 0 ? -1 : (int32_t)(0xffffffffu - (uint32_t)(k & 0xffffffffu));
+      *P.token_out = token;
+      if (P.out != nullptr) *P.out = token;
+    }
+  } else if (!W.wait(hfin, 512, tag_h, vec)) {  // the last layer is done
+    return;
+  }
+  if (t == 0) {
+    if (P.advance) {
+      if (pos_raw + 1 < P.max_seq) *P.pos = pos_raw + 1;
+      else __hip_atomic_fetch_or(P.status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __hip_atomic_store(P.seq, seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }

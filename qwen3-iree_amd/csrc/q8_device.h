@@ -79,8 +79,18 @@ __device__ __forceinline__ float f16_bits_to_f32(uint32_t bits16) {
   return (float)__builtin_bit_cast(_Float16, (uint16_t)bits16);
 }
 
+// f32 -> f16, RNE, of the f32 value v itself.  The empty asm makes v opaque:
+// otherwise the compiler may fold the multiply or add that produced v into a
+// mixed-precision v_fma_mix*_f16 that rounds the exact result to f16 once,
+// which differs from rounding the f32 value in rare halfway cases and differs
+// between kernels depending on where it folds.
+__device__ __forceinline__ _Float16 to_f16(float v) {
+  asm volatile("" : "+v"(v));
+  return (_Float16)v;  // v_cvt_f16_f32
+}
+
 __device__ __forceinline__ uint16_t f32_to_f16_bits(float v) {
-  return __builtin_bit_cast(uint16_t, (_Float16)v);  // v_cvt_f16_f32, RNE
+  return __builtin_bit_cast(uint16_t, to_f16(v));
 }
 
 template <int CTRL>
@@ -449,10 +459,12 @@ __device__ __forceinline__ float f16_row_dot(const u32x4& w, const u32x4& xv, fl
 // strictly-greater update keeps the first maximum; the 16 groups of a
 // workgroup are merged with argmax_better, and workgroups meet in a 64-bit
 // atomic max over argmax_key, whose order is the same rule.
-template <bool NT, bool ARGMAX, class XLoad>
-__device__ __forceinline__ void vocab_body_x(const uint16_t* __restrict__ W, XLoad&& xload,
-                                             uint16_t* __restrict__ logits, int n_rows,
-                                             uint8_t* __restrict__ ws) {
+// The workgroup's result reaches publish(key) on thread 0: key =
+// argmax_key(best) or 0 when the workgroup saw no candidate.
+template <bool NT, bool ARGMAX, class XLoad, class Publish>
+__device__ __forceinline__ void vocab_body_xp(const uint16_t* __restrict__ W, XLoad&& xload,
+                                              uint16_t* __restrict__ logits, int n_rows,
+                                              Publish&& publish) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int grp = lane >> 4;
@@ -543,11 +555,20 @@ __device__ __forceinline__ void vocab_body_x(const uint16_t* __restrict__ W, XLo
         bi = s_idx[c];
       }
     }
-    if (bi >= 0) {
-      __hip_atomic_fetch_max(reinterpret_cast<uint64_t*>(ws), argmax_key(bv, bi), __ATOMIC_RELAXED,
-                             __HIP_MEMORY_SCOPE_AGENT);
-    }
+    publish(bi >= 0 ? argmax_key(bv, bi) : (uint64_t)0);
   }
+}
+
+// Workgroups meet in one 64-bit atomic max on ws[0].
+template <bool NT, bool ARGMAX, class XLoad>
+__device__ __forceinline__ void vocab_body_x(const uint16_t* __restrict__ W, XLoad&& xload,
+                                             uint16_t* __restrict__ logits, int n_rows,
+                                             uint8_t* __restrict__ ws) {
+  vocab_body_xp<NT, ARGMAX>(W, xload, logits, n_rows, [&](uint64_t key) {
+    if (key != 0)
+      __hip_atomic_fetch_max(reinterpret_cast<uint64_t*>(ws), key, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+  });
 }
 
 // x for lane i of a row group: positions 128m + 8i .. +8, m = 0..7.

@@ -43,6 +43,7 @@ constexpr KindInfo kKinds[5] = {
 };
 
 constexpr int kVocabMaxWorkgroups = 8192;
+constexpr int kStepWorkgroups = 256;  // dec_step's fixed grid (one workgroup per CU)
 constexpr int kQ8MaxWorkgroups = 65536;
 constexpr size_t kVocabWorkspaceBytes = 256;
 constexpr int kBatchMaxCount = 1 << 20;
@@ -98,7 +99,9 @@ struct State {
   hipModule_t dec_module = nullptr;  // decode_gfx950.hsaco (optional)
   hipFunction_t dec_embed = nullptr, dec_qkv = nullptr, dec_attn = nullptr,
                 dec_o = nullptr, dec_gu = nullptr, dec_dn = nullptr, dec_vocab = nullptr,
-                dec_final = nullptr, dec_adv = nullptr;
+                dec_final = nullptr, dec_adv = nullptr, dec_clear = nullptr, dec_step = nullptr;
+  int step_single = -1;   // single-launch decode step: -1 unknown, 0 off, 1 on
+  bool step_capable = false;
   int vocab_wgs = 0;      // 0 = default
 };
 
@@ -252,7 +255,8 @@ int q8gemv_init(const char* code_object_path) {
                      {&g.dec_attn, "dec_attention"},
                      {&g.dec_o, "dec_o_res"},         {&g.dec_gu, "dec_gu_swiglu"},
                      {&g.dec_dn, "dec_down_res"},     {&g.dec_vocab, "dec_vocab_argmax"},
-                     {&g.dec_final, "dec_finalize"},  {&g.dec_adv, "dec_advance"}};
+                     {&g.dec_final, "dec_finalize"},  {&g.dec_adv, "dec_advance"},
+                     {&g.dec_clear, "dec_scratch_clear"}, {&g.dec_step, "dec_step"}};
         bool ok = true;
         for (auto& n : names) ok = ok && hipModuleGetFunction(n.fn, dm, n.name) == hipSuccess;
         if (ok) {
@@ -267,6 +271,20 @@ int q8gemv_init(const char* code_object_path) {
   int cus = 0;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
     cus = 256;
+  // The single-launch step needs its 256 workgroups resident together: a
+  // cooperative launch on a device with at least 256 CUs that fits one per CU.
+  g.step_capable = false;
+  if (g.dec_step) {
+    int coop = 0, per_cu = 0;
+    if (hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, dev) == hipSuccess &&
+        hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, g.dec_step, 256, 0) ==
+            hipSuccess)
+      g.step_capable = coop != 0 && per_cu >= 1 && (int64_t)per_cu * cus >= kStepWorkgroups;
+  }
+  // Launch per phase is the default: on MI355X it measures faster (880 vs 974
+  // us per token at context 1024) because a tagged-word hand-off between
+  // workgroups costs about as much as a kernel boundary.
+  if (g.step_single < 0) g.step_single = 0;
   g.module = mod;
   g.device = dev;
   g.compute_units = cus;
@@ -285,7 +303,8 @@ void q8gemv_shutdown(void) {
   if (g.dec_module) (void)hipModuleUnload(g.dec_module);
   g.dec_module = nullptr;
   g.dec_embed = g.dec_qkv = g.dec_attn = g.dec_o = g.dec_gu = g.dec_dn =
-      g.dec_vocab = g.dec_final = g.dec_adv = nullptr;
+      g.dec_vocab = g.dec_final = g.dec_adv = g.dec_clear = g.dec_step = nullptr;
+  g.step_capable = false;
   g.vocab = g.vocab_finalize = g.ws_reset = g.copy = nullptr;
   g.ready = false;
 }
@@ -731,6 +750,7 @@ constexpr int64_t kKvRow = 8 * 128;  // f16 elements per cache slot
 constexpr int kAttnGroupsHost = 8;  // attention workgroups (partials) per kv head
 constexpr int32_t kGenerateBatch = 4;  // tokens between EOS checks (qwen3_full.mlir:1412)
 
+
 // Scratch layout (bytes).  Key + status first; every region 256-byte aligned.
 constexpr size_t kScrKey = 0;        // u64 argmax key
 constexpr size_t kScrStatus = 8;     // u32 status
@@ -747,10 +767,93 @@ constexpr size_t kScrQr = kScrXn + 2048;     // f16[2048] q after head norm + Ro
 constexpr size_t kScrFn = kScrQr + 4096;     // f16[1024] rms_norm(res, ffn_norm)
 constexpr size_t kScrOn = kScrFn + 2048;     // f16[1024] rms_norm(h, output_norm)
 constexpr size_t kScrPart = kScrOn + 2048;   // f32[16][8][132] attention partials
-constexpr size_t kScrBytes = kScrPart + 16 * kAttnGroupsHost * 132 * 4;
+constexpr size_t kScrSeq = 16;       // u32 step sequence number (single-launch step)
+constexpr size_t kScrAbort = 20;     // u32 abort word (single-launch step)
+// tagged words of the single-launch step (u64; map in decode_kernels.hip)
+constexpr size_t kStepWordsParity = 512 + 1024 + 512 + 512 + 16 * 8 * 130 + 1024 + 512 + 1536;
+constexpr size_t kStepWords = 2 * kStepWordsParity + 2 * 256;
+constexpr size_t kScrWords = (kScrPart + 16 * kAttnGroupsHost * 132 * 4 + 255) / 256 * 256;
+constexpr size_t kScrBytes = kScrWords + kStepWords * 8;
+
 
 const uint8_t* cb(const void* p) { return static_cast<const uint8_t*>(p); }
 uint8_t* mb(void* p) { return static_cast<uint8_t*>(p); }
+
+// Kernel argument of dec_step (decode_kernels.hip, same member order).
+struct StepParams {
+  const void* token_embd;
+  const void* attn_norm;
+  const void* ffn_norm;
+  const void* q_norm;
+  const void* k_norm;
+  const void* wq;
+  const void* wk;
+  const void* wv;
+  const void* wo;
+  const void* wgu;
+  const void* wdn;
+  const void* output_norm;
+  const void* output_w;
+  void* k_cache;
+  void* v_cache;
+  const int32_t* token_in;
+  int32_t* token_out;
+  int32_t* pos;
+  void* logits;
+  int32_t* out;
+  void* words;
+  void* seq;
+  void* abort_word;
+  void* status;
+  void* on_out;
+  int32_t max_seq;
+  int32_t advance;
+  int32_t head;
+  int32_t pad;
+};
+
+// One single-launch decode step (dec_step).
+int launch_step(const qwen3_weights* w, void* k_cache, void* v_cache, int64_t max_seq,
+                const int32_t* token_in, int32_t* token_out, int32_t* pos, void* logits,
+                int32_t* out, int advance, int head, void* scratch, hipStream_t st) {
+  StepParams p;
+  p.token_embd = w->token_embd;
+  p.attn_norm = w->attn_norm;
+  p.ffn_norm = w->ffn_norm;
+  p.q_norm = w->q_norm;
+  p.k_norm = w->k_norm;
+  p.wq = w->wq;
+  p.wk = w->wk;
+  p.wv = w->wv;
+  p.wo = w->wo;
+  p.wgu = w->wgu;
+  p.wdn = w->wdn;
+  p.output_norm = w->output_norm;
+  p.output_w = w->output_w;
+  p.k_cache = k_cache;
+  p.v_cache = v_cache;
+  p.token_in = token_in;
+  p.token_out = token_out;
+  p.pos = pos;
+  p.logits = logits;
+  p.out = out;
+  p.words = mb(scratch) + kScrWords;
+  p.seq = mb(scratch) + kScrSeq;
+  p.abort_word = mb(scratch) + kScrAbort;
+  p.status = mb(scratch) + kScrStatus;
+  p.on_out = mb(scratch) + kScrOn;
+  p.max_seq = (int32_t)max_seq;
+  p.advance = advance ? 1 : 0;
+  p.head = head ? 1 : 0;
+  p.pad = 0;
+  void* args[] = {&p};
+  hipError_t e = hipModuleLaunchCooperativeKernel(g.dec_step, kStepWorkgroups, 1, 1, 256, 1, 1, 0,
+                                                  st, args);
+  if (e != hipSuccess) return hip_fail(e, "cooperative launch of dec_step");
+  return Q8_OK;
+}
+
+bool use_single() { return g.step_single == 1 && g.step_capable && g.dec_step != nullptr; }
 
 int check_decode_ready() {
   int rc = check_ready();
@@ -918,9 +1021,30 @@ int qwen3_scratch_reset(void* scratch, void* stream) {
   if (!aligned(scratch, 256)) return fail(Q8_ERR_MISALIGNED, "scratch must be 256-byte aligned");
   int rc = check_ready();
   if (rc) return rc;
-  void* ws = scratch;
-  void* args[] = {&ws};
-  return launch(g.ws_reset, 1, 64, args, static_cast<hipStream_t>(stream));
+  if ((rc = check_decode_ready())) return rc;
+  void* p = scratch;
+  uint32_t n = (uint32_t)(kScrBytes / 4);
+  void* args[] = {&p, &n};
+  return launch(g.dec_clear, 64, 256, args, static_cast<hipStream_t>(stream));
+}
+
+int qwen3_set_step_mode(int mode) {
+  if (mode != 0 && mode != 1) return fail(Q8_ERR_BAD_ARGUMENT, "step mode %d not in {0, 1}", mode);
+  int rc = check_decode_ready();
+  if (rc) return rc;
+  if (mode == 1 && !g.step_capable)
+    return fail(Q8_ERR_BAD_ARGUMENT, "this device cannot run the single-launch step "
+                "(needs cooperative launch of 256 resident workgroups)");
+  g.step_single = mode;
+  return Q8_OK;
+}
+
+int qwen3_get_step_mode(int* mode) {
+  if (!mode) return fail(Q8_ERR_NULL_POINTER, "null mode");
+  int rc = check_decode_ready();
+  if (rc) return rc;
+  *mode = use_single() ? 1 : 0;
+  return Q8_OK;
 }
 
 int qwen3_decode_embed(const qwen3_weights* w, const int32_t* token, void* h_out, void* stream) {
@@ -972,6 +1096,9 @@ int qwen3_decode_step(const qwen3_weights* w, void* k_cache, void* v_cache, int6
   if (logits && !aligned(logits, 2)) return fail(Q8_ERR_MISALIGNED, "logits 2-byte alignment");
   if ((rc = check_decode_ready())) return rc;
   hipStream_t st = static_cast<hipStream_t>(stream);
+  if (use_single())
+    return launch_step(w, k_cache, v_cache, max_seq, token, token, pos, logits, nullptr, advance,
+                       1, scratch, st);
   void* h = nullptr;
   if ((rc = launch_body(w, k_cache, v_cache, max_seq, token, pos, scratch, st, &h))) return rc;
   return launch_head(w, h, logits, token, pos, advance, max_seq, scratch, st);
@@ -990,6 +1117,15 @@ int qwen3_prefill(const qwen3_weights* w, void* k_cache, void* v_cache, int64_t 
   hipStream_t st = static_cast<hipStream_t>(stream);
   void* status = mb(scratch) + kScrStatus;
   int ms = (int)max_seq;
+  if (use_single()) {
+    for (int32_t i = 0; i < n_prompt; ++i) {
+      const bool last = i + 1 == n_prompt;
+      if ((rc = launch_step(w, k_cache, v_cache, max_seq, prompt + i, token, pos, nullptr, nullptr,
+                            1, last ? 1 : 0, scratch, st)))
+        return rc;
+    }
+    return Q8_OK;
+  }
   for (int32_t i = 0; i < n_prompt; ++i) {
     void* h = nullptr;
     if ((rc = launch_body(w, k_cache, v_cache, max_seq, prompt + i, pos, scratch, st, &h)))
@@ -1025,6 +1161,12 @@ int qwen3_generate(const qwen3_weights* w, void* k_cache, void* v_cache, int64_t
   while (idx < max_new) {
     const int32_t batch = max_new - idx < kGenerateBatch ? max_new - idx : kGenerateBatch;
     for (int32_t b = 0; b < batch; ++b) {
+      if (use_single()) {
+        if ((rc = launch_step(w, k_cache, v_cache, max_seq, token, token, pos, nullptr,
+                              out_tokens + idx + b, 1, 1, scratch, st)))
+          return rc;
+        continue;
+      }
       void* h = nullptr;
       if ((rc = launch_body(w, k_cache, v_cache, max_seq, token, pos, scratch, st, &h))) return rc;
       if ((rc = launch_head(w, h, nullptr, token, pos, 1, max_seq, scratch, st,

@@ -122,6 +122,17 @@ class DeviceWeights:
             b.free()
 
 
+def step_mode() -> int:
+    """1: each step is one cooperative launch (dec_step); 0: one launch per phase."""
+    m = ctypes.c_int(0)
+    Q._call("qwen3_get_step_mode", ctypes.byref(m))
+    return m.value
+
+
+def set_step_mode(mode: int) -> None:
+    Q._call("qwen3_set_step_mode", int(mode))
+
+
 def scratch_bytes() -> int:
     return int(Q.load_library().qwen3_scratch_bytes())
 

@@ -154,6 +154,8 @@ _SIGNATURES = {
     "qwen3_decode_head": [_P, _P, _P, _P, _P, _I, _I64, _P, _P],
     "qwen3_prefill": [_P, _P, _P, _I64, _P, ctypes.c_int32, _P, _P, _P, _P],
     "qwen3_generate": [_P, _P, _P, _I64, _P, _P, ctypes.c_int32, ctypes.c_int32, _P, _P, _P, _P],
+    "qwen3_set_step_mode": [_I],
+    "qwen3_get_step_mode": [_P],
 }
 _RESTYPES = {
     "q8gemv_shutdown": None,

@@ -1,0 +1,98 @@
+"""The single-launch decode step (qwen3_set_step_mode(1): one cooperative
+launch, phases handing activations over through tagged words) against the
+launch-per-phase step (mode 0, itself checked stage by stage against the
+oracle).  Both run the same operations in the same order, so logits, tokens,
+positions and the KV cache must agree bit for bit."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def D():
+    from qwen3_iree_amd import decode
+
+    return decode
+
+
+@pytest.fixture(scope="module")
+def dmodel(gpu, D, model_host):
+    m = D.DeviceWeights(model_host)
+    yield m
+    m.free()
+
+
+@pytest.fixture(scope="module")
+def single(gpu, D, dmodel):
+    before = D.step_mode()
+    D.set_step_mode(1)  # raises if the device cannot run the single-launch step
+    yield
+    D.set_step_mode(before)
+
+
+def run_steps(D, dmodel, mode, max_seq, token, pos, n, history=None):
+    D.set_step_mode(mode)
+    s = D.DecodeSession(dmodel, max_seq)
+    if history is not None:
+        s.k_cache.upload(history[0])
+        s.v_cache.upload(history[1])
+    s.set_state(token, pos)
+    out = []
+    for i in range(n):
+        print(f"mode {mode} step {i}", flush=True)
+        s.step(advance=True, logits=True)
+        out.append((s.get_state(), s.read_logits(), s.status()))
+    k, v = s.cache_rows(27, 0, max_seq)
+    k0, v0 = s.cache_rows(0, 0, max_seq)
+    s.free()
+    return out, (k, v, k0, v0)
+
+
+@pytest.mark.parametrize("max_seq,pos,n", [(16, 0, 5), (1024, 1020, 3), (40, 7, 2)])
+def test_single_launch_matches_per_phase(D, dmodel, single, max_seq, pos, n):
+    rng = np.random.default_rng(max_seq + pos)
+    hist = None
+    if pos > 0:
+        shape = (28 * max_seq * 1024,)
+        hist = (rng.standard_normal(shape, dtype=np.float32).astype(np.float16),
+                (0.6 * rng.standard_normal(shape, dtype=np.float32)).astype(np.float16))
+    a, ca = run_steps(D, dmodel, 0, max_seq, 4321, pos, n, hist)
+    b, cb = run_steps(D, dmodel, 1, max_seq, 4321, pos, n, hist)
+    for i, ((sa, la, st_a), (sb, lb, st_b)) in enumerate(zip(a, b)):
+        assert sa == sb, (i, sa, sb)
+        assert st_a == st_b, (i, st_a, st_b)
+        assert np.array_equal(la.view(np.uint16), lb.view(np.uint16)), i
+    for x, y in zip(ca, cb):
+        assert np.array_equal(x.view(np.uint16), y.view(np.uint16))
+
+
+def test_single_launch_generate_and_prefill(D, dmodel, single):
+    prompt = [17, 4, 151935, 99, 0, 12]
+    res = {}
+    for mode in (0, 1):
+        D.set_step_mode(mode)
+        s = D.DecodeSession(dmodel, 32)
+        s.set_state(-1, 0)
+        print(f"mode {mode}: prefill + generate", flush=True)
+        s.prefill(prompt)
+        st = s.get_state()
+        toks = s.generate(9, eos_id=-3)
+        res[mode] = (st, toks.tolist(), s.get_state(), s.status())
+        s.free()
+    assert res[0] == res[1]
+    assert res[1][2][1] == len(prompt) + 9
+
+
+def test_single_launch_repeated_steps_keep_sequence(D, dmodel, single):
+    """Many launches on one scratch: every step's tags differ from the last."""
+    D.set_step_mode(1)
+    s = D.DecodeSession(dmodel, 64)
+    s.set_state(5, 0)
+    for i in range(40):
+        s.step(advance=True, logits=False)
+    tok, pos = s.get_state()
+    assert pos == 40 and s.status() == 0 and 0 <= tok < D.VOCAB
+    s.free()
