@@ -160,6 +160,24 @@ __device__ __forceinline__ float merge_dim(const float (&acc)[kAttnGroups],
   return a;
 }
 
+// RoPE angles for this lane's dims 2*lane + dd at position pos
+// (qwen3_full.mlir:324-454): theta = pos * (1e6^(-(2i/128)) * 1), i = d mod 64.
+// They depend on the position only, so a step computes them once for all
+// layers.
+__device__ __forceinline__ void rope_angles(int pos, float (&cs)[2], float (&sn)[2]) {
+  const int lane = threadIdx.x & 63;
+  const float posf = (float)pos;
+#pragma unroll
+  for (int dd = 0; dd < 2; ++dd) {
+    const int d = 2 * lane + dd;
+    const int i = d < 64 ? d : d - 64;
+    const float e = -((2.0f * (float)i) / 128.0f);
+    const float th = posf * (powf(kRopeBase, e) * 1.0f);
+    cs[dd] = cosf(th);
+    sn[dd] = sinf(th);
+  }
+}
+
 // LDS of one attention workgroup.
 struct AttnLds {
   float xs[kAttnWaves][3][kHeadDim];  // normed q_A, q_B, k (f16 values)
@@ -193,8 +211,10 @@ struct AttnLds {
 // get_qkv(xw, v_new) fills this lane's words (dims 2*lane, 2*lane+1) of q
 // head 2g, q head 2g+1, k head g (xw[0..2]) and v head g; every thread of the
 // workgroup calls it once.
+// cs, sn: rope_angles of the clamped position.
 template <class GetQKV, class Publish>
 __device__ __forceinline__ void attention_group(AttnLds& L, int g, int sg, int pos_raw,
+                                                const float (&cs)[2], const float (&sn)[2],
                                                 int max_seq, const uint16_t* __restrict__ qn_w,
                                                 const uint16_t* __restrict__ kn_w,
                                                 uint16_t* __restrict__ k_cache,
@@ -259,17 +279,6 @@ __device__ __forceinline__ void attention_group(AttnLds& L, int g, int sg, int p
   __syncthreads();
 
   // ---- 1b. RoPE (rotate-half) ----
-  const float posf = (float)pos;
-  float cs[2], sn[2];
-#pragma unroll
-  for (int dd = 0; dd < 2; ++dd) {
-    const int d = 2 * lane + dd;
-    const int i = d < 64 ? d : d - 64;
-    const float e = -((2.0f * (float)i) / 128.0f);
-    const float th = posf * (powf(kRopeBase, e) * 1.0f);
-    cs[dd] = cosf(th);
-    sn[dd] = sinf(th);
-  }
   uint32_t roped[3];
 #pragma unroll
   for (int t = 0; t < 3; ++t) {

@@ -85,8 +85,11 @@ extern "C" __global__ __launch_bounds__(256) void dec_attention(
   const int g = blockIdx.x / kAttnGroups;
   const int sg = blockIdx.x % kAttnGroups;
   const int lane = threadIdx.x & 63;
+  const int pos_raw = *pos_ptr;
+  float cs[2], sn[2];
+  rope_angles(pos_raw < 0 ? 0 : (pos_raw >= max_seq ? max_seq - 1 : pos_raw), cs, sn);
   attention_group(
-      lds, g, sg, *pos_ptr, max_seq, qn_w, kn_w, k_cache, v_cache, q_roped,
+      lds, g, sg, pos_raw, cs, sn, max_seq, qn_w, kn_w, k_cache, v_cache, q_roped,
       [&](uint32_t (&xw)[3], uint32_t& v_new) {
         xw[0] = load_global(reinterpret_cast<const uint32_t*>(q_raw + (2 * g) * kHeadDim) + lane);
         xw[1] = load_global(reinterpret_cast<const uint32_t*>(q_raw + (2 * g + 1) * kHeadDim) + lane);
@@ -363,37 +366,60 @@ struct Waiter {
   uint32_t seq;
   int* s_abort;  // LDS flag of the workgroup
 
-  // Every thread of the workgroup calls this with the same arguments: words
-  // [0, n) of src with tag `tag` land (their data halves) in dst[0, n).
-  // Returns false (in every thread) when the step was aborted.
-  __device__ __forceinline__ bool wait(const uint64_t* __restrict__ src, int n, uint32_t tag,
-                                       uint32_t* __restrict__ dst) const {
+  // Every thread of the workgroup calls this with the same arguments: the
+  // data halves of words src(0..n-1), once each carries tag `tag`, land in
+  // dst[0, n).  A thread requests all of its words (i = threadIdx.x + 256 k)
+  // at once and re-requests only those not ready yet, so a wait costs one
+  // round trip once the data is there.  Returns false (in every thread)
+  // when the step was aborted.
+  template <class Src>
+  __device__ __forceinline__ bool wait_map(int n, uint32_t tag, uint32_t* __restrict__ dst,
+                                           Src src) const {
+    constexpr int kMax = 9;  // n <= 2304
+    const int t = threadIdx.x;
+    uint64_t w[kMax];
+#pragma unroll
+    for (int k = 0; k < kMax; ++k)
+      if (t + 256 * k < n) w[k] = get_word(src(t + 256 * k));
     bool ok = true;
-    for (int i = threadIdx.x; i < n; i += blockDim.x) {
-      uint64_t w = get_word(src + i);
-      uint32_t spins = 0;
-      while ((uint32_t)(w >> 32) != tag) {
-        ++spins;
-        if ((spins & 31u) == 0u &&
-            __hip_atomic_load(abort_word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == seq) {
-          ok = false;
-          break;
-        }
-        if (spins > kSpinLimit) {
-          __hip_atomic_fetch_or(status, 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          __hip_atomic_store(abort_word, seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          ok = false;
-          break;
-        }
-        __builtin_amdgcn_s_sleep(1);
-        w = get_word(src + i);
+    uint32_t spins = 0;
+    while (true) {
+      bool pending = false;
+#pragma unroll
+      for (int k = 0; k < kMax; ++k)
+        if (t + 256 * k < n && (uint32_t)(w[k] >> 32) != tag) pending = true;
+      if (!pending) break;
+      ++spins;
+      if ((spins & 31u) == 0u &&
+          __hip_atomic_load(abort_word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == seq) {
+        ok = false;
+        break;
       }
-      if (!ok) break;
-      dst[i] = (uint32_t)w;
+      if (spins > kSpinLimit) {
+        __hip_atomic_fetch_or(status, 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(abort_word, seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        ok = false;
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+      for (int k = 0; k < kMax; ++k)
+        if (t + 256 * k < n && (uint32_t)(w[k] >> 32) != tag) w[k] = get_word(src(t + 256 * k));
     }
-    if (!ok) *s_abort = 1;
+    if (ok) {
+#pragma unroll
+      for (int k = 0; k < kMax; ++k)
+        if (t + 256 * k < n) dst[t + 256 * k] = (uint32_t)w[k];
+    } else {
+      *s_abort = 1;
+    }
     __syncthreads();
     return *s_abort == 0;
+  }
+
+  __device__ __forceinline__ bool wait(const uint64_t* __restrict__ src, int n, uint32_t tag,
+                                       uint32_t* __restrict__ dst) const {
+    return wait_map(n, tag, dst, [=](int i) { return src + i; });
   }
 };
 
@@ -445,6 +471,10 @@ extern "C" __global__ __launch_bounds__(256) void dec_step(StepParams P) {
   tok = (tok < 0 || tok >= kVocab) ? 0 : tok;
   const uint16_t* emb = P.token_embd + (size_t)tok * kHidden;
   const Waiter W{P.abort_word, P.status, seq, &s_abort};
+  float rope_cs[2], rope_sn[2];  // the position's RoPE angles, for every layer
+  if (wg < 64)
+    rope_angles(pos_raw < 0 ? 0 : (pos_raw >= P.max_seq ? P.max_seq - 1 : pos_raw), rope_cs,
+                rope_sn);
   __syncthreads();
 
   for (int layer = 0; layer < kLayers; ++layer) {
@@ -487,13 +517,16 @@ extern "C" __global__ __launch_bounds__(256) void dec_step(StepParams P) {
       bool ok = true;
       const uint32_t tq = step_tag(seq, layer, kPhQKV);
       attention_group(
-          L, g, sg, pos_raw, P.max_seq, P.q_norm + layer * kHeadDim, P.k_norm + layer * kHeadDim,
+          L, g, sg, pos_raw, rope_cs, rope_sn, P.max_seq, P.q_norm + layer * kHeadDim,
+          P.k_norm + layer * kHeadDim,
           P.k_cache + cache_layer, P.v_cache + cache_layer, nullptr,
           [&](uint32_t (&xw)[3], uint32_t& v_new) {
             // q heads 2g, 2g+1 (words 128g..), k head g, v head g (words 64g..)
-            ok = W.wait(cur + kWQ + 128 * g, 128, tq, vec) &&
-                 W.wait(cur + kWK + 64 * g, 64, tq, vec + 128) &&
-                 W.wait(cur + kWV + 64 * g, 64, tq, vec + 192);
+            ok = W.wait_map(256, tq, vec, [&](int i) {
+              return i < 128 ? cur + kWQ + 128 * g + i
+                             : (i < 192 ? cur + kWK + 64 * g + (i - 128)
+                                        : cur + kWV + 64 * g + (i - 192));
+            });
             xw[0] = vec[lane];
             xw[1] = vec[64 + lane];
             xw[2] = vec[128 + lane];

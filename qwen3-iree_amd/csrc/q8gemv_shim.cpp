@@ -281,10 +281,9 @@ int q8gemv_init(const char* code_object_path) {
             hipSuccess)
       g.step_capable = coop != 0 && per_cu >= 1 && (int64_t)per_cu * cus >= kStepWorkgroups;
   }
-  // Launch per phase is the default: on MI355X it measures faster (880 vs 974
-  // us per token at context 1024) because a tagged-word hand-off between
-  // workgroups costs about as much as a kernel boundary.
-  if (g.step_single < 0) g.step_single = 0;
+  // The single launch is the default where it can run: no kernel boundaries,
+  // and every workgroup requests its next weights before it waits.
+  if (g.step_single < 0) g.step_single = g.step_capable ? 1 : 0;
   g.module = mod;
   g.device = dev;
   g.compute_units = cus;
