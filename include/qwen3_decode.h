@@ -104,6 +104,45 @@ int qwen3_prefill(const qwen3_weights* w, void* k_cache, void* v_cache, int64_t 
                   const int32_t* prompt, int32_t n_prompt, int32_t* token, int32_t* pos,
                   void* scratch, void* stream);
 
+/* Prompt ingestion with every prompt token of a layer processed together, the
+ * reference's @prefill (qwen3_full.mlir:2032-2111, layers :1731-2030): the
+ * layer matrices become GEMMs over the n_prompt tokens.  Token i (prompt[i],
+ * device int32 [n_prompt]) sits at position p0 + i, p0 = *pos (read on the
+ * host: the call synchronizes `stream` once); each layer writes the tokens'
+ * k/v to those cache slots, and token i attends to slots [lo, p0 + i] with
+ * lo = 0 when chunk_local == 0 (the whole cache, what qwen3_prefill's decode
+ * steps see) or lo = p0 when chunk_local != 0 (this call's tokens only, the
+ * reference's @prefill, whose mask j <= i covers its own tokens, :1700-1710;
+ * the same thing when p0 = 0).  Then, as in qwen3_prefill: the last token's
+ * logits (f16 [151936], may be NULL), *token = their argmax, *pos = p0 +
+ * n_prompt (at p0 + n_prompt = max_seq it stays at max_seq - 1 and status bit
+ * 0 is set).  Fails with Q8_ERR_BAD_SHAPE unless p0 + n_prompt <= max_seq.
+ * workspace: device memory of qwen3_prefill_workspace_bytes(n_prompt) bytes,
+ * 256-byte aligned (activations of all tokens; 30,720 bytes per token).  The
+ * reference reads f16 copies of the layer matrices for this function
+ * (@model_params.attn_q_weight etc., :1132-1210); this one reads the same
+ * Q8_0 stacks as the decode step, so prompt and decode share one set of
+ * weights. */
+size_t qwen3_prefill_workspace_bytes(int32_t n_prompt);
+int qwen3_prefill_batched(const qwen3_weights* w, void* k_cache, void* v_cache, int64_t max_seq,
+                          const int32_t* prompt, int32_t n_prompt, int32_t* token, int32_t* pos,
+                          void* logits, int chunk_local, void* workspace, size_t workspace_bytes,
+                          void* scratch, void* stream);
+
+/* One layer of qwen3_prefill_batched, for tests and for callers that
+ * interleave work (@transformer_layer_prefill, qwen3_full.mlir:1731-2030):
+ * the n_tokens hidden rows in the workspace's "h" region (f16 [n_tokens,
+ * 1024]) at positions start_pos.. (host int) are replaced by the layer's
+ * output; the layer's k/v go to those cache slots; the intermediates stay in
+ * the workspace.  qwen3_prefill_workspace_offset(n_tokens, name) = byte
+ * offset of a region ("h", "res", "xn", "q", "k", "v", "q_roped", "attn",
+ * "act", "fn"; f16 rows of 1024, 1024, 1024, 2048, 1024, 1024, 2048, 2048,
+ * 3072, 1024 columns), -1 for an unknown name. */
+int qwen3_prefill_layer(const qwen3_weights* w, int layer, void* k_cache, void* v_cache,
+                        int64_t max_seq, int32_t n_tokens, int32_t start_pos, int chunk_local,
+                        void* workspace, size_t workspace_bytes, void* stream);
+int64_t qwen3_prefill_workspace_offset(int32_t n_tokens, const char* name);
+
 /* The token loop of @generate (qwen3_full.mlir:1396-1534): starting from
  * *token at *pos, steps run in batches of 4 (fewer for the last) with the
  * token fed back and the position advanced on the device; step i's token goes

@@ -2,6 +2,7 @@
 
   lib/q8gemv_gfx950.hsaco  hipcc --genco --offload-arch=gfx950 of csrc/q8gemv_kernels.hip
   lib/decode_gfx950.hsaco  the same for csrc/decode_kernels.hip (decode-step kernels)
+  lib/prefill_gfx950.hsaco the same for csrc/prefill_kernels.hip (batched prompt ingestion)
   lib/libq8gemv.so         g++ of csrc/q8gemv_shim.cpp against libamdhip64
 
 Both cross-compile without a GPU.  Run as `python qwen3-iree_amd/build.py`.
@@ -21,6 +22,7 @@ ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
 
 CODE_OBJECT = LIB / "q8gemv_gfx950.hsaco"
 DECODE_OBJECT = LIB / "decode_gfx950.hsaco"
+PREFILL_OBJECT = LIB / "prefill_gfx950.hsaco"
 SHIM = LIB / "libq8gemv.so"
 
 HIPCC_FLAGS = [
@@ -57,6 +59,10 @@ def build_decode_object() -> Path:
     return _hsaco(CSRC / "decode_kernels.hip", DECODE_OBJECT)
 
 
+def build_prefill_object() -> Path:
+    return _hsaco(CSRC / "prefill_kernels.hip", PREFILL_OBJECT)
+
+
 def build_shim() -> Path:
     LIB.mkdir(exist_ok=True)
     tmp = SHIM.with_suffix(".so.tmp")
@@ -72,8 +78,8 @@ def build_shim() -> Path:
     return SHIM
 
 
-def build_all() -> tuple[Path, Path, Path]:
-    return build_code_object(), build_decode_object(), build_shim()
+def build_all() -> tuple[Path, Path, Path, Path]:
+    return build_code_object(), build_decode_object(), build_prefill_object(), build_shim()
 
 
 if __name__ == "__main__":

@@ -100,6 +100,10 @@ struct State {
   hipFunction_t dec_embed = nullptr, dec_qkv = nullptr, dec_attn = nullptr,
                 dec_o = nullptr, dec_gu = nullptr, dec_dn = nullptr, dec_vocab = nullptr,
                 dec_final = nullptr, dec_adv = nullptr, dec_clear = nullptr, dec_step = nullptr;
+  hipModule_t pf_module = nullptr;  // prefill_gfx950.hsaco (optional)
+  hipFunction_t pf_embed = nullptr, pf_norm = nullptr, pf_gemm = nullptr, pf_gemm_res = nullptr,
+                pf_gemm_swiglu = nullptr, pf_rope = nullptr, pf_attn = nullptr,
+                pf_set_pos = nullptr;
   int step_single = -1;   // single-launch decode step: -1 unknown, 0 off, 1 on
   bool step_capable = false;
   int vocab_wgs = 0;      // 0 = default
@@ -154,6 +158,13 @@ int launch(hipFunction_t fn, uint32_t grid, uint32_t block, void** args, hipStre
   } else {
     e = hipModuleLaunchKernel(fn, grid, 1, 1, block, 1, 1, 0, stream, args, nullptr);
   }
+  if (e != hipSuccess) return hip_fail(e, "kernel launch");
+  return Q8_OK;
+}
+
+int launch2(hipFunction_t fn, uint32_t gx, uint32_t gy, uint32_t block, void** args,
+            hipStream_t stream) {
+  hipError_t e = hipModuleLaunchKernel(fn, gx, gy, 1, block, 1, 1, 0, stream, args, nullptr);
   if (e != hipSuccess) return hip_fail(e, "kernel launch");
   return Q8_OK;
 }
@@ -268,6 +279,44 @@ int q8gemv_init(const char* code_object_path) {
       }
     }
   }
+  // The batched prompt kernels live in a third code object beside the decode
+  // one; without it qwen3_prefill_batched reports Q8_ERR_CODE_OBJECT.
+  if (g.dec_module) {
+    const size_t slash = path.rfind('/');
+    std::string dir = slash == std::string::npos ? std::string(".") : path.substr(0, slash);
+    std::string ppath = dir + "/prefill_gfx950.hsaco";
+    FILE* pf = std::fopen(ppath.c_str(), "rb");
+    if (!pf) {
+      std::string lib = default_code_object();
+      ppath = lib.substr(0, lib.rfind('/')) + "/prefill_gfx950.hsaco";
+      pf = std::fopen(ppath.c_str(), "rb");
+    }
+    if (pf) {
+      std::fclose(pf);
+      hipModule_t pm = nullptr;
+      if (hipModuleLoad(&pm, ppath.c_str()) == hipSuccess) {
+        struct {
+          hipFunction_t* fn;
+          const char* name;
+        } names[] = {{&g.pf_embed, "pf_embed"},
+                     {&g.pf_norm, "pf_rmsnorm"},
+                     {&g.pf_gemm, "pf_gemm_q8"},
+                     {&g.pf_gemm_res, "pf_gemm_q8_res"},
+                     {&g.pf_gemm_swiglu, "pf_gemm_q8_swiglu"},
+                     {&g.pf_rope, "pf_qk_rope_cache"},
+                     {&g.pf_attn, "pf_attention"},
+                     {&g.pf_set_pos, "pf_set_pos"}};
+        bool ok = true;
+        for (auto& n : names) ok = ok && hipModuleGetFunction(n.fn, pm, n.name) == hipSuccess;
+        if (ok) {
+          g.pf_module = pm;
+        } else {
+          (void)hipModuleUnload(pm);
+          for (auto& n : names) *n.fn = nullptr;
+        }
+      }
+    }
+  }
   int cus = 0;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
     cus = 256;
@@ -304,6 +353,10 @@ void q8gemv_shutdown(void) {
   g.dec_embed = g.dec_qkv = g.dec_attn = g.dec_o = g.dec_gu = g.dec_dn =
       g.dec_vocab = g.dec_final = g.dec_adv = g.dec_clear = g.dec_step = nullptr;
   g.step_capable = false;
+  if (g.pf_module) (void)hipModuleUnload(g.pf_module);
+  g.pf_module = nullptr;
+  g.pf_embed = g.pf_norm = g.pf_gemm = g.pf_gemm_res = g.pf_gemm_swiglu = g.pf_rope =
+      g.pf_attn = g.pf_set_pos = nullptr;
   g.vocab = g.vocab_finalize = g.ws_reset = g.copy = nullptr;
   g.ready = false;
 }
@@ -981,6 +1034,112 @@ int launch_body(const qwen3_weights* w, void* k_cache, void* v_cache, int64_t ma
   return Q8_OK;
 }
 
+// ---- batched prompt ingestion ----
+
+// Argument block of pf_gemm_q8* (layout shared with prefill_kernels.hip).
+struct GemmArgs {
+  const void* x;
+  const void* w;
+  void* y;
+  const void* r;
+  int M, K;
+  int n_tiles;
+  int ldx, ldy, ldr;
+  int up_row;
+};
+
+// Workspace regions, f16 elements per token: h, h1 (residual), xn
+// (rms_norm(h, attn_norm)), q, k, v, q_roped, attention output, SwiGLU
+// output, fn (rms_norm(h1, ffn_norm)).
+constexpr int kPfRegions = 10;
+constexpr int kPfCols[kPfRegions] = {1024, 1024, 1024, 2048, 1024, 1024, 2048, 2048, 3072, 1024};
+constexpr int32_t kPfMaxTokens = 1 << 20;
+
+size_t pf_region_bytes(int32_t n, int i) {
+  return ((size_t)n * kPfCols[i] * 2 + 255) / 256 * 256;
+}
+
+size_t pf_workspace_bytes(int32_t n) {
+  size_t b = 0;
+  for (int i = 0; i < kPfRegions; ++i) b += pf_region_bytes(n, i);
+  return b;
+}
+
+int launch_gemm(hipFunction_t fn, const void* x, int ldx, const void* wl, int K, int n_out,
+                int tile_cols, void* y, int ldy, const void* r, int ldr, int up_row, int M,
+                hipStream_t st) {
+  GemmArgs a{x, wl, y, r, M, K, n_out / tile_cols, ldx, ldy, ldr, up_row};
+  // the kernel maps workgroups to n tiles in groups of 8 (one per XCD)
+  if (n_out % tile_cols != 0 || a.n_tiles % 8 != 0 || K % 256 != 0)
+    return fail(Q8_ERR_BAD_SHAPE, "prefill GEMM shape N=%d K=%d", n_out, K);
+  const int64_t mt = ((int64_t)M + 63) / 64;
+  const int64_t grid = mt * a.n_tiles;
+  if (grid > 0x7fffffff) return fail(Q8_ERR_BAD_SHAPE, "prefill GEMM grid too large");
+  void* args[] = {&a};
+  return launch(fn, (uint32_t)grid, 256, args, st);
+}
+
+int launch_prefill_layer(const qwen3_weights* w, int layer, void* k_cache, void* v_cache,
+                         int64_t max_seq, int32_t n, int32_t p0, int chunk_local,
+                         void* const (&ws)[kPfRegions], hipStream_t st) {
+  const int64_t bpl_q = 2048LL * 1024 / 32 * 34, bpl_kv = 1024LL * 1024 / 32 * 34;
+  const int64_t bpl_o = 1024LL * 2048 / 32 * 34, bpl_gu = 6144LL * 1024 / 32 * 34;
+  const int64_t bpl_dn = 1024LL * 3072 / 32 * 34;
+  const void* an = cb(w->attn_norm) + layer * 2048;
+  const void* fn = cb(w->ffn_norm) + layer * 2048;
+  const void* qn = cb(w->q_norm) + layer * 256;
+  const void* kn = cb(w->k_norm) + layer * 256;
+  void* kc = mb(k_cache) + (int64_t)layer * max_seq * kKvRow * 2;
+  void* vc = mb(v_cache) + (int64_t)layer * max_seq * kKvRow * 2;
+  void *h = ws[0], *h1 = ws[1], *xn = ws[2], *q = ws[3], *k = ws[4], *v = ws[5], *qr = ws[6],
+       *attn = ws[7], *act = ws[8], *fnx = ws[9];
+  const uint32_t norm_grid = (uint32_t)((n + 15) / 16);
+  int rc;
+  {
+    void* args[] = {&h, &an, &xn, &n};
+    if ((rc = launch(g.pf_norm, norm_grid, 256, args, st))) return rc;
+  }
+  if ((rc = launch_gemm(g.pf_gemm, xn, 1024, cb(w->wq) + layer * bpl_q, 1024, 2048, 64, q, 2048,
+                        nullptr, 0, 0, n, st)))
+    return rc;
+  if ((rc = launch_gemm(g.pf_gemm, xn, 1024, cb(w->wk) + layer * bpl_kv, 1024, 1024, 64, k, 1024,
+                        nullptr, 0, 0, n, st)))
+    return rc;
+  if ((rc = launch_gemm(g.pf_gemm, xn, 1024, cb(w->wv) + layer * bpl_kv, 1024, 1024, 64, v, 1024,
+                        nullptr, 0, 0, n, st)))
+    return rc;
+  {
+    int start = p0;
+    void* args[] = {&q, &k, &v, &start, &qn, &kn, &qr, &kc, &vc};
+    if ((rc = launch2(g.pf_rope, (uint32_t)n, 8, 256, args, st))) return rc;
+  }
+  {
+    int start = p0, cl = chunk_local ? 1 : 0;
+    void* args[] = {&qr, &kc, &vc, &start, &cl, &attn};
+    if ((rc = launch2(g.pf_attn, (uint32_t)n, 8, 256, args, st))) return rc;
+  }
+  if ((rc = launch_gemm(g.pf_gemm_res, attn, 2048, cb(w->wo) + layer * bpl_o, 2048, 1024, 64, h1,
+                        1024, h, 1024, 0, n, st)))
+    return rc;
+  {
+    void* args[] = {&h1, &fn, &fnx, &n};
+    if ((rc = launch(g.pf_norm, norm_grid, 256, args, st))) return rc;
+  }
+  if ((rc = launch_gemm(g.pf_gemm_swiglu, fnx, 1024, cb(w->wgu) + layer * bpl_gu, 1024, 3072, 32,
+                        act, 3072, nullptr, 0, 3072, n, st)))
+    return rc;
+  return launch_gemm(g.pf_gemm_res, act, 3072, cb(w->wdn) + layer * bpl_dn, 3072, 1024, 64, h,
+                     1024, h1, 1024, 0, n, st);
+}
+
+int check_prefill_ready() {
+  int rc = check_decode_ready();
+  if (rc) return rc;
+  if (!g.pf_module)
+    return fail(Q8_ERR_CODE_OBJECT, "prefill_gfx950.hsaco was not found or lacks a kernel");
+  return Q8_OK;
+}
+
 int validate_step_args(const qwen3_weights* w, void* k_cache, void* v_cache, int64_t max_seq,
                        const int32_t* token, const int32_t* pos, const void* scratch) {
   int rc = validate_weights(w);
@@ -1180,6 +1339,99 @@ int qwen3_generate(const qwen3_weights* w, void* k_cache, void* v_cache, int64_t
     if (last == eos_id) break;
   }
   return Q8_OK;
+}
+
+int64_t qwen3_prefill_workspace_offset(int32_t n_prompt, const char* name) {
+  static const char* const kNames[kPfRegions] = {"h", "res", "xn", "q", "k", "v", "q_roped",
+                                                 "attn", "act", "fn"};
+  if (!name || n_prompt < 1 || n_prompt > kPfMaxTokens) return -1;
+  int64_t off = 0;
+  for (int i = 0; i < kPfRegions; ++i) {
+    if (std::strcmp(name, kNames[i]) == 0) return off;
+    off += (int64_t)pf_region_bytes(n_prompt, i);
+  }
+  return -1;
+}
+
+int qwen3_prefill_layer(const qwen3_weights* w, int layer, void* k_cache, void* v_cache,
+                        int64_t max_seq, int32_t n_tokens, int32_t start_pos, int chunk_local,
+                        void* workspace, size_t workspace_bytes, void* stream) {
+  int rc = validate_weights(w);
+  if (rc) return rc;
+  if ((rc = validate_cache(k_cache, v_cache, max_seq))) return rc;
+  if (layer < 0 || layer >= kLayers)
+    return fail(Q8_ERR_LAYER_RANGE, "layer %d outside [0, %d)", layer, kLayers);
+  if (!workspace) return fail(Q8_ERR_NULL_POINTER, "null workspace");
+  if (!aligned(workspace, 256)) return fail(Q8_ERR_MISALIGNED, "workspace 256-byte alignment");
+  if (n_tokens < 1 || n_tokens > kPfMaxTokens || start_pos < 0 ||
+      (int64_t)start_pos + n_tokens > max_seq)
+    return fail(Q8_ERR_BAD_SHAPE, "tokens [%d, %d + %d) outside the cache of %lld", start_pos,
+                start_pos, n_tokens, (long long)max_seq);
+  if (workspace_bytes < pf_workspace_bytes(n_tokens))
+    return fail(Q8_ERR_BAD_SHAPE, "workspace of %zu bytes < %zu needed for %d tokens",
+                workspace_bytes, pf_workspace_bytes(n_tokens), n_tokens);
+  if ((rc = check_prefill_ready())) return rc;
+  void* ws[kPfRegions];
+  size_t off = 0;
+  for (int i = 0; i < kPfRegions; ++i) {
+    ws[i] = mb(workspace) + off;
+    off += pf_region_bytes(n_tokens, i);
+  }
+  return launch_prefill_layer(w, layer, k_cache, v_cache, max_seq, n_tokens, start_pos,
+                              chunk_local, ws, static_cast<hipStream_t>(stream));
+}
+
+size_t qwen3_prefill_workspace_bytes(int32_t n_prompt) {
+  if (n_prompt < 1 || n_prompt > kPfMaxTokens) return 0;
+  return pf_workspace_bytes(n_prompt);
+}
+
+int qwen3_prefill_batched(const qwen3_weights* w, void* k_cache, void* v_cache, int64_t max_seq,
+                          const int32_t* prompt, int32_t n_prompt, int32_t* token, int32_t* pos,
+                          void* logits, int chunk_local, void* workspace, size_t workspace_bytes,
+                          void* scratch, void* stream) {
+  int rc = validate_step_args(w, k_cache, v_cache, max_seq, token, pos, scratch);
+  if (rc) return rc;
+  if (!prompt || !workspace) return fail(Q8_ERR_NULL_POINTER, "null prompt or workspace");
+  if (!aligned(prompt, 4) || !aligned(workspace, 256) || (logits && !aligned(logits, 16)))
+    return fail(Q8_ERR_MISALIGNED, "prompt 4, workspace 256, logits 16-byte alignment");
+  if (n_prompt < 1 || n_prompt > max_seq || n_prompt > kPfMaxTokens)
+    return fail(Q8_ERR_BAD_SHAPE, "n_prompt %d outside [1, min(max_seq, 2^20)]", n_prompt);
+  if (workspace_bytes < pf_workspace_bytes(n_prompt))
+    return fail(Q8_ERR_BAD_SHAPE, "workspace of %zu bytes < %zu needed for %d tokens",
+                workspace_bytes, pf_workspace_bytes(n_prompt), n_prompt);
+  if ((rc = check_prefill_ready())) return rc;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  int32_t p0 = 0;
+  HIP_TRY(hipMemcpyAsync(&p0, pos, sizeof(p0), hipMemcpyDeviceToHost, st));
+  HIP_TRY(hipStreamSynchronize(st));
+  if (p0 < 0 || (int64_t)p0 + n_prompt > max_seq)
+    return fail(Q8_ERR_BAD_SHAPE, "positions %d + %d prompt tokens exceed max_seq %lld", p0,
+                n_prompt, (long long)max_seq);
+  void* ws[kPfRegions];
+  size_t off = 0;
+  for (int i = 0; i < kPfRegions; ++i) {
+    ws[i] = mb(workspace) + off;
+    off += pf_region_bytes(n_prompt, i);
+  }
+  {
+    const void* tp = prompt;
+    const void* e = w->token_embd;
+    void* h = ws[0];
+    void* args[] = {&tp, &e, &h};
+    if ((rc = launch(g.pf_embed, (uint32_t)n_prompt, 128, args, st))) return rc;
+  }
+  for (int l = 0; l < kLayers; ++l)
+    if ((rc = launch_prefill_layer(w, l, k_cache, v_cache, max_seq, n_prompt, p0, chunk_local, ws,
+                                   st)))
+      return rc;
+  {
+    int last = p0 + n_prompt - 1;
+    void* args[] = {&pos, &last};
+    if ((rc = launch(g.pf_set_pos, 1, 64, args, st))) return rc;
+  }
+  const void* h_last = cb(ws[0]) + (size_t)(n_prompt - 1) * 2048;
+  return launch_head(w, h_last, logits, token, pos, 1, max_seq, scratch, st);
 }
 
 }  // extern "C"

@@ -35,6 +35,10 @@ WEIGHT_FIELDS = ("token_embd", "attn_norm", "ffn_norm", "q_norm", "k_norm", "wq"
 # (rows, cols) of each Q8_0 matrix per layer (qwen3_full.mlir:772-777)
 Q8_SHAPES = {"wq": (Q_DIM, HIDDEN), "wk": (KV_DIM, HIDDEN), "wv": (KV_DIM, HIDDEN),
              "wo": (HIDDEN, Q_DIM), "wgu": (2 * FFN, HIDDEN), "wdn": (HIDDEN, FFN)}
+# workspace regions of the batched prompt path (name, f16 columns per token)
+PREFILL_REGIONS = (("h", HIDDEN), ("res", HIDDEN), ("xn", HIDDEN), ("q", Q_DIM), ("k", KV_DIM),
+                   ("v", KV_DIM), ("q_roped", Q_DIM), ("attn", Q_DIM), ("act", FFN),
+                   ("fn", HIDDEN))
 NORM_STD = 0.1
 
 
@@ -236,6 +240,55 @@ class DecodeSession:
         finally:
             buf.free()
 
+    def prefill_batched(self, prompt, chunk_local: bool = False, logits: bool = False) -> None:
+        """The prompt's layers as GEMMs over all its tokens (qwen3_prefill_batched,
+        the reference's @prefill) from the current position; the token word
+        then holds the argmax after the last prompt token and the position has
+        moved past the prompt.  chunk_local: attend only to this call's
+        tokens, as the reference's @prefill does (the same when starting at
+        position 0)."""
+        prompt = np.ascontiguousarray(prompt, dtype=np.int32).reshape(-1)
+        if prompt.size == 0:
+            raise ValueError("empty prompt")
+        nbytes = int(Q.load_library().qwen3_prefill_workspace_bytes(int(prompt.size)))
+        if nbytes == 0:
+            raise ValueError(f"prompt of {prompt.size} tokens is too long")
+        buf = Q.DeviceBuffer.from_array(prompt)
+        ws = Q.DeviceBuffer(nbytes)
+        try:
+            Q._call("qwen3_prefill_batched", self.model.ref(), self.k_cache.ptr, self.v_cache.ptr,
+                    self.max_seq, buf.ptr, int(prompt.size), self.token_ptr, self.pos_ptr,
+                    self.logits.ptr if logits else None, int(bool(chunk_local)), ws.ptr, nbytes,
+                    self.scratch.ptr, Q._stream(self.stream))
+            self.synchronize()
+        finally:
+            ws.free()
+            buf.free()
+
+    def prefill_layer(self, layer: int, h_rows, start_pos: int,
+                      chunk_local: bool = False) -> dict[str, np.ndarray]:
+        """One layer of the batched prompt path on hidden rows h_rows (f16
+        [n, 1024]) at positions start_pos..; returns the workspace regions
+        (h = the layer's output, and its intermediates) as f16 arrays."""
+        h_rows = np.ascontiguousarray(h_rows, dtype=np.float16).reshape(-1, HIDDEN)
+        n = h_rows.shape[0]
+        lib = Q.load_library()
+        nbytes = int(lib.qwen3_prefill_workspace_bytes(n))
+        ws = Q.DeviceBuffer(nbytes)
+        try:
+            ws.upload(h_rows, int(lib.qwen3_prefill_workspace_offset(n, b"h")))
+            Q._call("qwen3_prefill_layer", self.model.ref(), int(layer), self.k_cache.ptr,
+                    self.v_cache.ptr, self.max_seq, n, int(start_pos), int(bool(chunk_local)),
+                    ws.ptr, nbytes, Q._stream(self.stream))
+            self.synchronize()
+            out = {}
+            for name, cols in PREFILL_REGIONS:
+                off = int(lib.qwen3_prefill_workspace_offset(n, name.encode()))
+                out[name] = ws.download(np.float16, n * cols, off).reshape(n, cols)
+            return out
+        finally:
+            ws.free()
+
     def generate(self, max_new: int, eos_id: int) -> np.ndarray:
         """@generate's loop from the current token / position: returns the
         produced tokens (int32; the EOS check runs after every 4 tokens)."""
@@ -286,16 +339,21 @@ class DecodeSession:
 
 
 def run(model: DeviceWeights, prompt, max_gen: int, eos_id: int,
-        stream: Q.Stream | None = None) -> np.ndarray:
+        stream: Q.Stream | None = None, batched: bool = True) -> np.ndarray:
     """The reference's @run (qwen3_full.mlir:2113-2167): a KV cache of
-    len(prompt) + max_gen positions, the prompt ingested from position 0, its
-    argmax as the first token, then @generate with max_gen tokens.  Returns the
-    generated tokens (the first token itself is not among them, as there)."""
+    len(prompt) + max_gen positions, the prompt ingested from position 0 (all
+    tokens at once as @prefill does, or as decode steps, @prefill_all, with
+    batched=False), its argmax as the first token, then @generate with max_gen
+    tokens.  Returns the generated tokens (the first token itself is not among
+    them, as there)."""
     prompt = np.asarray(prompt, dtype=np.int32).reshape(-1)
     sess = DecodeSession(model, int(prompt.size) + int(max_gen), stream)
     try:
         sess.set_state(0, 0)
-        sess.prefill(prompt)
+        if batched:
+            sess.prefill_batched(prompt)
+        else:
+            sess.prefill(prompt)
         return sess.generate(max_gen, eos_id)
     finally:
         sess.free()

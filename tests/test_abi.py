@@ -32,7 +32,8 @@ def test_header_declares_expected_entry_points():
                      "vocab_argmax_workspace_bytes", "q8gemv_shutdown",
                      "decode_dispatch_3_matmul_2048x1x1024_f16",
                      "decode_dispatch_24_matmul_151936x1x1024_f16",
-                     "qwen3_decode_step", "qwen3_decode_layer", "qwen3_scratch_bytes"):
+                     "qwen3_decode_step", "qwen3_decode_layer", "qwen3_scratch_bytes",
+                     "qwen3_prefill_batched", "qwen3_prefill_layer"):
         assert required in names
 
 
@@ -141,6 +142,11 @@ def test_code_object_targets_gfx950_and_has_every_kernel():
     for name in ("q8gemv_p1", "q8gemv_p2", "q8gemv_p3", "q8gemv_batch_k", "q8gemv_qkv_k", "vocab_gemv_argmax_k1024",
                  "vocab_argmax_finalize", "vocab_workspace_reset", "stream_copy_b128"):
         assert name.encode() in data
+    pf = (REPO / "qwen3-iree_amd" / "lib" / "prefill_gfx950.hsaco").read_bytes()
+    assert pf[:4] == b"\x7fELF" and b"amdgcn-amd-amdhsa--gfx950" in pf
+    for name in ("pf_embed", "pf_rmsnorm", "pf_gemm_q8", "pf_gemm_q8_res", "pf_gemm_q8_swiglu",
+                 "pf_qk_rope_cache", "pf_attention", "pf_set_pos"):
+        assert name.encode() in pf
 
 
 def test_desc_for_kind_addresses_the_layer(Q):
@@ -243,6 +249,25 @@ def test_decode_scratch_layout(Q):
     assert L.qwen3_scratch_offset(b"nope") == -1
 
 
+def test_prefill_workspace_layout(Q):
+    from qwen3_iree_amd import decode
+
+    L = Q.load_library()
+    assert L.qwen3_prefill_workspace_bytes(0) == 0
+    assert L.qwen3_prefill_workspace_bytes((1 << 20) + 1) == 0
+    for n in (1, 3, 37, 512):
+        total = L.qwen3_prefill_workspace_bytes(n)
+        assert total >= n * 30720 and total % 256 == 0
+        spans = sorted((L.qwen3_prefill_workspace_offset(n, name.encode()),
+                        L.qwen3_prefill_workspace_offset(n, name.encode()) + 2 * n * cols)
+                       for name, cols in decode.PREFILL_REGIONS)
+        assert spans[0][0] == 0 and spans[-1][1] <= total
+        for (a0, a1), (b0, _) in zip(spans, spans[1:]):
+            assert a0 % 256 == 0 and a1 <= b0
+    assert L.qwen3_prefill_workspace_offset(4, b"nope") == -1
+    assert L.qwen3_prefill_workspace_offset(0, b"h") == -1
+
+
 @pytest.mark.parametrize("call,code", [
     # layer outside [0, 28)
     (lambda L, w: L.qwen3_decode_layer(w, 28, A16, A16, 8, A16, A16, A16 + 4096, A16, None), 4),
@@ -270,6 +295,25 @@ def test_decode_scratch_layout(Q):
     (lambda L, w: L.qwen3_generate(w, A16, A16, 8, A16, A16, 4, 0, A16, None, A16, None), 3),
     (lambda L, w: L.qwen3_generate(w, A16, A16, 8, A16, A16, -1, 0, A16, A16, A16, None), 6),
     (lambda L, w: L.qwen3_generate(w, A16, A16, 8, A16, A16, 4, 0, A16 + 1, A16, A16, None), 5),
+    # batched prompt ingestion (workspace for 3 tokens: 3 * 30720 bytes)
+    (lambda L, w: L.qwen3_prefill_batched(w, A16, A16, 8, None, 3, A16, A16, None, 0, A16, 1 << 20,
+                                          A16, None), 3),
+    (lambda L, w: L.qwen3_prefill_batched(w, A16, A16, 8, A16, 3, A16, A16, None, 0, None, 1 << 20,
+                                          A16, None), 3),
+    (lambda L, w: L.qwen3_prefill_batched(w, A16, A16, 8, A16, 0, A16, A16, None, 0, A16, 1 << 20,
+                                          A16, None), 6),
+    (lambda L, w: L.qwen3_prefill_batched(w, A16, A16, 8, A16, 9, A16, A16, None, 0, A16, 1 << 20,
+                                          A16, None), 6),
+    (lambda L, w: L.qwen3_prefill_batched(w, A16, A16, 8, A16, 3, A16, A16, None, 0, A16 + 16,
+                                          1 << 20, A16, None), 5),
+    (lambda L, w: L.qwen3_prefill_batched(w, A16, A16, 8, A16, 3, A16, A16, A16 + 2, 0, A16,
+                                          1 << 20, A16, None), 5),
+    (lambda L, w: L.qwen3_prefill_batched(w, A16, A16, 8, A16, 3, A16, A16, None, 0, A16,
+                                          3 * 30720 - 1, A16, None), 6),
+    (lambda L, w: L.qwen3_prefill_layer(w, 28, A16, A16, 8, 3, 0, 0, A16, 1 << 20, None), 4),
+    (lambda L, w: L.qwen3_prefill_layer(w, 0, A16, A16, 8, 3, 6, 0, A16, 1 << 20, None), 6),
+    (lambda L, w: L.qwen3_prefill_layer(w, 0, A16, A16, 8, 3, -1, 0, A16, 1 << 20, None), 6),
+    (lambda L, w: L.qwen3_prefill_layer(w, 0, A16, A16, 8, 3, 0, 0, A16 + 128, 1 << 20, None), 5),
 ])
 def test_decode_validation_before_device(Q, call, code):
     L = Q.load_library()

@@ -1,0 +1,241 @@
+"""GPU parity of the batched prompt path (qwen3_prefill_batched /
+qwen3_prefill_layer) against the oracle and against the decode steps.
+
+One layer over n tokens is checked stage by stage, each stage against the
+oracle applied to the GPU's own input of that stage (the workspace keeps every
+intermediate), with the decode step's tolerances:
+
+  xn, fn        rms_norm per token row         within 1 f16 ulp
+  q, k, v       Q8_0 GEMM rows                 GEMV rule per row (2 ulp / 1e-3)
+  q_roped, K    head norm + RoPE at p0 + i     2 ulp + one input ulp
+  V slots       raw v                          bit-exact
+  attn          causal attention over the GPU  2 ulp + 1e-5
+                cache, slots [lo, p0 + i]
+  res, h        GEMM + f16 residual add        propagated GEMV rule
+  act           gate_up GEMM + SwiGLU          propagated GEMV rule + 4 ulp
+
+then the layer's output against the oracle's decode layer run token by token
+(relative L2), and the whole prompt path against the decode-step prompt path
+and the oracle's steps (logits, token, every cache row).
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from test_gpu_decode import (assert_gemv, assert_gemv_add, assert_norm_close, f64,
+                             fill_cache_layer, rope_tol, ulp)
+
+pytestmark = pytest.mark.gpu
+
+MAX_SEQ = 512
+
+
+@pytest.fixture(scope="module")
+def D():
+    from qwen3_iree_amd import decode
+
+    return decode
+
+
+@pytest.fixture(scope="module")
+def dmodel(gpu, D, model_host):
+    m = D.DeviceWeights(model_host)
+    yield m
+    m.free()
+
+
+@pytest.mark.parametrize("layer,n,p0,chunk_local", [
+    (0, 1, 0, False), (3, 37, 0, False), (11, 64, 5, False), (27, 130, 40, False),
+    (7, 20, 9, True), (16, 65, 0, True)])
+def test_prefill_layer_stages(O, gpu, D, dmodel, model_host, layer, n, p0, chunk_local):
+    w = model_host
+    rng = np.random.default_rng(7000 + 100 * layer + n)
+    sess = D.DecodeSession(dmodel, MAX_SEQ)
+    kc = np.zeros((28 * MAX_SEQ, 1024), np.float16)
+    vc = np.zeros_like(kc)
+    fill_cache_layer(sess, layer, p0, rng, kc, vc)
+    h_in = (1.5 * rng.standard_normal((n, 1024))).astype(np.float16)
+    print(f"prefill layer {layer} n {n} p0 {p0} chunk_local {chunk_local}", flush=True)
+    g = sess.prefill_layer(layer, h_in, p0, chunk_local)
+    k_rows, v_rows = sess.cache_rows(layer, 0, MAX_SEQ)
+    lo = p0 if chunk_local else 0
+
+    for i in range(n):
+        pos = p0 + i
+        assert_norm_close(O, g["xn"][i], O.rmsnorm(h_in[i], w.attn_norm[layer]), ("xn", i))
+        assert_gemv(O, w.wq[layer], 2048, 1024, g["xn"][i], g["q"][i], ("q", i))
+        assert_gemv(O, w.wk[layer], 1024, 1024, g["xn"][i], g["k"][i], ("k", i))
+        assert_gemv(O, w.wv[layer], 1024, 1024, g["xn"][i], g["v"][i], ("v", i))
+        qn = O.head_rmsnorm(g["q"][i], w.q_norm[layer])
+        q_want = O.rope(qn, pos)
+        assert (np.abs(f64(g["q_roped"][i]) - f64(q_want)) <= rope_tol(O, qn, q_want)).all(), i
+        kn = O.head_rmsnorm(g["k"][i], w.k_norm[layer])
+        k_want = O.rope(kn, pos)
+        assert (np.abs(f64(k_rows[pos]) - f64(k_want)) <= rope_tol(O, kn, k_want)).all(), i
+        assert np.array_equal(v_rows[pos].view(np.uint16), g["v"][i].view(np.uint16)), i
+        a_want = O.attention(g["q_roped"][i], k_rows[lo:pos + 1], v_rows[lo:pos + 1])
+        d = np.abs(f64(g["attn"][i]) - f64(a_want))
+        assert (d <= 2 * ulp(O, a_want) + 1e-5).all(), (i, d.max())
+        assert_gemv_add(O, h_in[i], w.wo[layer], 1024, 2048, g["attn"][i], g["res"][i], ("res", i))
+        assert_norm_close(O, g["fn"][i], O.rmsnorm(g["res"][i], w.ffn_norm[layer]), ("fn", i))
+        gu = O.q8_gemv(w.wgu[layer], 6144, 1024, g["fn"][i])
+        _, gmag = O.q8_gemv_f64(w.wgu[layer], 6144, 1024, g["fn"][i])
+        act_want = O.swiglu(gu[:3072], gu[3072:])
+        dg = 2 * ulp(O, gu) + 1e-3 * np.abs(f64(gu)) + 8 * 2.0 ** -24 * gmag
+        gate, up = f64(gu[:3072]), f64(gu[3072:])
+        silu = gate / (1 + np.exp(-gate))
+        tol = 1.1 * np.abs(up) * dg[:3072] + np.abs(silu) * dg[3072:] + 4 * ulp(O, act_want)
+        d = np.abs(f64(g["act"][i]) - f64(act_want))
+        assert (d <= tol).all(), (i, np.flatnonzero(d > tol)[:8], d.max())
+        assert_gemv_add(O, g["res"][i], w.wdn[layer], 1024, 3072, g["act"][i], g["h"][i], ("h", i))
+
+    # slots outside [p0, p0 + n) untouched
+    base = layer * MAX_SEQ
+    assert np.array_equal(k_rows[:p0], kc[base:base + p0])
+    assert np.array_equal(v_rows[:p0], vc[base:base + p0])
+    assert not k_rows[p0 + n:].any() and not v_rows[p0 + n:].any()
+
+    if not chunk_local or p0 == 0:
+        # the layer against the oracle's decode layer, token after token
+        h_ref = np.empty_like(h_in)
+        for i in range(n):
+            h_ref[i], _ = O.decode_layer(w, layer, kc, vc, MAX_SEQ, p0 + i, h_in[i])
+        rel = np.linalg.norm(f64(g["h"]) - f64(h_ref)) / np.linalg.norm(f64(h_ref))
+        assert rel < 5e-3, rel
+    sess.free()
+
+
+def _steps_logits(D, dmodel, prompt, p0_prompt=None):
+    """The decode-step path: prompt[:-1] as steps, the last token as a step
+    with logits.  Returns (session, logits)."""
+    sess = D.DecodeSession(dmodel, MAX_SEQ)
+    sess.set_state(0, 0)
+    if p0_prompt is not None:
+        sess.prefill(p0_prompt)
+    start = sess.get_state()[1]
+    if len(prompt) > 1:
+        sess.prefill(prompt[:-1])
+    sess.set_state(int(prompt[-1]), start + len(prompt) - 1)
+    sess.step(advance=True, logits=True)
+    return sess, sess.read_logits()
+
+
+def _compare_sessions(a, b, la, lb, n_slots):
+    dl = np.abs(f64(la) - f64(lb))
+    assert np.linalg.norm(dl) / np.linalg.norm(f64(lb)) < 2e-2
+    srt = np.sort(f64(lb))
+    ta, tb = a.get_state()[0], b.get_state()[0]
+    if srt[-1] - srt[-2] > 2 * dl.max():
+        assert ta == tb, (ta, tb, srt[-1] - srt[-2], dl.max())
+    assert a.get_state()[1] == b.get_state()[1]
+    for layer in range(28):
+        ka, va = a.cache_rows(layer, 0, n_slots)
+        kb, vb = b.cache_rows(layer, 0, n_slots)
+        for x, y in ((ka, kb), (va, vb)):
+            rel = np.linalg.norm(f64(x) - f64(y)) / np.linalg.norm(f64(y))
+            assert rel < 2e-2, (layer, rel)
+
+
+@pytest.mark.parametrize("n", [1, 7, 45])
+def test_prefill_batched_matches_decode_steps(gpu, D, dmodel, n):
+    rng = np.random.default_rng(50 + n)
+    prompt = rng.integers(0, D.VOCAB, n).astype(np.int32)
+    print(f"prefill batched n {n}", flush=True)
+    a = D.DecodeSession(dmodel, MAX_SEQ)
+    a.set_state(0, 0)
+    a.prefill_batched(prompt, logits=True)
+    la = a.read_logits()
+    assert a.get_state()[1] == n and a.status() == 0
+    # token = lowest index of the maximal f16 logit
+    lf = la.astype(np.float32)
+    assert a.get_state()[0] == int(np.flatnonzero(lf == lf.max())[0])
+    b, lb = _steps_logits(D, dmodel, prompt)
+    _compare_sessions(a, b, la, lb, n)
+    a.free()
+    b.free()
+
+
+def test_prefill_batched_matches_oracle_steps(O, gpu, D, dmodel, model_host):
+    w = model_host
+    prompt = np.array([151643, 9707, 11, 1879, 0, 151935], np.int32)
+    sess = D.DecodeSession(dmodel, MAX_SEQ)
+    sess.set_state(0, 0)
+    sess.prefill_batched(prompt, logits=True)
+    logits = sess.read_logits()
+    kc = np.zeros((28 * MAX_SEQ, 1024), np.float16)
+    vc = np.zeros_like(kc)
+    for i, t in enumerate(prompt):
+        ref_tok, ref_logits, _ = O.decode_step(w, kc, vc, MAX_SEQ, int(t), i, True)
+    dl = np.abs(f64(logits) - f64(ref_logits))
+    assert np.linalg.norm(dl) / np.linalg.norm(f64(ref_logits)) < 2e-2
+    srt = np.sort(f64(ref_logits))
+    if srt[-1] - srt[-2] > 2 * dl.max():
+        assert sess.get_state()[0] == ref_tok
+    for layer in (0, 13, 27):
+        k, v = sess.cache_rows(layer, 0, len(prompt))
+        base = layer * MAX_SEQ
+        for x, y in ((k, kc[base:base + len(prompt)]), (v, vc[base:base + len(prompt)])):
+            assert np.linalg.norm(f64(x) - f64(y)) / np.linalg.norm(f64(y)) < 2e-2
+    sess.free()
+
+
+def test_prefill_batched_continues_a_sequence(gpu, D, dmodel):
+    """A second prompt after a first one attends to the whole cache (the
+    decode steps' semantics)."""
+    rng = np.random.default_rng(77)
+    first = rng.integers(0, D.VOCAB, 10).astype(np.int32)
+    second = rng.integers(0, D.VOCAB, 13).astype(np.int32)
+    a = D.DecodeSession(dmodel, MAX_SEQ)
+    a.set_state(0, 0)
+    a.prefill_batched(first)
+    a.prefill_batched(second, logits=True)
+    la = a.read_logits()
+    assert a.get_state()[1] == 23
+    b, lb = _steps_logits(D, dmodel, second, p0_prompt=first)
+    _compare_sessions(a, b, la, lb, 23)
+    a.free()
+    b.free()
+
+
+def test_prefill_batched_chunk_local_ignores_history(gpu, D, dmodel):
+    """chunk_local: a prompt at p0 > 0 gives what the same prompt gives at
+    position 0 in a fresh cache, up to RoPE's position dependence, which
+    cancels in q.k for equal relative offsets: the logits match."""
+    rng = np.random.default_rng(78)
+    hist = rng.integers(0, D.VOCAB, 9).astype(np.int32)
+    prompt = rng.integers(0, D.VOCAB, 11).astype(np.int32)
+    a = D.DecodeSession(dmodel, MAX_SEQ)
+    a.set_state(0, 0)
+    a.prefill_batched(hist)
+    a.prefill_batched(prompt, chunk_local=True, logits=True)
+    la = a.read_logits()
+    b = D.DecodeSession(dmodel, MAX_SEQ)
+    b.set_state(0, 0)
+    b.prefill_batched(prompt, logits=True)
+    lb = b.read_logits()
+    rel = np.linalg.norm(f64(la) - f64(lb)) / np.linalg.norm(f64(lb))
+    assert rel < 2e-2, rel
+    # and it differs from attending to the history
+    c = D.DecodeSession(dmodel, MAX_SEQ)
+    c.set_state(0, 0)
+    c.prefill_batched(hist)
+    c.prefill_batched(prompt, logits=True)
+    lc = c.read_logits()
+    assert np.linalg.norm(f64(lc) - f64(lb)) / np.linalg.norm(f64(lb)) > 2e-2
+    for s in (a, b, c):
+        s.free()
+
+
+def test_prefill_batched_cache_edges(gpu, D, dmodel):
+    from qwen3_iree_amd import q8gemv as Q
+
+    sess = D.DecodeSession(dmodel, 16)
+    sess.set_state(0, 6)
+    sess.prefill_batched(np.arange(10, dtype=np.int32))  # fills slots 6..15
+    tok, pos = sess.get_state()
+    assert pos == 15 and sess.status() & 1 and 0 <= tok < D.VOCAB
+    sess.set_state(0, 7)
+    with pytest.raises(Q.Q8GemvError, match="exceed max_seq"):
+        sess.prefill_batched(np.arange(10, dtype=np.int32))
+    sess.free()
