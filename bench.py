@@ -17,8 +17,11 @@ pattern still rotates through the 28 layers).  Measured in the same run:
     gate_up, down) + vocab, stream-ordered, replayed from a hipGraph;
   * the full decode step (qwen3_decode_step: embedding, 28 layers with
     attention over a 1024-position KV cache, final norm, vocab, argmax) on
-    random-init Qwen3-0.6B weights, replayed from a hipGraph with the token
-    fed back on the device, checked against the oracle's step;
+    random-init Qwen3-0.6B weights, as one cooperative launch per step and as
+    a hipGraph of 143 per-phase launches, the token fed back on the device,
+    checked against the oracle's step;
+  * batched prompt ingestion (qwen3_prefill_batched) of 512 tokens, checked
+    against the decode-step prompt path;
   * parity of all 140 sweep outputs and of the vocab logits/token against the
     CPU oracle;
   * the CPU oracle on a bounded sample of the same sweep (cpu_baseline).
@@ -167,6 +170,89 @@ def bench_decode(Q, O, stream, args) -> dict:
             "token": step_tok, "oracle_token": ref_tok, "parity_ok": bool(step_ok)}
 
 
+def prefill_flops(n: int) -> tuple[int, int]:
+    """(GEMM flops, attention flops) of a prompt of n tokens from position 0."""
+    per_token = 2 * (2048 * 1024 + 2 * 1024 * 1024 + 1024 * 2048 + 6144 * 1024 + 1024 * 3072)
+    gemm = 28 * n * per_token
+    attn = 28 * 16 * 128 * 4 * (n * (n + 1) // 2)  # q.k and p.v over positions 0..i
+    return gemm, attn
+
+
+def bench_prefill(Q, stream, args) -> dict:
+    """Batched prompt ingestion (qwen3_prefill_batched) of args.prefill_tokens
+    tokens from position 0, checked against the decode-step prompt path, then
+    timed as whole calls (host wall clock, the call's own position read
+    included)."""
+    from qwen3_iree_amd import decode as D
+
+    n = args.prefill_tokens
+    mhost = D.synthetic_weights(seed=SEED, workers=16)
+    model = D.DeviceWeights(mhost)
+    sess = D.DecodeSession(model, n, stream)
+    rng = np.random.default_rng(SEED + 9)
+    prompt = rng.integers(0, D.VOCAB, n).astype(np.int32)
+    pbuf = Q.DeviceBuffer.from_array(prompt)
+    lib = Q.load_library()
+    nbytes = int(lib.qwen3_prefill_workspace_bytes(n))
+    ws = Q.DeviceBuffer(nbytes)
+
+    def one(logits=None):
+        # the previous call's kernels write the position on `stream`; the call
+        # itself waits for the stream anyway (it reads the position first)
+        stream.synchronize()
+        sess.set_state(0, 0)
+        Q._call("qwen3_prefill_batched", model.ref(), sess.k_cache.ptr, sess.v_cache.ptr, n,
+                pbuf.ptr, n, sess.token_ptr, sess.pos_ptr, logits, 0, ws.ptr, nbytes,
+                sess.scratch.ptr, Q._stream(stream))
+
+    # parity against the decode-step path on the same prompt
+    one(sess.logits.ptr)
+    stream.synchronize()
+    la = sess.read_logits()
+    tok_b = sess.get_state()[0]
+    ref = D.DecodeSession(model, n, stream)
+    ref.set_state(0, 0)
+    t0 = time.perf_counter()
+    if n > 1:
+        ref.prefill(prompt[:-1])
+    ref.set_state(int(prompt[-1]), n - 1)
+    ref.step(advance=True, logits=True)
+    ref.synchronize()
+    steps_ms = (time.perf_counter() - t0) * 1e3
+    lb = ref.read_logits()
+    tok_s = ref.get_state()[0]
+    dl = np.abs(la.astype(np.float64) - lb.astype(np.float64))
+    rel = float(np.linalg.norm(dl) / np.linalg.norm(lb.astype(np.float64)))
+    srt = np.sort(lb.astype(np.float64))
+    margin = float(srt[-1] - srt[-2])
+    ok = rel < 2e-2 and (tok_b == tok_s or margin <= 2 * dl.max())
+    ref.free()
+    log(f"prefill parity: token {tok_b} (decode steps {tok_s}, margin {margin:.4f}), logits rel L2 "
+        f"{rel:.2e}")
+    for _ in range(3):
+        one()
+    stream.synchronize()
+    reps = max(5, min(50, args.steps // 20))
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        one()
+    stream.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / reps
+    gemm, attn = prefill_flops(n)
+    log(f"prefill of {n} tokens: {ms:.3f} ms = {n / ms * 1e3:.0f} tok/s, "
+        f"{(gemm + attn) / ms / 1e9:.1f} TFLOP/s; as decode steps {steps_ms:.1f} ms")
+    ws.free()
+    pbuf.free()
+    sess.free()
+    model.free()
+    return {"tokens": n, "ms": round(ms, 3), "tok_per_s": round(n / ms * 1e3, 1),
+            "gemm_flops": gemm, "attention_flops": attn,
+            "TFLOPs": round((gemm + attn) / ms / 1e9, 2),
+            "decode_steps_ms": round(steps_ms, 2), "speedup_vs_steps": round(steps_ms / ms, 1),
+            "logits_rel_l2_vs_steps": rel, "token": tok_b, "steps_token": tok_s,
+            "parity_ok": bool(ok)}
+
+
 def bench_gguf(Q, tmpdir: Path) -> dict:
     """GGUF -> HostWeights -> device: throughput of each stage on the full-size
     synthetic checkpoint (1.09 GB of parameters)."""
@@ -215,6 +301,13 @@ def main() -> int:
                     help="positions attended by the timed decode step")
     ap.add_argument("--decode-only", action="store_true",
                     help="run only the full decode step and print its JSON line")
+    ap.add_argument("--step-mode", type=int, choices=(0, 1), default=None,
+                    help="decode step mode for the whole run (0: per-phase launches, 1: one "
+                         "cooperative launch; default: the library's)")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="run only batched prompt ingestion and print its JSON line")
+    ap.add_argument("--prefill-tokens", type=int, default=512,
+                    help="prompt length of the batched prompt ingestion measurement")
     ap.add_argument("--gguf-ingest", metavar="DIR", default=None,
                     help="only measure GGUF ingestion: write the synthetic model as a Q8_0 GGUF "
                          "under DIR, read it back into the device layout (cold, then warm page "
@@ -246,11 +339,18 @@ def main() -> int:
     sys.path.insert(0, str(REPO / "oracle"))
     import oracle as O  # the checker; also the CPU baseline below
 
+    if args.step_mode is not None:
+        from qwen3_iree_amd import decode as D
+
+        D.set_step_mode(args.step_mode)
     if args.gguf_ingest:
         print(json.dumps({"gguf_ingest": bench_gguf(Q, Path(args.gguf_ingest))}), flush=True)
         return 0
     if args.decode_only:
         print(json.dumps({"decode_step": bench_decode(Q, O, Q.Stream(), args)}), flush=True)
+        return 0
+    if args.prefill_only:
+        print(json.dumps({"prefill": bench_prefill(Q, Q.Stream(), args)}), flush=True)
         return 0
 
     # ---------------------------------------------------------------- inputs
@@ -379,6 +479,7 @@ def main() -> int:
 
     # ------------------------------------------- full decode step (C5)
     dec = bench_decode(Q, O, stream, args)
+    pre = bench_prefill(Q, stream, args)
     step_ok = dec["parity_ok"]
 
     parity_ok = fails == 0 and rep_v["fail"] == 0 and token == own and step_ok
@@ -454,6 +555,7 @@ def main() -> int:
                              "dispatches": 4 * layers + 2,
                              "launch": "eager" if args.no_graph else "hipGraph"},
         "decode_step": dec,
+        "prefill": pre,
         "parity_ok": bool(parity_ok),
         "copy_calibration": copy_cal,
         "cpu_baseline": cpu,
