@@ -178,6 +178,55 @@ __device__ __forceinline__ void rope_angles(int pos, float (&cs)[2], float (&sn)
   }
 }
 
+// Position range [start, end) of attention split s (of kAttnSplits) over ctx
+// = pos + 1 positions, and the last row a clamped load may touch.
+struct SplitRange {
+  int start, end, last;
+};
+__device__ __forceinline__ SplitRange split_range(int s, int pos) {
+  const int ctx = pos + 1;
+  SplitRange r;
+  r.start = (int)((int64_t)s * ctx / kAttnSplits);
+  r.end = (int)((int64_t)(s + 1) * ctx / kAttnSplits);
+  r.last = r.end - 1 > 0 ? r.end - 1 : 0;
+  return r;
+}
+
+// Bytes of one wave's prefetched first chunk: K (32 rows x this lane's half
+// row, 8 x 1 KiB) then V (32 rows x the lane's two dims, 32 x 256 B).
+constexpr int kKvPrefetchBytes = 8 * 1024 + 32 * 256;
+
+// The first chunk of a split's cache rows (the loads attention_group's step 0
+// issues) copied into LDS by the memory system (global_load_lds), so no
+// register holds them while they are in flight: lane l's K piece m lands at
+// kv + 1024 m + 16 l, its V word of row j at kv + 8192 + 256 j + 4 l.  kv is
+// the wave's kKvPrefetchBytes region; the data may be read once the wave's
+// vector memory counter has drained past these loads.
+__device__ __forceinline__ void kv_prefetch(uint8_t* kv, const uint16_t* __restrict__ k_cache,
+                                            const uint16_t* __restrict__ v_cache, int g,
+                                            const SplitRange& r) {
+  const int lane = threadIdx.x & 63;
+  const int half = lane >> 5;
+  const int pl = lane & 31;
+  const int p = r.start + pl < r.last ? r.start + pl : r.last;
+  const u32x4* krow = reinterpret_cast<const u32x4*>(
+      k_cache + ((size_t)p * kKvHeads + g) * kHeadDim + 64 * half);
+#pragma unroll
+  for (int m = 0; m < 8; ++m)
+    __builtin_amdgcn_global_load_lds((const GLOBAL_AS void*)(krow + m),
+                                     (__attribute__((address_space(3))) void*)(kv + 1024 * m), 16,
+                                     0, 0);
+#pragma unroll
+  for (int j = 0; j < 32; ++j) {
+    const int pj = r.start + j < r.last ? r.start + j : r.last;
+    __builtin_amdgcn_global_load_lds(
+        (const GLOBAL_AS void*)(reinterpret_cast<const uint32_t*>(
+                                    v_cache + ((size_t)pj * kKvHeads + g) * kHeadDim) +
+                                lane),
+        (__attribute__((address_space(3))) void*)(kv + 8192 + 256 * j), 4, 0, 0);
+  }
+}
+
 // LDS of one attention workgroup.
 struct AttnLds {
   float xs[kAttnWaves][3][kHeadDim];  // normed q_A, q_B, k (f16 values)
@@ -194,6 +243,8 @@ struct AttnLds {
 //  0. the split's first 32 cache rows (K: half a row per lane, V: the lane's
 //     two dims for each of the 32 positions) are requested before q/k/v are
 //     fetched (get_qkv), so their latency overlaps that wait and steps 1-2;
+//     with kv != null they were prefetched into LDS (kv_prefetch, this wave's
+//     region) and are read from there;
 //  1. q heads 2g, 2g+1 and k head g: per-head rms_norm with q_norm / k_norm
 //     (qwen3_full.mlir:648-702), then RoPE (:324-454) at position pos;
 //  2. the wave owning position pos writes the roped k and the raw v to cache
@@ -219,7 +270,8 @@ __device__ __forceinline__ void attention_group(AttnLds& L, int g, int sg, int p
                                                 const uint16_t* __restrict__ kn_w,
                                                 uint16_t* __restrict__ k_cache,
                                                 uint16_t* __restrict__ v_cache,
-                                                uint16_t* __restrict__ q_roped, GetQKV&& get_qkv,
+                                                uint16_t* __restrict__ q_roped,
+                                                const uint8_t* kv, GetQKV&& get_qkv,
                                                 Publish&& publish) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -234,14 +286,15 @@ __device__ __forceinline__ void attention_group(AttnLds& L, int g, int sg, int p
 
   const int pos = pos_raw < 0 ? 0 : (pos_raw >= max_seq ? max_seq - 1 : pos_raw);
   const int ctx = pos + 1;
-  const int start = (int)((int64_t)s * ctx / kAttnSplits);
-  const int end = (int)((int64_t)(s + 1) * ctx / kAttnSplits);
+  const SplitRange sr = split_range(s, pos);
+  const int start = sr.start;
+  const int end = sr.end;
   const int n_chunks = ((ctx + kAttnSplits - 1) / kAttnSplits + 31) / 32;  // workgroup-uniform
 
   // ---- 0. first chunk of the cache ----
   // Every lane issues every load (rows clamped into [start, end - 1], row 0
   // for an empty split) so the compiler's waits stay exact.
-  const int last = end - 1 > 0 ? end - 1 : 0;
+  const int last = sr.last;
   u32x4 kreg[8];
   uint32_t vreg[32];
   auto load_chunk = [&](int c0) {
@@ -257,11 +310,20 @@ __device__ __forceinline__ void attention_group(AttnLds& L, int g, int sg, int p
           reinterpret_cast<const uint32_t*>(v_cache + ((size_t)pj * kKvHeads + g) * kHeadDim) + lane);
     }
   };
-  load_chunk(start);
+  if (kv == nullptr) load_chunk(start);
   __builtin_amdgcn_sched_barrier(0);
 
   uint32_t xw[3], v_new;
   get_qkv(xw, v_new);
+  if (kv != nullptr) {  // the first chunk was prefetched into LDS (kv_prefetch)
+    // read after get_qkv's wait, when every earlier memory operation of the
+    // wave (the prefetch included) has completed
+#pragma unroll
+    for (int m = 0; m < 8; ++m) kreg[m] = *reinterpret_cast<const u32x4*>(kv + 1024 * m + 16 * lane);
+#pragma unroll
+    for (int j = 0; j < 32; ++j)
+      vreg[j] = *reinterpret_cast<const uint32_t*>(kv + 8192 + 256 * j + 4 * lane);
+  }
 
   // ---- 1. head norms: lane owns dims 2*lane, 2*lane+1 ----
 #pragma unroll

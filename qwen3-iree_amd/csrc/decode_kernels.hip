@@ -89,7 +89,7 @@ extern "C" __global__ __launch_bounds__(256) void dec_attention(
   float cs[2], sn[2];
   rope_angles(pos_raw < 0 ? 0 : (pos_raw >= max_seq ? max_seq - 1 : pos_raw), cs, sn);
   attention_group(
-      lds, g, sg, pos_raw, cs, sn, max_seq, qn_w, kn_w, k_cache, v_cache, q_roped,
+      lds, g, sg, pos_raw, cs, sn, max_seq, qn_w, kn_w, k_cache, v_cache, q_roped, nullptr,
       [&](uint32_t (&xw)[3], uint32_t& v_new) {
         xw[0] = load_global(reinterpret_cast<const uint32_t*>(q_raw + (2 * g) * kHeadDim) + lane);
         xw[1] = load_global(reinterpret_cast<const uint32_t*>(q_raw + (2 * g + 1) * kHeadDim) + lane);
@@ -472,9 +472,18 @@ extern "C" __global__ __launch_bounds__(256) void dec_step(StepParams P) {
   const uint16_t* emb = P.token_embd + (size_t)tok * kHidden;
   const Waiter W{P.abort_word, P.status, seq, &s_abort};
   float rope_cs[2], rope_sn[2];  // the position's RoPE angles, for every layer
-  if (wg < 64)
-    rope_angles(pos_raw < 0 ? 0 : (pos_raw >= P.max_seq ? P.max_seq - 1 : pos_raw), rope_cs,
-                rope_sn);
+  // Attention workgroups keep the first 32 cache rows of their split for the
+  // next layer in LDS: requested (global_load_lds) as soon as the current
+  // layer's attention is done, they arrive while the workgroup works on other
+  // phases (layer 0's at the start).
+  __shared__ __attribute__((aligned(16))) uint8_t kv_lds[kAttnWaves * kKvPrefetchBytes];
+  uint8_t* const kv_mine = kv_lds + wave * kKvPrefetchBytes;
+  const int pos_c = pos_raw < 0 ? 0 : (pos_raw >= P.max_seq ? P.max_seq - 1 : pos_raw);
+  const SplitRange my_split = split_range((wg % kAttnGroups) * kAttnWaves + wave, pos_c);
+  if (wg < 64) {
+    kv_prefetch(kv_mine, P.k_cache, P.v_cache, wg / kAttnGroups, my_split);
+    rope_angles(pos_c, rope_cs, rope_sn);
+  }
   __syncthreads();
 
   for (int layer = 0; layer < kLayers; ++layer) {
@@ -519,7 +528,7 @@ extern "C" __global__ __launch_bounds__(256) void dec_step(StepParams P) {
       attention_group(
           L, g, sg, pos_raw, rope_cs, rope_sn, P.max_seq, P.q_norm + layer * kHeadDim,
           P.k_norm + layer * kHeadDim,
-          P.k_cache + cache_layer, P.v_cache + cache_layer, nullptr,
+          P.k_cache + cache_layer, P.v_cache + cache_layer, nullptr, kv_mine,
           [&](uint32_t (&xw)[3], uint32_t& v_new) {
             // q heads 2g, 2g+1 (words 128g..), k head g, v head g (words 64g..)
             ok = W.wait_map(256, tq, vec, [&](int i) {
@@ -570,6 +579,10 @@ extern "C" __global__ __launch_bounds__(256) void dec_step(StepParams P) {
                    step_tag(seq, layer, kPhAtt));
         }
         __syncthreads();  // vec is reused by the next wait
+      }
+      if (layer + 1 < kLayers) {  // the next layer's first chunk, into this wave's LDS region
+        const int64_t next = (int64_t)(layer + 1) * P.max_seq * (kKvHeads * kHeadDim);
+        kv_prefetch(kv_mine, P.k_cache + next, P.v_cache + next, g, my_split);
       }
     }
 
