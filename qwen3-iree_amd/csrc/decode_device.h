@@ -229,9 +229,8 @@ __device__ __forceinline__ void kv_prefetch(uint8_t* kv, const uint16_t* __restr
 
 // LDS of one attention workgroup.
 struct AttnLds {
-  float xs[kAttnWaves][3][kHeadDim];  // normed q_A, q_B, k (f16 values)
-  uint32_t qh[kAttnWaves][2][64];     // roped q_A, q_B as f16 pairs
-  uint32_t kh[kAttnWaves][64];        // roped new k as f16 pairs
+  uint32_t qh[2][64];  // roped q_A, q_B as f16 pairs
+  uint32_t kh[64];     // roped new k as f16 pairs
   float pbuf[kAttnWaves][2][32];
   float mrg[kAttnWaves][2][2 + kHeadDim];
 };
@@ -245,11 +244,13 @@ struct AttnLds {
 //     fetched (get_qkv), so their latency overlaps that wait and steps 1-2;
 //     with kv != null they were prefetched into LDS (kv_prefetch, this wave's
 //     region) and are read from there;
-//  1. q heads 2g, 2g+1 and k head g: per-head rms_norm with q_norm / k_norm
-//     (qwen3_full.mlir:648-702), then RoPE (:324-454) at position pos;
-//  2. the wave owning position pos writes the roped k and the raw v to cache
-//     slot pos (k_cache / v_cache: the layer's base; slot layout [max_seq, 8,
-//     128]); split 0 stores the roped q heads to q_roped when it is not null;
+//  1. waves 0, 1, 2 take q head 2g, q head 2g+1 and k head g: per-head
+//     rms_norm with q_norm / k_norm (qwen3_full.mlir:648-702), then RoPE
+//     (:324-454) at position pos, shared with the other waves through LDS;
+//  2. the workgroup whose splits hold position pos writes the roped k (wave
+//     2) and the raw v (wave 3) to cache slot pos (k_cache / v_cache: the
+//     layer's base; slot layout [max_seq, 8, 128]); split group 0 stores the
+//     roped q heads to q_roped when it is not null;
 //  3. chunks of 32 positions: lane (j, half) scores position j of the chunk
 //     on dims [64*half, 64*half + 64) for both q heads, the halves meet in one
 //     cross-half add; s_j = (q . k_j) * rsqrt(128); online softmax; the
@@ -289,6 +290,9 @@ __device__ __forceinline__ void attention_group(AttnLds& L, int g, int sg, int p
   const SplitRange sr = split_range(s, pos);
   const int start = sr.start;
   const int end = sr.end;
+  // this workgroup's four splits hold position pos: it writes the new k / v
+  const bool owns_pos = split_range(sg * kAttnWaves, pos).start <= pos &&
+                        pos < split_range(sg * kAttnWaves + kAttnWaves - 1, pos).end;
   const int n_chunks = ((ctx + kAttnSplits - 1) / kAttnSplits + 31) / 32;  // workgroup-uniform
 
   // ---- 0. first chunk of the cache ----
@@ -325,52 +329,46 @@ __device__ __forceinline__ void attention_group(AttnLds& L, int g, int sg, int p
       vreg[j] = *reinterpret_cast<const uint32_t*>(kv + 8192 + 256 * j + 4 * lane);
   }
 
-  // ---- 1. head norms: lane owns dims 2*lane, 2*lane+1 ----
-#pragma unroll
-  for (int t = 0; t < 3; ++t) {
-    const f16x2 xv = as_f16x2(xw[t]);
-    const f16x2 wv = as_f16x2(nwv[t]);
+  // ---- 1. head norms + RoPE: wave t < 3 takes vector t (q head 2g, q head
+  // 2g+1, k head g), lane owns dims 2*lane, 2*lane+1; RoPE's partner dims
+  // d -+ 64 sit in lane ^ 32 ----
+  if (wave < 3) {
+    const f16x2 xv = as_f16x2(wave == 0 ? xw[0] : (wave == 1 ? xw[1] : xw[2]));
+    const f16x2 wv = as_f16x2(wave == 2 ? nwv[2] : nwv[0]);
     const float a = (float)xv.x, b = (float)xv.y;
     float ss = a * a;
     ss = ss + b * b;
     ss = wave_sum(ss);
     const float r = sqrtf(ss / 128.0f + kEps);
-    L.xs[wave][t][2 * lane] = (float)to_f16((a / r) * (float)wv.x);
-    L.xs[wave][t][2 * lane + 1] = (float)to_f16((b / r) * (float)wv.y);
-  }
-  __syncthreads();
-
-  // ---- 1b. RoPE (rotate-half) ----
-  uint32_t roped[3];
-#pragma unroll
-  for (int t = 0; t < 3; ++t) {
+    float xs[2];
+    xs[0] = (float)to_f16((a / r) * (float)wv.x);
+    xs[1] = (float)to_f16((b / r) * (float)wv.y);
     float r2[2];
 #pragma unroll
     for (int dd = 0; dd < 2; ++dd) {
-      const int d = 2 * lane + dd;
-      if (d < 64) {
-        const float a = L.xs[wave][t][d] * cs[dd];
-        const float b = L.xs[wave][t][d + 64] * sn[dd];
-        r2[dd] = a - b;
+      const float other = __shfl_xor(xs[dd], 32, 64);
+      if (lane < 32) {
+        const float u = xs[dd] * cs[dd];
+        const float w2 = other * sn[dd];
+        r2[dd] = u - w2;
       } else {
-        const float a = L.xs[wave][t][d - 64] * sn[dd];
-        const float b = L.xs[wave][t][d] * cs[dd];
-        r2[dd] = a + b;
+        const float u = other * sn[dd];
+        const float w2 = xs[dd] * cs[dd];
+        r2[dd] = u + w2;
       }
     }
-    roped[t] = pack_f16x2(r2[0], r2[1]);
-  }
-  L.qh[wave][0][lane] = roped[0];
-  L.qh[wave][1][lane] = roped[1];
-  L.kh[wave][lane] = roped[2];
-
-  // ---- 2. the new position into the cache, the roped q heads once ----
-  if (q_roped != nullptr && s == 0) {
-    reinterpret_cast<uint32_t*>(q_roped + (2 * g) * kHeadDim)[lane] = roped[0];
-    reinterpret_cast<uint32_t*>(q_roped + (2 * g + 1) * kHeadDim)[lane] = roped[1];
-  }
-  if (start <= pos && pos < end) {
-    reinterpret_cast<uint32_t*>(k_cache + ((size_t)pos * kKvHeads + g) * kHeadDim)[lane] = roped[2];
+    const uint32_t roped = pack_f16x2(r2[0], r2[1]);
+    // ---- 2. the roped q heads once, the new position into the cache ----
+    if (wave < 2) {
+      L.qh[wave][lane] = roped;
+      if (q_roped != nullptr && sg == 0)
+        reinterpret_cast<uint32_t*>(q_roped + (2 * g + wave) * kHeadDim)[lane] = roped;
+    } else {
+      L.kh[lane] = roped;
+      if (owns_pos)
+        reinterpret_cast<uint32_t*>(k_cache + ((size_t)pos * kKvHeads + g) * kHeadDim)[lane] = roped;
+    }
+  } else if (owns_pos) {
     reinterpret_cast<uint32_t*>(v_cache + ((size_t)pos * kKvHeads + g) * kHeadDim)[lane] = v_new;
   }
   __syncthreads();
@@ -392,9 +390,9 @@ __device__ __forceinline__ void attention_group(AttnLds& L, int g, int sg, int p
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int i = 32 * half + 4 * mm + j;
-        const f16x2 kv = as_f16x2(is_new ? L.kh[wave][i] : kreg[mm][j]);
-        dA = __builtin_amdgcn_fdot2(as_f16x2(L.qh[wave][0][i]), kv, dA, false);
-        dB = __builtin_amdgcn_fdot2(as_f16x2(L.qh[wave][1][i]), kv, dB, false);
+        const f16x2 kv = as_f16x2(is_new ? L.kh[i] : kreg[mm][j]);
+        dA = __builtin_amdgcn_fdot2(as_f16x2(L.qh[0][i]), kv, dA, false);
+        dB = __builtin_amdgcn_fdot2(as_f16x2(L.qh[1][i]), kv, dB, false);
       }
     }
     dA = dA + __shfl_xor(dA, 32, 64);
