@@ -97,7 +97,27 @@ __device__ __forceinline__ void rmsnorm_cols(const uint16_t* __restrict__ h,
   rmsnorm_apply(hv, wv, xr);
 }
 
+// The norm weights of columns col(m), loaded ahead of the vector they scale.
+template <class ColOf>
+__device__ __forceinline__ void norm_weights(const uint16_t* __restrict__ w, ColOf col,
+                                             u32x4 (&wv)[8]) {
+#pragma unroll
+  for (int m = 0; m < 8; ++m) wv[m] = load_global(reinterpret_cast<const u32x4*>(w + col(m)));
+}
+
+// rms_norm of an f16 vector in LDS with norm weights already in registers.
+template <class ColOf>
+__device__ __forceinline__ void rmsnorm_lds_w(const uint16_t* __restrict__ h, ColOf col,
+                                              const u32x4 (&wv)[8], u32x4 (&xr)[8]) {
+  u32x4 hv[8];
+#pragma unroll
+  for (int m = 0; m < 8; ++m) hv[m] = *reinterpret_cast<const u32x4*>(h + col(m));
+  rmsnorm_apply(hv, wv, xr);
+}
+
 // The Q8_0 GEMV lane layout: columns [64 p16, 64 p16 + 64) in 8 pieces of 8.
+__device__ __forceinline__ int gemv_col(int m) { return 64 * (threadIdx.x & 15) + 8 * m; }
+
 template <bool H_LDS>
 __device__ __forceinline__ void rmsnorm_gemv_x(const uint16_t* __restrict__ h,
                                                const uint16_t* __restrict__ w, u32x4 (&xr)[8]) {

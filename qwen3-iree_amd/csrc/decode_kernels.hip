@@ -620,10 +620,11 @@ extern "C" __global__ __launch_bounds__(256) void dec_step(StepParams P) {
       u32x4 bg[QuadShape<1>::LOADS], bu[QuadShape<1>::LOADS];
       q8_quad_load<1>(wl, 2 * kFfn, b, bg);
       q8_quad_load<1>(wl, 2 * kFfn, kFfn / 4 + b, bu);
+      u32x4 wv[8];
+      norm_weights(P.ffn_norm + layer * kHidden, gemv_col, wv);  // requested before the wait
       if (!W.wait(cur + kWRes, 512, step_tag(seq, layer, kPhRes), vec)) return;
       u32x4 xr[1][8];
-      rmsnorm_gemv_x<true>(reinterpret_cast<const uint16_t*>(vec), P.ffn_norm + layer * kHidden,
-                           xr[0]);
+      rmsnorm_lds_w(reinterpret_cast<const uint16_t*>(vec), gemv_col, wv, xr[0]);
       uint8_t* lds = stage + wave * kGemvLds;
       constexpr int LDSB = QuadShape<1>::LDS_BYTES;
       q8_quad_stage<1>(bg, lds);
@@ -670,10 +671,11 @@ extern "C" __global__ __launch_bounds__(256) void dec_step(StepParams P) {
     vocab_body_xp<VOCAB_NT_LOADS != 0, true>(
         P.output_w,
         [&](int li, u32x4 (&xr)[8]) {
+          const auto col = [=](int m) { return 128 * m + 8 * li; };
+          u32x4 wv[8];
+          norm_weights(P.output_norm, col, wv);  // requested before the wait
           ok = W.wait(hfin, 512, tag_h, vec);
-          if (ok)
-            rmsnorm_cols<true>(reinterpret_cast<const uint16_t*>(vec), P.output_norm,
-                               [=](int m) { return 128 * m + 8 * li; }, xr);
+          if (ok) rmsnorm_lds_w(reinterpret_cast<const uint16_t*>(vec), col, wv, xr);
           if (wg == 0 && t < 16) {
 #pragma unroll
             for (int m = 0; m < 8; ++m)
