@@ -291,7 +291,8 @@ extern "C" __global__ __launch_bounds__(256) void dec_scratch_clear(uint32_t* __
 //                     8 partials of its 2 query heads -> ATT words
 //   C  64..127        attn_o quads + residual -> RES words
 //   D  0..63,128..255 gate/up quad pairs + SwiGLU -> ACT words
-//   E  64..127        ffn_down quads + residual -> H words
+//   E  all 256        ffn_down + residual: row quad wg, waves 0-2 one
+//                     1024-column chunk each, summed in LDS -> H words
 // then the vocab GEMV over all workgroups (each publishes its best key as two
 // words), and workgroup 0 reduces the 256 keys: token, optional output slot,
 // position advance, sequence number.  Layer-indexed words alternate between
@@ -477,6 +478,7 @@ extern "C" __global__ __launch_bounds__(256) void dec_step(StepParams P) {
   // layer's attention is done, they arrive while the workgroup works on other
   // phases (layer 0's at the start).
   __shared__ __attribute__((aligned(16))) uint8_t kv_lds[kAttnWaves * kKvPrefetchBytes];
+  __shared__ float e_part[3][64];  // ffn_down: the chunks' lane sums
   uint8_t* const kv_mine = kv_lds + wave * kKvPrefetchBytes;
   const int pos_c = pos_raw < 0 ? 0 : (pos_raw >= P.max_seq ? P.max_seq - 1 : pos_raw);
   const SplitRange my_split = split_range((wg % kAttnGroups) * kAttnWaves + wave, pos_c);
@@ -639,26 +641,34 @@ extern "C" __global__ __launch_bounds__(256) void dec_step(StepParams P) {
                  step_tag(seq, layer, kPhAct));
     }
 
-    // ---- E: ffn_down + residual ----
-    if (wg >= 64 && wg < 128) {
-      const int quad = 4 * (wg - 64) + wave;
+    // ---- E: ffn_down + residual: every workgroup takes row quad wg, wave
+    // c < 3 the quad's chunk c; the chunks' lane sums meet in LDS in chunk
+    // order (the per-phase kernel's order) ----
+    {
+      const int quad = wg;
       constexpr int64_t bpl = (int64_t)kHidden * (kFfn / 32 * 34);
-      u32x4 buf[QuadShape<3>::LOADS];
-      q8_quad_load<3>(P.wdn + layer * bpl, kHidden, quad, buf);
-      if (!W.wait(cur + kWRes + 8 * (wg - 64), 8, step_tag(seq, layer, kPhRes), vec + 1536))
-        return;
-      const int row = 4 * quad + (lane >> 4);
-      const _Float16 r_row =
-          as_half(reinterpret_cast<const uint16_t*>(vec + 1536)[row - 16 * (wg - 64)]);
+      u32x4 buf[QuadShape<1>::LOADS];
+      if (wave < 3) q8_chunk_load<3>(P.wdn + layer * bpl, kHidden, quad, wave, buf);
+      // the quad's 4 residual rows: words 2 quad, 2 quad + 1
+      if (!W.wait(cur + kWRes + 2 * quad, 2, step_tag(seq, layer, kPhRes), vec + 1536)) return;
+      const _Float16 r_row = as_half(reinterpret_cast<const uint16_t*>(vec + 1536)[lane >> 4]);
       if (!W.wait(cur + kWAct, 1536, step_tag(seq, layer, kPhAct), vec)) return;
-      u32x4 xr[3][8];
-      lds_x_cols<3>(reinterpret_cast<const uint16_t*>(vec), xr);
-      uint8_t* lds = stage + wave * kGemvLds;
-      q8_quad_stage<3>(buf, lds);
+      if (wave < 3) {
+        u32x4 xr[1][8];
+        lds_x_cols<1>(reinterpret_cast<const uint16_t*>(vec) + 1024 * wave, xr);
+        uint8_t* lds = stage + wave * kGemvLds;
+        q8_quad_stage<1>(buf, lds);
+        e_part[wave][lane] = q8_quad_lane_dot<1>(lds, xr);
+      }
       __syncthreads();
-      const float acc = q8_quad_dot<3>(lds, xr);
-      put_quad(cur + kWH, quad, acc, step_tag(seq, layer, kPhH),
-               [&](float a, int) { return (uint32_t)residual_f16(r_row, a); });
+      if (wave == 0) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int c = 0; c < 3; ++c) acc += e_part[c][lane];
+        acc = reduce_row16(acc);
+        put_quad(cur + kWH, quad, acc, step_tag(seq, layer, kPhH),
+                 [&](float a, int) { return (uint32_t)residual_f16(r_row, a); });
+      }
     }
   }
 

@@ -321,11 +321,11 @@ __device__ __forceinline__ void q8_quad_stage(const u32x4 (&buf)[QuadShape<P>::L
   for (int i = 0; i < QuadShape<P>::LOADS; ++i) l4[i * 64 + lane] = buf[i];
 }
 
-// Row sum for this lane's row (lane >> 4) of a staged quad; every lane of the
-// row's 16-lane group returns the same value.
+// This lane's share of its row (lane >> 4) of a staged quad: the block-pair
+// dots of chunks 0..P-1 added in chunk order onto 0.
 template <int P>
-__device__ __forceinline__ float q8_quad_dot(const uint8_t* __restrict__ lds,
-                                             const u32x4 (&xr)[P][8]) {
+__device__ __forceinline__ float q8_quad_lane_dot(const uint8_t* __restrict__ lds,
+                                                  const u32x4 (&xr)[P][8]) {
   const int lane = threadIdx.x & 63;
   const int p16 = lane & 15;
   const int rsub = lane >> 4;
@@ -339,7 +339,38 @@ __device__ __forceinline__ float q8_quad_dot(const uint8_t* __restrict__ lds,
     for (int m = 0; m < 17; ++m) d[m] = pp[m];
     acc += q8_pair_dot(d, xr[c]);
   }
-  return reduce_row16(acc);
+  return acc;
+}
+
+// Row sum for this lane's row (lane >> 4) of a staged quad; every lane of the
+// row's 16-lane group returns the same value.
+template <int P>
+__device__ __forceinline__ float q8_quad_dot(const uint8_t* __restrict__ lds,
+                                             const u32x4 (&xr)[P][8]) {
+  return reduce_row16(q8_quad_lane_dot<P>(lds, xr));
+}
+
+// Chunk c (1024 columns) of row quad `quad` of a K = 1024 P matrix, loaded
+// for staging in the one-chunk quad layout (QuadShape<1>): 4 rows of 1088
+// bytes at a row stride of 1088 P.  Pieces past the last valid row re-read
+// the last valid piece, as in q8_quad_load.
+template <int P>
+__device__ __forceinline__ void q8_chunk_load(const uint8_t* __restrict__ w, int n_rows, int quad,
+                                              int c, u32x4 (&buf)[QuadShape<1>::LOADS]) {
+  const int lane = threadIdx.x & 63;
+  const int row0 = quad * 4;
+  int rows_here = n_rows - row0;
+  rows_here = rows_here < 4 ? rows_here : 4;
+  const int last = rows_here * 68 - 1;
+  const uint8_t* base = w + (size_t)row0 * (kChunkBytes * P) + kChunkBytes * c;
+#pragma unroll
+  for (int i = 0; i < QuadShape<1>::LOADS; ++i) {
+    int j = i * 64 + lane;
+    j = j < last ? j : last;
+    const int r = j / 68;
+    buf[i] = load_stream<Q8_NT_LOADS>(
+        reinterpret_cast<const u32x4*>(base + (size_t)r * (kChunkBytes * P) + 16 * (j - 68 * r)));
+  }
 }
 
 // x for this lane's 64 columns of each chunk straight from global memory.
