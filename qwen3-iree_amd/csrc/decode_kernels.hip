@@ -289,7 +289,8 @@ extern "C" __global__ __launch_bounds__(256) void dec_scratch_clear(uint32_t* __
 //                     (attention_group, q/k/v from the tagged words) -> PART
 //   B' 0,8,..,56      the split-group-0 workgroup of each kv head merges the
 //                     8 partials of its 2 query heads -> ATT words
-//   C  64..127        attn_o quads + residual -> RES words
+//   C  64..191        attn_o + residual: 2 row quads per workgroup, one
+//                     1024-column chunk per wave, summed in LDS -> RES words
 //   D  0..63,128..255 gate/up quad pairs + SwiGLU -> ACT words
 //   E  all 256        ffn_down + residual: row quad wg, waves 0-2 one
 //                     1024-column chunk each, summed in LDS -> H words
@@ -478,7 +479,7 @@ extern "C" __global__ __launch_bounds__(256) void dec_step(StepParams P) {
   // layer's attention is done, they arrive while the workgroup works on other
   // phases (layer 0's at the start).
   __shared__ __attribute__((aligned(16))) uint8_t kv_lds[kAttnWaves * kKvPrefetchBytes];
-  __shared__ float e_part[3][64];  // ffn_down: the chunks' lane sums
+  __shared__ float e_part[3][128];  // attn_o / ffn_down: the chunks' lane sums
   uint8_t* const kv_mine = kv_lds + wave * kKvPrefetchBytes;
   const int pos_c = pos_raw < 0 ? 0 : (pos_raw >= P.max_seq ? P.max_seq - 1 : pos_raw);
   const SplitRange my_split = split_range((wg % kAttnGroups) * kAttnWaves + wave, pos_c);
@@ -588,30 +589,39 @@ extern "C" __global__ __launch_bounds__(256) void dec_step(StepParams P) {
       }
     }
 
-    // ---- C: attn_o + residual ----
-    if (wg >= 64 && wg < 128) {
-      const int quad = 4 * (wg - 64) + wave;  // 0..255
+    // ---- C: attn_o + residual: workgroups 64..191, row quads 2 (wg - 64)
+    // and 2 (wg - 64) + 1 (waves 0-1 and 2-3), one 1024-column chunk per wave,
+    // the two chunk sums added in LDS in the per-phase kernel's order ----
+    if (wg >= 64 && wg < 192) {
+      const int quad = 2 * (wg - 64) + (wave >> 1);  // 0..255
+      const int c = wave & 1;
       constexpr int64_t bpl = (int64_t)kHidden * (2 * kHidden / 32 * 34);
-      u32x4 buf[QuadShape<2>::LOADS];
-      q8_quad_load<2>(P.wo + layer * bpl, kHidden, quad, buf);
+      u32x4 buf[QuadShape<1>::LOADS];
+      q8_chunk_load<2>(P.wo + layer * bpl, kHidden, quad, c, buf);
       const int row = 4 * quad + (lane >> 4);
       _Float16 h_row;
       if (layer == 0) {
         h_row = as_half(load_global_u16(emb + row));
       } else {
-        // this workgroup's 16 residual rows = h words [8 (wg - 64), +8)
-        if (!W.wait(prev + kWH + 8 * (wg - 64), 8, tag_prev_h, vec + 1024)) return;
-        h_row = as_half(reinterpret_cast<const uint16_t*>(vec + 1024)[row - 16 * (wg - 64)]);
+        // this workgroup's 8 residual rows = h words [4 (wg - 64), +4)
+        if (!W.wait(prev + kWH + 4 * (wg - 64), 4, tag_prev_h, vec + 1024)) return;
+        h_row = as_half(reinterpret_cast<const uint16_t*>(vec + 1024)[row - 8 * (wg - 64)]);
       }
       if (!W.wait(cur + kWAtt, 1024, step_tag(seq, layer, kPhAtt), vec)) return;
-      u32x4 xr[2][8];
-      lds_x_cols<2>(reinterpret_cast<const uint16_t*>(vec), xr);
+      u32x4 xr[1][8];
+      lds_x_cols<1>(reinterpret_cast<const uint16_t*>(vec) + 1024 * c, xr);
       uint8_t* lds = stage + wave * kGemvLds;
-      q8_quad_stage<2>(buf, lds);
+      q8_quad_stage<1>(buf, lds);
+      e_part[wave & 2][lane + 64 * c] = q8_quad_lane_dot<1>(lds, xr);
       __syncthreads();
-      const float acc = q8_quad_dot<2>(lds, xr);
-      put_quad(cur + kWRes, quad, acc, step_tag(seq, layer, kPhRes),
-               [&](float a, int) { return (uint32_t)residual_f16(h_row, a); });
+      if (c == 0) {
+        float acc = 0.0f;
+        acc += e_part[wave][lane];
+        acc += e_part[wave][lane + 64];
+        acc = reduce_row16(acc);
+        put_quad(cur + kWRes, quad, acc, step_tag(seq, layer, kPhRes),
+                 [&](float a, int) { return (uint32_t)residual_f16(h_row, a); });
+      }
     }
 
     // ---- D: gate/up + SwiGLU ----
