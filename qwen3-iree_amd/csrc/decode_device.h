@@ -282,9 +282,10 @@ struct AttnLds {
 //     exp(m_w - m).  An empty split (ctx < 32) contributes m = -inf, l = 0.
 // get_qkv(xw, v_new) fills this lane's words (dims 2*lane, 2*lane+1) of q
 // head 2g, q head 2g+1, k head g (xw[0..2]) and v head g; every thread of the
-// workgroup calls it once.
+// workgroup calls it once, and pre_qkv() once before any load of this
+// function (where get_qkv's requests can start early).
 // cs, sn: rope_angles of the clamped position.
-template <class GetQKV, class Publish>
+template <class PreQKV, class GetQKV, class Publish>
 __device__ __forceinline__ void attention_group(AttnLds& L, int g, int sg, int pos_raw,
                                                 const float (&cs)[2], const float (&sn)[2],
                                                 int max_seq, const uint16_t* __restrict__ qn_w,
@@ -292,14 +293,15 @@ __device__ __forceinline__ void attention_group(AttnLds& L, int g, int sg, int p
                                                 uint16_t* __restrict__ k_cache,
                                                 uint16_t* __restrict__ v_cache,
                                                 uint16_t* __restrict__ q_roped,
-                                                const uint8_t* kv, GetQKV&& get_qkv,
-                                                Publish&& publish) {
+                                                const uint8_t* kv, PreQKV&& pre_qkv,
+                                                GetQKV&& get_qkv, Publish&& publish) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int s = sg * kAttnWaves + wave;
   const int half = lane >> 5;
   const int pl = lane & 31;
 
+  pre_qkv();  // a wait's first round goes out ahead of this function's loads
   uint32_t nwv[3];
   nwv[0] = load_global(reinterpret_cast<const uint32_t*>(qn_w) + lane);
   nwv[2] = load_global(reinterpret_cast<const uint32_t*>(kn_w) + lane);

@@ -90,6 +90,7 @@ extern "C" __global__ __launch_bounds__(256) void dec_attention(
   rope_angles(pos_raw < 0 ? 0 : (pos_raw >= max_seq ? max_seq - 1 : pos_raw), cs, sn);
   attention_group(
       lds, g, sg, pos_raw, cs, sn, max_seq, qn_w, kn_w, k_cache, v_cache, q_roped, nullptr,
+      [] {},
       [&](uint32_t (&xw)[3], uint32_t& v_new) {
         xw[0] = load_global(reinterpret_cast<const uint32_t*>(q_raw + (2 * g) * kHeadDim) + lane);
         xw[1] = load_global(reinterpret_cast<const uint32_t*>(q_raw + (2 * g + 1) * kHeadDim) + lane);
@@ -302,16 +303,23 @@ extern "C" __global__ __launch_bounds__(256) void dec_scratch_clear(uint32_t* __
 namespace {
 
 constexpr int kStepWgs = 256;
+// Vectors that every (or nearly every) workgroup waits for -- h, the
+// attention output, the attn_o + residual output, the SwiGLU output -- are
+// published in kRep replicas and workgroup w polls replica w % kRep: with one
+// copy, hundreds of workgroups polling the same few cache lines queue at the
+// same memory channels.
+constexpr int kRep = 8;
+constexpr int kNH = 512, kNAtt = 1024, kNRes = 512, kNAct = 1536;  // words per replica
 // tagged-word map (u64 words) per layer parity
-constexpr int kWH = 0;                                     // 512: h (E output)
-constexpr int kWQ = kWH + 512;                             // 1024: q row pairs
+constexpr int kWH = 0;                                     // kRep x 512: h (E output)
+constexpr int kWQ = kWH + kRep * kNH;                      // 1024: q row pairs
 constexpr int kWK = kWQ + 1024;                            // 512
 constexpr int kWV = kWK + 512;                             // 512
 constexpr int kWPart = kWV + 512;                          // 16 x 8 x 130
-constexpr int kWAtt = kWPart + kQHeads * kAttnGroups * 130;  // 1024
-constexpr int kWRes = kWAtt + 1024;                        // 512
-constexpr int kWAct = kWRes + 512;                         // 1536
-constexpr int kWParity = kWAct + 1536;
+constexpr int kWAtt = kWPart + kQHeads * kAttnGroups * 130;  // kRep x 1024
+constexpr int kWRes = kWAtt + kRep * kNAtt;                // kRep x 512
+constexpr int kWAct = kWRes + kRep * kNRes;                // kRep x 1536
+constexpr int kWParity = kWAct + kRep * kNAct;
 constexpr int kWArg = 2 * kWParity;                        // 2 per workgroup
 constexpr int kWTotal = kWArg + 2 * kStepWgs;
 // phases in a tag
@@ -368,21 +376,29 @@ struct Waiter {
   uint32_t seq;
   int* s_abort;  // LDS flag of the workgroup
 
-  // Every thread of the workgroup calls this with the same arguments: the
-  // data halves of words src(0..n-1), once each carries tag `tag`, land in
-  // dst[0, n).  A thread requests all of its words (i = threadIdx.x + 256 k)
-  // at once and re-requests only those not ready yet, so a wait costs one
-  // round trip once the data is there.  Returns false (in every thread)
-  // when the step was aborted.
+  static constexpr int kMax = 9;  // words per thread: n <= 2304
+
+  // The first round of a wait: this thread's words (i = threadIdx.x + 256 k)
+  // requested at once.  Issued before a phase's own weight loads, the round
+  // trip overlaps them (vector loads complete in issue order, so a poll
+  // issued after them could not return before them).
   template <class Src>
-  __device__ __forceinline__ bool wait_map(int n, uint32_t tag, uint32_t* __restrict__ dst,
-                                           Src src) const {
-    constexpr int kMax = 9;  // n <= 2304
+  __device__ __forceinline__ void poll_begin(int n, Src src, uint64_t (&w)[kMax]) const {
     const int t = threadIdx.x;
-    uint64_t w[kMax];
 #pragma unroll
     for (int k = 0; k < kMax; ++k)
       if (t + 256 * k < n) w[k] = get_word(src(t + 256 * k));
+  }
+
+  // Every thread of the workgroup calls this with the same arguments, after
+  // poll_begin: the data halves of words src(0..n-1), once each carries tag
+  // `tag`, land in dst[0, n).  Only words not ready yet are requested again,
+  // so a wait costs one round trip once the data is there.  Returns false (in
+  // every thread) when the step was aborted.
+  template <class Src>
+  __device__ __forceinline__ bool poll_finish(int n, uint32_t tag, uint32_t* __restrict__ dst,
+                                              Src src, uint64_t (&w)[kMax]) const {
+    const int t = threadIdx.x;
     bool ok = true;
     uint32_t spins = 0;
     while (true) {
@@ -419,6 +435,15 @@ struct Waiter {
     return *s_abort == 0;
   }
 
+  // poll_begin + poll_finish.
+  template <class Src>
+  __device__ __forceinline__ bool wait_map(int n, uint32_t tag, uint32_t* __restrict__ dst,
+                                           Src src) const {
+    uint64_t w[kMax];
+    poll_begin(n, src, w);
+    return poll_finish(n, tag, dst, src, w);
+  }
+
   __device__ __forceinline__ bool wait(const uint64_t* __restrict__ src, int n, uint32_t tag,
                                        uint32_t* __restrict__ dst) const {
     return wait_map(n, tag, dst, [=](int i) { return src + i; });
@@ -426,16 +451,17 @@ struct Waiter {
 };
 
 // Row sums of a quad (rows q4, q4+1, q4+2, q4+3; row r's sum in lanes
-// 16(r - q4)..) published as two f16-pair words: word q4/2 by lane 0, q4/2 + 1
-// by lane 32.  f(acc) maps a row sum to its f16 bits.
-template <class F>
-__device__ __forceinline__ void put_quad(uint64_t* __restrict__ words, int quad, float acc,
-                                         uint32_t tag, F f) {
+// 16(r - q4)..) published as two f16-pair words, 2 quad and 2 quad + 1, in
+// REP replicas `stride` words apart: lanes 0..REP-1 write the first word,
+// lanes 32..32+REP-1 the second.  f(acc) maps a row sum to its f16 bits.
+template <int REP, class F>
+__device__ __forceinline__ void put_quad(uint64_t* __restrict__ words, int stride, int quad,
+                                         float acc, uint32_t tag, F f) {
   const int lane = threadIdx.x & 63;
   const uint32_t mine = f(acc, 4 * quad + (lane >> 4));
   const uint32_t next = __shfl(mine, (lane + 16) & 63, 64);
-  if (lane == 0 || lane == 32)
-    put_word(words + 2 * quad + (lane >> 5), mine | (next << 16), tag);
+  if ((lane & 31) < REP)
+    put_word(words + (lane & 31) * stride + 2 * quad + (lane >> 5), mine | (next << 16), tag);
 }
 
 // u64 max over the 64 lanes of a wave.
@@ -462,6 +488,7 @@ extern "C" __global__ __launch_bounds__(256) void dec_step(StepParams P) {
   uint32_t* vec = reinterpret_cast<uint32_t*>(smem);               // polled words' data
   uint8_t* stage = smem + 4 * kVecWords;                            // GEMV staging / attention
   const int wg = blockIdx.x;
+  const int rep = wg % kRep;  // the replica this workgroup polls
   const int t = threadIdx.x;
   const int wave = t >> 6;
   const int lane = t & 63;
@@ -501,6 +528,9 @@ extern "C" __global__ __launch_bounds__(256) void dec_step(StepParams P) {
       const int n = quad < 512 ? 2048 : 1024;
       const int qd = quad < 512 ? quad : (quad < 768 ? quad - 512 : quad - 768);
       const int64_t bpl = (int64_t)n * (kHidden / 32 * 34);
+      const auto h_src = [=](int i) { return prev + kWH + rep * kNH + i; };
+      uint64_t hp[Waiter::kMax];
+      if (layer > 0) W.poll_begin(512, h_src, hp);  // ahead of the weight loads
       u32x4 buf[QuadShape<1>::LOADS];
       q8_quad_load<1>(w + layer * bpl, n, qd, buf);
       u32x4 xr[1][8];
@@ -508,15 +538,17 @@ extern "C" __global__ __launch_bounds__(256) void dec_step(StepParams P) {
       if (layer == 0) {
         rmsnorm_gemv_x<false>(emb, an, xr[0]);
       } else {
-        if (!W.wait(prev + kWH, 512, tag_prev_h, vec)) return;
-        rmsnorm_gemv_x<true>(reinterpret_cast<const uint16_t*>(vec), an, xr[0]);
+        u32x4 wv[8];
+        norm_weights(an, gemv_col, wv);  // requested before the wait
+        if (!W.poll_finish(512, tag_prev_h, vec, h_src, hp)) return;
+        rmsnorm_lds_w(reinterpret_cast<const uint16_t*>(vec), gemv_col, wv, xr[0]);
       }
       uint8_t* lds = stage + wave * kGemvLds;
       q8_quad_stage<1>(buf, lds);
       __syncthreads();
       const float acc = q8_quad_dot<1>(lds, xr);
       uint64_t* dst = quad < 512 ? cur + kWQ : (quad < 768 ? cur + kWK : cur + kWV);
-      put_quad(dst, qd, acc, step_tag(seq, layer, kPhQKV),
+      put_quad<1>(dst, 0, qd, acc, step_tag(seq, layer, kPhQKV),
                [](float a, int) { return (uint32_t)f32_to_f16_bits(a); });
     }
 
@@ -528,17 +560,19 @@ extern "C" __global__ __launch_bounds__(256) void dec_step(StepParams P) {
       AttnLds& L = *reinterpret_cast<AttnLds*>(stage);
       bool ok = true;
       const uint32_t tq = step_tag(seq, layer, kPhQKV);
+      // q heads 2g, 2g+1 (words 128g..), k head g, v head g (words 64g..)
+      const auto qkv_src = [=](int i) {
+        return i < 128 ? cur + kWQ + 128 * g + i
+                       : (i < 192 ? cur + kWK + 64 * g + (i - 128) : cur + kWV + 64 * g + (i - 192));
+      };
+      uint64_t qkv_poll[Waiter::kMax];
       attention_group(
           L, g, sg, pos_raw, rope_cs, rope_sn, P.max_seq, P.q_norm + layer * kHeadDim,
           P.k_norm + layer * kHeadDim,
           P.k_cache + cache_layer, P.v_cache + cache_layer, nullptr, kv_mine,
+          [&] { W.poll_begin(256, qkv_src, qkv_poll); },
           [&](uint32_t (&xw)[3], uint32_t& v_new) {
-            // q heads 2g, 2g+1 (words 128g..), k head g, v head g (words 64g..)
-            ok = W.wait_map(256, tq, vec, [&](int i) {
-              return i < 128 ? cur + kWQ + 128 * g + i
-                             : (i < 192 ? cur + kWK + 64 * g + (i - 128)
-                                        : cur + kWV + 64 * g + (i - 192));
-            });
+            ok = W.poll_finish(256, tq, vec, qkv_src, qkv_poll);
             xw[0] = vec[lane];
             xw[1] = vec[64 + lane];
             xw[2] = vec[128 + lane];
@@ -578,8 +612,11 @@ extern "C" __global__ __launch_bounds__(256) void dec_step(StepParams P) {
             for (int gi = 0; gi < kAttnGroups; ++gi) accg[gi] = pv[gi * 130 + 2 + 2 * lane + e];
             a[e] = merge_dim(accg, wgt);
           }
-          put_word(cur + kWAtt + (2 * g + hh) * 64 + lane, pack_f16x2(a[0] / Ls, a[1] / Ls),
-                   step_tag(seq, layer, kPhAtt));
+          const uint32_t att = pack_f16x2(a[0] / Ls, a[1] / Ls);
+#pragma unroll
+          for (int r = 0; r < kRep; ++r)
+            put_word(cur + kWAtt + r * kNAtt + (2 * g + hh) * 64 + lane, att,
+                     step_tag(seq, layer, kPhAtt));
         }
         __syncthreads();  // vec is reused by the next wait
       }
@@ -604,10 +641,10 @@ extern "C" __global__ __launch_bounds__(256) void dec_step(StepParams P) {
         h_row = as_half(load_global_u16(emb + row));
       } else {
         // this workgroup's 8 residual rows = h words [4 (wg - 64), +4)
-        if (!W.wait(prev + kWH + 4 * (wg - 64), 4, tag_prev_h, vec + 1024)) return;
+        if (!W.wait(prev + kWH + rep * kNH + 4 * (wg - 64), 4, tag_prev_h, vec + 1024)) return;
         h_row = as_half(reinterpret_cast<const uint16_t*>(vec + 1024)[row - 8 * (wg - 64)]);
       }
-      if (!W.wait(cur + kWAtt, 1024, step_tag(seq, layer, kPhAtt), vec)) return;
+      if (!W.wait(cur + kWAtt + rep * kNAtt, 1024, step_tag(seq, layer, kPhAtt), vec)) return;
       u32x4 xr[1][8];
       lds_x_cols<1>(reinterpret_cast<const uint16_t*>(vec) + 1024 * c, xr);
       uint8_t* lds = stage + wave * kGemvLds;
@@ -619,7 +656,7 @@ extern "C" __global__ __launch_bounds__(256) void dec_step(StepParams P) {
         acc += e_part[wave][lane];
         acc += e_part[wave][lane + 64];
         acc = reduce_row16(acc);
-        put_quad(cur + kWRes, quad, acc, step_tag(seq, layer, kPhRes),
+        put_quad<kRep>(cur + kWRes, kNRes, quad, acc, step_tag(seq, layer, kPhRes),
                  [&](float a, int) { return (uint32_t)residual_f16(h_row, a); });
       }
     }
@@ -634,7 +671,7 @@ extern "C" __global__ __launch_bounds__(256) void dec_step(StepParams P) {
       q8_quad_load<1>(wl, 2 * kFfn, kFfn / 4 + b, bu);
       u32x4 wv[8];
       norm_weights(P.ffn_norm + layer * kHidden, gemv_col, wv);  // requested before the wait
-      if (!W.wait(cur + kWRes, 512, step_tag(seq, layer, kPhRes), vec)) return;
+      if (!W.wait(cur + kWRes + rep * kNRes, 512, step_tag(seq, layer, kPhRes), vec)) return;
       u32x4 xr[1][8];
       rmsnorm_lds_w(reinterpret_cast<const uint16_t*>(vec), gemv_col, wv, xr[0]);
       uint8_t* lds = stage + wave * kGemvLds;
@@ -646,8 +683,8 @@ extern "C" __global__ __launch_bounds__(256) void dec_step(StepParams P) {
       const float au = q8_quad_dot<1>(lds + LDSB, xr);
       const uint32_t act = swiglu_f16(ag, au);
       const uint32_t next = __shfl(act, (lane + 16) & 63, 64);
-      if (lane == 0 || lane == 32)
-        put_word(cur + kWAct + 2 * b + (lane >> 5), act | (next << 16),
+      if ((lane & 31) < kRep)
+        put_word(cur + kWAct + (lane & 31) * kNAct + 2 * b + (lane >> 5), act | (next << 16),
                  step_tag(seq, layer, kPhAct));
     }
 
@@ -660,9 +697,11 @@ extern "C" __global__ __launch_bounds__(256) void dec_step(StepParams P) {
       u32x4 buf[QuadShape<1>::LOADS];
       if (wave < 3) q8_chunk_load<3>(P.wdn + layer * bpl, kHidden, quad, wave, buf);
       // the quad's 4 residual rows: words 2 quad, 2 quad + 1
-      if (!W.wait(cur + kWRes + 2 * quad, 2, step_tag(seq, layer, kPhRes), vec + 1536)) return;
+      if (!W.wait(cur + kWRes + rep * kNRes + 2 * quad, 2, step_tag(seq, layer, kPhRes),
+                  vec + 1536))
+        return;
       const _Float16 r_row = as_half(reinterpret_cast<const uint16_t*>(vec + 1536)[lane >> 4]);
-      if (!W.wait(cur + kWAct, 1536, step_tag(seq, layer, kPhAct), vec)) return;
+      if (!W.wait(cur + kWAct + rep * kNAct, 1536, step_tag(seq, layer, kPhAct), vec)) return;
       if (wave < 3) {
         u32x4 xr[1][8];
         lds_x_cols<1>(reinterpret_cast<const uint16_t*>(vec) + 1024 * wave, xr);
@@ -676,14 +715,14 @@ extern "C" __global__ __launch_bounds__(256) void dec_step(StepParams P) {
 #pragma unroll
         for (int c = 0; c < 3; ++c) acc += e_part[c][lane];
         acc = reduce_row16(acc);
-        put_quad(cur + kWH, quad, acc, step_tag(seq, layer, kPhH),
+        put_quad<kRep>(cur + kWH, kNH, quad, acc, step_tag(seq, layer, kPhH),
                  [&](float a, int) { return (uint32_t)residual_f16(r_row, a); });
       }
     }
   }
 
   // ---- vocab GEMV + argmax ----
-  const uint64_t* hfin = P.words + ((kLayers - 1) & 1) * kWParity + kWH;
+  const uint64_t* hfin = P.words + ((kLayers - 1) & 1) * kWParity + kWH + rep * kNH;
   const uint32_t tag_h = step_tag(seq, kLayers - 1, kPhH);
   const uint32_t tag_arg = step_tag(seq, kLayers, kPhArg);
   if (P.head) {
