@@ -308,7 +308,7 @@ constexpr int kStepWgs = 256;
 // published in kRep replicas and workgroup w polls replica w % kRep: with one
 // copy, hundreds of workgroups polling the same few cache lines queue at the
 // same memory channels.
-constexpr int kRep = 8;
+constexpr int kRep = 4;
 constexpr int kNH = 512, kNAtt = 1024, kNRes = 512, kNAct = 1536;  // words per replica
 // tagged-word map (u64 words) per layer parity
 constexpr int kWH = 0;                                     // kRep x 512: h (E output)

@@ -823,10 +823,10 @@ constexpr size_t kScrSeq = 16;       // u32 step sequence number (single-launch 
 constexpr size_t kScrAbort = 20;     // u32 abort word (single-launch step)
 // tagged words of the single-launch step (u64; map in decode_kernels.hip)
 // the single-launch step's tagged words per layer parity: h, attention output,
-// attn_o + residual output and SwiGLU output in 8 replicas each, q/k/v and
+// attn_o + residual output and SwiGLU output in 4 replicas each, q/k/v and
 // the attention partials once (layout in decode_kernels.hip)
-constexpr size_t kStepWordsParity = 8 * 512 + 1024 + 512 + 512 + 16 * 8 * 130 + 8 * 1024 +
-                                    8 * 512 + 8 * 1536;
+constexpr size_t kStepWordsParity = 4 * 512 + 1024 + 512 + 512 + 16 * 8 * 130 + 4 * 1024 +
+                                    4 * 512 + 4 * 1536;
 constexpr size_t kStepWords = 2 * kStepWordsParity + 2 * 256;
 constexpr size_t kScrWords = (kScrPart + 16 * kAttnGroupsHost * 132 * 4 + 255) / 256 * 256;
 constexpr size_t kScrBytes = kScrWords + kStepWords * 8;
