@@ -382,12 +382,15 @@ struct Waiter {
   // requested at once.  Issued before a phase's own weight loads, the round
   // trip overlaps them (vector loads complete in issue order, so a poll
   // issued after them could not return before them).
+  // (Rounds that every thread has are issued unconditionally: the compiler
+  // then waits for them precisely instead of draining all memory operations
+  // after a per-lane branch.)
   template <class Src>
   __device__ __forceinline__ void poll_begin(int n, Src src, uint64_t (&w)[kMax]) const {
     const int t = threadIdx.x;
 #pragma unroll
     for (int k = 0; k < kMax; ++k)
-      if (t + 256 * k < n) w[k] = get_word(src(t + 256 * k));
+      if (256 * (k + 1) <= n || t + 256 * k < n) w[k] = get_word(src(t + 256 * k));
   }
 
   // Every thread of the workgroup calls this with the same arguments, after
