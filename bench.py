@@ -241,6 +241,19 @@ def bench_prefill(Q, stream, args) -> dict:
     gemm, attn = prefill_flops(n)
     log(f"prefill of {n} tokens: {ms:.3f} ms = {n / ms * 1e3:.0f} tok/s, "
         f"{(gemm + attn) / ms / 1e9:.1f} TFLOP/s; as decode steps {steps_ms:.1f} ms")
+    for spec in args.prefill_tiling or []:
+        rows, split = (int(x) for x in spec.split(":"))
+        D.set_prefill_tiling(rows, split)
+        for _ in range(3):
+            one()
+        stream.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            one()
+        stream.synchronize()
+        t = (time.perf_counter() - t0) * 1e3 / reps
+        log(f"  tiling gemm_rows {rows} attn_split_blocks {split}: {t:.3f} ms")
+    D.set_prefill_tiling(0, 0)
     ws.free()
     pbuf.free()
     sess.free()
@@ -308,6 +321,9 @@ def main() -> int:
                     help="run only batched prompt ingestion and print its JSON line")
     ap.add_argument("--prefill-tokens", type=int, default=512,
                     help="prompt length of the batched prompt ingestion measurement")
+    ap.add_argument("--prefill-tiling", nargs="*", metavar="ROWS:SPLIT",
+                    help="also time the prompt ingestion with these work divisions "
+                         "(qwen3_set_prefill_tiling; 0 = by shape)")
     ap.add_argument("--gguf-ingest", metavar="DIR", default=None,
                     help="only measure GGUF ingestion: write the synthetic model as a Q8_0 GGUF "
                          "under DIR, read it back into the device layout (cold, then warm page "

@@ -118,7 +118,9 @@ int qwen3_prefill(const qwen3_weights* w, void* k_cache, void* v_cache, int64_t 
  * n_prompt (at p0 + n_prompt = max_seq it stays at max_seq - 1 and status bit
  * 0 is set).  Fails with Q8_ERR_BAD_SHAPE unless p0 + n_prompt <= max_seq.
  * workspace: device memory of qwen3_prefill_workspace_bytes(n_prompt) bytes,
- * 256-byte aligned (activations of all tokens; 30,720 bytes per token).  The
+ * 256-byte aligned (activations of all tokens, 30,720 bytes per token, then
+ * the attention's split partials, 266,240 bytes per (query block of 32 tokens,
+ * split) pair for 2 ceil(n_prompt / 32) + 64 pairs).  The
  * reference reads f16 copies of the layer matrices for this function
  * (@model_params.attn_q_weight etc., :1132-1210); this one reads the same
  * Q8_0 stacks as the decode step, so prompt and decode share one set of
@@ -137,11 +139,26 @@ int qwen3_prefill_batched(const qwen3_weights* w, void* k_cache, void* v_cache, 
  * the workspace.  qwen3_prefill_workspace_offset(n_tokens, name) = byte
  * offset of a region ("h", "res", "xn", "q", "k", "v", "q_roped", "attn",
  * "act", "fn"; f16 rows of 1024, 1024, 1024, 2048, 1024, 1024, 2048, 2048,
- * 3072, 1024 columns), -1 for an unknown name. */
+ * 3072, 1024 columns; then "attn_part", the attention's split partials), -1
+ * for an unknown name. */
 int qwen3_prefill_layer(const qwen3_weights* w, int layer, void* k_cache, void* v_cache,
                         int64_t max_seq, int32_t n_tokens, int32_t start_pos, int chunk_local,
                         void* workspace, size_t workspace_bytes, void* stream);
 int64_t qwen3_prefill_workspace_offset(int32_t n_tokens, const char* name);
+
+/* Work division of qwen3_prefill_batched / qwen3_prefill_layer (0 = the
+ * default, for either):
+ * gemm_rows: token rows per workgroup of the q/k/v, attn_o and ffn_down GEMMs
+ *   (gate/up always uses 64): 32 or 64; default: 32 where 64 would give
+ *   fewer than 2 workgroups per CU.  Both tiles compute every output with the
+ *   same operations in the same order (tested bit for bit).
+ * attn_split_blocks: cache positions per attention split, in blocks of 32
+ *   (>= 1; raised where the workspace's partial slots would not hold the
+ *   splits); default 8.  Splits change the order of the softmax sums, within
+ *   the attention tolerance.
+ * Fails with Q8_ERR_BAD_ARGUMENT for other values.  No counterpart in the
+ * reference (IREE tiles its dispatches at compile time). */
+int qwen3_set_prefill_tiling(int gemm_rows, int attn_split_blocks);
 
 /* The token loop of @generate (qwen3_full.mlir:1396-1534): starting from
  * *token at *pos, steps run in batches of 4 (fewer for the last) with the

@@ -69,7 +69,7 @@ def build_shim() -> Path:
     _run([
         "g++", "-O2", "-std=c++17", "-Wall", "-Wextra", "-fPIC", "-shared",
         "-D__HIP_PLATFORM_AMD__",
-        f"-I{ROCM / 'include'}", f"-I{REPO / 'include'}",
+        f"-I{ROCM / 'include'}", f"-I{REPO / 'include'}", f"-I{CSRC}",
         str(CSRC / "q8gemv_shim.cpp"),
         f"-L{ROCM / 'lib'}", "-lamdhip64", "-ldl", f"-Wl,-rpath,{ROCM / 'lib'}",
         "-o", str(tmp),

@@ -24,6 +24,7 @@
 // accumulation) and add them into an f32 sum with the block's scale, as the
 // GEMV does; only the order of the f32 additions differs.
 #include "decode_device.h"
+#include "prefill_split.h"
 
 namespace {
 
@@ -45,14 +46,11 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 // (k / 8), element k % 8; B[k][j] in lane j + 16 (k / 8), element k % 8;
 // C[i][j] in lane j + 16 (i / 4), element i % 4.
 
-constexpr int kGemmBM = 64;
 constexpr int kGemmBN = 64;
 constexpr int kStageBlocks = 8;
 constexpr int kXRow = 2 * 32 * kStageBlocks + 16;  // 528
 constexpr int kWRow = 34 * kStageBlocks;           // 272
-constexpr int kXLds = kGemmBM * kXRow;
 constexpr int kWLds = kGemmBN * kWRow;
-constexpr int kXPieces = kGemmBM * 32;             // 16-byte pieces per stage
 constexpr int kWPieces = kGemmBN * 17;
 
 enum { kEpiStore = 0, kEpiResidual = 1, kEpiSwiGLU = 2 };
@@ -68,11 +66,15 @@ struct GemmArgs {
   int up_row;         // kEpiSwiGLU: first up row of W (gate rows are 0..up_row-1)
 };
 
-template <int EPI>
+template <int EPI, int BM>
 __device__ __forceinline__ void gemm_q8(const GemmArgs& A) {
-  __shared__ __attribute__((aligned(16))) uint8_t lds[kXLds + kWLds];
+  static_assert(BM == 64 || (BM == 32 && EPI != kEpiSwiGLU), "tile shapes");
+  constexpr int kXL = BM * kXRow;
+  constexpr int kXP = BM * 32;   // 16-byte X pieces per stage
+  constexpr int NS = BM == 64 ? 2 : 1;  // 16-column tiles per wave
+  __shared__ __attribute__((aligned(16))) uint8_t lds[kXL + kWLds];
   uint8_t* xl = lds;
-  uint8_t* wl = lds + kXLds;
+  uint8_t* wl = lds + kXL;
   const int t = threadIdx.x;
   const int wave = t >> 6;
   const int lane = t & 63;
@@ -82,11 +84,11 @@ __device__ __forceinline__ void gemm_q8(const GemmArgs& A) {
   // Workgroups are dealt to the 8 XCDs round robin; the m tiles of one n tile
   // go to the same XCD, one after another, so its weight rows are fetched
   // from HBM once and then hit that XCD's L2.
-  const int mt = (A.M + kGemmBM - 1) / kGemmBM;
+  const int mt = (A.M + BM - 1) / BM;
   const int xcd = blockIdx.x & 7;
   const int slot = blockIdx.x >> 3;
   const int n_tile = (slot / mt) * 8 + xcd;
-  const int m0 = (slot % mt) * kGemmBM;
+  const int m0 = (slot % mt) * BM;
   const int row_bytes = A.K / 32 * 34;
   const int stages = A.K / (32 * kStageBlocks);
 
@@ -97,10 +99,10 @@ __device__ __forceinline__ void gemm_q8(const GemmArgs& A) {
       return kGemmBN * n_tile + r;
   };
 
-  u32x4 xp[kXPieces / 256], wp[(kWPieces + 255) / 256];
+  u32x4 xp[kXP / 256], wp[(kWPieces + 255) / 256];
   auto gload = [&](int s) {
 #pragma unroll
-    for (int j = 0; j < kXPieces / 256; ++j) {
+    for (int j = 0; j < kXP / 256; ++j) {
       const int piece = t + 256 * j;
       const int row = piece >> 5;
       const int m = m0 + row < A.M ? m0 + row : A.M - 1;
@@ -119,7 +121,7 @@ __device__ __forceinline__ void gemm_q8(const GemmArgs& A) {
   };
   auto lstore = [&]() {
 #pragma unroll
-    for (int j = 0; j < kXPieces / 256; ++j) {
+    for (int j = 0; j < kXP / 256; ++j) {
       const int piece = t + 256 * j;
       *reinterpret_cast<u32x4*>(xl + (piece >> 5) * kXRow + 16 * (piece & 31)) = xp[j];
     }
@@ -133,35 +135,42 @@ __device__ __forceinline__ void gemm_q8(const GemmArgs& A) {
     }
   };
 
-  const int wm = wave & 1, wn = wave >> 1;
-  int nrow[2];  // LDS W rows of this lane's column in the two n tiles
+  // BM = 64: waves 2 (m) x 2 (n), each 32 x 32; BM = 32: waves 1 x 4, each
+  // 32 x 16
+  const int wm = BM == 64 ? (wave & 1) : 0;
+  const int wn = BM == 64 ? (wave >> 1) : wave;
+  int nrow[NS];  // LDS W rows of this lane's column in the wave's n tiles
   if constexpr (EPI == kEpiSwiGLU) {
     nrow[0] = 16 * wn + c16;       // gate row
     nrow[1] = 32 + 16 * wn + c16;  // the matching up row
-  } else {
+  } else if constexpr (BM == 64) {
     nrow[0] = 32 * wn + c16;
     nrow[1] = 32 * wn + 16 + c16;
+  } else {
+    nrow[0] = 16 * wn + c16;
   }
-  f32x4 acc[2][2];
+  f32x4 acc[2][NS];
 #pragma unroll
   for (int ms = 0; ms < 2; ++ms)
 #pragma unroll
-    for (int ns = 0; ns < 2; ++ns) acc[ms][ns] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+    for (int ns = 0; ns < NS; ++ns) acc[ms][ns] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
   const f32x4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
 
-  // Block b's four products are issued before block b - 1's are scaled into
-  // the sums, so the matrix unit works while the scale FMAs run.
-  f32x4 prev[2][2];
-  float prev_sc[2] = {0.0f, 0.0f};
+  // Block b's products are issued before block b - 1's are scaled into the
+  // sums, so the matrix unit works while the scale FMAs run.
+  f32x4 prev[2][NS];
+  float prev_sc[NS];
+#pragma unroll
+  for (int ns = 0; ns < NS; ++ns) prev_sc[ns] = 0.0f;
 #pragma unroll
   for (int ms = 0; ms < 2; ++ms)
 #pragma unroll
-    for (int ns = 0; ns < 2; ++ns) prev[ms][ns] = zero;
+    for (int ns = 0; ns < NS; ++ns) prev[ms][ns] = zero;
   auto scale_in = [&]() {
 #pragma unroll
     for (int ms = 0; ms < 2; ++ms)
 #pragma unroll
-      for (int ns = 0; ns < 2; ++ns)
+      for (int ns = 0; ns < NS; ++ns)
 #pragma unroll
         for (int i = 0; i < 4; ++i)
           acc[ms][ns][i] = __builtin_fmaf(prev_sc[ns], prev[ms][ns][i], acc[ms][ns][i]);
@@ -180,10 +189,10 @@ __device__ __forceinline__ void gemm_q8(const GemmArgs& A) {
       for (int ms = 0; ms < 2; ++ms)
         a[ms] = *reinterpret_cast<const f16x8*>(xl + (32 * wm + 16 * ms + c16) * kXRow +
                                                 2 * (32 * b + 8 * g));
-      f16x8 bq[2];
-      float sc[2];
+      f16x8 bq[NS];
+      float sc[NS];
 #pragma unroll
-      for (int ns = 0; ns < 2; ++ns) {
+      for (int ns = 0; ns < NS; ++ns) {
         const uint8_t* wr = wl + nrow[ns] * kWRow + 34 * b;
         sc[ns] = (float)*reinterpret_cast<const _Float16*>(wr);
         // the block's int8 k = 8 g .. 8 g + 7 sit at wr + 2 + 8 g: 4-byte
@@ -204,19 +213,19 @@ __device__ __forceinline__ void gemm_q8(const GemmArgs& A) {
         const f16x2 v2 = q8x2_to_f16x2(bh, kSelLo), v3 = q8x2_to_f16x2(bh, kSelHi);
         bq[ns] = (f16x8){v0.x, v0.y, v1.x, v1.y, v2.x, v2.y, v3.x, v3.y};
       }
-      f32x4 cur[2][2];
+      f32x4 cur[2][NS];
 #pragma unroll
       for (int ms = 0; ms < 2; ++ms)
 #pragma unroll
-        for (int ns = 0; ns < 2; ++ns)
+        for (int ns = 0; ns < NS; ++ns)
           cur[ms][ns] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[ms], bq[ns], zero, 0, 0, 0);
       scale_in();  // block b - 1 (zeros before the first block)
 #pragma unroll
       for (int ms = 0; ms < 2; ++ms)
 #pragma unroll
-        for (int ns = 0; ns < 2; ++ns) prev[ms][ns] = cur[ms][ns];
-      prev_sc[0] = sc[0];
-      prev_sc[1] = sc[1];
+        for (int ns = 0; ns < NS; ++ns) prev[ms][ns] = cur[ms][ns];
+#pragma unroll
+      for (int ns = 0; ns < NS; ++ns) prev_sc[ns] = sc[ns];
     }
   }
   scale_in();
@@ -233,8 +242,8 @@ __device__ __forceinline__ void gemm_q8(const GemmArgs& A) {
         A.y[(size_t)m * A.ldy + col] = swiglu_f16(acc[ms][0][i], acc[ms][1][i]);
       } else {
 #pragma unroll
-        for (int ns = 0; ns < 2; ++ns) {
-          const int col = kGemmBN * n_tile + 32 * wn + 16 * ns + c16;
+        for (int ns = 0; ns < NS; ++ns) {
+          const int col = kGemmBN * n_tile + (BM == 64 ? 32 * wn + 16 * ns : 16 * wn) + c16;
           if constexpr (EPI == kEpiResidual)
             A.y[(size_t)m * A.ldy + col] =
                 residual_f16(as_half(A.r[(size_t)m * A.ldr + col]), acc[ms][ns][i]);
@@ -245,14 +254,6 @@ __device__ __forceinline__ void gemm_q8(const GemmArgs& A) {
     }
   }
 }
-
-// ----------------------------------------------------------- attention ----
-
-struct PfAttnLds {
-  uint32_t qh[2][64];  // roped q heads 2g, 2g+1 as f16 pairs
-  float pbuf[kAttnWaves][2][32];
-  float mrg[kAttnWaves][2][2 + kHeadDim];
-};
 
 }  // namespace
 
@@ -286,13 +287,19 @@ extern "C" __global__ __launch_bounds__(256) void pf_rmsnorm(const uint16_t* __r
 }
 
 extern "C" __global__ __launch_bounds__(256) void pf_gemm_q8(GemmArgs A) {
-  gemm_q8<kEpiStore>(A);
+  gemm_q8<kEpiStore, 64>(A);
+}
+extern "C" __global__ __launch_bounds__(256) void pf_gemm_q8_m32(GemmArgs A) {
+  gemm_q8<kEpiStore, 32>(A);
 }
 extern "C" __global__ __launch_bounds__(256) void pf_gemm_q8_res(GemmArgs A) {
-  gemm_q8<kEpiResidual>(A);
+  gemm_q8<kEpiResidual, 64>(A);
+}
+extern "C" __global__ __launch_bounds__(256) void pf_gemm_q8_res_m32(GemmArgs A) {
+  gemm_q8<kEpiResidual, 32>(A);
 }
 extern "C" __global__ __launch_bounds__(256) void pf_gemm_q8_swiglu(GemmArgs A) {
-  gemm_q8<kEpiSwiGLU>(A);
+  gemm_q8<kEpiSwiGLU, 64>(A);
 }
 
 // Token i (position start + i), kv head g = blockIdx.y; waves 0, 1: q heads
@@ -355,134 +362,249 @@ extern "C" __global__ __launch_bounds__(256) void pf_qk_rope_cache(
 }
 
 // Causal GQA attention (@attention_prefill, qwen3_full.mlir:1571-1729, with the
-// mask j <= i of :1700-1710): token i at position start + i, kv head g =
-// blockIdx.y, both query heads 2g, 2g+1, over cache positions [lo, start + i]
-// where lo = 0 (the whole cache, as the decode steps of @prefill_all see it)
-// or lo = start with chunk_local != 0 (only this call's tokens, as the
-// reference's @prefill attends).  Four waves take four near-equal position
-// ranges; each runs the decode step's chunk loop (scores of 32 positions,
-// online softmax in f32, the weighted v sum in f32), and the four results
-// merge in LDS.  out: [n, 2048] f16.
+// mask j <= i of :1700-1710): workgroup (query block qb of 32 tokens, kv head
+// g) computes both query heads 2g, 2g+1 for tokens 32 qb .. 32 qb + 31 at
+// positions start + token over cache positions [lo, position], lo = 0 (the
+// whole cache, what the decode steps of @prefill_all see) or lo = start with
+// chunk_local != 0 (this call's tokens only, as the reference's @prefill
+// attends).  Wave w takes query head 2g + (w >> 1) and tokens 32 qb + 16 (w &
+// 1) .. + 15.  Per block of 32 cache positions: the K tile ([32][128], rows
+// padded to 272 bytes) and the transposed V tile ([128][32], rows padded to 80
+// bytes) go to LDS; S = Q K^T is 8 v_mfma_f32_16x16x32_f16 per wave (exact f16
+// products, f32 sums), scaled by rsqrt(128); the causal mask and an online
+// softmax in f32 (running max m and sum l per query row, as the decode step);
+// the weights p are split into f16 hi + lo (p - hi), so P V = hi V + lo V (8 + 8
+// MFMAs) carries p to about 2^-22.  out: [n, 2048] f16 = O / l.
+//
+// A query block's positions are divided into splits of split_blocks blocks of
+// 32 (prefill_split.h); grid (pairs of query block and split, 8).  A query
+// block with one split writes its output directly; otherwise each split
+// leaves its partial in its slot of `part` and pf_attn_merge, launched next,
+// combines them.
+namespace {
+__device__ __forceinline__ float max_row16(float v) {
+  v = fmaxf(v, dpp<0xB1>(v));
+  v = fmaxf(v, dpp<0x4E>(v));
+  v = fmaxf(v, dpp<0x141>(v));
+  v = fmaxf(v, dpp<0x140>(v));
+  return v;
+}
+}  // namespace
+
 extern "C" __global__ __launch_bounds__(256) void pf_attention(
     const uint16_t* __restrict__ q_roped, const uint16_t* __restrict__ k_cache,
-    const uint16_t* __restrict__ v_cache, int start, int chunk_local, uint16_t* __restrict__ out) {
-  __shared__ PfAttnLds L;
-  const int i = blockIdx.x;
+    const uint16_t* __restrict__ v_cache, int n, int start, int chunk_local, int split_blocks,
+    float* __restrict__ part, uint16_t* __restrict__ out) {
+  __shared__ __attribute__((aligned(16))) _Float16 kt[32][136];      // K tile [key][dim]
+  __shared__ __attribute__((aligned(16))) _Float16 vt[128][40];      // V tile [dim][key]
+  __shared__ __attribute__((aligned(16))) _Float16 pt[4][2][16][40];  // P hi / lo [row][key]
   const int g = blockIdx.y;
   const int t = threadIdx.x;
   const int wave = t >> 6;
   const int lane = t & 63;
-  const int half = lane >> 5;
-  const int pl = lane & 31;
-  const int pos = start + i;
+  const int c16 = lane & 15;
+  const int grp = lane >> 4;
+  const int head = 2 * g + (wave >> 1);
   const int lo = chunk_local ? start : 0;
-  const int n = pos - lo + 1;
-  if (t < 128)
-    L.qh[t >> 6][t & 63] = load_global(
-        reinterpret_cast<const uint32_t*>(q_roped + (size_t)i * 2048 + 2 * g * kHeadDim) + t);
-  const int beg = lo + (int)((int64_t)wave * n / kAttnWaves);
-  const int end = lo + (int)((int64_t)(wave + 1) * n / kAttnWaves);
-  const int n_chunks = ((n + kAttnWaves - 1) / kAttnWaves + 31) / 32;  // workgroup-uniform
-  const int last = end - 1 > lo ? end - 1 : lo;
-  __syncthreads();
+  const PfSplitGeometry G = pf_split_geometry(n, start, lo);
+  const PfSplitPair P = pf_split_pair(G, split_blocks, blockIdx.x);
+  const int qb = P.qb;
+  const int q0 = 32 * qb + 16 * (wave & 1);  // this wave's first token
 
-  float m = -__builtin_inff(), l = 0.0f;
-  float mB = -__builtin_inff(), lB = 0.0f;
-  float accA0 = 0.0f, accA1 = 0.0f, accB0 = 0.0f, accB1 = 0.0f;
-  for (int c = 0; c < n_chunks; ++c) {
-    const int c0 = beg + 32 * c;
-    const int p = c0 + pl;
-    const bool valid = p < end;
-    const int pr = p < last ? p : last;
-    u32x4 kreg[8];
-    const u32x4* krow = reinterpret_cast<const u32x4*>(
-        k_cache + ((size_t)pr * kKvHeads + g) * kHeadDim + 64 * half);
+  // Q rows as the MFMA A operand: row c16, dims 32 s + 8 grp .. + 7
+  f16x8 qa[4];
+  {
+    const int qi = q0 + c16 < n ? q0 + c16 : n - 1;
+    const _Float16* qs = reinterpret_cast<const _Float16*>(q_roped) + (size_t)qi * 2048 + head * 128;
 #pragma unroll
-    for (int mm = 0; mm < 8; ++mm) kreg[mm] = load_global(krow + mm);
-    uint32_t vreg[32];
+    for (int st = 0; st < 4; ++st)
+      qa[st] = *reinterpret_cast<const f16x8*>(qs + 32 * st + 8 * grp);
+  }
+  const int last_tok = 32 * qb + 31 < n ? 32 * qb + 31 : n - 1;
+  const int hi = start + last_tok;  // the last position any query here attends
+  // this split's positions: [kb_lo, kb_hi]
+  const int kb_lo = lo + 32 * split_blocks * P.s;
+  const int kb_hi = hi < kb_lo + 32 * split_blocks - 1 ? hi : kb_lo + 32 * split_blocks - 1;
+  // this lane's 4 query rows (4 grp + i) and their positions
+  int qpos[4];
+  bool qok[4];
 #pragma unroll
-    for (int j = 0; j < 32; ++j) {
-      const int pj = c0 + j < last ? c0 + j : last;
-      vreg[j] = load_global(
-          reinterpret_cast<const uint32_t*>(v_cache + ((size_t)pj * kKvHeads + g) * kHeadDim) + lane);
-    }
-    float dA = 0.0f, dB = 0.0f;
+  for (int i = 0; i < 4; ++i) {
+    const int tok = q0 + 4 * grp + i;
+    qok[i] = tok < n;
+    qpos[i] = start + tok;
+  }
+  float m[4], l[4];
+  f32x4 o[8];
 #pragma unroll
-    for (int mm = 0; mm < 8; ++mm) {
+  for (int i = 0; i < 4; ++i) {
+    m[i] = -__builtin_inff();
+    l[i] = 0.0f;
+  }
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int d = 32 * half + 4 * mm + j;
-        const f16x2 kv = as_f16x2(kreg[mm][j]);
-        dA = __builtin_amdgcn_fdot2(as_f16x2(L.qh[0][d]), kv, dA, false);
-        dB = __builtin_amdgcn_fdot2(as_f16x2(L.qh[1][d]), kv, dB, false);
+  for (int d = 0; d < 8; ++d) o[d] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+  const f32x4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
+
+  // thread t moves position kb + (t >> 3), dims 16 (t & 7) .. + 15 of K and V;
+  // the next block's loads are in flight while the current block is used
+  const int key = t >> 3;
+  const int dg = 16 * (t & 7);
+  u32x4 kr[2], vr[2];
+  auto load_tile = [&](int kb) {
+    const int kp = kb + key <= kb_hi ? kb + key : kb_hi;
+    const size_t row = ((size_t)kp * kKvHeads + g) * kHeadDim + dg;
+    kr[0] = load_global(reinterpret_cast<const u32x4*>(k_cache + row));
+    kr[1] = load_global(reinterpret_cast<const u32x4*>(k_cache + row + 8));
+    vr[0] = load_global(reinterpret_cast<const u32x4*>(v_cache + row));
+    vr[1] = load_global(reinterpret_cast<const u32x4*>(v_cache + row + 8));
+  };
+  load_tile(kb_lo);
+  for (int kb = kb_lo; kb <= kb_hi; kb += 32) {
+    __syncthreads();  // every wave is done with the previous tiles
+    {
+      *reinterpret_cast<u32x4*>(&kt[key][dg]) = kr[0];
+      *reinterpret_cast<u32x4*>(&kt[key][dg + 8]) = kr[1];
+      const _Float16* vh0 = reinterpret_cast<const _Float16*>(&vr[0]);
+      const _Float16* vh1 = reinterpret_cast<const _Float16*>(&vr[1]);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        vt[dg + j][key] = vh0[j];
+        vt[dg + 8 + j][key] = vh1[j];
       }
     }
-    dA = dA + __shfl_xor(dA, 32, 64);
-    dB = dB + __shfl_xor(dB, 32, 64);
-    const float sA = valid ? dA * kAttnScale : -__builtin_inff();
-    const float sB = valid ? dB * kAttnScale : -__builtin_inff();
-    const float mnA = fmaxf(m, max32(sA));
-    const float mnB = fmaxf(mB, max32(sB));
-    const float cA = mnA == -__builtin_inff() ? 1.0f : expf(m - mnA);
-    const float cB = mnB == -__builtin_inff() ? 1.0f : expf(mB - mnB);
-    const float pA = valid ? expf(sA - mnA) : 0.0f;
-    const float pB = valid ? expf(sB - mnB) : 0.0f;
-    l = l * cA + sum32(pA);
-    lB = lB * cB + sum32(pB);
-    m = mnA;
-    mB = mnB;
-    if (half == 0) {
-      L.pbuf[wave][0][pl] = pA;
-      L.pbuf[wave][1][pl] = pB;
-    }
     __syncthreads();
-    accA0 *= cA;
-    accA1 *= cA;
-    accB0 *= cB;
-    accB1 *= cB;
-    const int nv = end - c0 < 32 ? end - c0 : 32;
+    if (kb + 32 <= kb_hi) load_tile(kb + 32);
+
+    // S = Q K^T for positions kb .. kb + 15 (tile 0) and kb + 16 .. kb + 31 (tile 1)
+    f32x4 sc[2];
 #pragma unroll
-    for (int j = 0; j < 32; ++j) {
-      const uint32_t vw = j < nv ? vreg[j] : 0u;
-      const f16x2 vv = as_f16x2(vw);
-      const float v0 = (float)vv.x, v1 = (float)vv.y;
-      const float wa = L.pbuf[wave][0][j], wb = L.pbuf[wave][1][j];
-      accA0 = accA0 + wa * v0;
-      accA1 = accA1 + wa * v1;
-      accB0 = accB0 + wb * v0;
-      accB1 = accB1 + wb * v1;
+    for (int nt = 0; nt < 2; ++nt) {
+      sc[nt] = zero;
+#pragma unroll
+      for (int st = 0; st < 4; ++st) {
+        const f16x8 kf = *reinterpret_cast<const f16x8*>(&kt[16 * nt + c16][32 * st + 8 * grp]);
+        sc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[st], kf, sc[nt], 0, 0, 0);
+      }
     }
-    __syncthreads();
+    // online softmax per query row 4 grp + i (its 32 scores over the 16 lanes of the row group)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float sv[2];
+      bool ok[2];
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt) {
+        const int kp = kb + 16 * nt + c16;
+        ok[nt] = qok[i] && kp <= qpos[i];  // a split ends on a block edge or at hi
+        sv[nt] = ok[nt] ? sc[nt][i] * kAttnScale : -__builtin_inff();
+      }
+      const float mx = max_row16(fmaxf(sv[0], sv[1]));
+      const float mn = fmaxf(m[i], mx);
+      const float alpha = mn == -__builtin_inff() ? 1.0f : expf(m[i] - mn);
+      float p[2];
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt) p[nt] = ok[nt] ? expf(sv[nt] - mn) : 0.0f;
+      const float ps = reduce_row16(p[0] + p[1]);
+      l[i] = l[i] * alpha + ps;
+      m[i] = mn;
+#pragma unroll
+      for (int d = 0; d < 8; ++d) o[d][i] *= alpha;
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt) {
+        const _Float16 ph = to_f16(p[nt]);
+        const _Float16 pl = to_f16(p[nt] - (float)ph);
+        pt[wave][0][4 * grp + i][16 * nt + c16] = ph;
+        pt[wave][1][4 * grp + i][16 * nt + c16] = pl;
+      }
+    }
+    // O += P V: A = P rows (this wave's 16 queries x 32 positions), B = V^T
+    // tile (positions x 16 dims per tile); LDS is in order within the wave
+    const f16x8 ph = *reinterpret_cast<const f16x8*>(&pt[wave][0][c16][8 * grp]);
+    const f16x8 pl = *reinterpret_cast<const f16x8*>(&pt[wave][1][c16][8 * grp]);
+#pragma unroll
+    for (int d = 0; d < 8; ++d) {
+      const f16x8 vf = *reinterpret_cast<const f16x8*>(&vt[16 * d + c16][8 * grp]);
+      o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph, vf, o[d], 0, 0, 0);
+      o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pl, vf, o[d], 0, 0, 0);
+    }
   }
 
-  if (lane == 0) {
-    L.mrg[wave][0][0] = m;
-    L.mrg[wave][0][1] = l;
-    L.mrg[wave][1][0] = mB;
-    L.mrg[wave][1][1] = lB;
-  }
-  L.mrg[wave][0][2 + 2 * lane] = accA0;
-  L.mrg[wave][0][3 + 2 * lane] = accA1;
-  L.mrg[wave][1][2 + 2 * lane] = accB0;
-  L.mrg[wave][1][3 + 2 * lane] = accB1;
-  __syncthreads();
-  if (wave < 2) {
-    const int hh = wave;
-    float M = -__builtin_inff();
+  if (P.ns == 1) {
 #pragma unroll
-    for (int w = 0; w < kAttnWaves; ++w) M = fmaxf(M, L.mrg[w][hh][0]);
-    float Ls = 0.0f, a0 = 0.0f, a1 = 0.0f;
+    for (int i = 0; i < 4; ++i) {
+      const int tok = q0 + 4 * grp + i;
+      if (tok >= n) continue;
+      uint16_t* orow = out + (size_t)tok * 2048 + head * 128;
 #pragma unroll
-    for (int w = 0; w < kAttnWaves; ++w) {
-      const float mw = L.mrg[w][hh][0];
-      const float ww = mw == -__builtin_inff() ? 0.0f : expf(mw - M);
-      Ls = Ls + L.mrg[w][hh][1] * ww;
-      a0 = a0 + L.mrg[w][hh][2 + 2 * lane] * ww;
-      a1 = a1 + L.mrg[w][hh][3 + 2 * lane] * ww;
+      for (int d = 0; d < 8; ++d) orow[16 * d + c16] = f32_to_f16_bits(o[d][i] / l[i]);
     }
-    reinterpret_cast<uint32_t*>(out + (size_t)i * 2048 + (2 * g + hh) * kHeadDim)[lane] =
-        pack_f16x2(a0 / Ls, a1 / Ls);
+    return;
   }
+
+  // several splits: (m, l, O) of this split's positions to its slot, rows
+  // 16 wave + 4 grp + i; pf_attn_merge combines the slots
+  float* slot = part + ((size_t)blockIdx.x * kKvHeads + g) * kPfAttnSlotFloats;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = 16 * wave + 4 * grp + i;
+#pragma unroll
+    for (int d = 0; d < 8; ++d) slot[r * kHeadDim + 16 * d + c16] = o[d][i];
+    if (c16 == 0) {
+      slot[64 * kHeadDim + r] = m[i];
+      slot[64 * kHeadDim + 64 + r] = l[i];
+    }
+  }
+}
+
+// The splits of query block blockIdx.x, kv head g = blockIdx.y (nothing to do
+// for a block with one split): in split order,
+//   M = max_s m_s,  O = sum_s O_s e^(m_s - M),  l = sum_s l_s e^(m_s - M),
+// out = O / l.  Thread t: slot row t >> 2 (wave w = row >> 4 of pf_attention:
+// head 2g + (w >> 1), token 32 qb + 16 (w & 1) + (row & 15)), dims 32 (t & 3)
+// .. + 31.
+extern "C" __global__ __launch_bounds__(256) void pf_attn_merge(
+    const float* __restrict__ part, int n, int start, int chunk_local, int split_blocks,
+    uint16_t* __restrict__ out) {
+  const int qb = blockIdx.x;
+  const int g = blockIdx.y;
+  const PfSplitGeometry G = pf_split_geometry(n, start, chunk_local ? start : 0);
+  const int nb = qb == G.nqb - 1 ? G.nb_last : qb + G.c;
+  const int ns = (nb + split_blocks - 1) / split_blocks;
+  if (ns == 1) return;
+  const size_t first = (size_t)pf_pairs_before(G, qb, split_blocks) * kKvHeads + g;
+  const int t = threadIdx.x;
+  const int r = t >> 2;
+  const int d0 = 32 * (t & 3);
+  const int w = r >> 4;
+  const int tok = 32 * qb + 16 * (w & 1) + (r & 15);
+  if (tok >= n) return;
+  float mx = -__builtin_inff();
+  for (int s = 0; s < ns; ++s)
+    mx = fmaxf(mx, part[(first + (size_t)s * kKvHeads) * kPfAttnSlotFloats + 64 * kHeadDim + r]);
+  float acc[32], lsum = 0.0f;
+#pragma unroll
+  for (int d = 0; d < 32; ++d) acc[d] = 0.0f;
+  for (int s = 0; s < ns; ++s) {
+    const float* sl = part + (first + (size_t)s * kKvHeads) * kPfAttnSlotFloats;
+    const float ms = sl[64 * kHeadDim + r];
+    const float wgt = ms == -__builtin_inff() ? 0.0f : expf(ms - mx);
+    lsum += sl[64 * kHeadDim + 64 + r] * wgt;
+    const float4* orow = reinterpret_cast<const float4*>(sl + r * kHeadDim + d0);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float4 v = orow[j];
+      acc[4 * j] += v.x * wgt;
+      acc[4 * j + 1] += v.y * wgt;
+      acc[4 * j + 2] += v.z * wgt;
+      acc[4 * j + 3] += v.w * wgt;
+    }
+  }
+  uint32_t packed[16];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) packed[j] = pack_f16x2(acc[2 * j] / lsum, acc[2 * j + 1] / lsum);
+  u32x4* dst = reinterpret_cast<u32x4*>(out + (size_t)tok * 2048 + (2 * g + (w >> 1)) * kHeadDim + d0);
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    dst[j] = (u32x4){packed[4 * j], packed[4 * j + 1], packed[4 * j + 2], packed[4 * j + 3]};
 }
 
 // *pos = v (the position after the prompt, before the head's advance).

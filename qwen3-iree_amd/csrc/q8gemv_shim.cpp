@@ -5,10 +5,12 @@
 // include/q8gemv.h.
 #include "q8gemv.h"
 #include "qwen3_decode.h"
+#include "prefill_split.h"
 
 #include <dlfcn.h>
 #include <hip/hip_runtime_api.h>
 
+#include <algorithm>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -102,8 +104,11 @@ struct State {
                 dec_final = nullptr, dec_adv = nullptr, dec_clear = nullptr, dec_step = nullptr;
   hipModule_t pf_module = nullptr;  // prefill_gfx950.hsaco (optional)
   hipFunction_t pf_embed = nullptr, pf_norm = nullptr, pf_gemm = nullptr, pf_gemm_res = nullptr,
-                pf_gemm_swiglu = nullptr, pf_rope = nullptr, pf_attn = nullptr,
+                pf_gemm_m32 = nullptr, pf_gemm_res_m32 = nullptr, pf_gemm_swiglu = nullptr,
+                pf_rope = nullptr, pf_attn = nullptr, pf_attn_merge = nullptr,
                 pf_set_pos = nullptr;
+  int pf_tile_rows = 0;   // prefill GEMM token tile: 0 = by shape, 32 or 64
+  int pf_attn_split = 0;  // prefill attention positions per split in blocks of 32: 0 = by shape
   int step_single = -1;   // single-launch decode step: -1 unknown, 0 off, 1 on
   bool step_capable = false;
   int vocab_wgs = 0;      // 0 = default
@@ -302,9 +307,12 @@ int q8gemv_init(const char* code_object_path) {
                      {&g.pf_norm, "pf_rmsnorm"},
                      {&g.pf_gemm, "pf_gemm_q8"},
                      {&g.pf_gemm_res, "pf_gemm_q8_res"},
+                     {&g.pf_gemm_m32, "pf_gemm_q8_m32"},
+                     {&g.pf_gemm_res_m32, "pf_gemm_q8_res_m32"},
                      {&g.pf_gemm_swiglu, "pf_gemm_q8_swiglu"},
                      {&g.pf_rope, "pf_qk_rope_cache"},
                      {&g.pf_attn, "pf_attention"},
+                     {&g.pf_attn_merge, "pf_attn_merge"},
                      {&g.pf_set_pos, "pf_set_pos"}};
         bool ok = true;
         for (auto& n : names) ok = ok && hipModuleGetFunction(n.fn, pm, n.name) == hipSuccess;
@@ -355,8 +363,8 @@ void q8gemv_shutdown(void) {
   g.step_capable = false;
   if (g.pf_module) (void)hipModuleUnload(g.pf_module);
   g.pf_module = nullptr;
-  g.pf_embed = g.pf_norm = g.pf_gemm = g.pf_gemm_res = g.pf_gemm_swiglu = g.pf_rope =
-      g.pf_attn = g.pf_set_pos = nullptr;
+  g.pf_embed = g.pf_norm = g.pf_gemm = g.pf_gemm_res = g.pf_gemm_m32 = g.pf_gemm_res_m32 =
+      g.pf_gemm_swiglu = g.pf_rope = g.pf_attn = g.pf_attn_merge = g.pf_set_pos = nullptr;
   g.vocab = g.vocab_finalize = g.ws_reset = g.copy = nullptr;
   g.ready = false;
 }
@@ -799,6 +807,7 @@ namespace {
 constexpr int kLayers = 28;
 constexpr int kVocabRows = 151936;
 constexpr int64_t kKvRow = 8 * 128;  // f16 elements per cache slot
+constexpr int kKvHeads = 8;
 constexpr int kAttnGroupsHost = 8;  // attention workgroups (partials) per kv head
 constexpr int32_t kGenerateBatch = 4;  // tokens between EOS checks (qwen3_full.mlir:1412)
 
@@ -1055,12 +1064,48 @@ struct GemmArgs {
 // Workspace regions, f16 elements per token: h, h1 (residual), xn
 // (rms_norm(h, attn_norm)), q, k, v, q_roped, attention output, SwiGLU
 // output, fn (rms_norm(h1, ffn_norm)).
-constexpr int kPfRegions = 10;
-constexpr int kPfCols[kPfRegions] = {1024, 1024, 1024, 2048, 1024, 1024, 2048, 2048, 3072, 1024};
+// Then the attention's split partials (f32 slots of kPfAttnSlotFloats for
+// pf_attn_pair_cap(n) pairs x 8 kv heads).
+constexpr int kPfTokenRegions = 10;
+constexpr int kPfRegions = 11;
+constexpr int kPfCols[kPfTokenRegions] = {1024, 1024, 1024, 2048, 1024, 1024, 2048, 2048, 3072, 1024};
 constexpr int32_t kPfMaxTokens = 1 << 20;
 
+// (query block, split) pairs the partial slots hold: 2 per query block + 64
+int64_t pf_attn_pair_cap(int32_t n) { return 2LL * ((n + 31) / 32) + 64; }
+
 size_t pf_region_bytes(int32_t n, int i) {
-  return ((size_t)n * kPfCols[i] * 2 + 255) / 256 * 256;
+  size_t b;
+  if (i < kPfTokenRegions)
+    b = (size_t)n * kPfCols[i] * 2;
+  else
+    b = (size_t)pf_attn_pair_cap(n) * kKvHeads * kPfAttnSlotFloats * 4;
+  return (b + 255) / 256 * 256;
+}
+
+// Positions per attention split, in blocks of 32.  A query block's positions
+// are walked one block after another, so without splits the longest query
+// block sets the time; each split costs a partial written and merged.  8
+// blocks (256 positions) measured best for 512- and 2048-token prompts from
+// position 0 (sweep of 1 .. 24 and unsplit).  Raised where the partial slots
+// would not hold the splits.
+constexpr int32_t kPfAttnSplitDefault = 8;
+
+int32_t pf_attn_split_blocks(int32_t n, int32_t p0, int chunk_local) {
+  const PfSplitGeometry G = pf_split_geometry(n, p0, chunk_local ? p0 : 0);
+  const int64_t cap = pf_attn_pair_cap(n);
+  const int32_t nb_max = std::max(G.nb_last, G.c + G.nqb - 2);
+  const int32_t s0 = g.pf_attn_split > 0 ? g.pf_attn_split : kPfAttnSplitDefault;
+  int32_t lo_s = std::min(s0, nb_max), hi_s = nb_max;
+  // smallest S >= lo_s whose pairs fit (at S = nb_max there are nqb pairs)
+  while (lo_s < hi_s) {
+    const int32_t mid = lo_s + (hi_s - lo_s) / 2;
+    if (pf_pairs_total(G, mid) <= cap)
+      hi_s = mid;
+    else
+      lo_s = mid + 1;
+  }
+  return lo_s;
 }
 
 size_t pf_workspace_bytes(int32_t n) {
@@ -1069,14 +1114,26 @@ size_t pf_workspace_bytes(int32_t n) {
   return b;
 }
 
-int launch_gemm(hipFunction_t fn, const void* x, int ldx, const void* wl, int K, int n_out,
-                int tile_cols, void* y, int ldy, const void* r, int ldr, int up_row, int M,
-                hipStream_t st) {
+// fn covers 64 tokens per workgroup; fn_m32 (may be null) the same product
+// over 32 tokens (same operations per output element, so the same bits).  The
+// 32-token tile is used where the 64-token grid would leave the device with
+// fewer than 2 workgroups per CU.
+int launch_gemm(hipFunction_t fn, hipFunction_t fn_m32, const void* x, int ldx, const void* wl,
+                int K, int n_out, int tile_cols, void* y, int ldy, const void* r, int ldr,
+                int up_row, int M, hipStream_t st) {
   GemmArgs a{x, wl, y, r, M, K, n_out / tile_cols, ldx, ldy, ldr, up_row};
   // the kernel maps workgroups to n tiles in groups of 8 (one per XCD)
   if (n_out % tile_cols != 0 || a.n_tiles % 8 != 0 || K % 256 != 0)
     return fail(Q8_ERR_BAD_SHAPE, "prefill GEMM shape N=%d K=%d", n_out, K);
-  const int64_t mt = ((int64_t)M + 63) / 64;
+  int rows = 64;
+  if (fn_m32) {
+    if (g.pf_tile_rows == 32)
+      rows = 32;
+    else if (g.pf_tile_rows == 0 && ((int64_t)M + 63) / 64 * a.n_tiles < 2LL * g.compute_units)
+      rows = 32;
+  }
+  if (rows == 32) fn = fn_m32;
+  const int64_t mt = ((int64_t)M + rows - 1) / rows;
   const int64_t grid = mt * a.n_tiles;
   if (grid > 0x7fffffff) return fail(Q8_ERR_BAD_SHAPE, "prefill GEMM grid too large");
   void* args[] = {&a};
@@ -1096,20 +1153,20 @@ int launch_prefill_layer(const qwen3_weights* w, int layer, void* k_cache, void*
   void* kc = mb(k_cache) + (int64_t)layer * max_seq * kKvRow * 2;
   void* vc = mb(v_cache) + (int64_t)layer * max_seq * kKvRow * 2;
   void *h = ws[0], *h1 = ws[1], *xn = ws[2], *q = ws[3], *k = ws[4], *v = ws[5], *qr = ws[6],
-       *attn = ws[7], *act = ws[8], *fnx = ws[9];
+       *attn = ws[7], *act = ws[8], *fnx = ws[9], *part = ws[10];
   const uint32_t norm_grid = (uint32_t)((n + 15) / 16);
   int rc;
   {
     void* args[] = {&h, &an, &xn, &n};
     if ((rc = launch(g.pf_norm, norm_grid, 256, args, st))) return rc;
   }
-  if ((rc = launch_gemm(g.pf_gemm, xn, 1024, cb(w->wq) + layer * bpl_q, 1024, 2048, 64, q, 2048,
+  if ((rc = launch_gemm(g.pf_gemm, g.pf_gemm_m32, xn, 1024, cb(w->wq) + layer * bpl_q, 1024, 2048, 64, q, 2048,
                         nullptr, 0, 0, n, st)))
     return rc;
-  if ((rc = launch_gemm(g.pf_gemm, xn, 1024, cb(w->wk) + layer * bpl_kv, 1024, 1024, 64, k, 1024,
+  if ((rc = launch_gemm(g.pf_gemm, g.pf_gemm_m32, xn, 1024, cb(w->wk) + layer * bpl_kv, 1024, 1024, 64, k, 1024,
                         nullptr, 0, 0, n, st)))
     return rc;
-  if ((rc = launch_gemm(g.pf_gemm, xn, 1024, cb(w->wv) + layer * bpl_kv, 1024, 1024, 64, v, 1024,
+  if ((rc = launch_gemm(g.pf_gemm, g.pf_gemm_m32, xn, 1024, cb(w->wv) + layer * bpl_kv, 1024, 1024, 64, v, 1024,
                         nullptr, 0, 0, n, st)))
     return rc;
   {
@@ -1118,21 +1175,30 @@ int launch_prefill_layer(const qwen3_weights* w, int layer, void* k_cache, void*
     if ((rc = launch2(g.pf_rope, (uint32_t)n, 8, 256, args, st))) return rc;
   }
   {
-    int start = p0, cl = chunk_local ? 1 : 0;
-    void* args[] = {&qr, &kc, &vc, &start, &cl, &attn};
-    if ((rc = launch2(g.pf_attn, (uint32_t)n, 8, 256, args, st))) return rc;
+    int start = p0, cl = chunk_local ? 1 : 0, nn = n;
+    int sb = pf_attn_split_blocks(n, p0, chunk_local);
+    const PfSplitGeometry G = pf_split_geometry(n, p0, cl ? p0 : 0);
+    const int64_t pairs = pf_pairs_total(G, sb);
+    if (pairs > pf_attn_pair_cap(n))
+      return fail(Q8_ERR_BAD_SHAPE, "attention splits exceed the workspace");  // not reached
+    void* args[] = {&qr, &kc, &vc, &nn, &start, &cl, &sb, &part, &attn};
+    if ((rc = launch2(g.pf_attn, (uint32_t)pairs, 8, 256, args, st))) return rc;
+    if (pairs > G.nqb) {  // some query block has several splits
+      void* margs[] = {&part, &nn, &start, &cl, &sb, &attn};
+      if ((rc = launch2(g.pf_attn_merge, (uint32_t)G.nqb, 8, 256, margs, st))) return rc;
+    }
   }
-  if ((rc = launch_gemm(g.pf_gemm_res, attn, 2048, cb(w->wo) + layer * bpl_o, 2048, 1024, 64, h1,
+  if ((rc = launch_gemm(g.pf_gemm_res, g.pf_gemm_res_m32, attn, 2048, cb(w->wo) + layer * bpl_o, 2048, 1024, 64, h1,
                         1024, h, 1024, 0, n, st)))
     return rc;
   {
     void* args[] = {&h1, &fn, &fnx, &n};
     if ((rc = launch(g.pf_norm, norm_grid, 256, args, st))) return rc;
   }
-  if ((rc = launch_gemm(g.pf_gemm_swiglu, fnx, 1024, cb(w->wgu) + layer * bpl_gu, 1024, 3072, 32,
+  if ((rc = launch_gemm(g.pf_gemm_swiglu, nullptr, fnx, 1024, cb(w->wgu) + layer * bpl_gu, 1024, 3072, 32,
                         act, 3072, nullptr, 0, 3072, n, st)))
     return rc;
-  return launch_gemm(g.pf_gemm_res, act, 3072, cb(w->wdn) + layer * bpl_dn, 3072, 1024, 64, h,
+  return launch_gemm(g.pf_gemm_res, g.pf_gemm_res_m32, act, 3072, cb(w->wdn) + layer * bpl_dn, 3072, 1024, 64, h,
                      1024, h1, 1024, 0, n, st);
 }
 
@@ -1206,6 +1272,18 @@ int qwen3_get_step_mode(int* mode) {
   int rc = check_decode_ready();
   if (rc) return rc;
   *mode = use_single() ? 1 : 0;
+  return Q8_OK;
+}
+
+int qwen3_set_prefill_tiling(int gemm_rows, int attn_split_blocks) {
+  if (gemm_rows != 0 && gemm_rows != 32 && gemm_rows != 64)
+    return fail(Q8_ERR_BAD_ARGUMENT, "prefill GEMM rows %d not in {0, 32, 64}", gemm_rows);
+  if (attn_split_blocks < 0)
+    return fail(Q8_ERR_BAD_ARGUMENT, "attention split of %d blocks", attn_split_blocks);
+  int rc = check_prefill_ready();
+  if (rc) return rc;
+  g.pf_tile_rows = gemm_rows;
+  g.pf_attn_split = attn_split_blocks;
   return Q8_OK;
 }
 
@@ -1346,8 +1424,8 @@ int qwen3_generate(const qwen3_weights* w, void* k_cache, void* v_cache, int64_t
 }
 
 int64_t qwen3_prefill_workspace_offset(int32_t n_prompt, const char* name) {
-  static const char* const kNames[kPfRegions] = {"h", "res", "xn", "q", "k", "v", "q_roped",
-                                                 "attn", "act", "fn"};
+  static const char* const kNames[kPfRegions] = {"h", "res",     "xn",   "q",   "k",  "v",
+                                                 "q_roped", "attn", "act", "fn", "attn_part"};
   if (!name || n_prompt < 1 || n_prompt > kPfMaxTokens) return -1;
   int64_t off = 0;
   for (int i = 0; i < kPfRegions; ++i) {

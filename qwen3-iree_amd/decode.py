@@ -137,6 +137,13 @@ def set_step_mode(mode: int) -> None:
     Q._call("qwen3_set_step_mode", int(mode))
 
 
+def set_prefill_tiling(gemm_rows: int = 0, attn_split_blocks: int = 0) -> None:
+    """Work division of the batched prompt path (0 = by shape): token rows per
+    GEMM workgroup (32 or 64) and cache positions per attention split in
+    blocks of 32."""
+    Q._call("qwen3_set_prefill_tiling", int(gemm_rows), int(attn_split_blocks))
+
+
 def scratch_bytes() -> int:
     return int(Q.load_library().qwen3_scratch_bytes())
 

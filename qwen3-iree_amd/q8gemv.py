@@ -160,6 +160,7 @@ _SIGNATURES = {
     "qwen3_prefill_layer": [_P, _I, _P, _P, _I64, ctypes.c_int32, ctypes.c_int32, _I, _P, _SZ, _P],
     "qwen3_prefill_workspace_offset": [ctypes.c_int32, ctypes.c_char_p],
     "qwen3_set_step_mode": [_I],
+    "qwen3_set_prefill_tiling": [_I, _I],
     "qwen3_get_step_mode": [_P],
 }
 _RESTYPES = {

@@ -239,3 +239,62 @@ def test_prefill_batched_cache_edges(gpu, D, dmodel):
     with pytest.raises(Q.Q8GemvError, match="exceed max_seq"):
         sess.prefill_batched(np.arange(10, dtype=np.int32))
     sess.free()
+
+
+@pytest.mark.parametrize("n,p0", [(45, 3), (300, 0)])
+def test_prefill_tile_rows_bit_identical(gpu, D, dmodel, n, p0):
+    """The 32- and 64-token GEMM tiles give the same bits in every stage."""
+    rng = np.random.default_rng(9100 + n)
+    sess = D.DecodeSession(dmodel, MAX_SEQ)
+    kc = np.zeros((28 * MAX_SEQ, 1024), np.float16)
+    vc = np.zeros_like(kc)
+    fill_cache_layer(sess, 5, p0, rng, kc, vc)
+    h_in = (1.5 * rng.standard_normal((n, 1024))).astype(np.float16)
+    outs = []
+    try:
+        for rows in (32, 64, 0):
+            print(f"prefill tile rows {rows} n {n} p0 {p0}", flush=True)
+            D.set_prefill_tiling(rows, 0)
+            g = sess.prefill_layer(5, h_in, p0, False)
+            outs.append((g, sess.cache_rows(5, 0, MAX_SEQ)))
+    finally:
+        D.set_prefill_tiling(0, 0)
+    (g32, c32), (g64, c64), (ga, ca) = outs
+    for name in g32:
+        assert np.array_equal(g32[name].view(np.uint16), g64[name].view(np.uint16)), name
+        assert np.array_equal(g32[name].view(np.uint16), ga[name].view(np.uint16)), name
+    for a, b in zip(c32, c64):
+        assert np.array_equal(a.view(np.uint16), b.view(np.uint16))
+    with pytest.raises(Exception):
+        D.set_prefill_tiling(48, 0)
+    with pytest.raises(Exception):
+        D.set_prefill_tiling(0, -1)
+    sess.free()
+
+
+@pytest.mark.parametrize("split", [1, 2, 5, 1000])
+def test_prefill_attention_splits(O, gpu, D, dmodel, split):
+    """Every division of the cache positions into splits (merged by the last
+    split of a query block) gives the attention within its tolerance."""
+    n, p0, layer = 100, 50, 9
+    rng = np.random.default_rng(9300 + split)
+    sess = D.DecodeSession(dmodel, MAX_SEQ)
+    kc = np.zeros((28 * MAX_SEQ, 1024), np.float16)
+    vc = np.zeros_like(kc)
+    fill_cache_layer(sess, layer, p0, rng, kc, vc)
+    h_in = (1.5 * rng.standard_normal((n, 1024))).astype(np.float16)
+    try:
+        for chunk_local in (False, True):
+            print(f"prefill attention split {split} chunk_local {chunk_local}", flush=True)
+            D.set_prefill_tiling(0, split)
+            g = sess.prefill_layer(layer, h_in, p0, chunk_local)
+            k_rows, v_rows = sess.cache_rows(layer, 0, MAX_SEQ)
+            lo = p0 if chunk_local else 0
+            for i in range(n):
+                pos = p0 + i
+                a_want = O.attention(g["q_roped"][i], k_rows[lo:pos + 1], v_rows[lo:pos + 1])
+                d = np.abs(f64(g["attn"][i]) - f64(a_want))
+                assert (d <= 2 * ulp(O, a_want) + 1e-5).all(), (chunk_local, i, d.max())
+    finally:
+        D.set_prefill_tiling(0, 0)
+    sess.free()
