@@ -248,7 +248,7 @@ __device__ __forceinline__ void kv_prefetch(uint8_t* kv, const uint16_t* __restr
 }
 
 // LDS of one attention workgroup.
-struct AttnLds {
+struct __attribute__((aligned(16))) AttnLds {
   uint32_t qh[2][64];  // roped q_A, q_B as f16 pairs
   uint32_t kh[64];     // roped new k as f16 pairs
   float pbuf[kAttnWaves][2][32];
@@ -404,19 +404,28 @@ __device__ __forceinline__ void attention_group(AttnLds& L, int g, int sg, int p
     const int p = c0 + pl;
     const bool valid = p < end;
     // the row of position pos is this step's k (in LDS; the cache slot was
-    // requested before it was written)
-    const bool is_new = p == pos;
-    float dA = 0.0f, dB = 0.0f;
+    // requested before it was written): one lane takes it over
+    if (p == pos) {
 #pragma unroll
-    for (int mm = 0; mm < 8; ++mm) {
+      for (int mm = 0; mm < 8; ++mm)
+        kreg[mm] = *reinterpret_cast<const u32x4*>(&L.kh[32 * half + 4 * mm]);
+    }
+    // two partial sums per head (dims of even / odd 8-dim groups) halve the
+    // dependent chain
+    float dA0 = 0.0f, dB0 = 0.0f, dA1 = 0.0f, dB1 = 0.0f;
+#pragma unroll
+    for (int mm = 0; mm < 8; mm += 2) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int i = 32 * half + 4 * mm + j;
-        const f16x2 kv = as_f16x2(is_new ? L.kh[i] : kreg[mm][j]);
-        dA = __builtin_amdgcn_fdot2(as_f16x2(L.qh[0][i]), kv, dA, false);
-        dB = __builtin_amdgcn_fdot2(as_f16x2(L.qh[1][i]), kv, dB, false);
+        const f16x2 k0 = as_f16x2(kreg[mm][j]), k1 = as_f16x2(kreg[mm + 1][j]);
+        dA0 = __builtin_amdgcn_fdot2(as_f16x2(L.qh[0][i]), k0, dA0, false);
+        dB0 = __builtin_amdgcn_fdot2(as_f16x2(L.qh[1][i]), k0, dB0, false);
+        dA1 = __builtin_amdgcn_fdot2(as_f16x2(L.qh[0][i + 4]), k1, dA1, false);
+        dB1 = __builtin_amdgcn_fdot2(as_f16x2(L.qh[1][i + 4]), k1, dB1, false);
       }
     }
+    float dA = dA0 + dA1, dB = dB0 + dB1;
     dA = dA + __shfl_xor(dA, 32, 64);
     dB = dB + __shfl_xor(dB, 32, 64);
     const float sA = valid ? dA * kAttnScale : -__builtin_inff();
@@ -450,10 +459,10 @@ __device__ __forceinline__ void attention_group(AttnLds& L, int g, int sg, int p
       const f16x2 vv = as_f16x2(vw);
       const float v0 = (float)vv.x, v1 = (float)vv.y;
       const float wa = L.pbuf[wave][0][j], wb = L.pbuf[wave][1][j];
-      accA0 = accA0 + wa * v0;
-      accA1 = accA1 + wa * v1;
-      accB0 = accB0 + wb * v0;
-      accB1 = accB1 + wb * v1;
+      accA0 = __builtin_fmaf(wa, v0, accA0);
+      accA1 = __builtin_fmaf(wa, v1, accA1);
+      accB0 = __builtin_fmaf(wb, v0, accB0);
+      accB1 = __builtin_fmaf(wb, v1, accB1);
     }
     __syncthreads();
     if (c + 1 < n_chunks) load_chunk(c0 + 32);

@@ -91,6 +91,7 @@ struct State {
   hipModule_t module = nullptr;
   hipFunction_t q8[3] = {};  // K = 1024, 2048, 3072
   hipFunction_t q8batch = nullptr;
+  int batch_threads = 64;  // q8gemv_batch_k's declared workgroup size
   hipFunction_t q8qkv = nullptr;
   hipFunction_t hal[6] = {};  // IREE HAL-ABI kernels, in kHalDispatches order
   hipFunction_t vocab = nullptr;
@@ -232,6 +233,14 @@ int q8gemv_init(const char* code_object_path) {
   if (e == hipSuccess) e = hipModuleGetFunction(&g.q8[1], mod, "q8gemv_p2");
   if (e == hipSuccess) e = hipModuleGetFunction(&g.q8[2], mod, "q8gemv_p3");
   if (e == hipSuccess) e = hipModuleGetFunction(&g.q8batch, mod, "q8gemv_batch_k");
+  g.batch_threads = 64;
+  if (e == hipSuccess) {
+    int threads = 0;
+    if (hipFuncGetAttribute(&threads, HIP_FUNC_ATTRIBUTE_MAX_THREADS_PER_BLOCK, g.q8batch) ==
+            hipSuccess &&
+        threads >= 64 && threads % 64 == 0)
+      g.batch_threads = threads;
+  }
   if (e == hipSuccess) e = hipModuleGetFunction(&g.q8qkv, mod, "q8gemv_qkv_k");
   for (int i = 0; i < 6 && e == hipSuccess; ++i)
     e = hipModuleGetFunction(&g.hal[i], mod, kHalDispatches[i].name);
@@ -553,13 +562,15 @@ int q8gemv_batch(const void* device_table, int count, int32_t total_units, void*
   if (total_units < count) return fail(Q8_ERR_BAD_ARGUMENT, "total_units %d < count", total_units);
   int rc = check_ready();
   if (rc) return rc;
-  const int64_t cap = g.batch_wgs > 0 ? g.batch_wgs : 12LL * cu_count();
+  // default: 12 waves per CU
+  const int64_t cap = g.batch_wgs > 0 ? g.batch_wgs : 12LL * 64 / g.batch_threads * cu_count();
   const int64_t grid = total_units < cap ? total_units : cap;
   const void* t_arg = device_table;
   int c_arg = count;
   int u_arg = total_units;
   void* args[] = {&t_arg, &c_arg, &u_arg};
-  return launch(g.q8batch, (uint32_t)grid, 64, args, static_cast<hipStream_t>(stream));
+  return launch(g.q8batch, (uint32_t)grid, (uint32_t)g.batch_threads, args,
+                static_cast<hipStream_t>(stream));
 }
 
 size_t vocab_argmax_workspace_bytes(void) { return kVocabWorkspaceBytes; }
