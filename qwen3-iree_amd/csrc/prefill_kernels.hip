@@ -64,6 +64,14 @@ struct GemmArgs {
   int n_tiles;        // output tiles of 64 columns (kEpiSwiGLU: 32 gate + 32 up rows)
   int ldx, ldy, ldr;
   int up_row;         // kEpiSwiGLU: first up row of W (gate rows are 0..up_row-1)
+  // Up to three products with the same x in one launch: tiles [seg_tile[0],
+  // seg_tile[1]) use w_seg[0] / y_seg[0] / ldy_seg[0], tiles from seg_tile[1]
+  // on the second set (tile numbers counted from the set's first tile);
+  // seg_tile = n_tiles when unused.
+  const uint8_t* w_seg[2];
+  uint16_t* y_seg[2];
+  int ldy_seg[2];
+  int seg_tile[2];
 };
 
 template <int EPI, int BM>
@@ -87,8 +95,18 @@ __device__ __forceinline__ void gemm_q8(const GemmArgs& A) {
   const int mt = (A.M + BM - 1) / BM;
   const int xcd = blockIdx.x & 7;
   const int slot = blockIdx.x >> 3;
-  const int n_tile = (slot / mt) * 8 + xcd;
+  int n_tile = (slot / mt) * 8 + xcd;
   const int m0 = (slot % mt) * BM;
+  const uint8_t* wb = A.w;
+  uint16_t* yb = A.y;
+  int ldy = A.ldy;
+  if (n_tile >= A.seg_tile[0]) {
+    const int sg = n_tile >= A.seg_tile[1] ? 1 : 0;
+    wb = A.w_seg[sg];
+    yb = A.y_seg[sg];
+    ldy = A.ldy_seg[sg];
+    n_tile -= A.seg_tile[sg];
+  }
   const int row_bytes = A.K / 32 * 34;
   const int stages = A.K / (32 * kStageBlocks);
 
@@ -115,7 +133,7 @@ __device__ __forceinline__ void gemm_q8(const GemmArgs& A) {
       if (piece < kWPieces) {
         const int row = piece / 17;
         wp[j] = load_global(reinterpret_cast<const u32x4*>(
-            A.w + (size_t)w_row(row) * row_bytes + kWRow * s + 16 * (piece - 17 * row)));
+            wb + (size_t)w_row(row) * row_bytes + kWRow * s + 16 * (piece - 17 * row)));
       }
     }
   };
@@ -239,16 +257,16 @@ __device__ __forceinline__ void gemm_q8(const GemmArgs& A) {
       if (m >= A.M) continue;
       if constexpr (EPI == kEpiSwiGLU) {
         const int col = 32 * n_tile + 16 * wn + c16;
-        A.y[(size_t)m * A.ldy + col] = swiglu_f16(acc[ms][0][i], acc[ms][1][i]);
+        yb[(size_t)m * ldy + col] = swiglu_f16(acc[ms][0][i], acc[ms][1][i]);
       } else {
 #pragma unroll
         for (int ns = 0; ns < NS; ++ns) {
           const int col = kGemmBN * n_tile + (BM == 64 ? 32 * wn + 16 * ns : 16 * wn) + c16;
           if constexpr (EPI == kEpiResidual)
-            A.y[(size_t)m * A.ldy + col] =
+            yb[(size_t)m * ldy + col] =
                 residual_f16(as_half(A.r[(size_t)m * A.ldr + col]), acc[ms][ns][i]);
           else
-            A.y[(size_t)m * A.ldy + col] = f32_to_f16_bits(acc[ms][ns][i]);
+            yb[(size_t)m * ldy + col] = f32_to_f16_bits(acc[ms][ns][i]);
         }
       }
     }

@@ -1070,6 +1070,21 @@ struct GemmArgs {
   int n_tiles;
   int ldx, ldy, ldr;
   int up_row;
+  const void* w_seg[2];  // further products with the same x (see prefill_kernels.hip)
+  void* y_seg[2];
+  int ldy_seg[2];
+  int seg_tile[2];
+};
+
+// A second and third product in the same launch: output rows n_out of w
+// / y first, then n2 rows of w2 / y2, then n3 rows of w3 / y3.
+struct GemmMore {
+  const void* w2;
+  void* y2;
+  int ldy2, n2;
+  const void* w3;
+  void* y3;
+  int ldy3, n3;
 };
 
 // Workspace regions, f16 elements per token: h, h1 (residual), xn
@@ -1131,8 +1146,23 @@ size_t pf_workspace_bytes(int32_t n) {
 // fewer than 2 workgroups per CU.
 int launch_gemm(hipFunction_t fn, hipFunction_t fn_m32, const void* x, int ldx, const void* wl,
                 int K, int n_out, int tile_cols, void* y, int ldy, const void* r, int ldr,
-                int up_row, int M, hipStream_t st) {
-  GemmArgs a{x, wl, y, r, M, K, n_out / tile_cols, ldx, ldy, ldr, up_row};
+                int up_row, int M, hipStream_t st, const GemmMore* more = nullptr) {
+  GemmArgs a{x, wl, y, r, M, K, n_out / tile_cols, ldx, ldy, ldr, up_row,
+             {nullptr, nullptr}, {nullptr, nullptr}, {0, 0}, {0, 0}};
+  a.seg_tile[0] = a.seg_tile[1] = a.n_tiles;
+  if (more) {
+    if (more->n2 % tile_cols != 0 || more->n3 % tile_cols != 0)
+      return fail(Q8_ERR_BAD_SHAPE, "prefill GEMM segments N=%d, %d", more->n2, more->n3);
+    a.w_seg[0] = more->w2;
+    a.y_seg[0] = more->y2;
+    a.ldy_seg[0] = more->ldy2;
+    a.w_seg[1] = more->w3;
+    a.y_seg[1] = more->y3;
+    a.ldy_seg[1] = more->ldy3;
+    a.seg_tile[0] = a.n_tiles;
+    a.seg_tile[1] = a.n_tiles + more->n2 / tile_cols;
+    a.n_tiles = a.seg_tile[1] + more->n3 / tile_cols;
+  }
   // the kernel maps workgroups to n tiles in groups of 8 (one per XCD)
   if (n_out % tile_cols != 0 || a.n_tiles % 8 != 0 || K % 256 != 0)
     return fail(Q8_ERR_BAD_SHAPE, "prefill GEMM shape N=%d K=%d", n_out, K);
@@ -1171,15 +1201,13 @@ int launch_prefill_layer(const qwen3_weights* w, int layer, void* k_cache, void*
     void* args[] = {&h, &an, &xn, &n};
     if ((rc = launch(g.pf_norm, norm_grid, 256, args, st))) return rc;
   }
-  if ((rc = launch_gemm(g.pf_gemm, g.pf_gemm_m32, xn, 1024, cb(w->wq) + layer * bpl_q, 1024, 2048, 64, q, 2048,
-                        nullptr, 0, 0, n, st)))
-    return rc;
-  if ((rc = launch_gemm(g.pf_gemm, g.pf_gemm_m32, xn, 1024, cb(w->wk) + layer * bpl_kv, 1024, 1024, 64, k, 1024,
-                        nullptr, 0, 0, n, st)))
-    return rc;
-  if ((rc = launch_gemm(g.pf_gemm, g.pf_gemm_m32, xn, 1024, cb(w->wv) + layer * bpl_kv, 1024, 1024, 64, v, 1024,
-                        nullptr, 0, 0, n, st)))
-    return rc;
+  {  // q, k, v in one launch (tiles 0-31 q, 32-47 k, 48-63 v)
+    const GemmMore kv{cb(w->wk) + layer * bpl_kv, k, 1024, 1024,
+                      cb(w->wv) + layer * bpl_kv, v, 1024, 1024};
+    if ((rc = launch_gemm(g.pf_gemm, g.pf_gemm_m32, xn, 1024, cb(w->wq) + layer * bpl_q, 1024,
+                          2048, 64, q, 2048, nullptr, 0, 0, n, st, &kv)))
+      return rc;
+  }
   {
     int start = p0;
     void* args[] = {&q, &k, &v, &start, &qn, &kn, &qr, &kc, &vc};
