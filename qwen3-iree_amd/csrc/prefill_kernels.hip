@@ -320,63 +320,79 @@ extern "C" __global__ __launch_bounds__(256) void pf_gemm_q8_swiglu(GemmArgs A) 
   gemm_q8<kEpiSwiGLU, 64>(A);
 }
 
-// Token i (position start + i), kv head g = blockIdx.y; waves 0, 1: q heads
-// 2g, 2g+1, wave 2: k head g -> per-head rms_norm with q_norm / k_norm
-// (qwen3_full.mlir:1812-1879) and RoPE (@position_components.rope,
-// :1060-1130, the decode step's formula) -> q_roped[i] / the k cache slot;
-// wave 3: v head g -> the v cache slot (the cache scatter of :1979-1983).
-// Lane owns dims 2 lane, 2 lane + 1; the same operations as the decode step's
-// attention prologue.  k_cache, v_cache: the layer's base ([max_seq, 8, 128]).
+// Token i = blockIdx.x (position start + i): per-head rms_norm with q_norm /
+// k_norm (qwen3_full.mlir:1812-1879) and RoPE (@position_components.rope,
+// :1060-1130, the decode step's formula) -> q_roped[i] / the k cache slot,
+// and v to its cache slot (the cache scatter of :1979-1983).  Wave w takes q
+// heads 4w .. 4w + 3, k heads 2w, 2w + 1 and v heads 2w, 2w + 1; the six
+// vectors are independent chains in the same wave.  Lane owns dims 2 lane,
+// 2 lane + 1; per vector the same operations as the decode step's attention
+// prologue.  k_cache, v_cache: the layer's base ([max_seq, 8, 128]).
 extern "C" __global__ __launch_bounds__(256) void pf_qk_rope_cache(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ v, int start, const uint16_t* __restrict__ qn_w,
     const uint16_t* __restrict__ kn_w, uint16_t* __restrict__ q_roped,
     uint16_t* __restrict__ k_cache, uint16_t* __restrict__ v_cache) {
   const int i = blockIdx.x;
-  const int g = blockIdx.y;
-  const int wave = threadIdx.x >> 6;
+  const int w = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const int pos = start + i;
-  const size_t slot = ((size_t)pos * kKvHeads + g) * kHeadDim;
-  if (wave == 3) {
-    reinterpret_cast<uint32_t*>(v_cache + slot)[lane] =
-        load_global(reinterpret_cast<const uint32_t*>(v + (size_t)i * 1024 + g * kHeadDim) + lane);
-    return;
-  }
-  const uint16_t* src = wave < 2 ? q + (size_t)i * 2048 + (2 * g + wave) * kHeadDim
-                                 : k + (size_t)i * 1024 + g * kHeadDim;
-  const f16x2 xv = as_f16x2(load_global(reinterpret_cast<const uint32_t*>(src) + lane));
-  const f16x2 wv = as_f16x2(
-      load_global(reinterpret_cast<const uint32_t*>(wave < 2 ? qn_w : kn_w) + lane));
+  constexpr int kVecs = 6;  // 4 q heads, 2 k heads
+  f16x2 xv[kVecs];
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    xv[j] = as_f16x2(load_global(
+        reinterpret_cast<const uint32_t*>(q + (size_t)i * 2048 + (4 * w + j) * kHeadDim) + lane));
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+    xv[4 + j] = as_f16x2(load_global(
+        reinterpret_cast<const uint32_t*>(k + (size_t)i * 1024 + (2 * w + j) * kHeadDim) + lane));
+  uint32_t vv[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+    vv[j] = load_global(
+        reinterpret_cast<const uint32_t*>(v + (size_t)i * 1024 + (2 * w + j) * kHeadDim) + lane);
+  const f16x2 qwv = as_f16x2(load_global(reinterpret_cast<const uint32_t*>(qn_w) + lane));
+  const f16x2 kwv = as_f16x2(load_global(reinterpret_cast<const uint32_t*>(kn_w) + lane));
   float cs[2], sn[2];
   rope_angles(pos, cs, sn);
-  const float a = (float)xv.x, b = (float)xv.y;
-  float ss = a * a;
-  ss = ss + b * b;
-  ss = wave_sum(ss);
-  const float r = sqrtf(ss / 128.0f + kEps);
-  float xs[2];
-  xs[0] = (float)to_f16((a / r) * (float)wv.x);
-  xs[1] = (float)to_f16((b / r) * (float)wv.y);
-  float r2[2];
+  uint32_t out[kVecs];
 #pragma unroll
-  for (int dd = 0; dd < 2; ++dd) {
-    const float other = __shfl_xor(xs[dd], 32, 64);  // dim d + 64 or d - 64
-    if (lane < 32) {
-      const float u = xs[dd] * cs[dd];
-      const float w2 = other * sn[dd];
-      r2[dd] = u - w2;
-    } else {
-      const float u = other * sn[dd];
-      const float w2 = xs[dd] * cs[dd];
-      r2[dd] = u + w2;
+  for (int j = 0; j < kVecs; ++j) {
+    const f16x2 wv = j < 4 ? qwv : kwv;
+    const float a = (float)xv[j].x, b = (float)xv[j].y;
+    float ss = a * a;
+    ss = ss + b * b;
+    ss = wave_sum(ss);
+    const float r = sqrtf(ss / 128.0f + kEps);
+    float xs[2];
+    xs[0] = (float)to_f16((a / r) * (float)wv.x);
+    xs[1] = (float)to_f16((b / r) * (float)wv.y);
+    float r2[2];
+#pragma unroll
+    for (int dd = 0; dd < 2; ++dd) {
+      const float other = __shfl_xor(xs[dd], 32, 64);  // dim d + 64 or d - 64
+      if (lane < 32) {
+        const float u = xs[dd] * cs[dd];
+        const float w2 = other * sn[dd];
+        r2[dd] = u - w2;
+      } else {
+        const float u = other * sn[dd];
+        const float w2 = xs[dd] * cs[dd];
+        r2[dd] = u + w2;
+      }
     }
+    out[j] = pack_f16x2(r2[0], r2[1]);
   }
-  const uint32_t out = pack_f16x2(r2[0], r2[1]);
-  if (wave < 2)
-    reinterpret_cast<uint32_t*>(q_roped + (size_t)i * 2048 + (2 * g + wave) * kHeadDim)[lane] = out;
-  else
-    reinterpret_cast<uint32_t*>(k_cache + slot)[lane] = out;
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    reinterpret_cast<uint32_t*>(q_roped + (size_t)i * 2048 + (4 * w + j) * kHeadDim)[lane] = out[j];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const size_t slot = ((size_t)pos * kKvHeads + 2 * w + j) * kHeadDim;
+    reinterpret_cast<uint32_t*>(k_cache + slot)[lane] = out[4 + j];
+    reinterpret_cast<uint32_t*>(v_cache + slot)[lane] = vv[j];
+  }
 }
 
 // Causal GQA attention (@attention_prefill, qwen3_full.mlir:1571-1729, with the
@@ -574,11 +590,13 @@ extern "C" __global__ __launch_bounds__(256) void pf_attention(
 }
 
 // The splits of query block blockIdx.x, kv head g = blockIdx.y (nothing to do
-// for a block with one split): in split order,
-//   M = max_s m_s,  O = sum_s O_s e^(m_s - M),  l = sum_s l_s e^(m_s - M),
-// out = O / l.  Thread t: slot row t >> 2 (wave w = row >> 4 of pf_attention:
-// head 2g + (w >> 1), token 32 qb + 16 (w & 1) + (row & 15)), dims 32 (t & 3)
-// .. + 31.
+// for a block with one split), merged in split order with a running maximum:
+//   M' = max(M, m_s),  O' = O e^(M - M') + O_s e^(m_s - M'),
+//   l' = l e^(M - M') + l_s e^(m_s - M'),
+// out = O / l.  The partials of up to 2 splits are requested before any is
+// used.  Thread t: slot row t >> 2 (wave w = row >> 4 of pf_attention: head
+// 2g + (w >> 1), token 32 qb + 16 (w & 1) + (row & 15)), dims 32 (t & 3) ..
+// + 31.
 extern "C" __global__ __launch_bounds__(256) void pf_attn_merge(
     const float* __restrict__ part, int n, int start, int chunk_local, int split_blocks,
     uint16_t* __restrict__ out) {
@@ -595,30 +613,44 @@ extern "C" __global__ __launch_bounds__(256) void pf_attn_merge(
   const int w = r >> 4;
   const int tok = 32 * qb + 16 * (w & 1) + (r & 15);
   if (tok >= n) return;
-  float mx = -__builtin_inff();
-  for (int s = 0; s < ns; ++s)
-    mx = fmaxf(mx, part[(first + (size_t)s * kKvHeads) * kPfAttnSlotFloats + 64 * kHeadDim + r]);
-  float acc[32], lsum = 0.0f;
+  constexpr int kGroup = 2;
+  float M = -__builtin_inff(), L = 0.0f, acc[32];
 #pragma unroll
   for (int d = 0; d < 32; ++d) acc[d] = 0.0f;
-  for (int s = 0; s < ns; ++s) {
-    const float* sl = part + (first + (size_t)s * kKvHeads) * kPfAttnSlotFloats;
-    const float ms = sl[64 * kHeadDim + r];
-    const float wgt = ms == -__builtin_inff() ? 0.0f : expf(ms - mx);
-    lsum += sl[64 * kHeadDim + 64 + r] * wgt;
-    const float4* orow = reinterpret_cast<const float4*>(sl + r * kHeadDim + d0);
+  for (int s0 = 0; s0 < ns; s0 += kGroup) {
+    float ms[kGroup], ls[kGroup];
+    float4 os[kGroup][8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const float4 v = orow[j];
-      acc[4 * j] += v.x * wgt;
-      acc[4 * j + 1] += v.y * wgt;
-      acc[4 * j + 2] += v.z * wgt;
-      acc[4 * j + 3] += v.w * wgt;
+    for (int k = 0; k < kGroup; ++k) {
+      const int s = s0 + k < ns ? s0 + k : ns - 1;
+      const float* sl = part + (first + (size_t)s * kKvHeads) * kPfAttnSlotFloats;
+      ms[k] = sl[64 * kHeadDim + r];
+      ls[k] = sl[64 * kHeadDim + 64 + r];
+      const float4* orow = reinterpret_cast<const float4*>(sl + r * kHeadDim + d0);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) os[k][j] = orow[j];
+    }
+#pragma unroll
+    for (int k = 0; k < kGroup; ++k) {
+      if (s0 + k < ns) {
+        const float mn = fmaxf(M, ms[k]);
+        const float a = M == -__builtin_inff() ? 0.0f : expf(M - mn);
+        const float b = ms[k] == -__builtin_inff() ? 0.0f : expf(ms[k] - mn);
+        L = L * a + ls[k] * b;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          acc[4 * j] = acc[4 * j] * a + os[k][j].x * b;
+          acc[4 * j + 1] = acc[4 * j + 1] * a + os[k][j].y * b;
+          acc[4 * j + 2] = acc[4 * j + 2] * a + os[k][j].z * b;
+          acc[4 * j + 3] = acc[4 * j + 3] * a + os[k][j].w * b;
+        }
+        M = mn;
+      }
     }
   }
   uint32_t packed[16];
 #pragma unroll
-  for (int j = 0; j < 16; ++j) packed[j] = pack_f16x2(acc[2 * j] / lsum, acc[2 * j + 1] / lsum);
+  for (int j = 0; j < 16; ++j) packed[j] = pack_f16x2(acc[2 * j] / L, acc[2 * j + 1] / L);
   u32x4* dst = reinterpret_cast<u32x4*>(out + (size_t)tok * 2048 + (2 * g + (w >> 1)) * kHeadDim + d0);
 #pragma unroll
   for (int j = 0; j < 4; ++j)

@@ -1211,7 +1211,7 @@ int launch_prefill_layer(const qwen3_weights* w, int layer, void* k_cache, void*
   {
     int start = p0;
     void* args[] = {&q, &k, &v, &start, &qn, &kn, &qr, &kc, &vc};
-    if ((rc = launch2(g.pf_rope, (uint32_t)n, 8, 256, args, st))) return rc;
+    if ((rc = launch(g.pf_rope, (uint32_t)n, 256, args, st))) return rc;
   }
   {
     int start = p0, cl = chunk_local ? 1 : 0, nn = n;
