@@ -79,7 +79,12 @@ __device__ __forceinline__ void gemm_q8(const GemmArgs& A) {
   static_assert(BM == 64 || (BM == 32 && EPI != kEpiSwiGLU), "tile shapes");
   constexpr int kXL = BM * kXRow;
   constexpr int kXP = BM * 32;   // 16-byte X pieces per stage
-  constexpr int NS = BM == 64 ? 2 : 1;  // 16-column tiles per wave
+  // waves 2 (m) x 2 (n) of 32 x 32 (SwiGLU: 32 tokens x 16 gate + 16 up
+  // columns), else waves 1 x 4 of BM x 16: a wave converts each B fragment
+  // once and uses it for all BM / 16 of its m tiles
+  constexpr bool kSplitM = EPI == kEpiSwiGLU;
+  constexpr int MS = kSplitM ? 2 : BM / 16;  // 16-row tiles per wave
+  constexpr int NS = kSplitM ? 2 : 1;        // 16-column tiles per wave
   __shared__ __attribute__((aligned(16))) uint8_t lds[kXL + kWLds];
   uint8_t* xl = lds;
   uint8_t* wl = lds + kXL;
@@ -153,40 +158,35 @@ __device__ __forceinline__ void gemm_q8(const GemmArgs& A) {
     }
   };
 
-  // BM = 64: waves 2 (m) x 2 (n), each 32 x 32; BM = 32: waves 1 x 4, each
-  // 32 x 16
-  const int wm = BM == 64 ? (wave & 1) : 0;
-  const int wn = BM == 64 ? (wave >> 1) : wave;
+  const int wm = kSplitM ? (wave & 1) : 0;
+  const int wn = kSplitM ? (wave >> 1) : wave;
   int nrow[NS];  // LDS W rows of this lane's column in the wave's n tiles
-  if constexpr (EPI == kEpiSwiGLU) {
+  if constexpr (kSplitM) {
     nrow[0] = 16 * wn + c16;       // gate row
     nrow[1] = 32 + 16 * wn + c16;  // the matching up row
-  } else if constexpr (BM == 64) {
-    nrow[0] = 32 * wn + c16;
-    nrow[1] = 32 * wn + 16 + c16;
   } else {
     nrow[0] = 16 * wn + c16;
   }
-  f32x4 acc[2][NS];
+  f32x4 acc[MS][NS];
 #pragma unroll
-  for (int ms = 0; ms < 2; ++ms)
+  for (int ms = 0; ms < MS; ++ms)
 #pragma unroll
     for (int ns = 0; ns < NS; ++ns) acc[ms][ns] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
   const f32x4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
 
   // Block b's products are issued before block b - 1's are scaled into the
   // sums, so the matrix unit works while the scale FMAs run.
-  f32x4 prev[2][NS];
+  f32x4 prev[MS][NS];
   float prev_sc[NS];
 #pragma unroll
   for (int ns = 0; ns < NS; ++ns) prev_sc[ns] = 0.0f;
 #pragma unroll
-  for (int ms = 0; ms < 2; ++ms)
+  for (int ms = 0; ms < MS; ++ms)
 #pragma unroll
     for (int ns = 0; ns < NS; ++ns) prev[ms][ns] = zero;
   auto scale_in = [&]() {
 #pragma unroll
-    for (int ms = 0; ms < 2; ++ms)
+    for (int ms = 0; ms < MS; ++ms)
 #pragma unroll
       for (int ns = 0; ns < NS; ++ns)
 #pragma unroll
@@ -202,9 +202,9 @@ __device__ __forceinline__ void gemm_q8(const GemmArgs& A) {
     if (s + 1 < stages) gload(s + 1);
 #pragma unroll
     for (int b = 0; b < kStageBlocks; ++b) {
-      f16x8 a[2];
+      f16x8 a[MS];
 #pragma unroll
-      for (int ms = 0; ms < 2; ++ms)
+      for (int ms = 0; ms < MS; ++ms)
         a[ms] = *reinterpret_cast<const f16x8*>(xl + (32 * wm + 16 * ms + c16) * kXRow +
                                                 2 * (32 * b + 8 * g));
       f16x8 bq[NS];
@@ -231,15 +231,15 @@ __device__ __forceinline__ void gemm_q8(const GemmArgs& A) {
         const f16x2 v2 = q8x2_to_f16x2(bh, kSelLo), v3 = q8x2_to_f16x2(bh, kSelHi);
         bq[ns] = (f16x8){v0.x, v0.y, v1.x, v1.y, v2.x, v2.y, v3.x, v3.y};
       }
-      f32x4 cur[2][NS];
+      f32x4 cur[MS][NS];
 #pragma unroll
-      for (int ms = 0; ms < 2; ++ms)
+      for (int ms = 0; ms < MS; ++ms)
 #pragma unroll
         for (int ns = 0; ns < NS; ++ns)
           cur[ms][ns] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[ms], bq[ns], zero, 0, 0, 0);
       scale_in();  // block b - 1 (zeros before the first block)
 #pragma unroll
-      for (int ms = 0; ms < 2; ++ms)
+      for (int ms = 0; ms < MS; ++ms)
 #pragma unroll
         for (int ns = 0; ns < NS; ++ns) prev[ms][ns] = cur[ms][ns];
 #pragma unroll
@@ -250,7 +250,7 @@ __device__ __forceinline__ void gemm_q8(const GemmArgs& A) {
 
   // epilogue: lane holds rows 4 g + i, column c16 of each 16 x 16 tile
 #pragma unroll
-  for (int ms = 0; ms < 2; ++ms) {
+  for (int ms = 0; ms < MS; ++ms) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int m = m0 + 32 * wm + 16 * ms + 4 * g + i;
@@ -261,7 +261,7 @@ __device__ __forceinline__ void gemm_q8(const GemmArgs& A) {
       } else {
 #pragma unroll
         for (int ns = 0; ns < NS; ++ns) {
-          const int col = kGemmBN * n_tile + (BM == 64 ? 32 * wn + 16 * ns : 16 * wn) + c16;
+          const int col = kGemmBN * n_tile + 16 * wn + c16;
           if constexpr (EPI == kEpiResidual)
             yb[(size_t)m * ldy + col] =
                 residual_f16(as_half(A.r[(size_t)m * A.ldr + col]), acc[ms][ns][i]);
