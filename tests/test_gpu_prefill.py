@@ -298,3 +298,30 @@ def test_prefill_attention_splits(O, gpu, D, dmodel, split):
     finally:
         D.set_prefill_tiling(0, 0)
     sess.free()
+
+
+@pytest.mark.parametrize("chunk_local", [False, True])
+def test_prefill_long_history(O, gpu, D, dmodel, chunk_local):
+    """Three tokens after 30,000 cached positions: with the default split of
+    256 positions a query block would need 118 (block, split) pairs, more
+    than the workspace's partial slots hold, so the split is raised; the
+    attention still matches the oracle over the whole history."""
+    n, p0, layer, max_seq = 3, 30000, 3, 30016
+    rng = np.random.default_rng(9400)
+    sess = D.DecodeSession(dmodel, max_seq)
+    k = rng.standard_normal((p0, 1024)).astype(np.float16)
+    v = (0.6 * rng.standard_normal((p0, 1024))).astype(np.float16)
+    base = layer * max_seq
+    sess.k_cache.upload(k, base * 2048)
+    sess.v_cache.upload(v, base * 2048)
+    h_in = (1.5 * rng.standard_normal((n, 1024))).astype(np.float16)
+    print(f"prefill long history p0 {p0} chunk_local {chunk_local}", flush=True)
+    g = sess.prefill_layer(layer, h_in, p0, chunk_local)
+    k_rows, v_rows = sess.cache_rows(layer, 0, p0 + n)
+    assert np.array_equal(k_rows[:p0], k) and np.array_equal(v_rows[:p0], v)
+    lo = p0 if chunk_local else 0
+    for i in range(n):
+        a_want = O.attention(g["q_roped"][i], k_rows[lo:p0 + i + 1], v_rows[lo:p0 + i + 1])
+        d = np.abs(f64(g["attn"][i]) - f64(a_want))
+        assert (d <= 2 * ulp(O, a_want) + 1e-5).all(), (i, d.max())
+    sess.free()
