@@ -3,13 +3,15 @@
 // :1731-2030) runs all prompt tokens of a layer together, so the layer
 // matrices become GEMMs [n_tokens, K] x [K, N] instead of n_tokens GEMVs.
 //
-// Per layer (eight launches):
+// Per layer (eight launches, nine when an attention query block has several
+// position splits):
 //   pf_rmsnorm       rms_norm(h, attn_norm) of every token row
-//   pf_gemm_q8 x3    q, k, v projections (MFMA, Q8_0 weights dequantized in
-//                    registers, the per-block scale applied in f32)
+//   pf_gemm_q8       q, k and v projections in one launch (MFMA, Q8_0 weights
+//                    converted in registers, the per-block scale applied in f32)
 //   pf_qk_rope_cache per-head rms_norm of q and k, RoPE at each token's
 //                    position, k and v written to their cache slots
 //   pf_attention     causal GQA attention of every token over the cache
+//   pf_attn_merge    the position splits' partial results combined
 //   pf_gemm_q8       attn_o + residual
 //   pf_rmsnorm       rms_norm(res, ffn_norm)
 //   pf_gemm_q8       gate/up with SwiGLU in the epilogue
