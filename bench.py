@@ -112,7 +112,10 @@ def bench_decode(Q, O, stream, args) -> dict:
     sess.step(advance=False, logits=True)
     step_tok, step_pos = sess.get_state()
     step_logits = sess.read_logits()
+    # the same step by the CPU oracle (OpenMP over the GEMV rows), timed
+    t_cpu = time.perf_counter()
     ref_tok, ref_logits, _ = O.decode_step(mhost, kc, vc, max_seq, first_token, ctx - 1, True)
+    cpu_step_us = (time.perf_counter() - t_cpu) * 1e6
     dl = np.abs(step_logits.astype(np.float64) - ref_logits.astype(np.float64))
     srt = np.sort(ref_logits.astype(np.float64))
     margin = float(srt[-1] - srt[-2])
@@ -167,7 +170,11 @@ def bench_decode(Q, O, stream, args) -> dict:
             "single_launch_us": None if single_us is None else round(single_us, 2),
             "per_phase_us": round(dec_us, 2), "per_phase_launches": 3 + 5 * layers,
             "per_phase_launch": "eager" if args.no_graph else "hipGraph",
-            "token": step_tok, "oracle_token": ref_tok, "parity_ok": bool(step_ok)}
+            "token": step_tok, "oracle_token": ref_tok, "parity_ok": bool(step_ok),
+            "cpu_oracle": {"us": round(cpu_step_us, 1), "threads": O.num_threads(),
+                           "kind": "port",
+                           "sample": "one step of the C oracle at the same context and inputs "
+                                     "(the parity check's step)"}}
 
 
 def prefill_flops(n: int) -> tuple[int, int]:
