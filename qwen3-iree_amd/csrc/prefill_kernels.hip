@@ -410,7 +410,10 @@ extern "C" __global__ __launch_bounds__(256) void pf_qk_rope_cache(
 // products, f32 sums), scaled by rsqrt(128); the causal mask and an online
 // softmax in f32 (running max m and sum l per query row, as the decode step);
 // the weights p are split into f16 hi + lo (p - hi), so P V = hi V + lo V (8 + 8
-// MFMAs) carries p to about 2^-22.  out: [n, 2048] f16 = O / l.
+// MFMAs) carries p to about 2^-22.  out: [n, 2048] f16 = O / l.  The softmax
+// runs in base 2: scores are scaled by rsqrt(128) log2(e), so each weight is
+// one exp2 (v_exp_f32) instead of a range-reduced exp; m is kept in those
+// units, in the partials too.
 //
 // A query block's positions are divided into splits of split_blocks blocks of
 // 32 (prefill_split.h); grid (pairs of query block and split, 8).  A query
@@ -418,6 +421,8 @@ extern "C" __global__ __launch_bounds__(256) void pf_qk_rope_cache(
 // leaves its partial in its slot of `part` and pf_attn_merge, launched next,
 // combines them.
 namespace {
+constexpr float kScoreScaleLog2 = 0.0883883461356163f * 1.44269504088896341f;
+
 __device__ __forceinline__ float max_row16(float v) {
   v = fmaxf(v, dpp<0xB1>(v));
   v = fmaxf(v, dpp<0x4E>(v));
@@ -531,14 +536,14 @@ extern "C" __global__ __launch_bounds__(256) void pf_attention(
       for (int nt = 0; nt < 2; ++nt) {
         const int kp = kb + 16 * nt + c16;
         ok[nt] = qok[i] && kp <= qpos[i];  // a split ends on a block edge or at hi
-        sv[nt] = ok[nt] ? sc[nt][i] * kAttnScale : -__builtin_inff();
+        sv[nt] = ok[nt] ? sc[nt][i] * kScoreScaleLog2 : -__builtin_inff();
       }
       const float mx = max_row16(fmaxf(sv[0], sv[1]));
       const float mn = fmaxf(m[i], mx);
-      const float alpha = mn == -__builtin_inff() ? 1.0f : expf(m[i] - mn);
+      const float alpha = mn == -__builtin_inff() ? 1.0f : exp2f(m[i] - mn);
       float p[2];
 #pragma unroll
-      for (int nt = 0; nt < 2; ++nt) p[nt] = ok[nt] ? expf(sv[nt] - mn) : 0.0f;
+      for (int nt = 0; nt < 2; ++nt) p[nt] = ok[nt] ? exp2f(sv[nt] - mn) : 0.0f;
       const float ps = reduce_row16(p[0] + p[1]);
       l[i] = l[i] * alpha + ps;
       m[i] = mn;
@@ -592,9 +597,10 @@ extern "C" __global__ __launch_bounds__(256) void pf_attention(
 }
 
 // The splits of query block blockIdx.x, kv head g = blockIdx.y (nothing to do
-// for a block with one split), merged in split order with a running maximum:
-//   M' = max(M, m_s),  O' = O e^(M - M') + O_s e^(m_s - M'),
-//   l' = l e^(M - M') + l_s e^(m_s - M'),
+// for a block with one split), merged in split order with a running maximum
+// (m in base-2 units, as pf_attention keeps it):
+//   M' = max(M, m_s),  O' = O 2^(M - M') + O_s 2^(m_s - M'),
+//   l' = l 2^(M - M') + l_s 2^(m_s - M'),
 // out = O / l.  The partials of up to 2 splits are requested before any is
 // used.  Thread t: slot row t >> 2 (wave w = row >> 4 of pf_attention: head
 // 2g + (w >> 1), token 32 qb + 16 (w & 1) + (row & 15)), dims 32 (t & 3) ..
@@ -636,8 +642,8 @@ extern "C" __global__ __launch_bounds__(256) void pf_attn_merge(
     for (int k = 0; k < kGroup; ++k) {
       if (s0 + k < ns) {
         const float mn = fmaxf(M, ms[k]);
-        const float a = M == -__builtin_inff() ? 0.0f : expf(M - mn);
-        const float b = ms[k] == -__builtin_inff() ? 0.0f : expf(ms[k] - mn);
+        const float a = M == -__builtin_inff() ? 0.0f : exp2f(M - mn);
+        const float b = ms[k] == -__builtin_inff() ? 0.0f : exp2f(ms[k] - mn);
         L = L * a + ls[k] * b;
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
