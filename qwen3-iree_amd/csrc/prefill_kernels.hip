@@ -32,6 +32,9 @@ namespace {
 
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+typedef short v8i16 __attribute__((ext_vector_type(8)));
+#define LDS_AS __attribute__((address_space(3)))
 
 // ---------------------------------------------------------------- GEMM ----
 //
@@ -405,8 +408,8 @@ extern "C" __global__ __launch_bounds__(256) void pf_qk_rope_cache(
 // chunk_local != 0 (this call's tokens only, as the reference's @prefill
 // attends).  Wave w takes query head 2g + (w >> 1) and tokens 32 qb + 16 (w &
 // 1) .. + 15.  Per block of 32 cache positions: the K tile ([32][128], rows
-// padded to 272 bytes) and the transposed V tile ([128][32], rows padded to 80
-// bytes) go to LDS; S = Q K^T is 8 v_mfma_f32_16x16x32_f16 per wave (exact f16
+// padded to 272 bytes) and the V tile ([32][128], rows padded to 288 bytes, read
+// back transposed) go to LDS; S = Q K^T is 8 v_mfma_f32_16x16x32_f16 per wave (exact f16
 // products, f32 sums), scaled by rsqrt(128); the causal mask and an online
 // softmax in f32 (running max m and sum l per query row, as the decode step);
 // the weights p are split into f16 hi + lo (p - hi), so P V = hi V + lo V (8 + 8
@@ -437,7 +440,7 @@ extern "C" __global__ __launch_bounds__(256) void pf_attention(
     const uint16_t* __restrict__ v_cache, int n, int start, int chunk_local, int split_blocks,
     float* __restrict__ part, uint16_t* __restrict__ out) {
   __shared__ __attribute__((aligned(16))) _Float16 kt[32][136];      // K tile [key][dim]
-  __shared__ __attribute__((aligned(16))) _Float16 vt[128][40];      // V tile [dim][key]
+  __shared__ __attribute__((aligned(16))) _Float16 vt[32][144];      // V tile [key][dim]
   __shared__ __attribute__((aligned(16))) _Float16 pt[4][2][16][40];  // P hi / lo [row][key]
   const int g = blockIdx.y;
   const int t = threadIdx.x;
@@ -505,13 +508,8 @@ extern "C" __global__ __launch_bounds__(256) void pf_attention(
     {
       *reinterpret_cast<u32x4*>(&kt[key][dg]) = kr[0];
       *reinterpret_cast<u32x4*>(&kt[key][dg + 8]) = kr[1];
-      const _Float16* vh0 = reinterpret_cast<const _Float16*>(&vr[0]);
-      const _Float16* vh1 = reinterpret_cast<const _Float16*>(&vr[1]);
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        vt[dg + j][key] = vh0[j];
-        vt[dg + 8 + j][key] = vh1[j];
-      }
+      *reinterpret_cast<u32x4*>(&vt[key][dg]) = vr[0];
+      *reinterpret_cast<u32x4*>(&vt[key][dg + 8]) = vr[1];
     }
     __syncthreads();
     if (kb + 32 <= kb_hi) load_tile(kb + 32);
@@ -557,13 +555,25 @@ extern "C" __global__ __launch_bounds__(256) void pf_attention(
         pt[wave][1][4 * grp + i][16 * nt + c16] = pl;
       }
     }
-    // O += P V: A = P rows (this wave's 16 queries x 32 positions), B = V^T
-    // tile (positions x 16 dims per tile); LDS is in order within the wave
+    // O += P V: A = P rows (this wave's 16 queries x 32 positions), B = V
+    // (positions x 16 dims per tile); LDS is in order within the wave.  B's
+    // lane c16 + 16 grp needs V[8 grp .. 8 grp + 7][16 d + c16]: two
+    // transposing reads (ds_read_b64_tr_b16, lane i of a 16-lane group gets
+    // element i % 4 of the 8-byte pieces addressed by lanes i / 4 + 4 r,
+    // r = 0..3), lane j of the group addressing row 8 grp + 4 h + j / 4,
+    // columns 16 d + 4 (j % 4) .. + 3, for positions 8 grp + 4 h .. + 3
     const f16x8 ph = *reinterpret_cast<const f16x8*>(&pt[wave][0][c16][8 * grp]);
     const f16x8 pl = *reinterpret_cast<const f16x8*>(&pt[wave][1][c16][8 * grp]);
+    const int vrow = 8 * grp + (c16 >> 2);
+    const int vcol = 4 * (c16 & 3);
 #pragma unroll
     for (int d = 0; d < 8; ++d) {
-      const f16x8 vf = *reinterpret_cast<const f16x8*>(&vt[16 * d + c16][8 * grp]);
+      const v4i16 v0 =
+          __builtin_amdgcn_ds_read_tr16_b64_v4i16((LDS_AS v4i16*)(&vt[vrow][16 * d + vcol]));
+      const v4i16 v1 =
+          __builtin_amdgcn_ds_read_tr16_b64_v4i16((LDS_AS v4i16*)(&vt[vrow + 4][16 * d + vcol]));
+      const f16x8 vf = __builtin_bit_cast(
+          f16x8, (v8i16){v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w});
       o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph, vf, o[d], 0, 0, 0);
       o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pl, vf, o[d], 0, 0, 0);
     }
