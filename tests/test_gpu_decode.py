@@ -82,6 +82,19 @@ def rope_tol(O, normed, want):
     return 2 * ulp(O, want) + np.repeat(ulp(O, hmax), 128)
 
 
+def rope_tol_far(O, normed, want, pos):
+    """rope_tol plus the spread of two correct f32 evaluations of the angle
+    at a large position: theta = f32(pos) * powf(1e6, -2i/128) carries up to
+    ~2 ulp of powf and 0.5 ulp of the product in each library, so two
+    evaluations may differ by about 2^-21 theta (0.01 rad at theta = 2e4),
+    which moves an output by up to (|x_d| + |x_d+-64|) times that."""
+    x = np.abs(f64(normed)).reshape(-1, 128)
+    i = np.arange(128) % 64
+    theta = float(pos) * 1e6 ** (-(2.0 * i) / 128.0)
+    pair = x + np.concatenate([x[:, 64:], x[:, :64]], axis=1)
+    return rope_tol(O, normed, want) + (pair * theta * 2.0 ** -21).reshape(-1)
+
+
 def fill_cache_layer(sess, layer, n, rng, kc, vc):
     """Random history in slots [0, n) of `layer`, on the device and in the
     host copies kc / vc ([28 * max_seq, 1024])."""
@@ -94,6 +107,47 @@ def fill_cache_layer(sess, layer, n, rng, kc, vc):
     vc[base:base + n] = v
     sess.k_cache.upload(k, base * 2048)
     sess.v_cache.upload(v, base * 2048)
+
+
+def test_layer_attention_long_context(O, gpu, D, dmodel, model_host):
+    """One layer at position 20,000 (each of the 32 position splits walks 20
+    chunks of 32 cached rows): head norms + RoPE (within the spread of two f32
+    evaluations of the angle at that position), the cache write, and the
+    attention over the GPU's own cache against the oracle."""
+    Q = gpu
+    w = model_host
+    layer, pos, max_seq = 9, 20000, 20008
+    rng = np.random.default_rng(4242)
+    sess = D.DecodeSession(dmodel, max_seq)
+    k = rng.standard_normal((pos, 1024)).astype(np.float16)
+    v = (0.6 * rng.standard_normal((pos, 1024))).astype(np.float16)
+    sess.k_cache.upload(k, layer * max_seq * 2048)
+    sess.v_cache.upload(v, layer * max_seq * 2048)
+    h_in = (1.5 * rng.standard_normal(1024)).astype(np.float16)
+    hin, hout = Q.DeviceBuffer.from_array(h_in), Q.DeviceBuffer(2048)
+    sess.set_state(0, pos)
+    print(f"decode layer {layer} pos {pos}", flush=True)
+    sess.layer(layer, hin, hout)
+    g = {name: sess.scratch_f16(name, n) for name, n in
+         (("q", 2048), ("k", 1024), ("v", 1024), ("q_roped", 2048), ("attn", 2048))}
+    k_rows, v_rows = sess.cache_rows(layer, 0, pos + 1)
+    assert np.array_equal(k_rows[:pos], k) and np.array_equal(v_rows[:pos], v)
+    qn = O.head_rmsnorm(g["q"], w.q_norm[layer])
+    q_want = O.rope(qn, pos)
+    dq = np.abs(f64(g["q_roped"]) - f64(q_want))
+    assert (dq <= rope_tol_far(O, qn, q_want, pos)).all(), dq.max()
+    kn = O.head_rmsnorm(g["k"], w.k_norm[layer])
+    k_want = O.rope(kn, pos)
+    dk = np.abs(f64(k_rows[pos]) - f64(k_want))
+    assert (dk <= rope_tol_far(O, kn, k_want, pos)).all(), dk.max()
+    assert np.array_equal(v_rows[pos].view(np.uint16), g["v"].view(np.uint16))
+    # attention over the GPU's own cache with the GPU's roped q
+    a_want = O.attention(g["q_roped"], k_rows, v_rows)
+    d = np.abs(f64(g["attn"]) - f64(a_want))
+    assert (d <= 2 * ulp(O, a_want) + 1e-5).all(), d.max()
+    hin.free()
+    hout.free()
+    sess.free()
 
 
 @pytest.mark.parametrize("layer,pos", [(0, 0), (5, 5), (13, 31), (27, 32), (2, 33),

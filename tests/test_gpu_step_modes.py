@@ -51,14 +51,17 @@ def run_steps(D, dmodel, mode, max_seq, token, pos, n, history=None):
     return out, (k, v, k0, v0)
 
 
-@pytest.mark.parametrize("max_seq,pos,n", [(16, 0, 5), (1024, 1020, 3), (40, 7, 2)])
+@pytest.mark.parametrize("max_seq,pos,n", [(16, 0, 5), (1024, 1020, 3), (40, 7, 2),
+                                           (20000, 19998, 2)])
 def test_single_launch_matches_per_phase(D, dmodel, single, max_seq, pos, n):
     rng = np.random.default_rng(max_seq + pos)
     hist = None
     if pos > 0:
-        shape = (28 * max_seq * 1024,)
-        hist = (rng.standard_normal(shape, dtype=np.float32).astype(np.float16),
-                (0.6 * rng.standard_normal(shape, dtype=np.float32)).astype(np.float16))
+        size = 28 * max_seq * 1024
+        base = min(size, 1 << 22)  # long caches: a random block repeated
+        k = rng.standard_normal(base, dtype=np.float32).astype(np.float16)
+        v = (0.6 * rng.standard_normal(base, dtype=np.float32)).astype(np.float16)
+        hist = (np.resize(k, size), np.resize(v, size))
     a, ca = run_steps(D, dmodel, 0, max_seq, 4321, pos, n, hist)
     b, cb = run_steps(D, dmodel, 1, max_seq, 4321, pos, n, hist)
     for i, ((sa, la, st_a), (sb, lb, st_b)) in enumerate(zip(a, b)):
