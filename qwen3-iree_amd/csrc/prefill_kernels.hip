@@ -58,7 +58,7 @@ constexpr int kWRow = 34 * kStageBlocks;           // 272
 constexpr int kWLds = kGemmBN * kWRow;
 constexpr int kWPieces = kGemmBN * 17;
 
-enum { kEpiStore = 0, kEpiResidual = 1, kEpiSwiGLU = 2 };
+enum { kEpiStore = 0, kEpiResidual = 1, kEpiSwiGLU = 2, kEpiPartial = 3 };
 
 struct GemmArgs {
   const uint16_t* x;  // [M, ldx] f16
@@ -77,6 +77,10 @@ struct GemmArgs {
   uint16_t* y_seg[2];
   int ldy_seg[2];
   int seg_tile[2];
+  // kEpiPartial: K in `splits` equal ranges, one per group of workgroups;
+  // split s stores its f32 sums at part[(s M + m) N + n], N = 64 n_tiles
+  float* part;
+  int splits;
 };
 
 template <int EPI, int BM>
@@ -103,8 +107,11 @@ __device__ __forceinline__ void gemm_q8(const GemmArgs& A) {
   // go to the same XCD, one after another, so its weight rows are fetched
   // from HBM once and then hit that XCD's L2.
   const int mt = (A.M + BM - 1) / BM;
-  const int xcd = blockIdx.x & 7;
-  const int slot = blockIdx.x >> 3;
+  const int tiles = mt * A.n_tiles;
+  const int split = EPI == kEpiPartial ? (int)blockIdx.x / tiles : 0;
+  const int bid = (int)blockIdx.x - split * tiles;
+  const int xcd = bid & 7;
+  const int slot = bid >> 3;
   int n_tile = (slot / mt) * 8 + xcd;
   const int m0 = (slot % mt) * BM;
   const uint8_t* wb = A.w;
@@ -118,7 +125,8 @@ __device__ __forceinline__ void gemm_q8(const GemmArgs& A) {
     n_tile -= A.seg_tile[sg];
   }
   const int row_bytes = A.K / 32 * 34;
-  const int stages = A.K / (32 * kStageBlocks);
+  const int stages = A.K / (32 * kStageBlocks) / (EPI == kEpiPartial ? A.splits : 1);
+  const int s_base = split * stages;  // this split's first stage
 
   auto w_row = [&](int r) -> int {
     if constexpr (EPI == kEpiSwiGLU)
@@ -135,7 +143,7 @@ __device__ __forceinline__ void gemm_q8(const GemmArgs& A) {
       const int row = piece >> 5;
       const int m = m0 + row < A.M ? m0 + row : A.M - 1;
       xp[j] = load_global(reinterpret_cast<const u32x4*>(
-          A.x + (size_t)m * A.ldx + 256 * s + 8 * (piece & 31)));
+          A.x + (size_t)m * A.ldx + 256 * (s_base + s) + 8 * (piece & 31)));
     }
 #pragma unroll
     for (int j = 0; j < (kWPieces + 255) / 256; ++j) {
@@ -143,7 +151,7 @@ __device__ __forceinline__ void gemm_q8(const GemmArgs& A) {
       if (piece < kWPieces) {
         const int row = piece / 17;
         wp[j] = load_global(reinterpret_cast<const u32x4*>(
-            wb + (size_t)w_row(row) * row_bytes + kWRow * s + 16 * (piece - 17 * row)));
+            wb + (size_t)w_row(row) * row_bytes + kWRow * (s_base + s) + 16 * (piece - 17 * row)));
       }
     }
   };
@@ -270,6 +278,8 @@ __device__ __forceinline__ void gemm_q8(const GemmArgs& A) {
           if constexpr (EPI == kEpiResidual)
             yb[(size_t)m * ldy + col] =
                 residual_f16(as_half(A.r[(size_t)m * A.ldr + col]), acc[ms][ns][i]);
+          else if constexpr (EPI == kEpiPartial)
+            A.part[((size_t)split * A.M + m) * (kGemmBN * A.n_tiles) + col] = acc[ms][ns][i];
           else
             yb[(size_t)m * ldy + col] = f32_to_f16_bits(acc[ms][ns][i]);
         }
@@ -321,6 +331,27 @@ extern "C" __global__ __launch_bounds__(256) void pf_gemm_q8_res(GemmArgs A) {
 extern "C" __global__ __launch_bounds__(256) void pf_gemm_q8_res_m32(GemmArgs A) {
   gemm_q8<kEpiResidual, 32>(A);
 }
+extern "C" __global__ __launch_bounds__(256) void pf_gemm_q8_part(GemmArgs A) {
+  gemm_q8<kEpiPartial, 64>(A);
+}
+extern "C" __global__ __launch_bounds__(256) void pf_gemm_q8_part_m32(GemmArgs A) {
+  gemm_q8<kEpiPartial, 32>(A);
+}
+
+// y[m, n] = residual_f16(r[m, n], sum over s in order of part[(s M + m) N + n])
+// (the split-K form of pf_gemm_q8_res: the same residual add, the K ranges'
+// f32 sums added one after another).
+extern "C" __global__ __launch_bounds__(256) void pf_res_reduce(
+    const float* __restrict__ part, int splits, int M, int N, const uint16_t* __restrict__ r,
+    int ldr, uint16_t* __restrict__ y, int ldy) {
+  const int e = (int)(blockIdx.x * 256 + threadIdx.x);
+  if (e >= M * N) return;
+  const int m = e / N, n = e - m * N;
+  float acc = part[e];
+  for (int s = 1; s < splits; ++s) acc += part[(size_t)s * M * N + e];
+  y[(size_t)m * ldy + n] = residual_f16(as_half(r[(size_t)m * ldr + n]), acc);
+}
+
 extern "C" __global__ __launch_bounds__(256) void pf_gemm_q8_swiglu(GemmArgs A) {
   gemm_q8<kEpiSwiGLU, 64>(A);
 }

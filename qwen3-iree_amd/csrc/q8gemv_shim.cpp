@@ -106,6 +106,7 @@ struct State {
   hipModule_t pf_module = nullptr;  // prefill_gfx950.hsaco (optional)
   hipFunction_t pf_embed = nullptr, pf_norm = nullptr, pf_gemm = nullptr, pf_gemm_res = nullptr,
                 pf_gemm_m32 = nullptr, pf_gemm_res_m32 = nullptr, pf_gemm_swiglu = nullptr,
+                pf_gemm_part = nullptr, pf_gemm_part_m32 = nullptr, pf_res_reduce = nullptr,
                 pf_rope = nullptr, pf_attn = nullptr, pf_attn_merge = nullptr,
                 pf_set_pos = nullptr;
   int pf_tile_rows = 0;   // prefill GEMM token tile: 0 = by shape, 32 or 64
@@ -322,6 +323,9 @@ int q8gemv_init(const char* code_object_path) {
                      {&g.pf_rope, "pf_qk_rope_cache"},
                      {&g.pf_attn, "pf_attention"},
                      {&g.pf_attn_merge, "pf_attn_merge"},
+                     {&g.pf_gemm_part, "pf_gemm_q8_part"},
+                     {&g.pf_gemm_part_m32, "pf_gemm_q8_part_m32"},
+                     {&g.pf_res_reduce, "pf_res_reduce"},
                      {&g.pf_set_pos, "pf_set_pos"}};
         bool ok = true;
         for (auto& n : names) ok = ok && hipModuleGetFunction(n.fn, pm, n.name) == hipSuccess;
@@ -374,6 +378,7 @@ void q8gemv_shutdown(void) {
   g.pf_module = nullptr;
   g.pf_embed = g.pf_norm = g.pf_gemm = g.pf_gemm_res = g.pf_gemm_m32 = g.pf_gemm_res_m32 =
       g.pf_gemm_swiglu = g.pf_rope = g.pf_attn = g.pf_attn_merge = g.pf_set_pos = nullptr;
+  g.pf_gemm_part = g.pf_gemm_part_m32 = g.pf_res_reduce = nullptr;
   g.vocab = g.vocab_finalize = g.ws_reset = g.copy = nullptr;
   g.ready = false;
 }
@@ -1074,6 +1079,8 @@ struct GemmArgs {
   void* y_seg[2];
   int ldy_seg[2];
   int seg_tile[2];
+  float* part;  // split-K partial sums (pf_gemm_q8_part*)
+  int splits;
 };
 
 // A second and third product in the same launch: output rows n_out of w
@@ -1146,9 +1153,10 @@ size_t pf_workspace_bytes(int32_t n) {
 // fewer than 2 workgroups per CU.
 int launch_gemm(hipFunction_t fn, hipFunction_t fn_m32, const void* x, int ldx, const void* wl,
                 int K, int n_out, int tile_cols, void* y, int ldy, const void* r, int ldr,
-                int up_row, int M, hipStream_t st, const GemmMore* more = nullptr) {
+                int up_row, int M, hipStream_t st, const GemmMore* more = nullptr,
+                float* part = nullptr, int splits = 1) {
   GemmArgs a{x, wl, y, r, M, K, n_out / tile_cols, ldx, ldy, ldr, up_row,
-             {nullptr, nullptr}, {nullptr, nullptr}, {0, 0}, {0, 0}};
+             {nullptr, nullptr}, {nullptr, nullptr}, {0, 0}, {0, 0}, part, splits};
   a.seg_tile[0] = a.seg_tile[1] = a.n_tiles;
   if (more) {
     if (more->n2 % tile_cols != 0 || more->n3 % tile_cols != 0)
@@ -1175,10 +1183,43 @@ int launch_gemm(hipFunction_t fn, hipFunction_t fn_m32, const void* x, int ldx, 
   }
   if (rows == 32) fn = fn_m32;
   const int64_t mt = ((int64_t)M + rows - 1) / rows;
-  const int64_t grid = mt * a.n_tiles;
+  const int64_t grid = mt * a.n_tiles * splits;
   if (grid > 0x7fffffff) return fail(Q8_ERR_BAD_SHAPE, "prefill GEMM grid too large");
   void* args[] = {&a};
   return launch(fn, (uint32_t)grid, 256, args, st);
+}
+
+// y = r + x W^T for N = 1024 (attn_o, ffn_down).  Where 32-token tiles would
+// leave CUs idle (fewer workgroups than CUs: short prompts), K is split into
+// equal ranges of whole stages, each range's f32 sums go to `part`, and
+// pf_res_reduce adds them in order with the residual.  The split count
+// depends on M only, so every token tile gives the same bits.
+int launch_gemm_res(const void* x, int ldx, const void* wl, int K, void* y, const void* r,
+                    int M, void* part, size_t part_bytes, hipStream_t st) {
+  constexpr int kN = 1024;
+  const int n_tiles = kN / 64;
+  const int stages = K / 256;
+  int splits = 1;
+  const int64_t wgs32 = ((int64_t)M + 31) / 32 * n_tiles;
+  if (g.pf_gemm_part && g.pf_gemm_part_m32 && g.pf_res_reduce && wgs32 < g.compute_units) {
+    splits = stages;
+    for (int d = 1; d <= stages; ++d)
+      if (stages % d == 0 && wgs32 * d >= g.compute_units) {
+        splits = d;
+        break;
+      }
+    if ((size_t)splits * M * kN * 4 > part_bytes) splits = 1;
+  }
+  if (splits == 1)
+    return launch_gemm(g.pf_gemm_res, g.pf_gemm_res_m32, x, ldx, wl, K, kN, 64, y, kN, r, kN, 0,
+                       M, st);
+  int rc = launch_gemm(g.pf_gemm_part, g.pf_gemm_part_m32, x, ldx, wl, K, kN, 64, nullptr, kN,
+                       nullptr, 0, 0, M, st, nullptr, static_cast<float*>(part), splits);
+  if (rc) return rc;
+  const void* pp = part;
+  int sp = splits, mm = M, nn = kN, ld = kN;
+  void* args[] = {&pp, &sp, &mm, &nn, &r, &ld, &y, &ld};
+  return launch(g.pf_res_reduce, (uint32_t)(((int64_t)M * kN + 255) / 256), 256, args, st);
 }
 
 int launch_prefill_layer(const qwen3_weights* w, int layer, void* k_cache, void* v_cache,
@@ -1227,8 +1268,11 @@ int launch_prefill_layer(const qwen3_weights* w, int layer, void* k_cache, void*
       if ((rc = launch2(g.pf_attn_merge, (uint32_t)G.nqb, 8, 256, margs, st))) return rc;
     }
   }
-  if ((rc = launch_gemm(g.pf_gemm_res, g.pf_gemm_res_m32, attn, 2048, cb(w->wo) + layer * bpl_o, 2048, 1024, 64, h1,
-                        1024, h, 1024, 0, n, st)))
+  // the attention partials are consumed by now: their region holds the
+  // split-K sums of attn_o and ffn_down
+  const size_t part_bytes = pf_region_bytes(n, kPfTokenRegions);
+  if ((rc = launch_gemm_res(attn, 2048, cb(w->wo) + layer * bpl_o, 2048, h1, h, n, part,
+                            part_bytes, st)))
     return rc;
   {
     void* args[] = {&h1, &fn, &fnx, &n};
@@ -1237,8 +1281,8 @@ int launch_prefill_layer(const qwen3_weights* w, int layer, void* k_cache, void*
   if ((rc = launch_gemm(g.pf_gemm_swiglu, nullptr, fnx, 1024, cb(w->wgu) + layer * bpl_gu, 1024, 3072, 32,
                         act, 3072, nullptr, 0, 3072, n, st)))
     return rc;
-  return launch_gemm(g.pf_gemm_res, g.pf_gemm_res_m32, act, 3072, cb(w->wdn) + layer * bpl_dn, 3072, 1024, 64, h,
-                     1024, h1, 1024, 0, n, st);
+  return launch_gemm_res(act, 3072, cb(w->wdn) + layer * bpl_dn, 3072, h, h1, n, part, part_bytes,
+                         st);
 }
 
 int check_prefill_ready() {

@@ -165,7 +165,8 @@ def test_code_object_targets_gfx950_and_has_every_kernel():
     assert pf[:4] == b"\x7fELF" and b"amdgcn-amd-amdhsa--gfx950" in pf
     for name in ("pf_embed", "pf_rmsnorm", "pf_gemm_q8", "pf_gemm_q8_res", "pf_gemm_q8_swiglu",
                  "pf_gemm_q8_m32", "pf_gemm_q8_res_m32",
-                 "pf_qk_rope_cache", "pf_attention", "pf_attn_merge", "pf_set_pos"):
+                 "pf_qk_rope_cache", "pf_attention", "pf_attn_merge", "pf_set_pos",
+                 "pf_gemm_q8_part", "pf_gemm_q8_part_m32", "pf_res_reduce"):
         assert name.encode() in pf
 
 
