@@ -43,10 +43,10 @@ def _run(cmd: list[str]) -> None:
         raise RuntimeError(f"build step failed ({proc.returncode}): {' '.join(cmd)}\n{out}")
 
 
-def _hsaco(src: Path, out: Path) -> Path:
+def _hsaco(src: Path, out: Path, extra: tuple[str, ...] = ()) -> Path:
     LIB.mkdir(exist_ok=True)
     tmp = out.with_suffix(".hsaco.tmp")
-    _run([str(ROCM / "bin" / "hipcc"), *HIPCC_FLAGS, f"-I{CSRC}", str(src), "-o", str(tmp)])
+    _run([str(ROCM / "bin" / "hipcc"), *HIPCC_FLAGS, *extra, f"-I{CSRC}", str(src), "-o", str(tmp)])
     os.replace(tmp, out)
     return out
 
@@ -60,7 +60,11 @@ def build_decode_object() -> Path:
 
 
 def build_prefill_object() -> Path:
-    return _hsaco(CSRC / "prefill_kernels.hip", PREFILL_OBJECT)
+    # MFMA results in ordinary VGPRs rather than AGPRs: the GEMMs scale every
+    # block's products with VALU FMAs, and AGPR results would first be copied
+    # out (v_accvgpr_read, 4.5 per MFMA); same instructions otherwise, same bits
+    return _hsaco(CSRC / "prefill_kernels.hip", PREFILL_OBJECT,
+                  ("-mllvm", "-amdgpu-mfma-vgpr-form=1"))
 
 
 def build_shim() -> Path:
