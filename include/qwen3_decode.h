@@ -122,9 +122,13 @@ int qwen3_prefill(const qwen3_weights* w, void* k_cache, void* v_cache, int64_t 
  * the attention's split partials, 266,240 bytes per (query block of 32 tokens,
  * split) pair for 2 ceil(n_prompt / 32) + 64 pairs).  The
  * reference reads f16 copies of the layer matrices for this function
- * (@model_params.attn_q_weight etc., :1132-1210); this one reads the same
- * Q8_0 stacks as the decode step, so prompt and decode share one set of
- * weights. */
+ * (@model_params.attn_q_weight etc., :1132-1210), made from a Q8_0 file as
+ * f16(scale * q) with the product exact (tools/convert_gguf_to_irpa.py:28-44,
+ * 174-199); this one reads the same Q8_0 stacks as the decode step and forms
+ * those f16 weights in registers, so prompt and decode share one set of
+ * weights.  (The decode GEMVs scale each block's exact dot instead, as the
+ * reference's decode kernels do; the two routes' logits differ by about 2e-3
+ * relative.) */
 size_t qwen3_prefill_workspace_bytes(int32_t n_prompt);
 int qwen3_prefill_batched(const qwen3_weights* w, void* k_cache, void* v_cache, int64_t max_seq,
                           const int32_t* prompt, int32_t n_prompt, int32_t* token, int32_t* pos,

@@ -108,6 +108,16 @@ def q8_dequant(blocks: np.ndarray) -> np.ndarray:
     return out
 
 
+def q8_dequant_f16(w_layer: np.ndarray, N: int, K: int) -> np.ndarray:
+    """The f16 [N, K] matrix the reference's @prefill reads for a Q8_0 layer
+    matrix: each weight f32(scale) * f32(q), exact in f32, rounded once to f16
+    (tools/convert_gguf_to_irpa.py:28-44 dequant_q8_0, then .astype(np.float16)
+    at :178 and :197-198)."""
+    w_layer = np.ascontiguousarray(w_layer, dtype=np.uint8).reshape(-1)
+    assert w_layer.size >= N * K // 32 * 34 and K % 32 == 0
+    return f32_to_f16(q8_dequant(w_layer[:N * K // 32 * 34])).reshape(N, K)
+
+
 def q8_gemv(w_layer: np.ndarray, N: int, K: int, x: np.ndarray) -> np.ndarray:
     """f16 y[N] in the reference MLIR kernels' f32 order."""
     w_layer = np.ascontiguousarray(w_layer, dtype=np.uint8).reshape(-1)

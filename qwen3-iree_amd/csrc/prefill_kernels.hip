@@ -7,7 +7,7 @@
 // position splits):
 //   pf_rmsnorm       rms_norm(h, attn_norm) of every token row
 //   pf_gemm_q8       q, k and v projections in one launch (MFMA, Q8_0 weights
-//                    converted in registers, the per-block scale applied in f32)
+//                    dequantized to f16 in registers)
 //   pf_qk_rope_cache per-head rms_norm of q and k, RoPE at each token's
 //                    position, k and v written to their cache slots
 //   pf_attention     causal GQA attention of every token over the cache
@@ -21,10 +21,13 @@
 //
 // Numerics follow the decode step op for op (f16 tensors between ops, f32 in
 // sums, norms and transcendental math): the norms, RoPE, SwiGLU and residual
-// adds are the same device functions the decode kernels call, the GEMMs form
-// each Q8_0 block's 32 products exactly (int8 and f16 inputs, f32 MFMA
-// accumulation) and add them into an f32 sum with the block's scale, as the
-// GEMV does; only the order of the f32 additions differs.
+// adds are the same device functions the decode kernels call.  The GEMMs use
+// the weights @prefill itself reads: the f16 layer matrices the reference's
+// converter makes from a Q8_0 file, f16(scale * q) with the product exact in
+// f32 and rounded once (tools/convert_gguf_to_irpa.py:28-44, 174-199); every
+// weight is formed that way in registers (one f16 multiply of the exact
+// integer q by the f16 scale) and the MFMA accumulates f16 x * f16 w in f32
+// over the whole K.
 #include "decode_device.h"
 #include "prefill_split.h"
 
@@ -185,27 +188,6 @@ __device__ __forceinline__ void gemm_q8(const GemmArgs& A) {
   for (int ms = 0; ms < MS; ++ms)
 #pragma unroll
     for (int ns = 0; ns < NS; ++ns) acc[ms][ns] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
-  const f32x4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
-
-  // Block b's products are issued before block b - 1's are scaled into the
-  // sums, so the matrix unit works while the scale FMAs run.
-  f32x4 prev[MS][NS];
-  float prev_sc[NS];
-#pragma unroll
-  for (int ns = 0; ns < NS; ++ns) prev_sc[ns] = 0.0f;
-#pragma unroll
-  for (int ms = 0; ms < MS; ++ms)
-#pragma unroll
-    for (int ns = 0; ns < NS; ++ns) prev[ms][ns] = zero;
-  auto scale_in = [&]() {
-#pragma unroll
-    for (int ms = 0; ms < MS; ++ms)
-#pragma unroll
-      for (int ns = 0; ns < NS; ++ns)
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          acc[ms][ns][i] = __builtin_fmaf(prev_sc[ns], prev[ms][ns][i], acc[ms][ns][i]);
-  };
 
   gload(0);
   for (int s = 0; s < stages; ++s) {
@@ -221,11 +203,11 @@ __device__ __forceinline__ void gemm_q8(const GemmArgs& A) {
         a[ms] = *reinterpret_cast<const f16x8*>(xl + (32 * wm + 16 * ms + c16) * kXRow +
                                                 2 * (32 * b + 8 * g));
       f16x8 bq[NS];
-      float sc[NS];
 #pragma unroll
       for (int ns = 0; ns < NS; ++ns) {
         const uint8_t* wr = wl + nrow[ns] * kWRow + 34 * b;
-        sc[ns] = (float)*reinterpret_cast<const _Float16*>(wr);
+        const _Float16 sc = *reinterpret_cast<const _Float16*>(wr);
+        const f16x2 s2 = {sc, sc};
         // the block's int8 k = 8 g .. 8 g + 7 sit at wr + 2 + 8 g: 4-byte
         // aligned for odd b, 2 bytes past a dword boundary for even b
         uint32_t lo, hi;
@@ -240,26 +222,18 @@ __device__ __forceinline__ void gemm_q8(const GemmArgs& A) {
           hi = p[1];
         }
         const uint32_t bl = lo ^ 0x80808080u, bh = hi ^ 0x80808080u;
-        const f16x2 v0 = q8x2_to_f16x2(bl, kSelLo), v1 = q8x2_to_f16x2(bl, kSelHi);
-        const f16x2 v2 = q8x2_to_f16x2(bh, kSelLo), v3 = q8x2_to_f16x2(bh, kSelHi);
+        // exact q in f16, then one rounding of scale * q (contraction is off)
+        const f16x2 v0 = q8x2_to_f16x2(bl, kSelLo) * s2, v1 = q8x2_to_f16x2(bl, kSelHi) * s2;
+        const f16x2 v2 = q8x2_to_f16x2(bh, kSelLo) * s2, v3 = q8x2_to_f16x2(bh, kSelHi) * s2;
         bq[ns] = (f16x8){v0.x, v0.y, v1.x, v1.y, v2.x, v2.y, v3.x, v3.y};
       }
-      f32x4 cur[MS][NS];
 #pragma unroll
       for (int ms = 0; ms < MS; ++ms)
 #pragma unroll
         for (int ns = 0; ns < NS; ++ns)
-          cur[ms][ns] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[ms], bq[ns], zero, 0, 0, 0);
-      scale_in();  // block b - 1 (zeros before the first block)
-#pragma unroll
-      for (int ms = 0; ms < MS; ++ms)
-#pragma unroll
-        for (int ns = 0; ns < NS; ++ns) prev[ms][ns] = cur[ms][ns];
-#pragma unroll
-      for (int ns = 0; ns < NS; ++ns) prev_sc[ns] = sc[ns];
+          acc[ms][ns] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[ms], bq[ns], acc[ms][ns], 0, 0, 0);
     }
   }
-  scale_in();
 
   // epilogue: lane holds rows 4 g + i, column c16 of each 16 x 16 tile
 #pragma unroll

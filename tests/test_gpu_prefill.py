@@ -6,13 +6,19 @@ oracle applied to the GPU's own input of that stage (the workspace keeps every
 intermediate), with the decode step's tolerances:
 
   xn, fn        rms_norm per token row         within 1 f16 ulp
-  q, k, v       Q8_0 GEMM rows                 GEMV rule per row (2 ulp / 1e-3)
+  q, k, v       GEMM rows over the f16 weights GEMV rule per row (2 ulp / 1e-3)
+                @prefill reads (f16(scale * q))
   q_roped, K    head norm + RoPE at p0 + i     2 ulp + one input ulp
   V slots       raw v                          bit-exact
   attn          causal attention over the GPU  2 ulp + 1e-5
                 cache, slots [lo, p0 + i]
   res, h        GEMM + f16 residual add        propagated GEMV rule
   act           gate_up GEMM + SwiGLU          propagated GEMV rule + 4 ulp
+
+(the GEMM references are the oracle's f16 GEMV over O.q8_dequant_f16 of the
+layer's Q8_0 matrix: the decode GEMVs scale each block's exact dot instead,
+as the reference's decode kernels do, so the two paths differ by the weights'
+f16 rounding, well inside the whole-path tolerances below)
 
 then the layer's output against the oracle's decode layer run token by token
 (relative L2), and the whole prompt path against the decode-step prompt path
@@ -23,12 +29,30 @@ from __future__ import annotations
 import numpy as np
 import pytest
 
-from test_gpu_decode import (assert_gemv, assert_gemv_add, assert_norm_close, f64,
-                             fill_cache_layer, rope_tol, ulp)
+from test_gpu_decode import assert_norm_close, f64, fill_cache_layer, rope_tol, ulp
 
 pytestmark = pytest.mark.gpu
 
 MAX_SEQ = 512
+
+
+def assert_gemm(O, W16, x, got, what):
+    """One GEMM row against the oracle's f16 GEMV of the same f16 weights."""
+    ref = O.f16_gemv(W16, x)
+    _, mag = O.f16_gemv_f64(W16, x)
+    rep = O.gemv_tolerance_report(got, ref, mag)
+    assert rep["fail"] == 0, (what, rep)
+
+
+def assert_gemm_add(O, base, W16, x, got, what):
+    """got = f16(base + f16(W x)): the GEMV rule carried through one f16 add."""
+    o_ref = O.f16_gemv(W16, x)
+    _, mag = O.f16_gemv_f64(W16, x)
+    want = O.add_f16(base, o_ref)
+    tol = (ulp(O, want) + 2 * ulp(O, o_ref) + 1e-3 * np.abs(f64(o_ref))
+           + 8 * 2.0 ** -24 * mag)
+    d = np.abs(f64(got) - f64(want))
+    assert (d <= tol).all(), (what, np.flatnonzero(d > tol)[:8], d.max())
 
 
 @pytest.fixture(scope="module")
@@ -60,13 +84,18 @@ def test_prefill_layer_stages(O, gpu, D, dmodel, model_host, layer, n, p0, chunk
     g = sess.prefill_layer(layer, h_in, p0, chunk_local)
     k_rows, v_rows = sess.cache_rows(layer, 0, MAX_SEQ)
     lo = p0 if chunk_local else 0
+    wq, wk, wv = (O.q8_dequant_f16(m[layer], nr, 1024)
+                  for m, nr in ((w.wq, 2048), (w.wk, 1024), (w.wv, 1024)))
+    wo = O.q8_dequant_f16(w.wo[layer], 1024, 2048)
+    wgu = O.q8_dequant_f16(w.wgu[layer], 6144, 1024)
+    wdn = O.q8_dequant_f16(w.wdn[layer], 1024, 3072)
 
     for i in range(n):
         pos = p0 + i
         assert_norm_close(O, g["xn"][i], O.rmsnorm(h_in[i], w.attn_norm[layer]), ("xn", i))
-        assert_gemv(O, w.wq[layer], 2048, 1024, g["xn"][i], g["q"][i], ("q", i))
-        assert_gemv(O, w.wk[layer], 1024, 1024, g["xn"][i], g["k"][i], ("k", i))
-        assert_gemv(O, w.wv[layer], 1024, 1024, g["xn"][i], g["v"][i], ("v", i))
+        assert_gemm(O, wq, g["xn"][i], g["q"][i], ("q", i))
+        assert_gemm(O, wk, g["xn"][i], g["k"][i], ("k", i))
+        assert_gemm(O, wv, g["xn"][i], g["v"][i], ("v", i))
         qn = O.head_rmsnorm(g["q"][i], w.q_norm[layer])
         q_want = O.rope(qn, pos)
         assert (np.abs(f64(g["q_roped"][i]) - f64(q_want)) <= rope_tol(O, qn, q_want)).all(), i
@@ -77,10 +106,10 @@ def test_prefill_layer_stages(O, gpu, D, dmodel, model_host, layer, n, p0, chunk
         a_want = O.attention(g["q_roped"][i], k_rows[lo:pos + 1], v_rows[lo:pos + 1])
         d = np.abs(f64(g["attn"][i]) - f64(a_want))
         assert (d <= 2 * ulp(O, a_want) + 1e-5).all(), (i, d.max())
-        assert_gemv_add(O, h_in[i], w.wo[layer], 1024, 2048, g["attn"][i], g["res"][i], ("res", i))
+        assert_gemm_add(O, h_in[i], wo, g["attn"][i], g["res"][i], ("res", i))
         assert_norm_close(O, g["fn"][i], O.rmsnorm(g["res"][i], w.ffn_norm[layer]), ("fn", i))
-        gu = O.q8_gemv(w.wgu[layer], 6144, 1024, g["fn"][i])
-        _, gmag = O.q8_gemv_f64(w.wgu[layer], 6144, 1024, g["fn"][i])
+        gu = O.f16_gemv(wgu, g["fn"][i])
+        _, gmag = O.f16_gemv_f64(wgu, g["fn"][i])
         act_want = O.swiglu(gu[:3072], gu[3072:])
         dg = 2 * ulp(O, gu) + 1e-3 * np.abs(f64(gu)) + 8 * 2.0 ** -24 * gmag
         gate, up = f64(gu[:3072]), f64(gu[3072:])
@@ -88,7 +117,7 @@ def test_prefill_layer_stages(O, gpu, D, dmodel, model_host, layer, n, p0, chunk
         tol = 1.1 * np.abs(up) * dg[:3072] + np.abs(silu) * dg[3072:] + 4 * ulp(O, act_want)
         d = np.abs(f64(g["act"][i]) - f64(act_want))
         assert (d <= tol).all(), (i, np.flatnonzero(d > tol)[:8], d.max())
-        assert_gemv_add(O, g["res"][i], w.wdn[layer], 1024, 3072, g["act"][i], g["h"][i], ("h", i))
+        assert_gemm_add(O, g["res"][i], wdn, g["act"][i], g["h"][i], ("h", i))
 
     # slots outside [p0, p0 + n) untouched
     base = layer * MAX_SEQ

@@ -98,6 +98,30 @@ def test_dequant_known_answer(O):
     assert np.array_equal(got, want.astype(np.float32))
 
 
+def test_dequant_f16_rounds_each_exact_product_once(O):
+    """The prompt path's f16 weights: f16(scale * q), one rounding of the exact
+    product.  Checked against float64 products (exact: 11 x 8 bits) converted
+    by numpy's correctly rounded float64 -> float16, with scales whose products
+    need rounding (1/3, 0.0123), that land on f16 subnormals (2^-20) and that
+    make every product exact (powers of two)."""
+    q = RNG.integers(-128, 128, (6, 32)).astype(np.int32)
+    q[0, :3] = (-128, 127, 0)
+    scales = [1.0 / 3.0, 0.0123, 2.0 ** -20, 0.5, 4.0, -0.7]
+    raw = np.concatenate([_block_bytes(sc, q[i]) for i, sc in enumerate(scales)])
+    got = O.q8_dequant_f16(raw, 6, 32)
+    s16 = np.array(scales, np.float16).astype(np.float64)
+    want = (s16[:, None] * q).astype(np.float16)
+    assert np.array_equal(got.view(np.uint16), want.view(np.uint16))
+    # powers of two: no rounding at all
+    assert np.array_equal(got[3:5].astype(np.float64), s16[3:5, None] * q[3:5])
+    # f16(1/3) * 3 = 1 - 2^-12 exactly: a tie between 1 - 2^-11 and 1, which
+    # round-to-nearest-even sends to 1; f16(1/3) * -3 likewise to -1
+    third = _block_bytes(1.0 / 3.0, np.array([3, -3] * 16))
+    got = O.q8_dequant_f16(third, 1, 32)[0, :2]
+    assert float(np.float16(1.0 / 3.0)) * 3 == 1 - 2.0 ** -12
+    assert got[0] == np.float16(1.0) and got[1] == np.float16(-1.0)
+
+
 # ---------------------------------------------------------------- GEMV ------
 
 def _q8_layer(n, k, seed):
