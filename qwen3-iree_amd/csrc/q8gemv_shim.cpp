@@ -1190,10 +1190,12 @@ int launch_gemm(hipFunction_t fn, hipFunction_t fn_m32, const void* x, int ldx, 
 }
 
 // y = r + x W^T for N = 1024 (attn_o, ffn_down).  Where 32-token tiles would
-// leave CUs idle (fewer workgroups than CUs: short prompts), K is split into
-// equal ranges of whole stages, each range's f32 sums go to `part`, and
-// pf_res_reduce adds them in order with the residual.  The split count
-// depends on M only, so every token tile gives the same bits.
+// leave CUs idle (short prompts), K is split into equal ranges of whole stages
+// (the fewest that fill the CUs), each range's f32 sums go to `part`, and
+// pf_res_reduce adds them in order with the residual; where they fill the CUs
+// once but not twice (about 512-1023 tokens), K is split in two, since one
+// workgroup per CU walking all of K hides too little load latency.  The split
+// count depends on M only, so every token tile gives the same bits.
 int launch_gemm_res(const void* x, int ldx, const void* wl, int K, void* y, const void* r,
                     int M, void* part, size_t part_bytes, hipStream_t st) {
   constexpr int kN = 1024;
@@ -1201,13 +1203,17 @@ int launch_gemm_res(const void* x, int ldx, const void* wl, int K, void* y, cons
   const int stages = K / 256;
   int splits = 1;
   const int64_t wgs32 = ((int64_t)M + 31) / 32 * n_tiles;
-  if (g.pf_gemm_part && g.pf_gemm_part_m32 && g.pf_res_reduce && wgs32 < g.compute_units) {
-    splits = stages;
-    for (int d = 1; d <= stages; ++d)
-      if (stages % d == 0 && wgs32 * d >= g.compute_units) {
-        splits = d;
-        break;
-      }
+  if (g.pf_gemm_part && g.pf_gemm_part_m32 && g.pf_res_reduce) {
+    if (wgs32 < g.compute_units) {
+      splits = stages;
+      for (int d = 1; d <= stages; ++d)
+        if (stages % d == 0 && wgs32 * d >= g.compute_units) {
+          splits = d;
+          break;
+        }
+    } else if (wgs32 < 2 * g.compute_units && stages % 2 == 0) {
+      splits = 2;
+    }
     if ((size_t)splits * M * kN * 4 > part_bytes) splits = 1;
   }
   if (splits == 1)

@@ -71,7 +71,8 @@ def dmodel(gpu, D, model_host):
 
 @pytest.mark.parametrize("layer,n,p0,chunk_local", [
     (0, 1, 0, False), (3, 37, 0, False), (11, 64, 5, False), (27, 130, 40, False),
-    (7, 20, 9, True), (16, 65, 0, True)])
+    (7, 20, 9, True), (16, 65, 0, True),
+    (20, 500, 0, False)])  # attn_o / ffn_down with K split in two
 def test_prefill_layer_stages(O, gpu, D, dmodel, model_host, layer, n, p0, chunk_local):
     w = model_host
     rng = np.random.default_rng(7000 + 100 * layer + n)
