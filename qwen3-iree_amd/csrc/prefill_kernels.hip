@@ -17,7 +17,11 @@
 //   pf_gemm_q8       gate/up with SwiGLU in the epilogue
 //   pf_gemm_q8       ffn_down + residual
 // plus pf_embed (token rows) before the first layer.  The vocab GEMV + argmax
-// of the last token reuses the decode kernels.
+// of the last token reuses the decode kernels.  Prompts below 1024 tokens run
+// attn_o and ffn_down with K split (pf_gemm_q8_part); their reduce
+// (pf_res_reduce_norm) then also forms the rms_norm that follows (ffn_norm of
+// the row after attn_o, the next layer's attn_norm after ffn_down), so those
+// two pf_rmsnorm launches drop out.
 //
 // Numerics follow the decode step op for op (f16 tensors between ops, f32 in
 // sums, norms and transcendental math): the norms, RoPE, SwiGLU and residual
@@ -324,6 +328,53 @@ extern "C" __global__ __launch_bounds__(256) void pf_res_reduce(
   float acc = part[e];
   for (int s = 1; s < splits; ++s) acc += part[(size_t)s * M * N + e];
   y[(size_t)m * ldy + n] = residual_f16(as_half(r[(size_t)m * ldr + n]), acc);
+}
+
+// pf_res_reduce for N = 1024 (y, r ld 1024) followed by out = rms_norm(y, w)
+// of the same row, so no separate pf_rmsnorm launch is needed.  Workgroup =
+// one row: every thread reduces 4 columns (all splits' loads issued first,
+// then added in split order, as pf_res_reduce adds them) and adds the
+// residual; the row goes through LDS to the first 16 lanes, which normalise
+// it with pf_rmsnorm's lane layout and device function.  y and out are those
+// two kernels' bits.  splits <= kPfMaxSplits.
+constexpr int kPfMaxSplits = 12;
+extern "C" __global__ __launch_bounds__(256) void pf_res_reduce_norm(
+    const float* __restrict__ part, int splits, int M, const uint16_t* __restrict__ r,
+    uint16_t* __restrict__ y, const uint16_t* __restrict__ w, uint16_t* __restrict__ out) {
+  __shared__ __attribute__((aligned(16))) uint16_t row_h[kHidden];
+  const int m = blockIdx.x;
+  const int c = 4 * threadIdx.x;
+  const size_t e = (size_t)m * kHidden + c;
+  const size_t plane = (size_t)M * kHidden;
+  float4 v[kPfMaxSplits];
+#pragma unroll
+  for (int s = 0; s < kPfMaxSplits; ++s)
+    if (s < splits) v[s] = *reinterpret_cast<const float4*>(part + s * plane + e);
+  float4 a = v[0];
+#pragma unroll
+  for (int s = 1; s < kPfMaxSplits; ++s)
+    if (s < splits) {
+      a.x += v[s].x;
+      a.y += v[s].y;
+      a.z += v[s].z;
+      a.w += v[s].w;
+    }
+  const uint2 rv = *reinterpret_cast<const uint2*>(r + e);
+  const uint32_t lo = (uint32_t)residual_f16(as_half((uint16_t)(rv.x & 0xffffu)), a.x) |
+                      ((uint32_t)residual_f16(as_half((uint16_t)(rv.x >> 16)), a.y) << 16);
+  const uint32_t hi = (uint32_t)residual_f16(as_half((uint16_t)(rv.y & 0xffffu)), a.z) |
+                      ((uint32_t)residual_f16(as_half((uint16_t)(rv.y >> 16)), a.w) << 16);
+  const uint2 o = {lo, hi};
+  *reinterpret_cast<uint2*>(y + e) = o;
+  *reinterpret_cast<uint2*>(row_h + c) = o;
+  __syncthreads();
+  if (threadIdx.x < 16) {
+    u32x4 xr[8];
+    rmsnorm_cols<true>(row_h, w, gemv_col, xr);
+    u32x4* xo = reinterpret_cast<u32x4*>(out + (size_t)m * kHidden + gemv_col(0));
+#pragma unroll
+    for (int k = 0; k < 8; ++k) xo[k] = xr[k];
+  }
 }
 
 extern "C" __global__ __launch_bounds__(256) void pf_gemm_q8_swiglu(GemmArgs A) {

@@ -107,7 +107,7 @@ struct State {
   hipFunction_t pf_embed = nullptr, pf_norm = nullptr, pf_gemm = nullptr, pf_gemm_res = nullptr,
                 pf_gemm_m32 = nullptr, pf_gemm_res_m32 = nullptr, pf_gemm_swiglu = nullptr,
                 pf_gemm_part = nullptr, pf_gemm_part_m32 = nullptr, pf_res_reduce = nullptr,
-                pf_rope = nullptr, pf_attn = nullptr, pf_attn_merge = nullptr,
+                pf_res_reduce_norm = nullptr, pf_rope = nullptr, pf_attn = nullptr, pf_attn_merge = nullptr,
                 pf_set_pos = nullptr;
   int pf_tile_rows = 0;   // prefill GEMM token tile: 0 = by shape, 32 or 64
   int pf_attn_split = 0;  // prefill attention positions per split in blocks of 32: 0 = by shape
@@ -326,6 +326,7 @@ int q8gemv_init(const char* code_object_path) {
                      {&g.pf_gemm_part, "pf_gemm_q8_part"},
                      {&g.pf_gemm_part_m32, "pf_gemm_q8_part_m32"},
                      {&g.pf_res_reduce, "pf_res_reduce"},
+                     {&g.pf_res_reduce_norm, "pf_res_reduce_norm"},
                      {&g.pf_set_pos, "pf_set_pos"}};
         bool ok = true;
         for (auto& n : names) ok = ok && hipModuleGetFunction(n.fn, pm, n.name) == hipSuccess;
@@ -378,7 +379,7 @@ void q8gemv_shutdown(void) {
   g.pf_module = nullptr;
   g.pf_embed = g.pf_norm = g.pf_gemm = g.pf_gemm_res = g.pf_gemm_m32 = g.pf_gemm_res_m32 =
       g.pf_gemm_swiglu = g.pf_rope = g.pf_attn = g.pf_attn_merge = g.pf_set_pos = nullptr;
-  g.pf_gemm_part = g.pf_gemm_part_m32 = g.pf_res_reduce = nullptr;
+  g.pf_gemm_part = g.pf_gemm_part_m32 = g.pf_res_reduce = g.pf_res_reduce_norm = nullptr;
   g.vocab = g.vocab_finalize = g.ws_reset = g.copy = nullptr;
   g.ready = false;
 }
@@ -1195,9 +1196,17 @@ int launch_gemm(hipFunction_t fn, hipFunction_t fn_m32, const void* x, int ldx, 
 // pf_res_reduce adds them in order with the residual; where they fill the CUs
 // once but not twice (about 512-1023 tokens), K is split in two, since one
 // workgroup per CU walking all of K hides too little load latency.  The split
-// count depends on M only, so every token tile gives the same bits.
+// count depends on M only, so every token tile gives the same bits.  With
+// norm_w set and K split, the reduce also writes norm_out = rms_norm(y,
+// norm_w) (pf_res_reduce_norm, the bits of a separate pf_rmsnorm) and
+// *normed becomes true; otherwise the caller runs the norm itself.
+constexpr int kPfMaxSplits = 12;  // pf_res_reduce_norm's limit (prefill_kernels.hip)
+
 int launch_gemm_res(const void* x, int ldx, const void* wl, int K, void* y, const void* r,
-                    int M, void* part, size_t part_bytes, hipStream_t st) {
+                    int M, void* part, size_t part_bytes, hipStream_t st,
+                    const void* norm_w = nullptr, void* norm_out = nullptr,
+                    bool* normed = nullptr) {
+  if (normed) *normed = false;
   constexpr int kN = 1024;
   const int n_tiles = kN / 64;
   const int stages = K / 256;
@@ -1224,13 +1233,24 @@ int launch_gemm_res(const void* x, int ldx, const void* wl, int K, void* y, cons
   if (rc) return rc;
   const void* pp = part;
   int sp = splits, mm = M, nn = kN, ld = kN;
+  if (norm_w && splits <= kPfMaxSplits) {
+    void* args[] = {&pp, &sp, &mm, &r, &y, &norm_w, &norm_out};
+    if ((rc = launch(g.pf_res_reduce_norm, (uint32_t)M, 256, args, st))) return rc;
+    if (normed) *normed = true;
+    return Q8_OK;
+  }
   void* args[] = {&pp, &sp, &mm, &nn, &r, &ld, &y, &ld};
   return launch(g.pf_res_reduce, (uint32_t)(((int64_t)M * kN + 255) / 256), 256, args, st);
 }
 
+// One layer.  xn_ready: the workspace's xn already holds rms_norm(h,
+// attn_norm of this layer) (written by the previous layer's last reduce).
+// next_norm (the next layer's attn_norm, or null): if ffn_down's reduce can
+// also form the next layer's xn it does so and *next_xn_ready becomes true.
 int launch_prefill_layer(const qwen3_weights* w, int layer, void* k_cache, void* v_cache,
                          int64_t max_seq, int32_t n, int32_t p0, int chunk_local,
-                         void* const (&ws)[kPfRegions], hipStream_t st) {
+                         void* const (&ws)[kPfRegions], hipStream_t st, bool xn_ready = false,
+                         const void* next_norm = nullptr, bool* next_xn_ready = nullptr) {
   const int64_t bpl_q = 2048LL * 1024 / 32 * 34, bpl_kv = 1024LL * 1024 / 32 * 34;
   const int64_t bpl_o = 1024LL * 2048 / 32 * 34, bpl_gu = 6144LL * 1024 / 32 * 34;
   const int64_t bpl_dn = 1024LL * 3072 / 32 * 34;
@@ -1244,7 +1264,7 @@ int launch_prefill_layer(const qwen3_weights* w, int layer, void* k_cache, void*
        *attn = ws[7], *act = ws[8], *fnx = ws[9], *part = ws[10];
   const uint32_t norm_grid = (uint32_t)((n + 15) / 16);
   int rc;
-  {
+  if (!xn_ready) {
     void* args[] = {&h, &an, &xn, &n};
     if ((rc = launch(g.pf_norm, norm_grid, 256, args, st))) return rc;
   }
@@ -1277,10 +1297,11 @@ int launch_prefill_layer(const qwen3_weights* w, int layer, void* k_cache, void*
   // the attention partials are consumed by now: their region holds the
   // split-K sums of attn_o and ffn_down
   const size_t part_bytes = pf_region_bytes(n, kPfTokenRegions);
+  bool fn_done = false;
   if ((rc = launch_gemm_res(attn, 2048, cb(w->wo) + layer * bpl_o, 2048, h1, h, n, part,
-                            part_bytes, st)))
+                            part_bytes, st, fn, fnx, &fn_done)))
     return rc;
-  {
+  if (!fn_done) {
     void* args[] = {&h1, &fn, &fnx, &n};
     if ((rc = launch(g.pf_norm, norm_grid, 256, args, st))) return rc;
   }
@@ -1288,7 +1309,7 @@ int launch_prefill_layer(const qwen3_weights* w, int layer, void* k_cache, void*
                         act, 3072, nullptr, 0, 3072, n, st)))
     return rc;
   return launch_gemm_res(act, 3072, cb(w->wdn) + layer * bpl_dn, 3072, h, h1, n, part, part_bytes,
-                         st);
+                         st, next_norm, xn, next_xn_ready);
 }
 
 int check_prefill_ready() {
@@ -1592,10 +1613,13 @@ int qwen3_prefill_batched(const qwen3_weights* w, void* k_cache, void* v_cache, 
     void* args[] = {&tp, &e, &h};
     if ((rc = launch(g.pf_embed, (uint32_t)n_prompt, 128, args, st))) return rc;
   }
-  for (int l = 0; l < kLayers; ++l)
+  bool xn_ready = false;
+  for (int l = 0; l < kLayers; ++l) {
+    const void* next_norm = l + 1 < kLayers ? cb(w->attn_norm) + (l + 1) * 2048 : nullptr;
     if ((rc = launch_prefill_layer(w, l, k_cache, v_cache, max_seq, n_prompt, p0, chunk_local, ws,
-                                   st)))
+                                   st, xn_ready, next_norm, &xn_ready)))
       return rc;
+  }
   {
     int last = p0 + n_prompt - 1;
     void* args[] = {&pos, &last};

@@ -166,7 +166,8 @@ def test_code_object_targets_gfx950_and_has_every_kernel():
     for name in ("pf_embed", "pf_rmsnorm", "pf_gemm_q8", "pf_gemm_q8_res", "pf_gemm_q8_swiglu",
                  "pf_gemm_q8_m32", "pf_gemm_q8_res_m32",
                  "pf_qk_rope_cache", "pf_attention", "pf_attn_merge", "pf_set_pos",
-                 "pf_gemm_q8_part", "pf_gemm_q8_part_m32", "pf_res_reduce"):
+                 "pf_gemm_q8_part", "pf_gemm_q8_part_m32", "pf_res_reduce",
+                 "pf_res_reduce_norm"):
         assert name.encode() in pf
 
 

@@ -186,6 +186,30 @@ def test_prefill_batched_matches_decode_steps(gpu, D, dmodel, n):
     b.free()
 
 
+@pytest.mark.parametrize("n", [45, 500])
+def test_prefill_batched_equals_layer_by_layer(gpu, D, dmodel, model_host, n):
+    """The whole-prompt call forms each next layer's attention norm inside
+    ffn_down's split-K reduce (pf_res_reduce_norm); layer by layer
+    (qwen3_prefill_layer) runs pf_rmsnorm instead.  Every layer's k/v slots
+    depend on that norm, so they must agree bit for bit."""
+    rng = np.random.default_rng(900 + n)
+    prompt = rng.integers(0, D.VOCAB, n).astype(np.int32)
+    print(f"prefill batched vs layers n {n}", flush=True)
+    a = D.DecodeSession(dmodel, MAX_SEQ)
+    a.set_state(0, 0)
+    a.prefill_batched(prompt)
+    b = D.DecodeSession(dmodel, MAX_SEQ)
+    h = model_host.token_embd[prompt]
+    for layer in range(28):
+        h = b.prefill_layer(layer, h, 0)["h"]
+        ka, va = a.cache_rows(layer, 0, n)
+        kb, vb = b.cache_rows(layer, 0, n)
+        assert np.array_equal(ka.view(np.uint16), kb.view(np.uint16)), layer
+        assert np.array_equal(va.view(np.uint16), vb.view(np.uint16)), layer
+    a.free()
+    b.free()
+
+
 def test_prefill_batched_matches_oracle_steps(O, gpu, D, dmodel, model_host):
     w = model_host
     prompt = np.array([151643, 9707, 11, 1879, 0, 151935], np.int32)
