@@ -186,19 +186,21 @@ def test_prefill_batched_matches_decode_steps(gpu, D, dmodel, n):
     b.free()
 
 
-@pytest.mark.parametrize("n", [45, 500])
+@pytest.mark.parametrize("n", [45, 500, 1100])
 def test_prefill_batched_equals_layer_by_layer(gpu, D, dmodel, model_host, n):
     """The whole-prompt call forms each next layer's attention norm inside
-    ffn_down's split-K reduce (pf_res_reduce_norm); layer by layer
+    ffn_down's reduce (pf_res_reduce_norm; K split in many ranges at 45
+    tokens, in two at 500, one range at 1100); layer by layer
     (qwen3_prefill_layer) runs pf_rmsnorm instead.  Every layer's k/v slots
     depend on that norm, so they must agree bit for bit."""
     rng = np.random.default_rng(900 + n)
     prompt = rng.integers(0, D.VOCAB, n).astype(np.int32)
     print(f"prefill batched vs layers n {n}", flush=True)
-    a = D.DecodeSession(dmodel, MAX_SEQ)
+    max_seq = max(MAX_SEQ, n)
+    a = D.DecodeSession(dmodel, max_seq)
     a.set_state(0, 0)
     a.prefill_batched(prompt)
-    b = D.DecodeSession(dmodel, MAX_SEQ)
+    b = D.DecodeSession(dmodel, max_seq)
     h = model_host.token_embd[prompt]
     for layer in range(28):
         h = b.prefill_layer(layer, h, 0)["h"]
