@@ -337,7 +337,6 @@ extern "C" __global__ __launch_bounds__(256) void pf_res_reduce(
 // residual; the row goes through LDS to the first 16 lanes, which normalise
 // it with pf_rmsnorm's lane layout and device function.  y and out are those
 // two kernels' bits.  splits <= kPfMaxSplits.
-constexpr int kPfMaxSplits = 12;
 extern "C" __global__ __launch_bounds__(256) void pf_res_reduce_norm(
     const float* __restrict__ part, int splits, int M, const uint16_t* __restrict__ r,
     uint16_t* __restrict__ y, const uint16_t* __restrict__ w, uint16_t* __restrict__ out) {

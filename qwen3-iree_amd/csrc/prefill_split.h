@@ -19,6 +19,11 @@
 // 16 wave + r of the workgroup's four waves.
 constexpr int kPfAttnSlotFloats = 64 * 128 + 2 * 64;
 
+// Most K ranges a split attn_o / ffn_down product may have where its reduce
+// also forms the following rms_norm (pf_res_reduce_norm keeps every range's
+// sums in registers): K <= 3072 gives at most 12 stages of 256.
+constexpr int kPfMaxSplits = 12;
+
 struct PfSplitGeometry {
   int32_t nqb;      // query blocks
   int32_t c;        // nb(q) = q + c for q < nqb - 1

@@ -1200,8 +1200,6 @@ int launch_gemm(hipFunction_t fn, hipFunction_t fn_m32, const void* x, int ldx, 
 // norm_w set and K split, the reduce also writes norm_out = rms_norm(y,
 // norm_w) (pf_res_reduce_norm, the bits of a separate pf_rmsnorm) and
 // *normed becomes true; otherwise the caller runs the norm itself.
-constexpr int kPfMaxSplits = 12;  // pf_res_reduce_norm's limit (prefill_kernels.hip)
-
 int launch_gemm_res(const void* x, int ldx, const void* wl, int K, void* y, const void* r,
                     int M, void* part, size_t part_bytes, hipStream_t st,
                     const void* norm_w = nullptr, void* norm_out = nullptr,
