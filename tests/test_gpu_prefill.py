@@ -297,12 +297,15 @@ def test_prefill_batched_cache_edges(gpu, D, dmodel):
     sess.free()
 
 
-@pytest.mark.parametrize("n,p0", [(45, 3), (300, 0)])
+@pytest.mark.parametrize("n,p0", [(45, 3), (300, 0), (600, 0), (1030, 0)])
 def test_prefill_tile_rows_bit_identical(gpu, D, dmodel, n, p0):
-    """The 32- and 64-token GEMM tiles give the same bits in every stage."""
+    """The 32- and 64-token GEMM tiles give the same bits in every stage
+    (attn_o / ffn_down with K in many ranges at 45 and 300 tokens, in two at
+    600, in one range through the reduce at 1030)."""
     rng = np.random.default_rng(9100 + n)
-    sess = D.DecodeSession(dmodel, MAX_SEQ)
-    kc = np.zeros((28 * MAX_SEQ, 1024), np.float16)
+    max_seq = max(MAX_SEQ, p0 + n)
+    sess = D.DecodeSession(dmodel, max_seq)
+    kc = np.zeros((28 * max_seq, 1024), np.float16)
     vc = np.zeros_like(kc)
     fill_cache_layer(sess, 5, p0, rng, kc, vc)
     h_in = (1.5 * rng.standard_normal((n, 1024))).astype(np.float16)
@@ -312,7 +315,7 @@ def test_prefill_tile_rows_bit_identical(gpu, D, dmodel, n, p0):
             print(f"prefill tile rows {rows} n {n} p0 {p0}", flush=True)
             D.set_prefill_tiling(rows, 0)
             g = sess.prefill_layer(5, h_in, p0, False)
-            outs.append((g, sess.cache_rows(5, 0, MAX_SEQ)))
+            outs.append((g, sess.cache_rows(5, 0, max_seq)))
     finally:
         D.set_prefill_tiling(0, 0)
     (g32, c32), (g64, c64), (ga, ca) = outs
