@@ -5,7 +5,8 @@ Workload (the headline metric's configuration): the 28-layer stacked
 cold-cache Q8_0 GEMV sweep -- five stacked weight sets (attn_q, attn_kv, attn_o,
 gate_up, ffn_dn; 436,731,904 bytes, more than the 256 MB MALL); for layer
 0..27 the five GEMVs in that order, 140 GEMVs per step, each with its own f16 x
-and y.  Inputs are resident in HBM before timing.
+and y (qwen3_iree_amd/sweep.py, shared with the parity tests).  Inputs are
+resident in HBM before timing.
 
 One step = one sweep executed as a single batched launch (q8gemv_batch: the
 140 GEMVs listed in sweep order; waves stream the list in order, so the access
@@ -22,9 +23,21 @@ pattern still rotates through the 28 layers).  Measured in the same run:
     checked against the oracle's step;
   * batched prompt ingestion (qwen3_prefill_batched) of 512 tokens, checked
     against the decode-step prompt path;
+  * end-to-end generation, the reference's own published measure
+    (scripts/benchmark.py:52-81: wall time of one `run` call = prompt
+    ingestion + up to 128 greedy tokens with the EOS check after every 4,
+    tok/s = tokens generated before EOS / that time), for a chat-sized prompt
+    and a 512-token prompt, checked token for token against single steps;
   * parity of all 140 sweep outputs and of the vocab logits/token against the
     CPU oracle;
-  * the CPU oracle on a bounded sample of the same sweep (cpu_baseline).
+  * the CPU oracle on a bounded sample of the same sweep (cpu_baseline), at
+    every host thread and at one.
+
+Timing: every timed kernel is first run for at least 200 ms (whatever
+--warmup says; the GPU clock ramps over the first ~100 ms of sustained work),
+then exactly --steps calls are timed with HIP events on the launch stream in
+10 blocks: `ms_per_step` / `value` come from the mean over all steps, and the
+median over the blocks is reported beside it.
 
 Prints one JSON line.  Only --gpus 1 is supported: this path runs on one GPU.
 """
@@ -33,6 +46,8 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import platform
+import statistics
 import sys
 import time
 from pathlib import Path
@@ -45,50 +60,88 @@ sys.path.insert(0, str(REPO))
 HBM_PEAK_GBS = 8000.0
 METRIC = "achieved HBM GB/s (% of peak) on 28-layer Q8_0 GEMV sweep; µs per decode step"
 SEED = 20261201
+MIN_WARM_MS = 200.0
+TIMING_BLOCKS = 10
+EOS_TOKEN = 151645   # scripts/benchmark.py:21
+MAX_NEW_TOKENS = 128  # scripts/benchmark.py:22
 
 
 def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def algorithmic_bytes(d) -> int:
-    """Weights + x + y of one GEMV, each byte counted once."""
-    return d.bytes_per_layer + 2 * d.k + 2 * d.n
+def cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
 
 
-def profiled_traffic(name: str, grid_threads: int):
-    """HBM bytes per dispatch of kernel `name` at this grid, from the committed
+def profiled_traffic(name: str, grid_threads: int) -> dict:
+    """HBM bytes per dispatch of kernel `name` at this grid from the committed
     rocprofv3 counter summary (FETCH_SIZE + WRITE_SIZE, each scaled by what it
-    reads for a copy kernel of known size); None if not profiled."""
+    reads for a copy kernel of known size), with whether the summary was taken
+    on the device sources of this tree."""
+    from qwen3_iree_amd import build as B
+
+    out = {"bytes": None, "source_digest": None, "stale": None}
     path = REPO / "profiles" / "traffic.json"
     if not path.exists():
-        return None
-    for k in json.loads(path.read_text()).get("kernels", []):
+        return out
+    rep = json.loads(path.read_text())
+    out["source_digest"] = rep.get("source_digest")
+    out["stale"] = rep.get("source_digest") != B.source_digest()
+    for k in rep.get("kernels", []):
         if k.get("name") == name and k.get("grid") == grid_threads and k.get("hbm_bytes"):
-            return int(k["hbm_bytes"])
-    return None
+            out["bytes"] = int(k["hbm_bytes"])
+            out["profiled_mean_us"] = round(float(k["mean_us"]), 3)
+    return out
 
 
-def timed_ms(Q, stream, fn, reps: int) -> float:
-    """Mean ms per call of fn() over `reps` back-to-back calls on `stream`,
-    bracketed by HIP events on that stream."""
-    e0, e1 = Q.Event(), Q.Event()
+def warm(stream, fn, n: int, min_ms: float = MIN_WARM_MS) -> int:
+    """At least n calls of fn() and at least min_ms of them (host clock)."""
+    calls = 0
+    t0 = time.perf_counter()
+    while calls < n or (time.perf_counter() - t0) * 1e3 < min_ms:
+        for _ in range(8):
+            fn()
+        calls += 8
+        stream.synchronize()
+    return calls
+
+
+def timed(Q, stream, fn, reps: int, blocks: int = TIMING_BLOCKS) -> dict:
+    """Exactly `reps` back-to-back calls of fn() on `stream`, HIP events on
+    that stream between `blocks` blocks of calls.  Mean ms per call over all
+    of them, and the median (min, max) of the blocks' means."""
+    reps = max(1, int(reps))
+    blocks = max(1, min(blocks, reps))
+    sizes = [reps // blocks + (1 if i < reps % blocks else 0) for i in range(blocks)]
+    ev = [Q.Event() for _ in range(blocks + 1)]
     stream.synchronize()
-    e0.record(stream)
-    for _ in range(reps):
-        fn()
-    e1.record(stream)
-    e1.synchronize()
-    ms = e0.elapsed_ms(e1) / reps
-    e0.destroy()
-    e1.destroy()
-    return ms
+    ev[0].record(stream)
+    for i, n in enumerate(sizes):
+        for _ in range(n):
+            fn()
+        ev[i + 1].record(stream)
+    ev[-1].synchronize()
+    per = [ev[i].elapsed_ms(ev[i + 1]) / sizes[i] for i in range(blocks)]
+    total = ev[0].elapsed_ms(ev[-1])
+    for e in ev:
+        e.destroy()
+    return {"mean_ms": total / reps, "median_ms": statistics.median(per), "min_ms": min(per),
+            "max_ms": max(per), "reps": reps, "blocks": blocks}
 
 
 def bench_decode(Q, O, stream, args) -> dict:
     """The full decode step at context args.context: one step checked against
-    the oracle's, then replays of the captured step timed with HIP events."""
+    the oracle's, then steps timed with HIP events (token fed back, position
+    kept)."""
     from qwen3_iree_amd import decode as D
+    from qwen3_iree_amd import sweep as S
 
     layers = D.LAYERS
     vocab_bytes = Q.VOCAB.bytes_per_layer + 2 * Q.HIDDEN + 2 * Q.VOCAB_ROWS + 4
@@ -123,8 +176,8 @@ def bench_decode(Q, O, stream, args) -> dict:
                and (step_tok == ref_tok or margin <= 2 * dl.max()))
     log(f"decode step parity: token {step_tok} (oracle {ref_tok}, margin {margin:.4f}, "
         f"max |dlogit| {dl.max():.4f})")
-    # timed: replays of the captured per-phase step (143 launches), each
-    # consuming the previous token
+    reps = max(50, args.steps // 4)
+    # the per-phase step (143 launches) replayed from a hipGraph
     default_mode = D.step_mode()
     D.set_step_mode(0)
     sess.set_state(first_token, ctx - 1)
@@ -133,19 +186,18 @@ def bench_decode(Q, O, stream, args) -> dict:
     else:
         sess.capture(advance=False, logits=False)
         dec_fn = lambda: sess.replay(advance=False, logits=False)  # noqa: E731
-    for _ in range(20):
-        dec_fn()
-    dec_us = timed_ms(Q, stream, dec_fn, max(50, args.steps // 4)) * 1e3
+    warm(stream, dec_fn, 20)
+    tp = timed(Q, stream, dec_fn, reps)
+    dec_us = tp["mean_ms"] * 1e3
     norm_bytes = 2 * (D.LAYERS * (2 * D.HIDDEN + 2 * D.HEAD_DIM) + D.HIDDEN)
     kv_bytes = D.LAYERS * ctx * 2 * D.KV_DIM * 2
-    dec_bytes = (sum(algorithmic_bytes(d) for d in Q.LAYER_ORDER) * layers + vocab_bytes
+    dec_bytes = (sum(S.algorithmic_bytes(d) for d in Q.LAYER_ORDER) * layers + vocab_bytes
                  + kv_bytes + norm_bytes + 2 * D.HIDDEN)
-    dec_gbs = dec_bytes / dec_us / 1e3
     log(f"decode step (context {ctx}, {3 + 5 * layers} launches"
-        f"{'' if args.no_graph else ', hipGraph'}): {dec_us:.1f} us/token, "
-        f"{1e6 / dec_us:.0f} tok/s, {dec_gbs:.0f} GB/s")
+        f"{'' if args.no_graph else ', hipGraph'}): {dec_us:.1f} us/token (median "
+        f"{tp['median_ms'] * 1e3:.1f}), {1e6 / dec_us:.0f} tok/s")
     # the same step as one cooperative launch (qwen3_set_step_mode(1)), eager
-    single_us = None
+    ts = None
     try:
         D.set_step_mode(1)
     except Q.Q8GemvError as e:
@@ -153,23 +205,26 @@ def bench_decode(Q, O, stream, args) -> dict:
     else:
         sess.set_state(first_token, ctx - 1)
         one = lambda: sess.step(advance=False, logits=False)  # noqa: E731
-        for _ in range(20):
-            one()
-        single_us = timed_ms(Q, stream, one, max(50, args.steps // 4)) * 1e3
-        ok1 = sess.get_state()[1] == ctx - 1 and sess.status() == 0
-        log(f"decode step as one cooperative launch: {single_us:.1f} us/token (status ok={ok1})")
+        warm(stream, one, 20)
+        ts = timed(Q, stream, one, reps)
+        ok1 = sess.get_state()[1] == ctx - 1 and sess.check_status() == 0
+        log(f"decode step as one cooperative launch: {ts['mean_ms'] * 1e3:.1f} us/token "
+            f"(median {ts['median_ms'] * 1e3:.1f}; status ok={ok1})")
     D.set_step_mode(default_mode)
     sess.free()
     model.free()
-    best = single_us if single_us is not None else dec_us
-    best_gbs = dec_bytes / best / 1e3
-    return {"us": round(best, 2), "tok_per_s": round(1e6 / best, 1), "context": ctx,
+    best = ts if ts is not None else tp
+    best_us = best["mean_ms"] * 1e3
+    best_gbs = dec_bytes / best_us / 1e3
+    return {"us": round(best_us, 2), "median_us": round(best["median_ms"] * 1e3, 2),
+            "tok_per_s": round(1e6 / best_us, 1), "context": ctx,
             "bytes": dec_bytes, "GBps": round(best_gbs, 1), "frac": round(best_gbs / HBM_PEAK_GBS, 4),
-            "launch": "one cooperative launch per step" if single_us is not None else
+            "launch": "one cooperative launch per step" if ts is not None else
                       ("hipGraph of 143 launches" if not args.no_graph else "143 eager launches"),
-            "single_launch_us": None if single_us is None else round(single_us, 2),
-            "per_phase_us": round(dec_us, 2), "per_phase_launches": 3 + 5 * layers,
-            "per_phase_launch": "eager" if args.no_graph else "hipGraph",
+            "single_launch_us": None if ts is None else round(ts["mean_ms"] * 1e3, 2),
+            "per_phase_us": round(dec_us, 2), "per_phase_median_us": round(tp["median_ms"] * 1e3, 2),
+            "per_phase_launches": 3 + 5 * layers,
+            "per_phase_launch": "eager" if args.no_graph else "hipGraph", "steps_timed": reps,
             "token": step_tok, "oracle_token": ref_tok, "parity_ok": bool(step_ok),
             "cpu_oracle": {"us": round(cpu_step_us, 1), "threads": O.num_threads(),
                            "kind": "port",
@@ -236,18 +291,22 @@ def bench_prefill(Q, stream, args) -> dict:
     ref.free()
     log(f"prefill parity: token {tok_b} (decode steps {tok_s}, margin {margin:.4f}), logits rel L2 "
         f"{rel:.2e}")
-    for _ in range(3):
+    t0 = time.perf_counter()
+    while (time.perf_counter() - t0) * 1e3 < MIN_WARM_MS:
         one()
     stream.synchronize()
     reps = max(5, min(50, args.steps // 20))
-    t0 = time.perf_counter()
+    times = []
     for _ in range(reps):
+        t0 = time.perf_counter()
         one()
-    stream.synchronize()
-    ms = (time.perf_counter() - t0) * 1e3 / reps
+        stream.synchronize()
+        times.append((time.perf_counter() - t0) * 1e3)
+    ms = statistics.mean(times)
     gemm, attn = prefill_flops(n)
-    log(f"prefill of {n} tokens: {ms:.3f} ms = {n / ms * 1e3:.0f} tok/s, "
-        f"{(gemm + attn) / ms / 1e9:.1f} TFLOP/s; as decode steps {steps_ms:.1f} ms")
+    log(f"prefill of {n} tokens: {ms:.3f} ms (median {statistics.median(times):.3f}) = "
+        f"{n / ms * 1e3:.0f} tok/s, {(gemm + attn) / ms / 1e9:.1f} TFLOP/s; as decode steps "
+        f"{steps_ms:.1f} ms")
     for spec in args.prefill_tiling or []:
         rows, split = (int(x) for x in spec.split(":"))
         D.set_prefill_tiling(rows, split)
@@ -265,12 +324,77 @@ def bench_prefill(Q, stream, args) -> dict:
     pbuf.free()
     sess.free()
     model.free()
-    return {"tokens": n, "ms": round(ms, 3), "tok_per_s": round(n / ms * 1e3, 1),
+    return {"tokens": n, "ms": round(ms, 3), "median_ms": round(statistics.median(times), 3),
+            "tok_per_s": round(n / ms * 1e3, 1),
             "gemm_flops": gemm, "attention_flops": attn,
             "TFLOPs": round((gemm + attn) / ms / 1e9, 2),
             "decode_steps_ms": round(steps_ms, 2), "speedup_vs_steps": round(steps_ms / ms, 1),
             "logits_rel_l2_vs_steps": rel, "token": tok_b, "steps_token": tok_s,
             "parity_ok": bool(ok)}
+
+
+def bench_generate(Q, stream, args) -> dict:
+    """End-to-end generation as the reference measures it
+    (scripts/benchmark.py:52-81): the wall time of one `run` = a fresh KV
+    cache, prompt ingestion (batched, the reference's @prefill), then up to
+    128 greedy tokens with the EOS check after every 4 (qwen3_full.mlir:
+    2113-2167); tok/s = tokens before EOS / that time.  Prompts: a chat-sized
+    one (the reference's prompts with its chat template are ~10-30 tokens) and
+    512 tokens.  Parity: the same tokens as the prompt followed by single
+    decode steps read back one at a time."""
+    from qwen3_iree_amd import decode as D
+
+    mhost = D.synthetic_weights(seed=SEED, workers=16)
+    model = D.DeviceWeights(mhost)
+    rng = np.random.default_rng(SEED + 13)
+    out = {}
+    for name, n in (("chat_prompt", args.chat_prompt_tokens), ("prompt_512", 512)):
+        prompt = rng.integers(0, D.VOCAB, n).astype(np.int32)
+        toks = D.run(model, prompt, MAX_NEW_TOKENS, EOS_TOKEN, stream)  # warm-up + parity
+        # parity: prompt, then single steps with the token read back each time
+        sess = D.DecodeSession(model, n + MAX_NEW_TOKENS, stream)
+        sess.set_state(0, 0)
+        sess.prefill_batched(prompt)
+        steps = []
+        while len(steps) < len(toks):
+            sess.step(advance=True, logits=False)
+            steps.append(sess.get_state()[0])
+        sess.check_status()
+        sess.free()
+        parity = steps == toks.tolist()
+        times = []
+        reps = max(3, args.generate_reps)
+        t_end = time.perf_counter() + MIN_WARM_MS / 1e3
+        while time.perf_counter() < t_end:
+            D.run(model, prompt, MAX_NEW_TOKENS, EOS_TOKEN, stream)
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            got = D.run(model, prompt, MAX_NEW_TOKENS, EOS_TOKEN, stream)
+            times.append(time.perf_counter() - t0)
+        produced = got.tolist()
+        n_out = produced.index(EOS_TOKEN) if EOS_TOKEN in produced else len(produced)
+        # the token loop alone (qwen3_generate), after the prompt
+        sess = D.DecodeSession(model, n + MAX_NEW_TOKENS, stream)
+        sess.set_state(0, 0)
+        sess.prefill_batched(prompt)
+        t0 = time.perf_counter()
+        loop = sess.generate(MAX_NEW_TOKENS, EOS_TOKEN)
+        loop_s = time.perf_counter() - t0
+        sess.free()
+        dt = statistics.median(times)
+        rec = {"prompt_tokens": n, "max_new_tokens": MAX_NEW_TOKENS, "tokens_out": n_out,
+               "run_ms": round(dt * 1e3, 3), "run_ms_mean": round(statistics.mean(times) * 1e3, 3),
+               "tok_per_s": round(n_out / dt, 1), "runs": reps,
+               "loop_ms_per_token": round(loop_s * 1e3 / max(1, len(loop)), 4),
+               "parity_ok": bool(parity and got.tolist() == toks.tolist())}
+        log(f"generate ({name}: {n}-token prompt + {MAX_NEW_TOKENS} tokens): run {dt * 1e3:.2f} ms "
+            f"-> {rec['tok_per_s']:.0f} tok/s ({n_out} tokens before EOS), token loop "
+            f"{rec['loop_ms_per_token']:.4f} ms/token, parity {rec['parity_ok']}")
+        out[name] = rec
+    model.free()
+    out["reference_published"] = {"tok_per_s": 25.52, "where": "Jetson AGX Orin, "
+                                  "benchmark.json:71-72 (other hardware)"}
+    return out
 
 
 def bench_gguf(Q, tmpdir: Path) -> dict:
@@ -310,17 +434,60 @@ def bench_gguf(Q, tmpdir: Path) -> dict:
             "bit_identical": bool(same)}
 
 
+def cpu_baseline(O, sw, args) -> dict:
+    """The C oracle (reference kernels' f32 order) over whole sweeps of the same
+    inputs: at every host thread for ~cpu_seconds, then at one thread for
+    ~cpu_seconds / 2."""
+    host = {k: v for k, v in sw.host_w.items()}
+
+    def sample(threads: int, budget: float):
+        O.set_num_threads(threads)
+        sweeps = 0
+        t0 = time.perf_counter()
+        while True:
+            for layer, d in sw.order:
+                O.q8_gemv(host[d.kind][layer], d.n, d.k, sw.host_x[(layer, d.kind)])
+            sweeps += 1
+            if time.perf_counter() - t0 >= budget:
+                break
+        return sweeps, time.perf_counter() - t0
+
+    # every thread OpenMP is allowed (OMP_NUM_THREADS: the host's share of
+    # cores for this GPU), then one
+    all_threads = O.num_threads()
+    n_all, s_all = sample(all_threads, args.cpu_seconds)
+    threads_used = O.num_threads()
+    n_one, s_one = sample(1, args.cpu_seconds / 2)
+    O.set_num_threads(all_threads)
+    gbs_all = sw.bytes_per_step * n_all / s_all / 1e9
+    gbs_one = sw.bytes_per_step * n_one / s_one / 1e9
+    log(f"cpu oracle: {gbs_all:.2f} GB/s over {n_all} sweeps ({threads_used} threads), "
+        f"{gbs_one:.2f} GB/s over {n_one} sweeps (1 thread); {cpu_model()}")
+    return {"value": round(gbs_all, 3), "unit": "GB/s", "cores": threads_used, "kind": "port",
+            "sample": f"{n_all} full 28-layer sweeps (140 Q8_0 GEMVs each, the same inputs) with the "
+                      f"C oracle in the reference kernels' f32 order, OpenMP {threads_used} threads, "
+                      f"{s_all:.1f}s; then {n_one} sweeps on 1 thread, {s_one:.1f}s",
+            "ms_per_step": round(1e3 * s_all / n_all, 3),
+            "single_thread": {"value": round(gbs_one, 3), "unit": "GB/s",
+                              "ms_per_step": round(1e3 * s_one / n_one, 3), "cores": 1},
+            "cpu_model": cpu_model(), "host_logical_cpus": os.cpu_count()}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=1000)
     ap.add_argument("--warmup", type=int, default=1000,
-                    help="untimed steps before timing (the GPU clock ramps up over the first "
-                         "~100 ms of sustained work)")
+                    help="untimed steps before timing; at least 200 ms of the timed kernel runs "
+                         "whatever this is (the GPU clock ramps over the first ~100 ms)")
     ap.add_argument("--context", type=int, default=1024,
                     help="positions attended by the timed decode step")
     ap.add_argument("--decode-only", action="store_true",
                     help="run only the full decode step and print its JSON line")
+    ap.add_argument("--sweep-only", action="store_true",
+                    help="run only the batched sweep (timed, parity-checked) and print its line")
+    ap.add_argument("--generate-only", action="store_true",
+                    help="run only end-to-end generation and print its JSON line")
     ap.add_argument("--step-mode", type=int, choices=(0, 1), default=None,
                     help="decode step mode for the whole run (0: per-phase launches, 1: one "
                          "cooperative launch; default: the library's)")
@@ -331,6 +498,9 @@ def main() -> int:
     ap.add_argument("--prefill-tiling", nargs="*", metavar="ROWS:SPLIT",
                     help="also time the prompt ingestion with these work divisions "
                          "(qwen3_set_prefill_tiling; 0 = by shape)")
+    ap.add_argument("--chat-prompt-tokens", type=int, default=24,
+                    help="prompt length of the chat-sized generation measurement")
+    ap.add_argument("--generate-reps", type=int, default=5, help="timed runs per generation case")
     ap.add_argument("--gguf-ingest", metavar="DIR", default=None,
                     help="only measure GGUF ingestion: write the synthetic model as a Q8_0 GGUF "
                          "under DIR, read it back into the device layout (cold, then warm page "
@@ -354,7 +524,7 @@ def main() -> int:
 
     load_package()
     from qwen3_iree_amd import q8gemv as Q
-    from qwen3_iree_amd import weights as Wt
+    from qwen3_iree_amd import sweep as S
 
     Q.init()
     info = Q.device_info()
@@ -362,6 +532,13 @@ def main() -> int:
     sys.path.insert(0, str(REPO / "oracle"))
     import oracle as O  # the checker; also the CPU baseline below
 
+    try:
+        return run(Q, S, O, info, args)
+    finally:
+        Q.teardown()
+
+
+def run(Q, S, O, info, args) -> int:
     if args.step_mode is not None:
         from qwen3_iree_amd import decode as D
 
@@ -375,34 +552,25 @@ def main() -> int:
     if args.prefill_only:
         print(json.dumps({"prefill": bench_prefill(Q, Q.Stream(), args)}), flush=True)
         return 0
+    if args.generate_only:
+        print(json.dumps({"generate": bench_generate(Q, Q.Stream(), args)}), flush=True)
+        return 0
 
     # ---------------------------------------------------------------- inputs
     t0 = time.time()
-    kinds = Q.Q8_KINDS  # sweep order per layer: q, kv, o, gate_up, dn
-    layers = Q.NUM_LAYERS
-    stacks = {}
-    for d in kinds:
-        host = Wt.synthetic_q8_stack(d.n, d.k, layers, seed=SEED, tensor=d.kind, workers=16)
-        stacks[d.kind] = (host, Q.DeviceBuffer.from_array(host))
-    xs, ys = {}, {}
-    for layer in range(layers):
-        for d in kinds:
-            x = Wt.synthetic_x(d.k, SEED, index=layer * 8 + d.kind)
-            xs[(layer, d.kind)] = (x, Q.DeviceBuffer.from_array(x))
-            ys[(layer, d.kind)] = Q.DeviceBuffer(2 * d.n)
-    sweep_bytes = sum(algorithmic_bytes(d) for d in kinds) * layers
-    weight_bytes = sum(d.bytes_per_layer for d in kinds) * layers
-    log(f"sweep inputs ready in {time.time() - t0:.1f}s: {weight_bytes} weight bytes, "
+    sw = S.build(SEED)
+    layers = S.LAYERS
+    sweep_bytes = sw.bytes_per_step
+    log(f"sweep inputs ready in {time.time() - t0:.1f}s: {sw.weight_bytes} weight bytes, "
         f"{sweep_bytes} algorithmic bytes per step")
-
     stream = Q.Stream()
-    sweep_order = [(layer, d) for layer in range(layers) for d in kinds]
 
     copy_cal = None
     if args.copy_calibration > 0:
         nbytes = args.copy_calibration << 20
         src, dst = Q.DeviceBuffer(nbytes), Q.DeviceBuffer(nbytes)
-        copy_ms = timed_ms(Q, stream, lambda: Q.stream_copy(dst, src, nbytes, stream), 5)
+        tc = timed(Q, stream, lambda: Q.stream_copy(dst, src, nbytes, stream), 5, 1)
+        copy_ms = tc["mean_ms"]
         copy_cal = {"bytes_read": nbytes, "bytes_written": nbytes, "us": round(copy_ms * 1e3, 2),
                     "GBps_read_plus_write": round(2 * nbytes / (copy_ms * 1e-3) / 1e9, 1)}
         log(f"copy calibration: {nbytes} B read + written in {copy_ms * 1e3:.1f} us")
@@ -410,128 +578,35 @@ def main() -> int:
         dst.free()
 
     # ------------------------------------------- headline: batched sweep
-    batch = Q.Q8Batch([Q.desc_for_kind(d.kind, stacks[d.kind][1], layer, xs[(layer, d.kind)][1],
-                                       ys[(layer, d.kind)]) for layer, d in sweep_order])
-    for _ in range(args.warmup):
-        batch.launch(stream)
+    batch = sw.batch()
+    launch = lambda: batch.launch(stream)  # noqa: E731
+    warm_calls = warm(stream, launch, args.warmup)
     t_wall = time.perf_counter()
-    ms_per_step = timed_ms(Q, stream, lambda: batch.launch(stream), args.steps)
+    th = timed(Q, stream, launch, args.steps)
     wall_s = time.perf_counter() - t_wall
+    ms_per_step = th["mean_ms"]
     value = sweep_bytes / (ms_per_step * 1e-3) / 1e9
-    log(f"batched sweep: {ms_per_step * 1e3:.2f} us/step, {value:.1f} GB/s "
+    log(f"batched sweep: {ms_per_step * 1e3:.2f} us/step (median of {th['blocks']} blocks "
+        f"{th['median_ms'] * 1e3:.2f}, after {warm_calls} warm-up launches), {value:.1f} GB/s "
         f"({100 * value / HBM_PEAK_GBS:.1f}% of peak); host wall {wall_s:.3f}s")
 
     # parity of every sweep output (the last timed launch wrote them)
     fails = floor = 0
-    for layer, d in sweep_order:
-        raw = stacks[d.kind][0][layer]
-        x = xs[(layer, d.kind)][0]
-        rep = O.gemv_tolerance_report(ys[(layer, d.kind)].download(np.float16),
+    for layer, d in sw.order:
+        raw = sw.host_w[d.kind][layer]
+        x = sw.host_x[(layer, d.kind)]
+        rep = O.gemv_tolerance_report(sw.dev_y[(layer, d.kind)].download(np.float16),
                                       O.q8_gemv(raw, d.n, d.k, x), O.q8_gemv_f64(raw, d.n, d.k, x)[1])
         fails += rep["fail"]
         floor += rep["on_floor"]
-    log(f"parity: {fails} failing outputs of {sum(d.n for _, d in sweep_order)} ({floor} on the noise floor)")
+    log(f"parity: {fails} failing outputs of {sw.outputs} ({floor} on the noise floor)")
 
-    # ------------------------------- the same sweep as 140 dispatches
-    def record_sweep():
-        for layer, d in sweep_order:
-            Q.q8gemv(d.kind, stacks[d.kind][1], layer, xs[(layer, d.kind)][1], ys[(layer, d.kind)], stream)
-
-    if args.no_graph:
-        chain_fn = record_sweep
-    else:
-        graph = Q.Graph(stream, record_sweep)
-        chain_fn = lambda: graph.launch(stream)  # noqa: E731
-    for _ in range(3):
-        chain_fn()
-    chain_reps = max(10, args.steps // 4)
-    chain_ms = timed_ms(Q, stream, chain_fn, chain_reps)
-    chain_gbs = sweep_bytes / (chain_ms * 1e-3) / 1e9
-    log(f"per-dispatch sweep (140 launches{'' if args.no_graph else ', hipGraph'}): "
-        f"{chain_ms * 1e3:.1f} us, {chain_gbs:.1f} GB/s")
-
-    # ------------------------------------------------------------- vocab
-    t0 = time.time()
-    Wv = Wt.synthetic_f16_matrix(Q.VOCAB_ROWS, Q.HIDDEN, seed=SEED, tensor=24, workers=16)
-    xv = Wt.synthetic_x(Q.HIDDEN, SEED, index=9999)
-    wv_dev = Q.DeviceBuffer.from_array(Wv)
-    xv_dev = Q.DeviceBuffer.from_array(xv)
-    logits_dev = Q.DeviceBuffer(2 * Q.VOCAB_ROWS)
-    tok_dev = Q.DeviceBuffer(16)
-    ws = Q.DeviceBuffer(Q.vocab_workspace_bytes())
-    Q.vocab_workspace_reset(ws, stream)
-    log(f"vocab inputs ready in {time.time() - t0:.1f}s")
-    vocab_bytes = Q.VOCAB.bytes_per_layer + 2 * Q.HIDDEN + 2 * Q.VOCAB_ROWS + 4
-    vocab_fn = lambda: Q.vocab_gemv_argmax(wv_dev, xv_dev, logits_dev, tok_dev, ws, stream)  # noqa: E731
-    for _ in range(5):
-        vocab_fn()
-    v_ms = timed_ms(Q, stream, vocab_fn, 50)
-    v_gbs = vocab_bytes / (v_ms * 1e-3) / 1e9
-    token = int(tok_dev.download(np.int32, 1)[0])
-    logits = logits_dev.download(np.float16, Q.VOCAB_ROWS)
-    rep_v = O.gemv_tolerance_report(logits, O.f16_gemv(Wv, xv), O.f16_gemv_f64(Wv, xv)[1])
-    own = O.argmax_tiled(logits)
-    log(f"vocab GEMV + argmax: {v_ms * 1e3:.2f} us/op, {v_gbs:.0f} GB/s, token {token} "
-        f"(argmax of own logits {own}, {rep_v['fail']} failing logits)")
-
-    # ---------------------------------------- GEMV share of a decode step
-    # Separate K and V weights (the attn_kv stack above serves as K).
-    v_host = Wt.synthetic_q8_stack(1024, 1024, layers, seed=SEED, tensor=7, workers=16)
-    v_dev = Q.DeviceBuffer.from_array(v_host)
-    step_y = {name: Q.DeviceBuffer(2 * 6144) for name in ("q", "k", "v", "o", "gu", "dn")}
-
-    def record_decode_gemvs():
-        for layer in range(layers):
-            Q.q8gemv_qkv(stacks[Q.ATTN_Q.kind][1], stacks[Q.ATTN_KV.kind][1], v_dev, layer,
-                         xs[(layer, Q.ATTN_Q.kind)][1], step_y["q"], step_y["k"], step_y["v"], stream)
-            for d, yname in ((Q.ATTN_O, "o"), (Q.GATE_UP, "gu"), (Q.FFN_DN, "dn")):
-                Q.q8gemv(d.kind, stacks[d.kind][1], layer, xs[(layer, d.kind)][1], step_y[yname], stream)
-        vocab_fn()
-
-    if args.no_graph:
-        dstep_fn = record_decode_gemvs
-    else:
-        dgraph = Q.Graph(stream, record_decode_gemvs)
-        dstep_fn = lambda: dgraph.launch(stream)  # noqa: E731
-    for _ in range(3):
-        dstep_fn()
-    decode_gemv_us = timed_ms(Q, stream, dstep_fn, 30) * 1e3
-    decode_bytes = (sum(algorithmic_bytes(d) for d in Q.LAYER_ORDER) * layers + vocab_bytes)
-    log(f"decode-step GEMVs (28 x [q8gemv_qkv, o, gate_up, down] + vocab, 114 dispatches): "
-        f"{decode_gemv_us:.1f} us, {decode_bytes / decode_gemv_us / 1e3:.0f} GB/s")
-
-    # ------------------------------------------- full decode step (C5)
-    dec = bench_decode(Q, O, stream, args)
-    pre = bench_prefill(Q, stream, args)
-    step_ok = dec["parity_ok"]
-
-    parity_ok = fails == 0 and rep_v["fail"] == 0 and token == own and step_ok
     batch_grid = min(batch.total_units, 12 * info["compute_units"]) * 64
     traffic = profiled_traffic("q8gemv_batch_k", batch_grid)
-
-    # ------------------------------------------------------ CPU baseline
-    cpu = None
-    if not args.no_cpu:
-        threads = O.num_threads()
-        host = {d.kind: stacks[d.kind][0] for d in kinds}
-        hx = {key: v[0] for key, v in xs.items()}
-        sweeps = 0
-        t0 = time.perf_counter()
-        while True:
-            for layer, d in sweep_order:
-                O.q8_gemv(host[d.kind][layer], d.n, d.k, hx[(layer, d.kind)])
-            sweeps += 1
-            if time.perf_counter() - t0 >= args.cpu_seconds:
-                break
-        cpu_s = time.perf_counter() - t0
-        cpu_gbs = sweep_bytes * sweeps / cpu_s / 1e9
-        cpu = {"value": round(cpu_gbs, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-               "sample": f"{sweeps} full 28-layer sweeps (140 Q8_0 GEMVs each, the same inputs) with "
-                         f"the C oracle in the reference kernels' f32 order, OpenMP {threads} threads, "
-                         f"{cpu_s:.1f}s", "ms_per_step": round(1e3 * cpu_s / sweeps, 3)}
-        log(f"cpu oracle: {cpu_gbs:.2f} GB/s over {sweeps} sweeps ({threads} threads)")
-
-    out = {
+    if traffic["stale"]:
+        log("profiles/traffic.json was taken on other device sources (digest "
+            f"{traffic['source_digest']}): its traffic figure does not describe this build")
+    headline = {
         "metric": METRIC,
         "value": round(value, 2),
         "unit": "GB/s",
@@ -548,13 +623,15 @@ def main() -> int:
             "workload": "28-layer stacked cold-cache Q8_0 GEMV sweep: per layer attn_q, attn_kv, "
                         "attn_o, gate_up, ffn_dn (140 GEMVs), one batched launch per step",
             "layers": layers,
-            "gemvs_per_step": len(sweep_order),
-            "weight_bytes": weight_bytes,
+            "gemvs_per_step": len(sw.order),
+            "weight_bytes": sw.weight_bytes,
             "algorithmic_bytes_per_step": sweep_bytes,
             "device": info["name"],
         },
         "pct_of_peak": round(100 * value / HBM_PEAK_GBS, 2),
         "us_per_step": round(ms_per_step * 1e3, 2),
+        "median_us_per_step": round(th["median_ms"] * 1e3, 2),
+        "warmup_launches": warm_calls,
         "roofline": {
             "bound": "hbm",
             "kernel": "q8gemv_batch_k (28-layer sweep, 140 GEMVs)",
@@ -563,26 +640,127 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(value / HBM_PEAK_GBS, 4),
             "avg_us": round(ms_per_step * 1e3, 2),
+            "median_us": round(th["median_ms"] * 1e3, 2),
             "bytes_per_launch": sweep_bytes,
-            "traffic": traffic,
+            "traffic": traffic["bytes"],
             "traffic_source": "profiles/traffic.json: rocprofv3 FETCH_SIZE + WRITE_SIZE per dispatch, "
                               "each scaled by its reading for the plain copy kernel of known size",
+            "traffic_source_digest": traffic["source_digest"],
+            "traffic_stale": traffic["stale"],
+            "profiled_mean_us": traffic.get("profiled_mean_us"),
         },
-        "per_dispatch_sweep": {"us": round(chain_ms * 1e3, 1), "GBps": round(chain_gbs, 1),
+        "parity_ok": fails == 0,
+        "copy_calibration": copy_cal,
+    }
+    batch.free()
+    if args.sweep_only:
+        print(json.dumps(headline), flush=True)
+        sw.free()
+        return 0
+
+    # ------------------------------- the same sweep as 140 dispatches
+    if args.no_graph:
+        chain_fn = lambda: sw.record_dispatches(stream)  # noqa: E731
+    else:
+        graph = Q.Graph(stream, lambda: sw.record_dispatches(stream))
+        chain_fn = lambda: graph.launch(stream)  # noqa: E731
+    warm(stream, chain_fn, 3)
+    tc = timed(Q, stream, chain_fn, max(10, args.steps // 4))
+    chain_ms = tc["mean_ms"]
+    chain_gbs = sweep_bytes / (chain_ms * 1e-3) / 1e9
+    log(f"per-dispatch sweep (140 launches{'' if args.no_graph else ', hipGraph'}): "
+        f"{chain_ms * 1e3:.1f} us (median {tc['median_ms'] * 1e3:.1f}), {chain_gbs:.1f} GB/s")
+
+    # ------------------------------------------------------------- vocab
+    from qwen3_iree_amd import weights as Wt
+
+    t0 = time.time()
+    Wv = Wt.synthetic_f16_matrix(Q.VOCAB_ROWS, Q.HIDDEN, seed=SEED, tensor=24, workers=16)
+    xv = Wt.synthetic_x(Q.HIDDEN, SEED, index=9999)
+    wv_dev = Q.DeviceBuffer.from_array(Wv)
+    xv_dev = Q.DeviceBuffer.from_array(xv)
+    logits_dev = Q.DeviceBuffer(2 * Q.VOCAB_ROWS)
+    tok_dev = Q.DeviceBuffer(16)
+    ws = Q.DeviceBuffer(Q.vocab_workspace_bytes())
+    Q.vocab_workspace_reset(ws, stream)
+    log(f"vocab inputs ready in {time.time() - t0:.1f}s")
+    vocab_bytes = Q.VOCAB.bytes_per_layer + 2 * Q.HIDDEN + 2 * Q.VOCAB_ROWS + 4
+    vocab_fn = lambda: Q.vocab_gemv_argmax(wv_dev, xv_dev, logits_dev, tok_dev, ws, stream)  # noqa: E731
+    warm(stream, vocab_fn, 5)
+    tv = timed(Q, stream, vocab_fn, 200)
+    v_ms = tv["mean_ms"]
+    v_gbs = vocab_bytes / (v_ms * 1e-3) / 1e9
+    token = int(tok_dev.download(np.int32, 1)[0])
+    logits = logits_dev.download(np.float16, Q.VOCAB_ROWS)
+    rep_v = O.gemv_tolerance_report(logits, O.f16_gemv(Wv, xv), O.f16_gemv_f64(Wv, xv)[1])
+    own = O.argmax_tiled(logits)
+    log(f"vocab GEMV + argmax: {v_ms * 1e3:.2f} us/op (median {tv['median_ms'] * 1e3:.2f}), "
+        f"{v_gbs:.0f} GB/s, token {token} (argmax of own logits {own}, {rep_v['fail']} failing "
+        f"logits)")
+
+    # ---------------------------------------- GEMV share of a decode step
+    # Separate K and V weights (the attn_kv stack above serves as K).
+    v_host = Wt.synthetic_q8_stack(1024, 1024, layers, seed=SEED, tensor=7, workers=16)
+    v_dev = Q.DeviceBuffer.from_array(v_host)
+    step_y = {name: Q.DeviceBuffer(2 * 6144) for name in ("q", "k", "v", "o", "gu", "dn")}
+
+    def record_decode_gemvs():
+        for layer in range(layers):
+            Q.q8gemv_qkv(sw.dev_w[Q.ATTN_Q.kind], sw.dev_w[Q.ATTN_KV.kind], v_dev, layer,
+                         sw.dev_x[(layer, Q.ATTN_Q.kind)], step_y["q"], step_y["k"], step_y["v"],
+                         stream)
+            for d, yname in ((Q.ATTN_O, "o"), (Q.GATE_UP, "gu"), (Q.FFN_DN, "dn")):
+                Q.q8gemv(d.kind, sw.dev_w[d.kind], layer, sw.dev_x[(layer, d.kind)], step_y[yname],
+                         stream)
+        vocab_fn()
+
+    if args.no_graph:
+        dstep_fn = record_decode_gemvs
+    else:
+        dgraph = Q.Graph(stream, record_decode_gemvs)
+        dstep_fn = lambda: dgraph.launch(stream)  # noqa: E731
+    warm(stream, dstep_fn, 3)
+    td = timed(Q, stream, dstep_fn, 50)
+    decode_gemv_us = td["mean_ms"] * 1e3
+    decode_bytes = (sum(S.algorithmic_bytes(d) for d in Q.LAYER_ORDER) * layers + vocab_bytes)
+    log(f"decode-step GEMVs (28 x [q8gemv_qkv, o, gate_up, down] + vocab, 114 dispatches): "
+        f"{decode_gemv_us:.1f} us, {decode_bytes / decode_gemv_us / 1e3:.0f} GB/s")
+    for b in (wv_dev, xv_dev, logits_dev, tok_dev, ws, v_dev, *step_y.values()):
+        b.free()
+
+    # ------------------------------------------- full decode step (C5)
+    dec = bench_decode(Q, O, stream, args)
+    pre = bench_prefill(Q, stream, args)
+    gen = bench_generate(Q, stream, args)
+    gen_ok = all(v.get("parity_ok", True) for v in gen.values() if isinstance(v, dict))
+
+    parity_ok = (fails == 0 and rep_v["fail"] == 0 and token == own and dec["parity_ok"]
+                 and pre["parity_ok"] and gen_ok)
+
+    # ------------------------------------------------------ CPU baseline
+    cpu = None if args.no_cpu else cpu_baseline(O, sw, args)
+    sw.free()
+
+    out = dict(headline)
+    out.update({
+        "per_dispatch_sweep": {"us": round(chain_ms * 1e3, 1),
+                               "median_us": round(tc["median_ms"] * 1e3, 1),
+                               "GBps": round(chain_gbs, 1),
                                "frac": round(chain_gbs / HBM_PEAK_GBS, 4), "dispatches": 140,
                                "launch": "eager" if args.no_graph else "hipGraph"},
-        "vocab": {"us": round(v_ms * 1e3, 2), "GBps": round(v_gbs, 1),
-                  "frac": round(v_gbs / HBM_PEAK_GBS, 4), "bytes": vocab_bytes, "token": token},
+        "vocab": {"us": round(v_ms * 1e3, 2), "median_us": round(tv["median_ms"] * 1e3, 2),
+                  "GBps": round(v_gbs, 1), "frac": round(v_gbs / HBM_PEAK_GBS, 4),
+                  "bytes": vocab_bytes, "token": token},
         "decode_step_gemv": {"us": round(decode_gemv_us, 2), "bytes": decode_bytes,
                              "GBps": round(decode_bytes / decode_gemv_us / 1e3, 1),
                              "dispatches": 4 * layers + 2,
                              "launch": "eager" if args.no_graph else "hipGraph"},
         "decode_step": dec,
         "prefill": pre,
+        "generate": gen,
         "parity_ok": bool(parity_ok),
-        "copy_calibration": copy_cal,
         "cpu_baseline": cpu,
-    }
+    })
     print(json.dumps(out), flush=True)
     return 0
 

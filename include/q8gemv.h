@@ -46,6 +46,7 @@ extern "C" {
 #define Q8_ERR_CODE_OBJECT     7  /* code object missing, unreadable or lacks a kernel */
 #define Q8_ERR_HIP             8  /* a HIP runtime call failed (message has details) */
 #define Q8_ERR_BAD_ARGUMENT    9  /* other invalid argument (tuning values, sizes) */
+#define Q8_ERR_STEP_ABORTED   10  /* a single-launch decode step gave up waiting (qwen3_decode.h) */
 
 /* ---- model constants (model/qwen3_full.mlir:29-64; tools/create_q8_irpa.py:16-25) ---- */
 #define Q8_NUM_LAYERS   28
@@ -198,6 +199,15 @@ int f16_gemv_argmax_rows(const void* w_f16, int64_t n_rows, const void* x_f16,
  * c1 | c2 << 32; dispatch 24: c0 = output byte offset, logits only). */
 int q8gemv_hal_dispatch(int ordinal, const void* binding0, const void* binding1, void* binding2,
                         const uint32_t* push_constants, int n_constants, void* stream);
+/* The same with the stub's launch shape: `workgroups` x `workgroup_size`
+ * threads (0 = this build's stub shape: 64 threads and N/4 workgroups, 256
+ * threads and 1024 workgroups for ordinal 24).  The kernels compute every
+ * output under any shape with 64, 128, 192 or 256 threads per workgroup,
+ * including the reference stubs' own (256 threads; 256, 128, 128, 768, 128 and
+ * 18992 workgroups, kernels/cuda/dispatch_{3,4,12,18,20,24}.mlir:5-9). */
+int q8gemv_hal_dispatch_grid(int ordinal, const void* binding0, const void* binding1,
+                             void* binding2, const uint32_t* push_constants, int n_constants,
+                             uint32_t workgroups, uint32_t workgroup_size, void* stream);
 
 /* ---- launch-shape tuning (no reference counterpart) ---- */
 

@@ -58,8 +58,15 @@ int qwen3_scratch_reset(void* scratch, void* stream);
 /* Byte offset in the scratch of the u32 status word: bit 0 = a step asked to
  * advance past the last cache slot (the position then stays); bit 1 = a
  * single-launch step gave up waiting for a hand-off (its results are not
- * valid; never expected on a working device). */
+ * valid; never expected on a working device).  Bit 1 stays set until
+ * qwen3_scratch_reset; the steps after an aborted one run normally (each
+ * launch takes a fresh sequence number, so nothing the aborted step left
+ * behind is mistaken for its data), but qwen3_generate and
+ * qwen3_prefill_batched refuse to start on a scratch that carries it. */
 size_t qwen3_scratch_status_offset(void);
+/* Synchronizes `stream`, then *status = the status word; returns
+ * Q8_ERR_STEP_ABORTED if bit 1 is set, else Q8_OK. */
+int qwen3_check_status(const void* scratch, uint32_t* status, void* stream);
 
 /* One token: h = token_embd[*token]; 28 layers at position *pos (attention
  * over slots 0..*pos of each layer, the new k/v written to slot *pos); final
@@ -82,6 +89,12 @@ int qwen3_decode_step(const qwen3_weights* w, void* k_cache, void* v_cache, int6
  * dispatches itself). */
 int qwen3_set_step_mode(int mode);
 int qwen3_get_step_mode(int* mode);
+/* Every wait of the single-launch step is bounded: after `polls` poll rounds
+ * (0 = the default, 2^20, about a second) the workgroup gives up, sets status
+ * bit 1 and makes every other waiter of the step give up too, so the launch
+ * always completes.  A small limit forces that path (tests of the error
+ * reporting); no counterpart in the reference. */
+int qwen3_set_step_spin_limit(uint32_t polls);
 
 /* The same step in parts, for tests and for callers that interleave work:
  * embed: h_out = token_embd[*token];
@@ -99,7 +112,9 @@ int qwen3_decode_head(const qwen3_weights* w, const void* h, void* logits, int32
  * (qwen3_full.mlir:1541-1561): for i in [0, n_prompt) one step at position
  * *pos with input token prompt[i] (device int32 [n_prompt]); logits are only
  * formed after the last prompt token, whose argmax goes to *token.  *pos ends
- * n_prompt slots further (not past max_seq - 1; see the status word). */
+ * n_prompt slots further (not past max_seq - 1; see the status word).  Only
+ * enqueues: check the status word (qwen3_check_status) before trusting the
+ * token. */
 int qwen3_prefill(const qwen3_weights* w, void* k_cache, void* v_cache, int64_t max_seq,
                   const int32_t* prompt, int32_t n_prompt, int32_t* token, int32_t* pos,
                   void* scratch, void* stream);
@@ -171,7 +186,9 @@ int qwen3_set_prefill_tiling(int gemm_rows, int attn_split_blocks);
  * the last token and stops if it equals eos_id, so up to 3 tokens past an EOS
  * are produced, as in the reference.  The input token itself is not output.
  * *n_generated (host) = tokens produced.  Blocks until the loop ends; fails
- * with Q8_ERR_BAD_SHAPE unless *pos + max_new <= max_seq. */
+ * with Q8_ERR_BAD_SHAPE unless *pos + max_new <= max_seq, and with
+ * Q8_ERR_STEP_ABORTED if the scratch carries status bit 1 before the loop or
+ * after a batch (then *n_generated counts only the batches before). */
 int qwen3_generate(const qwen3_weights* w, void* k_cache, void* v_cache, int64_t max_seq,
                    int32_t* token, int32_t* pos, int32_t max_new, int32_t eos_id,
                    int32_t* out_tokens, int32_t* n_generated, void* scratch, void* stream);

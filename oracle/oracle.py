@@ -55,6 +55,8 @@ def lib() -> ctypes.CDLL:
         L.oracle_argmax_tiled.argtypes = [_P, _I64, _I64]
         L.oracle_argmax_tiled.restype = ctypes.c_int64
         L.oracle_num_threads.restype = ctypes.c_int
+        L.oracle_set_num_threads.argtypes = [ctypes.c_int]
+        L.oracle_set_num_threads.restype = None
         # decode_oracle.c
         L.oracle_rmsnorm.argtypes = [_P, _P, ctypes.c_int, ctypes.c_float, _P]
         L.oracle_head_rmsnorm.argtypes = [_P, ctypes.c_int, _P, ctypes.c_float, _P]
@@ -166,6 +168,11 @@ def argmax_tiled(v: np.ndarray, tile: int = 256) -> int:
 
 def num_threads() -> int:
     return int(lib().oracle_num_threads())
+
+
+def set_num_threads(n: int) -> None:
+    """OpenMP threads of the oracle's following calls."""
+    lib().oracle_set_num_threads(int(n))
 
 
 # ---------------------------------------------------------- decode step ----

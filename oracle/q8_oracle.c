@@ -268,6 +268,16 @@ int64_t oracle_argmax_tiled(const uint16_t* v, int64_t n, int64_t tile) {
   return best_i;
 }
 
+/* OpenMP threads of the following calls (n >= 1); the CPU baseline times the
+ * oracle at 1 thread and at all host threads. */
+void oracle_set_num_threads(int n) {
+#ifdef _OPENMP
+  if (n >= 1) omp_set_num_threads(n);
+#else
+  (void)n;
+#endif
+}
+
 int oracle_num_threads(void) {
 #ifdef _OPENMP
   return omp_get_max_threads();

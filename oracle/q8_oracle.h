@@ -65,6 +65,7 @@ int64_t  oracle_argmax_tiled(const uint16_t* v, int64_t n, int64_t tile);
 
 /* Number of OpenMP threads the oracle uses (1 when built without OpenMP). */
 int      oracle_num_threads(void);
+void     oracle_set_num_threads(int n);
 
 #ifdef __cplusplus
 }

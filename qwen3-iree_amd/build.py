@@ -82,6 +82,19 @@ def build_shim() -> Path:
     return SHIM
 
 
+def source_digest() -> str:
+    """sha256 (16 hex digits) over the device sources (csrc/*.hip, csrc/*.h):
+    the build a profile's counter figures belong to.  Computed from the files,
+    so it can be checked where the tree has no git history."""
+    import hashlib
+
+    h = hashlib.sha256()
+    for f in sorted(list(CSRC.glob("*.hip")) + list(CSRC.glob("*.h"))):
+        h.update(f.name.encode())
+        h.update(f.read_bytes())
+    return h.hexdigest()[:16]
+
+
 def build_all() -> tuple[Path, Path, Path, Path]:
     return build_code_object(), build_decode_object(), build_prefill_object(), build_shim()
 

@@ -324,7 +324,6 @@ constexpr int kWArg = 2 * kWParity;                        // 2 per workgroup
 constexpr int kWTotal = kWArg + 2 * kStepWgs;
 // phases in a tag
 constexpr int kPhQKV = 0, kPhPart = 1, kPhAtt = 2, kPhRes = 3, kPhAct = 4, kPhH = 5, kPhArg = 6;
-constexpr uint32_t kSpinLimit = 1u << 20;
 
 struct StepParams {
   const uint16_t* token_embd;
@@ -355,7 +354,7 @@ struct StepParams {
   int max_seq;
   int advance;
   int head;                 // 0: no vocab / argmax (a prompt step); pos still advances
-  int pad;
+  uint32_t spin_limit;      // poll rounds after which a wait gives up (2^20 by default)
 };
 
 __device__ __forceinline__ uint32_t step_tag(uint32_t seq, int layer, int phase) {
@@ -370,10 +369,24 @@ __device__ __forceinline__ uint64_t get_word(const uint64_t* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// *p = v unless *p already holds v or a newer sequence number (compared
+// modulo 2^32).  A workgroup that started late may have read the sequence
+// word after an abort advanced it and so run with seq + 1; the words then end
+// at the newest number any workgroup of the aborted launch used.
+__device__ __forceinline__ void advance_seq_word(uint32_t* p, uint32_t v) {
+  uint32_t cur = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  while ((int32_t)(v - cur) > 0 &&
+         !__hip_atomic_compare_exchange_strong(p, &cur, v, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                               __HIP_MEMORY_SCOPE_AGENT)) {
+  }
+}
+
 struct Waiter {
   uint32_t* abort_word;
   uint32_t* status;
+  uint32_t* seq_word;  // the step sequence number in the scratch
   uint32_t seq;
+  uint32_t spin_limit;
   int* s_abort;  // LDS flag of the workgroup
 
   static constexpr int kMax = 9;  // words per thread: n <= 2304
@@ -412,13 +425,18 @@ struct Waiter {
       if (!pending) break;
       ++spins;
       if ((spins & 31u) == 0u &&
-          __hip_atomic_load(abort_word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == seq) {
+          (int32_t)(__hip_atomic_load(abort_word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) -
+                    seq) >= 0) {  // this step (or a newer one) was aborted
         ok = false;
         break;
       }
-      if (spins > kSpinLimit) {
+      if (spins > spin_limit) {
+        // Give up: report, make every other waiter of this step give up, and
+        // mark this sequence number as used, so the next launch runs with a
+        // newer one that matches neither this step's tags nor its abort word.
         __hip_atomic_fetch_or(status, 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(abort_word, seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        advance_seq_word(abort_word, seq);
+        advance_seq_word(seq_word, seq);
         ok = false;
         break;
       }
@@ -502,7 +520,7 @@ extern "C" __global__ __launch_bounds__(256) void dec_step(StepParams P) {
   int tok = *P.token_in;
   tok = (tok < 0 || tok >= kVocab) ? 0 : tok;
   const uint16_t* emb = P.token_embd + (size_t)tok * kHidden;
-  const Waiter W{P.abort_word, P.status, seq, &s_abort};
+  const Waiter W{P.abort_word, P.status, P.seq, seq, P.spin_limit, &s_abort};
   float rope_cs[2], rope_sn[2];  // the position's RoPE angles, for every layer
   // Attention workgroups keep the first 32 cache rows of their split for the
   // next layer in LDS: requested (global_load_lds) as soon as the current

@@ -500,11 +500,14 @@ __device__ __forceinline__ void vocab_body_xp(const uint16_t* __restrict__ W, XL
   const int wave = threadIdx.x >> 6;
   const int grp = lane >> 4;
   const int li = lane & 15;
-  const int64_t gw = (int64_t)blockIdx.x * 4 + wave;
-  const int64_t tw = (int64_t)gridDim.x * 4;
+  // full waves of the grid (a partial last wave of an odd-sized workgroup
+  // takes no rows)
+  const int64_t wpb = blockDim.x >> 6;
+  const int64_t gw = (int64_t)blockIdx.x * wpb + wave;
+  const int64_t tw = (int64_t)gridDim.x * wpb;
   const int64_t nbatch = ((int64_t)n_rows + 3) / 4;
-  const int b_begin = (int)(gw * nbatch / tw);
-  const int b_end = (int)((gw + 1) * nbatch / tw);
+  const int b_begin = wave < wpb ? (int)(gw * nbatch / tw) : 0;
+  const int b_end = wave < wpb ? (int)((gw + 1) * nbatch / tw) : 0;
 
   const u32x4* Wv = reinterpret_cast<const u32x4*>(W);
   u32x4 xr[8];  // this lane's x columns, formed by xload below

@@ -119,18 +119,48 @@ extern "C" __global__ __launch_bounds__(256) void stream_copy_b128(const u32x4* 
 // object: binding base pointers, then the i32 push constants, with x and y at
 // the byte offsets the reference bakes in (kernels/cuda/dispatch_3.cu:8-22,
 // dispatch_4.cu:8-22, dispatch_12.cu:19-21, dispatch_18.cu:19-21,
-// dispatch_20.cu:19-21, dispatch_24.cu:11-20).  Launch shape (the stub's
-// workgroup count): Q8_0 dispatches 64-thread workgroups, N/4 of them; the
-// vocab dispatch 1024 workgroups of 256 threads, logits only (the reference
-// runs its argmax as separate dispatches).
+// dispatch_20.cu:19-21, dispatch_24.cu:11-20).  Any launch shape with 64-256
+// threads per workgroup computes every row: the reference's own stubs
+// (workgroup_size 256, counts N/8 and 18992, kernels/cuda/dispatch_*.mlir:5-9)
+// as well as this build's (64 threads, N/4 workgroups, one quad each).  Each
+// full wave takes row quads blockIdx.x * waves + wave, stepping by the grid's
+// wave count; a partial wave (blockDim.x % 64 != 0) only joins the barriers.
+// Workgroups of fewer than 64 threads compute nothing (the shim rejects them).
+
+// Every wave of the workgroup runs the same rounds (the round count depends
+// on the workgroup only), so the barriers inside q8_quad_core match; a wave
+// without a quad in the last round recomputes the last quad and stores
+// nothing.
+template <int P>
+__device__ __forceinline__ void hal_q8_quads(const uint8_t* __restrict__ w,
+                                             const uint16_t* __restrict__ x,
+                                             uint16_t* __restrict__ y, int n_rows,
+                                             uint8_t* __restrict__ lds) {
+  const int waves = (int)(blockDim.x >> 6);
+  if (waves == 0) return;
+  const int wave = threadIdx.x >> 6;
+  const int nq = (n_rows + 3) / 4;
+  uint8_t* mine = lds + wave * QuadShape<P>::LDS_BYTES;
+  const int step = (int)gridDim.x * waves;
+  for (int base = (int)blockIdx.x * waves; base < nq; base += step) {
+    const int quad = base + wave;
+    const bool store = wave < waves && quad < nq;
+    q8_quad_core<P>(w, n_rows, quad < nq ? quad : nq - 1, mine,
+                    [&](u32x4 (&xr)[P][8]) { load_x_cols<P>(x, xr); },
+                    [&](int row, float acc) {
+                      if (store) y[row] = f32_to_f16_bits(acc);
+                    });
+  }
+}
+
 #define HAL_Q8_DISPATCH(NAME, P, N, BPL, X_OFF, Y_OFF)                                      \
-  extern "C" __global__ __launch_bounds__(64) void NAME(                                      \
+  extern "C" __global__ __launch_bounds__(256) void NAME(                                     \
       const uint8_t* __restrict__ q8_stacked, const char* __restrict__ b1,                    \
       char* __restrict__ b2, uint32_t c0, uint32_t c1) {                                      \
-    __shared__ __attribute__((aligned(16))) uint8_t lds[QuadShape<P>::LDS_BYTES];             \
+    __shared__ __attribute__((aligned(16))) uint8_t lds[4 * QuadShape<P>::LDS_BYTES];         \
     const uint64_t layer = (uint64_t)c0 | ((uint64_t)c1 << 32);                               \
-    q8_quad<P>(q8_stacked + layer * (BPL), reinterpret_cast<const uint16_t*>(b1 + (X_OFF)),  \
-               reinterpret_cast<uint16_t*>(b2 + (Y_OFF)), N, blockIdx.x, lds);                \
+    hal_q8_quads<P>(q8_stacked + layer * (BPL), reinterpret_cast<const uint16_t*>(b1 + (X_OFF)), \
+                    reinterpret_cast<uint16_t*>(b2 + (Y_OFF)), N, lds);                       \
   }
 
 HAL_Q8_DISPATCH(decode_dispatch_3_matmul_2048x1x1024_f16, 1, 2048, 2228224ULL, 2112, 4160)
@@ -139,19 +169,22 @@ HAL_Q8_DISPATCH(decode_dispatch_18_matmul_6144x1x1024_f16, 1, 6144, 6684672ULL, 
 HAL_Q8_DISPATCH(decode_dispatch_20_matmul_1024x1x3072_f16, 3, 1024, 3342336ULL, 18432, 0)
 
 // dispatch_4 takes the output byte offset as c0 and the layer as c1 | c2 << 32.
-extern "C" __global__ __launch_bounds__(64) void decode_dispatch_4_matmul_1024x1x1024_f16(
+extern "C" __global__ __launch_bounds__(256) void decode_dispatch_4_matmul_1024x1x1024_f16(
     const uint8_t* __restrict__ q8_stacked, const char* __restrict__ b1, char* __restrict__ b2,
     uint32_t c0, uint32_t c1, uint32_t c2) {
-  __shared__ __attribute__((aligned(16))) uint8_t lds[5 * 1024];
+  __shared__ __attribute__((aligned(16))) uint8_t lds[4 * QuadShape<1>::LDS_BYTES];
   const uint64_t layer = (uint64_t)c1 | ((uint64_t)c2 << 32);
-  q8_quad<1>(q8_stacked + layer * 1114112ULL, reinterpret_cast<const uint16_t*>(b1 + 2112),
-             reinterpret_cast<uint16_t*>(b2 + (int)c0), 1024, blockIdx.x, lds);
+  hal_q8_quads<1>(q8_stacked + layer * 1114112ULL, reinterpret_cast<const uint16_t*>(b1 + 2112),
+                  reinterpret_cast<uint16_t*>(b2 + (int)c0), 1024, lds);
 }
 
-// dispatch_24 takes the output byte offset as c0.
+// dispatch_24 takes the output byte offset as c0 (logits only; the reference
+// runs its argmax as separate dispatches).  The vocab body spreads the row
+// batches over however many full waves the grid has.
 extern "C" __global__ __launch_bounds__(256) void decode_dispatch_24_matmul_151936x1x1024_f16(
     const uint16_t* __restrict__ weight, const char* __restrict__ b1, char* __restrict__ b2,
     uint32_t c0) {
+  if ((blockDim.x >> 6) == 0) return;
   vocab_body<VOCAB_NT_LOADS != 0, false>(weight, reinterpret_cast<const uint16_t*>(b1 + 64),
                                          reinterpret_cast<uint16_t*>(b2 + (int)c0), 151936,
                                          nullptr);

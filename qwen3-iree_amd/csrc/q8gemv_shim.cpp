@@ -46,6 +46,7 @@ constexpr KindInfo kKinds[5] = {
 
 constexpr int kVocabMaxWorkgroups = 8192;
 constexpr int kStepWorkgroups = 256;  // dec_step's fixed grid (one workgroup per CU)
+constexpr uint32_t kDefaultSpinLimit = 1u << 20;  // dec_step: poll rounds before a wait gives up
 constexpr int kQ8MaxWorkgroups = 65536;
 constexpr size_t kVocabWorkspaceBytes = 256;
 constexpr int kBatchMaxCount = 1 << 20;
@@ -113,6 +114,7 @@ struct State {
   int pf_attn_split = 0;  // prefill attention positions per split in blocks of 32: 0 = by shape
   int step_single = -1;   // single-launch decode step: -1 unknown, 0 off, 1 on
   bool step_capable = false;
+  uint32_t step_spin_limit = kDefaultSpinLimit;  // poll rounds before a dec_step wait gives up
   int vocab_wgs = 0;      // 0 = default
 };
 
@@ -485,6 +487,13 @@ int q8gemv_qkv(const void* wq_stacked, const void* wk_stacked, const void* wv_st
 
 int q8gemv_hal_dispatch(int ordinal, const void* binding0, const void* binding1, void* binding2,
                         const uint32_t* push_constants, int n_constants, void* stream) {
+  return q8gemv_hal_dispatch_grid(ordinal, binding0, binding1, binding2, push_constants,
+                                  n_constants, 0, 0, stream);
+}
+
+int q8gemv_hal_dispatch_grid(int ordinal, const void* binding0, const void* binding1,
+                             void* binding2, const uint32_t* push_constants, int n_constants,
+                             uint32_t workgroups, uint32_t workgroup_size, void* stream) {
   int idx = -1;
   for (int i = 0; i < 6; ++i)
     if (kHalDispatches[i].ordinal == ordinal) idx = i;
@@ -506,6 +515,12 @@ int q8gemv_hal_dispatch(int ordinal, const void* binding0, const void* binding1,
   }
   if ((ordinal == 4 || ordinal == 24) && (push_constants[0] & 1u))
     return fail(Q8_ERR_MISALIGNED, "output byte offset %u is odd", push_constants[0]);
+  const uint32_t block = workgroup_size ? workgroup_size : hd.block;
+  const uint32_t grid = workgroups ? workgroups : hd.grid;
+  if (block % 64 != 0 || block > 256)
+    return fail(Q8_ERR_BAD_ARGUMENT, "workgroup size %u is not 64, 128, 192 or 256", block);
+  if (grid > 0x7fffffffu)
+    return fail(Q8_ERR_BAD_ARGUMENT, "%u workgroups is too many", grid);
   int rc = check_ready();
   if (rc) return rc;
   const void* b0 = binding0;
@@ -517,7 +532,7 @@ int q8gemv_hal_dispatch(int ordinal, const void* binding0, const void* binding1,
   void* args5[] = {&b0, &b1, &b2, &c[0], &c[1]};
   void* args6[] = {&b0, &b1, &b2, &c[0], &c[1], &c[2]};
   void** args = hd.constants == 1 ? args3 : hd.constants == 2 ? args5 : args6;
-  return launch(g.hal[idx], hd.grid, hd.block, args, static_cast<hipStream_t>(stream));
+  return launch(g.hal[idx], grid, block, args, static_cast<hipStream_t>(stream));
 }
 
 size_t q8gemv_batch_table_bytes(int count) {
@@ -891,7 +906,7 @@ struct StepParams {
   int32_t max_seq;
   int32_t advance;
   int32_t head;
-  int32_t pad;
+  uint32_t spin_limit;
 };
 
 // One single-launch decode step (dec_step).
@@ -927,7 +942,7 @@ int launch_step(const qwen3_weights* w, void* k_cache, void* v_cache, int64_t ma
   p.max_seq = (int32_t)max_seq;
   p.advance = advance ? 1 : 0;
   p.head = head ? 1 : 0;
-  p.pad = 0;
+  p.spin_limit = g.step_spin_limit;
   void* args[] = {&p};
   hipError_t e = hipModuleLaunchCooperativeKernel(g.dec_step, kStepWorkgroups, 1, 1, 256, 1, 1, 0,
                                                   st, args);
@@ -936,6 +951,21 @@ int launch_step(const qwen3_weights* w, void* k_cache, void* v_cache, int64_t ma
 }
 
 bool use_single() { return g.step_single == 1 && g.step_capable && g.dec_step != nullptr; }
+
+// Status bit 1 of a scratch: a single-launch step gave up waiting for a
+// hand-off (its outputs are not valid).  Reads the word on `st` (which the
+// caller has just synchronized or is about to: the copy is stream-ordered).
+int check_not_aborted(void* scratch, hipStream_t st, const char* when) {
+  uint32_t status = 0;
+  HIP_TRY(hipMemcpyAsync(&status, mb(scratch) + kScrStatus, sizeof(status),
+                         hipMemcpyDeviceToHost, st));
+  HIP_TRY(hipStreamSynchronize(st));
+  if (status & 2u)
+    return fail(Q8_ERR_STEP_ABORTED,
+                "%s: a single-launch decode step gave up waiting for a hand-off (status bit 1); "
+                "its outputs are invalid; qwen3_scratch_reset clears the scratch", when);
+  return Q8_OK;
+}
 
 int check_decode_ready() {
   int rc = check_ready();
@@ -1378,6 +1408,28 @@ int qwen3_set_step_mode(int mode) {
   return Q8_OK;
 }
 
+int qwen3_set_step_spin_limit(uint32_t polls) {
+  g.step_spin_limit = polls == 0 ? kDefaultSpinLimit : polls;
+  return Q8_OK;
+}
+
+int qwen3_check_status(const void* scratch, uint32_t* status, void* stream) {
+  if (!scratch || !status) return fail(Q8_ERR_NULL_POINTER, "null scratch or status");
+  if (!aligned(scratch, 256)) return fail(Q8_ERR_MISALIGNED, "scratch must be 256-byte aligned");
+  int rc = check_ready();
+  if (rc) return rc;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  *status = 0;
+  HIP_TRY(hipMemcpyAsync(status, cb(scratch) + kScrStatus, sizeof(*status), hipMemcpyDeviceToHost,
+                         st));
+  HIP_TRY(hipStreamSynchronize(st));
+  if (*status & 2u)
+    return fail(Q8_ERR_STEP_ABORTED,
+                "a single-launch decode step gave up waiting for a hand-off (status bit 1); "
+                "its outputs are invalid; qwen3_scratch_reset clears the scratch");
+  return Q8_OK;
+}
+
 int qwen3_get_step_mode(int* mode) {
   if (!mode) return fail(Q8_ERR_NULL_POINTER, "null mode");
   int rc = check_decode_ready();
@@ -1504,7 +1556,7 @@ int qwen3_generate(const qwen3_weights* w, void* k_cache, void* v_cache, int64_t
   hipStream_t st = static_cast<hipStream_t>(stream);
   int32_t p0 = 0;
   HIP_TRY(hipMemcpyAsync(&p0, pos, sizeof(p0), hipMemcpyDeviceToHost, st));
-  HIP_TRY(hipStreamSynchronize(st));
+  if ((rc = check_not_aborted(scratch, st, "before qwen3_generate"))) return rc;
   if (p0 < 0 || (int64_t)p0 + max_new > max_seq)
     return fail(Q8_ERR_BAD_SHAPE, "positions %d + %d new tokens exceed max_seq %lld", p0, max_new,
                 (long long)max_seq);
@@ -1527,7 +1579,9 @@ int qwen3_generate(const qwen3_weights* w, void* k_cache, void* v_cache, int64_t
     idx += batch;
     int32_t last = 0;
     HIP_TRY(hipMemcpyAsync(&last, token, sizeof(last), hipMemcpyDeviceToHost, st));
-    HIP_TRY(hipStreamSynchronize(st));
+    // the batch's steps must all have completed; otherwise its tokens are not
+    // valid and n_generated stays at the previous batch
+    if ((rc = check_not_aborted(scratch, st, "qwen3_generate"))) return rc;
     *n_generated = idx;
     if (last == eos_id) break;
   }
@@ -1597,7 +1651,7 @@ int qwen3_prefill_batched(const qwen3_weights* w, void* k_cache, void* v_cache, 
   hipStream_t st = static_cast<hipStream_t>(stream);
   int32_t p0 = 0;
   HIP_TRY(hipMemcpyAsync(&p0, pos, sizeof(p0), hipMemcpyDeviceToHost, st));
-  HIP_TRY(hipStreamSynchronize(st));
+  if ((rc = check_not_aborted(scratch, st, "before qwen3_prefill_batched"))) return rc;
   if (p0 < 0 || (int64_t)p0 + n_prompt > max_seq)
     return fail(Q8_ERR_BAD_SHAPE, "positions %d + %d prompt tokens exceed max_seq %lld", p0,
                 n_prompt, (long long)max_seq);

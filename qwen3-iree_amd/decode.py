@@ -137,6 +137,12 @@ def set_step_mode(mode: int) -> None:
     Q._call("qwen3_set_step_mode", int(mode))
 
 
+def set_step_spin_limit(polls: int = 0) -> None:
+    """Poll rounds after which a wait of the single-launch step gives up (0 =
+    the library default); a small value forces the abort path."""
+    Q._call("qwen3_set_step_spin_limit", int(polls))
+
+
 def set_prefill_tiling(gemm_rows: int = 0, attn_split_blocks: int = 0) -> None:
     """Work division of the batched prompt path (0 = by shape): token rows per
     GEMM workgroup (32 or 64) and cache positions per attention split in
@@ -203,6 +209,17 @@ class DecodeSession:
         off = int(Q.load_library().qwen3_scratch_status_offset())
         return int(self.scratch.download(np.uint32, 1, off)[0])
 
+    def check_status(self) -> int:
+        """Synchronizes the stream and returns the status word; raises
+        Q8GemvError(Q8_ERR_STEP_ABORTED) if a single-launch step gave up."""
+        st = ctypes.c_uint32(0)
+        Q._call("qwen3_check_status", self.scratch.ptr, ctypes.byref(st), Q._stream(self.stream))
+        return int(st.value)
+
+    def reset_scratch(self) -> None:
+        """Clears the scratch (status word, sequence number, hand-off words)."""
+        Q._call("qwen3_scratch_reset", self.scratch.ptr, Q._stream(self.stream))
+
     def step(self, advance: bool = True, logits: bool = True) -> None:
         Q._call("qwen3_decode_step", self.model.ref(), self.k_cache.ptr, self.v_cache.ptr,
                 self.max_seq, self.token_ptr, self.pos_ptr,
@@ -243,7 +260,7 @@ class DecodeSession:
             Q._call("qwen3_prefill", self.model.ref(), self.k_cache.ptr, self.v_cache.ptr,
                     self.max_seq, buf.ptr, int(prompt.size), self.token_ptr, self.pos_ptr,
                     self.scratch.ptr, Q._stream(self.stream))
-            self.synchronize()
+            self.check_status()
         finally:
             buf.free()
 

@@ -11,10 +11,17 @@ memory is owned by DeviceBuffer objects allocated through the library.
 
 Every call raises Q8GemvError with the library's status code and message when
 the library reports a failure; nothing falls back to a CPU path.
+
+At interpreter exit (atexit) the module releases what is still alive in an
+order the HIP runtime accepts: it waits for the device, destroys graph execs,
+events and streams, frees device buffers, then unloads the code objects
+(q8gemv_shutdown) -- so no HIP object outlives the runtime's own teardown.
 """
 from __future__ import annotations
 
+import atexit
 import ctypes
+import weakref
 from dataclasses import dataclass
 from pathlib import Path
 
@@ -35,6 +42,7 @@ Q8_ERR_BAD_SHAPE = 6
 Q8_ERR_CODE_OBJECT = 7
 Q8_ERR_HIP = 8
 Q8_ERR_BAD_ARGUMENT = 9
+Q8_ERR_STEP_ABORTED = 10
 
 NUM_LAYERS = 28
 HIDDEN = 1024
@@ -112,6 +120,7 @@ _SIGNATURES = {
     "f16_gemv_argmax_rows": [_P, _I64, _P, _P, _P, _P, _P],
     "q8gemv_qkv": [_P, _P, _P, _I64, _P, _P, _P, _P, _P],
     "q8gemv_hal_dispatch": [_I, _P, _P, _P, _P, _I, _P],
+    "q8gemv_hal_dispatch_grid": [_I, _P, _P, _P, _P, _I, ctypes.c_uint32, ctypes.c_uint32, _P],
     "q8gemv_desc_for_kind": [_I, _P, _I64, _P, _P, _P],
     "q8gemv_batch_table_bytes": [_I],
     "q8gemv_batch_encode": [_P, _I, _P, _SZ, _P],
@@ -160,6 +169,8 @@ _SIGNATURES = {
     "qwen3_prefill_layer": [_P, _I, _P, _P, _I64, ctypes.c_int32, ctypes.c_int32, _I, _P, _SZ, _P],
     "qwen3_prefill_workspace_offset": [ctypes.c_int32, ctypes.c_char_p],
     "qwen3_set_step_mode": [_I],
+    "qwen3_set_step_spin_limit": [ctypes.c_uint32],
+    "qwen3_check_status": [_P, _P, _P],
     "qwen3_set_prefill_tiling": [_I, _I],
     "qwen3_get_step_mode": [_P],
 }
@@ -176,6 +187,9 @@ _RESTYPES = {
 }
 
 _lib: ctypes.CDLL | None = None
+# Device objects still alive (DeviceBuffer, Stream, Event, Graph), released in
+# order by teardown() at exit.
+_live: "weakref.WeakSet" = weakref.WeakSet()
 
 
 def load_library(path: str | Path | None = None) -> ctypes.CDLL:
@@ -218,6 +232,33 @@ def shutdown() -> None:
     load_library().q8gemv_shutdown()
 
 
+def teardown() -> None:
+    """Release every live device object, then unload the code objects.
+
+    Order: device synchronize; graph execs; events; streams; device buffers;
+    q8gemv_shutdown.  Errors are ignored (this runs at exit).  Registered with
+    atexit; safe to call more than once."""
+    if _lib is None:
+        return
+    try:
+        _lib.q8rt_device_synchronize()
+    except Exception:
+        pass
+    for kind in (Graph, Event, Stream, DeviceBuffer):
+        for obj in [o for o in list(_live) if isinstance(o, kind)]:
+            try:
+                obj._release()
+            except Exception:
+                pass
+    try:
+        _lib.q8gemv_shutdown()
+    except Exception:
+        pass
+
+
+atexit.register(teardown)
+
+
 def device_count() -> int:
     n = ctypes.c_int(0)
     _call("q8rt_device_count", ctypes.byref(n))
@@ -246,6 +287,7 @@ class DeviceBuffer:
         p = ctypes.c_void_p(0)
         _call("q8rt_malloc", ctypes.byref(p), max(self.nbytes, 1))
         self.ptr = p.value
+        _live.add(self)
 
     @classmethod
     def from_array(cls, arr: np.ndarray) -> "DeviceBuffer":
@@ -278,6 +320,11 @@ class DeviceBuffer:
             _call("q8rt_free", self.ptr)
             self.ptr = None
 
+    def _release(self) -> None:
+        if self.ptr and _lib is not None:
+            _lib.q8rt_free(self.ptr)
+        self.ptr = None
+
     def __enter__(self):
         return self
 
@@ -297,6 +344,7 @@ class Stream:
         p = ctypes.c_void_p(0)
         _call("q8rt_stream_create", ctypes.byref(p))
         self.handle = p.value
+        _live.add(self)
 
     def synchronize(self) -> None:
         _call("q8rt_stream_synchronize", self.handle)
@@ -306,12 +354,18 @@ class Stream:
             _call("q8rt_stream_destroy", self.handle)
             self.handle = None
 
+    def _release(self) -> None:
+        if self.handle and _lib is not None:
+            _lib.q8rt_stream_destroy(self.handle)
+        self.handle = None
+
 
 class Event:
     def __init__(self):
         p = ctypes.c_void_p(0)
         _call("q8rt_event_create", ctypes.byref(p))
         self.handle = p.value
+        _live.add(self)
 
     def record(self, stream: Stream | None = None) -> None:
         _call("q8rt_event_record", self.handle, stream.handle if stream else None)
@@ -329,6 +383,11 @@ class Event:
             _call("q8rt_event_destroy", self.handle)
             self.handle = None
 
+    def _release(self) -> None:
+        if self.handle and _lib is not None:
+            _lib.q8rt_event_destroy(self.handle)
+        self.handle = None
+
 
 class Graph:
     """A captured hipGraph of library launches on one stream."""
@@ -341,6 +400,7 @@ class Graph:
             p = ctypes.c_void_p(0)
             _call("q8rt_graph_end_capture", stream.handle, ctypes.byref(p))
         self.exec = p.value
+        _live.add(self)
 
     def launch(self, stream: Stream) -> None:
         _call("q8rt_graph_launch", self.exec, stream.handle)
@@ -349,6 +409,11 @@ class Graph:
         if self.exec:
             _call("q8rt_graph_destroy", self.exec)
             self.exec = None
+
+    def _release(self) -> None:
+        if self.exec and _lib is not None:
+            _lib.q8rt_graph_destroy(self.exec)
+        self.exec = None
 
 
 def stream_copy(dst, src, nbytes: int, stream=None) -> None:
@@ -411,11 +476,14 @@ def decode_dispatch(ordinal: int, *args, stream=None) -> None:
         _call(d.export, _ptr(w), _ptr(x), _ptr(logits), _ptr(token), _ptr(ws), _stream(stream))
 
 
-def hal_dispatch(ordinal: int, binding0, binding1, binding2, constants, stream=None) -> None:
-    """Launch a reference executable through its IREE HAL binding ABI."""
+def hal_dispatch(ordinal: int, binding0, binding1, binding2, constants, stream=None,
+                 workgroups: int = 0, workgroup_size: int = 0) -> None:
+    """Launch a reference executable through its IREE HAL binding ABI, with
+    this build's stub shape (0, 0) or an explicit one (e.g. the reference
+    stubs' 256-thread workgroups)."""
     c = (ctypes.c_uint32 * max(1, len(constants)))(*[int(v) & 0xffffffff for v in constants])
-    _call("q8gemv_hal_dispatch", int(ordinal), _ptr(binding0), _ptr(binding1), _ptr(binding2), c,
-          len(constants), _stream(stream))
+    _call("q8gemv_hal_dispatch_grid", int(ordinal), _ptr(binding0), _ptr(binding1), _ptr(binding2),
+          c, len(constants), int(workgroups), int(workgroup_size), _stream(stream))
 
 
 def vocab_workspace_bytes() -> int:

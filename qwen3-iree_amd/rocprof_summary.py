@@ -70,10 +70,13 @@ def main() -> int:
         return args.copy_bytes / 1024.0 / statistics.mean(copy)
 
     fs, ws = scale(fetch), scale(write)
+    from build import source_digest  # the package directory is this script's
+
+    digest = source_digest()
     print("| kernel | grid (threads) | dispatches | mean us | median us | min us |"
           " FETCH_SIZE KiB | WRITE_SIZE KiB | HBM bytes / dispatch |")
     print("|---|---|---|---|---|---|---|---|---|")
-    report = {"fetch_scale": fs, "write_scale": ws, "kernels": []}
+    report = {"source_digest": digest, "fetch_scale": fs, "write_scale": ws, "kernels": []}
     for key in sorted(durs, key=lambda k: -sum(durs[k])):
         name, grid = key
         if args.kernels and name not in args.kernels:
@@ -88,10 +91,12 @@ def main() -> int:
               f" {min(d):.3f} | {'' if f is None else f'{f:.1f}'} | {'' if w is None else f'{w:.1f}'} |"
               f" {'' if traffic is None else traffic} |")
         report["kernels"].append({"name": name, "grid": grid, "dispatches": len(d),
-                                  "mean_us": statistics.mean(d), "fetch_kib": f, "write_kib": w,
-                                  "hbm_bytes": traffic})
+                                  "mean_us": statistics.mean(d),
+                                  "median_us": statistics.median(d), "fetch_kib": f,
+                                  "write_kib": w, "hbm_bytes": traffic})
     print()
     print(f"FETCH_SIZE scale (copy kernel): {fs}; WRITE_SIZE scale: {ws}")
+    print(f"Device sources (csrc/*.hip, csrc/*.h) sha256: {digest}")
     if args.json:
         args.json.write_text(json.dumps(report, indent=1) + "\n")
     return 0

@@ -1,0 +1,85 @@
+"""The 28-layer stacked cold-cache Q8_0 GEMV sweep, as device buffers.
+
+Five stacked weight sets [28, BPL] (attn_q, attn_kv, attn_o, gate_up, ffn_dn;
+436,731,904 bytes, more than the 256 MB MALL), and for layer 0..27 the five
+GEMVs in that order (the per-layer dispatch order of model/qwen3_full.mlir:
+751-864, one attn_kv for k and v), 140 GEMVs, each with its own f16 x and y.
+Built once here so the benchmark and the parity tests use the same table.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+
+import numpy as np
+
+from . import q8gemv as Q
+from . import weights as Wt
+
+LAYERS = Q.NUM_LAYERS
+KINDS = Q.Q8_KINDS  # per layer: q, kv, o, gate_up, dn
+
+
+def algorithmic_bytes(d) -> int:
+    """Weights + x + y of one GEMV, each byte counted once."""
+    return d.bytes_per_layer + 2 * d.k + 2 * d.n
+
+
+@dataclass
+class Sweep:
+    seed: int
+    host_w: dict            # kind -> u8 [28, BPL] (host copy, the oracle's input)
+    dev_w: dict             # kind -> DeviceBuffer
+    host_x: dict            # (layer, kind) -> f16 [K]
+    dev_x: dict             # (layer, kind) -> DeviceBuffer
+    dev_y: dict             # (layer, kind) -> DeviceBuffer (f16 [N])
+    order: list = field(default_factory=list)  # [(layer, Dispatch)] in sweep order
+
+    @property
+    def weight_bytes(self) -> int:
+        return sum(d.bytes_per_layer for d in KINDS) * LAYERS
+
+    @property
+    def bytes_per_step(self) -> int:
+        return sum(algorithmic_bytes(d) for d in KINDS) * LAYERS
+
+    @property
+    def outputs(self) -> int:
+        return sum(d.n for _, d in self.order)
+
+    def descs(self) -> list:
+        return [Q.desc_for_kind(d.kind, self.dev_w[d.kind], layer, self.dev_x[(layer, d.kind)],
+                                self.dev_y[(layer, d.kind)]) for layer, d in self.order]
+
+    def batch(self) -> "Q.Q8Batch":
+        """The whole sweep as one batched launch (entries in sweep order)."""
+        return Q.Q8Batch(self.descs())
+
+    def record_dispatches(self, stream=None) -> None:
+        """The sweep as 140 stream-ordered dispatches of the per-GEMV entry."""
+        for layer, d in self.order:
+            Q.q8gemv(d.kind, self.dev_w[d.kind], layer, self.dev_x[(layer, d.kind)],
+                     self.dev_y[(layer, d.kind)], stream)
+
+    def free(self) -> None:
+        for b in (*self.dev_w.values(), *self.dev_x.values(), *self.dev_y.values()):
+            b.free()
+
+
+def build(seed: int, workers: int = 16) -> Sweep:
+    """Seeded sweep inputs resident on the device: W_kind ~ N(0, 0.02)
+    quantised by the reference quantizer (one stream per (seed, kind, layer)),
+    x = f16(N(0, 1)) with index layer * 8 + kind."""
+    host_w, dev_w = {}, {}
+    for d in KINDS:
+        host = Wt.synthetic_q8_stack(d.n, d.k, LAYERS, seed=seed, tensor=d.kind, workers=workers)
+        host_w[d.kind] = host
+        dev_w[d.kind] = Q.DeviceBuffer.from_array(host)
+    host_x, dev_x, dev_y = {}, {}, {}
+    for layer in range(LAYERS):
+        for d in KINDS:
+            x = Wt.synthetic_x(d.k, seed, index=layer * 8 + d.kind)
+            host_x[(layer, d.kind)] = x
+            dev_x[(layer, d.kind)] = Q.DeviceBuffer.from_array(x)
+            dev_y[(layer, d.kind)] = Q.DeviceBuffer(2 * d.n)
+    order = [(layer, d) for layer in range(LAYERS) for d in KINDS]
+    return Sweep(seed, host_w, dev_w, host_x, dev_x, dev_y, order)

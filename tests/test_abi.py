@@ -244,6 +244,17 @@ def test_hal_dispatch_validation(Q, ordinal, consts, code):
     assert lib.q8gemv_hal_dispatch(ordinal, A16, A16, A16, c, len(consts), None) == code
 
 
+@pytest.mark.parametrize("wgs,wgsize", [(256, 32), (256, 100), (256, 320), (1 << 31, 256)])
+def test_hal_dispatch_grid_rejects_bad_shapes(Q, wgs, wgsize):
+    """Workgroups of 64, 128, 192 or 256 threads only, and a grid that fits."""
+    import ctypes
+
+    lib = Q.load_library()
+    c = (ctypes.c_uint32 * 2)(0, 0)
+    assert lib.q8gemv_hal_dispatch_grid(3, A16, A16, A16, c, 2, wgs, wgsize, None) == \
+        Q.Q8_ERR_BAD_ARGUMENT
+
+
 # ------------------------------------------------------------ decode step ----
 
 def _fake_weights(Q, **override):

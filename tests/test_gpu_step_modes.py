@@ -99,3 +99,49 @@ def test_single_launch_repeated_steps_keep_sequence(D, dmodel, single):
     tok, pos = s.get_state()
     assert pos == 40 and s.status() == 0 and 0 <= tok < D.VOCAB
     s.free()
+
+
+def test_single_launch_abort_is_reported_and_recoverable(gpu, D, dmodel, single):
+    """A poll limit of one round makes the step's bounded waits give up (the
+    host forces the condition; every workgroup still exits normally): status
+    bit 1 is set, the position is not advanced, qwen3_check_status and
+    qwen3_generate report Q8_ERR_STEP_ABORTED, the next step on the same
+    scratch runs normally with a fresh sequence number (the bits of a fresh
+    session's step), and a scratch reset clears the status."""
+    Q = gpu
+    ref = D.DecodeSession(dmodel, 64)
+    ref.set_state(77, 5)
+    ref.step(advance=False, logits=True)
+    want_state, want_logits = ref.get_state(), ref.read_logits()
+    ref.free()
+
+    s = D.DecodeSession(dmodel, 64)
+    s.set_state(77, 5)
+    D.set_step_spin_limit(1)
+    try:
+        print("single-launch step with a one-round poll limit", flush=True)
+        s.step(advance=True, logits=True)
+        s.synchronize()
+    finally:
+        D.set_step_spin_limit(0)
+    assert s.status() & 2
+    assert s.get_state()[1] == 5
+    with pytest.raises(Q.Q8GemvError) as e:
+        s.check_status()
+    assert e.value.code == Q.Q8_ERR_STEP_ABORTED
+    with pytest.raises(Q.Q8GemvError) as e:
+        s.generate(4, eos_id=-1)
+    assert e.value.code == Q.Q8_ERR_STEP_ABORTED
+
+    s.set_state(77, 5)
+    print("step after the aborted one", flush=True)
+    s.step(advance=False, logits=True)
+    assert s.get_state() == want_state
+    assert np.array_equal(s.read_logits().view(np.uint16), want_logits.view(np.uint16))
+    assert s.status() & 2  # sticky until the scratch is reset
+
+    s.reset_scratch()
+    assert s.check_status() == 0
+    toks = s.generate(4, eos_id=-1)
+    assert len(toks) == 4 and s.get_state()[1] == 9 and s.check_status() == 0
+    s.free()
