@@ -82,16 +82,16 @@ def build_shim() -> Path:
     return SHIM
 
 
-def source_digest() -> str:
-    """sha256 (16 hex digits) over the device sources (csrc/*.hip, csrc/*.h):
-    the build a profile's counter figures belong to.  Computed from the files,
-    so it can be checked where the tree has no git history."""
+def source_digest(code_object: str = "q8gemv") -> str:
+    """sha256 (16 hex digits) over the sources of one code object: the build
+    a profile's figures belong to.  Computed from the files, so it can be
+    checked where the tree has no git history."""
     import hashlib
 
     h = hashlib.sha256()
-    for f in sorted(list(CSRC.glob("*.hip")) + list(CSRC.glob("*.h"))):
-        h.update(f.name.encode())
-        h.update(f.read_bytes())
+    for name in OBJECT_SOURCES[code_object]:
+        h.update(name.encode())
+        h.update((CSRC / name).read_bytes())
     return h.hexdigest()[:16]
 
 

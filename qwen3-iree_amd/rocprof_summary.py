@@ -96,7 +96,8 @@ def main() -> int:
                                   "write_kib": w, "hbm_bytes": traffic})
     print()
     print(f"FETCH_SIZE scale (copy kernel): {fs}; WRITE_SIZE scale: {ws}")
-    print(f"Device sources (csrc/*.hip, csrc/*.h) sha256: {digest}")
+    print(f"Sources of the q8gemv code object (csrc/q8gemv_kernels.hip, csrc/q8_device.h) "
+          f"sha256: {digest}")
     if args.json:
         args.json.write_text(json.dumps(report, indent=1) + "\n")
     return 0
