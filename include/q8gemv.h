@@ -185,6 +185,20 @@ int decode_dispatch_24_matmul_151936x1x1024_f16(const void* w_f16, const void* x
 int f16_gemv_argmax_rows(const void* w_f16, int64_t n_rows, const void* x_f16,
                          void* logits_f16, int32_t* token, void* workspace, void* stream);
 
+/* f16_gemv_argmax_rows without a workspace argument: allocates nothing and
+ * takes no caller memory beyond inputs and outputs.  No counterpart in the
+ * reference; for callers that cannot allocate (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).  The argmax key lives
+ * in a 256-byte device array inside this library, one per GPU, held until the
+ * process ends and set up (address lookup, zero fill) by q8gemv_init on its
+ * device; the fixed size serves any n_rows in [1, 2^31), and every call leaves
+ * the key zero again.  All calls on one GPU share that array: calls that
+ * overlap on one GPU (streams not ordered with each other) race on it.
+ * Returns Q8_ERR_NOT_INITIALIZED if q8gemv_init has not set it up on the
+ * current device.  Outputs are bit-identical to f16_gemv_argmax_rows. */
+int f16_gemv_argmax_rows_noalloc(const void* w_f16, int64_t n_rows, const void* x_f16,
+                                 void* logits_f16, int32_t* token, void* stream);
+
 /* ---- the reference's own binding ABI ----
  *
  * The code object also exports the six kernels under the reference's

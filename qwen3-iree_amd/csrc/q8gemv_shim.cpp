@@ -6,6 +6,7 @@
 #include "q8gemv.h"
 #include "qwen3_decode.h"
 #include "prefill_split.h"
+#include "shim_internal.h"
 
 #include <dlfcn.h>
 #include <hip/hip_runtime_api.h>
@@ -115,6 +116,8 @@ struct State {
   int step_single = -1;   // single-launch decode step: -1 unknown, 0 off, 1 on
   bool step_capable = false;
   uint32_t step_spin_limit = kDefaultSpinLimit;  // poll rounds before a dec_step wait gives up
+  int noalloc_rc = Q8_ERR_NOT_INITIALIZED;  // set-up status of the allocation-free entry point
+  std::string noalloc_err;
   int vocab_wgs = 0;      // 0 = default
 };
 
@@ -362,6 +365,10 @@ int q8gemv_init(const char* code_object_path) {
   g.compute_units = cus;
   g.batch_wgs = g.vocab_wgs = 0;
   g.ready = true;
+  // the allocation-free entry point's scratch on this device (address and a
+  // zero fill; an error here leaves that one entry point unavailable)
+  g.noalloc_rc = q8_shim::noalloc_setup(dev);
+  if (g.noalloc_rc != Q8_OK) g.noalloc_err = t_err;
   return Q8_OK;
 }
 
@@ -608,8 +615,33 @@ int vocab_argmax_workspace_reset(void* workspace, void* stream) {
 
 int f16_gemv_argmax_rows(const void* w_f16, int64_t n_rows, const void* x_f16, void* logits_f16,
                          int32_t* token, void* workspace, void* stream) {
-  if (!w_f16 || !x_f16 || !token || !workspace)
-    return fail(Q8_ERR_NULL_POINTER, "null w, x, token or workspace");
+  if (!workspace) return fail(Q8_ERR_NULL_POINTER, "null workspace");
+  if (!aligned(workspace, 16)) return fail(Q8_ERR_MISALIGNED, "workspace not 16-byte aligned");
+  int rc = q8_shim::validate_f16_argmax(w_f16, n_rows, x_f16, logits_f16, token);
+  if (rc) return rc;
+  return q8_shim::launch_f16_argmax(w_f16, n_rows, x_f16, logits_f16, token, workspace,
+                                    static_cast<hipStream_t>(stream));
+}
+
+}  // extern "C"
+
+namespace q8_shim {
+
+int error(int code, const char* msg) { return fail(code, "%s", msg); }
+
+int hip_error(hipError_t e, const char* what) { return hip_fail(e, what); }
+
+int noalloc_ready() {
+  int rc = check_ready();
+  if (rc) return rc;
+  if (g.noalloc_rc != Q8_OK)
+    return fail(g.noalloc_rc, "allocation-free scratch unavailable: %s", g.noalloc_err.c_str());
+  return Q8_OK;
+}
+
+int validate_f16_argmax(const void* w_f16, int64_t n_rows, const void* x_f16,
+                        const void* logits_f16, const int32_t* token) {
+  if (!w_f16 || !x_f16 || !token) return fail(Q8_ERR_NULL_POINTER, "null w, x or token");
   if (n_rows < 1 || n_rows >= (1LL << 31))
     return fail(Q8_ERR_BAD_SHAPE, "n_rows=%lld outside [1, 2^31)", (long long)n_rows);
   if (!aligned(w_f16, 16)) return fail(Q8_ERR_MISALIGNED, "weights not 16-byte aligned");
@@ -617,9 +649,12 @@ int f16_gemv_argmax_rows(const void* w_f16, int64_t n_rows, const void* x_f16, v
   if (logits_f16 && !aligned(logits_f16, 2))
     return fail(Q8_ERR_MISALIGNED, "logits not 2-byte aligned");
   if (!aligned(token, 4)) return fail(Q8_ERR_MISALIGNED, "token not 4-byte aligned");
-  if (!aligned(workspace, 16)) return fail(Q8_ERR_MISALIGNED, "workspace not 16-byte aligned");
-  int rc = check_ready();
-  if (rc) return rc;
+  return check_ready();
+}
+
+int launch_f16_argmax(const void* w_f16, int64_t n_rows, const void* x_f16, void* logits_f16,
+                      int32_t* token, void* workspace, hipStream_t s) {
+  int rc;
   const void* w_arg = w_f16;
   const void* x_arg = x_f16;
   void* l_arg = logits_f16;
@@ -627,12 +662,15 @@ int f16_gemv_argmax_rows(const void* w_f16, int64_t n_rows, const void* x_f16, v
   int32_t* t_arg = token;
   void* ws_arg = workspace;
   void* args[] = {&w_arg, &x_arg, &l_arg, &n_arg, &ws_arg};
-  hipStream_t s = static_cast<hipStream_t>(stream);
   rc = launch(g.vocab, (uint32_t)vocab_grid(), 256, args, s);
   if (rc) return rc;
   void* fargs[] = {&ws_arg, &t_arg};
   return launch(g.vocab_finalize, 1, 64, fargs, s);
 }
+
+}  // namespace q8_shim
+
+extern "C" {
 
 int vocab_gemv_argmax(const void* w_f16, const void* x_f16, void* logits_f16, int32_t* token,
                       void* workspace, void* stream) {

@@ -118,6 +118,7 @@ _SIGNATURES = {
     "vocab_gemv_argmax": [_P, _P, _P, _P, _P, _P],
     "decode_dispatch_24_matmul_151936x1x1024_f16": [_P, _P, _P, _P, _P, _P],
     "f16_gemv_argmax_rows": [_P, _I64, _P, _P, _P, _P, _P],
+    "f16_gemv_argmax_rows_noalloc": [_P, _I64, _P, _P, _P, _P],
     "q8gemv_qkv": [_P, _P, _P, _I64, _P, _P, _P, _P, _P],
     "q8gemv_hal_dispatch": [_I, _P, _P, _P, _P, _I, _P],
     "q8gemv_hal_dispatch_grid": [_I, _P, _P, _P, _P, _I, ctypes.c_uint32, ctypes.c_uint32, _P],
@@ -502,6 +503,13 @@ def vocab_gemv_argmax(w, x, logits, token, workspace, stream=None) -> None:
 def f16_gemv_argmax_rows(w, n_rows: int, x, logits, token, workspace, stream=None) -> None:
     _call("f16_gemv_argmax_rows", _ptr(w), int(n_rows), _ptr(x), _ptr(logits), _ptr(token),
           _ptr(workspace), _stream(stream))
+
+
+def f16_gemv_argmax_rows_noalloc(w, n_rows: int, x, logits, token, stream=None) -> None:
+    """f16_gemv_argmax_rows with the argmax key in the library's own device
+    scratch (no workspace, nothing allocated)."""
+    _call("f16_gemv_argmax_rows_noalloc", _ptr(w), int(n_rows), _ptr(x), _ptr(logits),
+          _ptr(token), _stream(stream))
 
 
 def set_batch_workgroups(n: int) -> None:
