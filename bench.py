@@ -486,6 +486,10 @@ def main() -> int:
                     help="run only the full decode step and print its JSON line")
     ap.add_argument("--sweep-only", action="store_true",
                     help="run only the batched sweep (timed, parity-checked) and print its line")
+    ap.add_argument("--kernels-only", action="store_true",
+                    help="run only the GEMV kernels (batched sweep, per-dispatch sweep, vocab, the "
+                         "decode step's GEMV share) and print the line without the decode step, "
+                         "prompt, generation and CPU parts (for counter runs)")
     ap.add_argument("--generate-only", action="store_true",
                     help="run only end-to-end generation and print its JSON line")
     ap.add_argument("--step-mode", type=int, choices=(0, 1), default=None,
@@ -727,6 +731,27 @@ def run(Q, S, O, info, args) -> int:
         f"{decode_gemv_us:.1f} us, {decode_bytes / decode_gemv_us / 1e3:.0f} GB/s")
     for b in (wv_dev, xv_dev, logits_dev, tok_dev, ws, v_dev, *step_y.values()):
         b.free()
+    kernels = {
+        "per_dispatch_sweep": {"us": round(chain_ms * 1e3, 1),
+                               "median_us": round(tc["median_ms"] * 1e3, 1),
+                               "GBps": round(chain_gbs, 1),
+                               "frac": round(chain_gbs / HBM_PEAK_GBS, 4), "dispatches": 140,
+                               "launch": "eager" if args.no_graph else "hipGraph"},
+        "vocab": {"us": round(v_ms * 1e3, 2), "median_us": round(tv["median_ms"] * 1e3, 2),
+                  "GBps": round(v_gbs, 1), "frac": round(v_gbs / HBM_PEAK_GBS, 4),
+                  "bytes": vocab_bytes, "token": token, "parity_ok": rep_v["fail"] == 0 and token == own},
+        "decode_step_gemv": {"us": round(decode_gemv_us, 2), "bytes": decode_bytes,
+                             "GBps": round(decode_bytes / decode_gemv_us / 1e3, 1),
+                             "dispatches": 4 * layers + 2,
+                             "launch": "eager" if args.no_graph else "hipGraph"},
+    }
+    if args.kernels_only:
+        out = dict(headline)
+        out.update(kernels)
+        out["parity_ok"] = bool(fails == 0 and rep_v["fail"] == 0 and token == own)
+        print(json.dumps(out), flush=True)
+        sw.free()
+        return 0
 
     # ------------------------------------------- full decode step (C5)
     dec = bench_decode(Q, O, stream, args)
@@ -742,19 +767,8 @@ def run(Q, S, O, info, args) -> int:
     sw.free()
 
     out = dict(headline)
+    out.update(kernels)
     out.update({
-        "per_dispatch_sweep": {"us": round(chain_ms * 1e3, 1),
-                               "median_us": round(tc["median_ms"] * 1e3, 1),
-                               "GBps": round(chain_gbs, 1),
-                               "frac": round(chain_gbs / HBM_PEAK_GBS, 4), "dispatches": 140,
-                               "launch": "eager" if args.no_graph else "hipGraph"},
-        "vocab": {"us": round(v_ms * 1e3, 2), "median_us": round(tv["median_ms"] * 1e3, 2),
-                  "GBps": round(v_gbs, 1), "frac": round(v_gbs / HBM_PEAK_GBS, 4),
-                  "bytes": vocab_bytes, "token": token},
-        "decode_step_gemv": {"us": round(decode_gemv_us, 2), "bytes": decode_bytes,
-                             "GBps": round(decode_bytes / decode_gemv_us / 1e3, 1),
-                             "dispatches": 4 * layers + 2,
-                             "launch": "eager" if args.no_graph else "hipGraph"},
         "decode_step": dec,
         "prefill": pre,
         "generate": gen,
