@@ -199,7 +199,10 @@ int qwen3_generate(const qwen3_weights* w, void* k_cache, void* v_cache, int64_t
  * "q_roped" [2048] q after head norm and RoPE; "attn" [2048] attention
  * output; "res" [1024] residual after attention; "fn" [1024]
  * rms_norm(res, ffn_norm); "act" [3072] SwiGLU output; "on" [1024] the final
- * rms_norm(h, output_norm) of the head.  -1 for an unknown name. */
+ * rms_norm(h, output_norm) of the head; "part" f32 [16][8][132] the attention
+ * partials of the per-phase layer (the single-launch step does not use this
+ * region; its timestamp build records its clock reads there).  -1 for an
+ * unknown name. */
 int64_t qwen3_scratch_offset(const char* name);
 
 #ifdef __cplusplus

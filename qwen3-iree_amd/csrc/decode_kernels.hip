@@ -292,7 +292,10 @@ extern "C" __global__ __launch_bounds__(256) void dec_scratch_clear(uint32_t* __
 //                     8 partials of its 2 query heads -> ATT words
 //   C  64..191        attn_o + residual: 2 row quads per workgroup, one
 //                     1024-column chunk per wave, summed in LDS -> RES words
-//   D  0..63,128..255 gate/up quad pairs + SwiGLU -> ACT words
+//   D  64..255        gate/up quad pairs + SwiGLU -> ACT words (not on the
+//                     attention workgroups: their merge and cache prefetch
+//                     would sit ahead of the residual poll in their load
+//                     queues and delay every workgroup's SwiGLU input)
 //   E  all 256        ffn_down + residual: row quad wg, waves 0-2 one
 //                     1024-column chunk each, summed in LDS -> H words
 // then the vocab GEMV over all workgroups (each publishes its best key as two
@@ -351,6 +354,7 @@ struct StepParams {
   uint32_t* abort_word;
   uint32_t* status;
   uint16_t* on_out;         // the final rms_norm(h, output_norm) (f16[1024])
+  uint64_t* stamps;         // timestamp build only (DEC_STEP_STAMPS): per-phase clock reads
   int max_seq;
   int advance;
   int head;                 // 0: no vocab / argmax (a prompt step); pos still advances
@@ -497,6 +501,29 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
   return v;
 }
 
+// Timestamp build (-DDEC_STEP_STAMPS=1, for measuring where a step's time
+// goes; the product build compiles none of this): thread 0 of the workgroups
+// listed in stamp_slot reads the 100 MHz real-time counter at the phase
+// boundaries below into LDS, [layer][point] for layers 0..27 and [28][point]
+// for the vocab phase, and copies them to P.stamps[slot][29][16] at the end.
+//   per layer: 0 layer start, 1 h ready (A), 2 q/k/v published, 3 q/k/v ready
+//   (B), 4 partial published, 5 partials ready (B'), 6 attention output
+//   published, 7 attention output ready (C), 8 residual published, 9 residual
+//   ready (D), 10 SwiGLU published, 11 SwiGLU ready (E), 12 h published,
+//   13 A: x normalised, 14 A: weights staged in LDS, 15 A: row sums formed
+//   vocab: 0 start, 1 h ready, 2 key published, 3 keys ready (wg 0), 4 token
+#ifndef DEC_STEP_STAMPS
+#define DEC_STEP_STAMPS 0
+#endif
+constexpr int kStampWgs[16] = {0, 1, 7, 8, 56, 63, 64, 65, 127, 128, 191, 192, 200, 224, 254, 255};
+constexpr int kStampPoints = 16;
+__device__ __forceinline__ int stamp_slot(int wg) {
+#pragma unroll
+  for (int i = 0; i < 16; ++i)
+    if (kStampWgs[i] == wg) return i;
+  return -1;
+}
+
 constexpr int kGemvLds = QuadShape<3>::LDS_BYTES;  // the largest per-wave staging
 constexpr int kVecWords = 2 * kAttnGroups * 130;     // 2080: the largest polled vector
 constexpr int kStepLds = 4 * kVecWords + 4 * kGemvLds;
@@ -514,6 +541,20 @@ extern "C" __global__ __launch_bounds__(256) void dec_step(StepParams P) {
   const int wave = t >> 6;
   const int lane = t & 63;
   if (t == 0) s_abort = 0;
+#if DEC_STEP_STAMPS
+  __shared__ uint64_t s_stamp[kLayers + 1][kStampPoints];
+  const int stamp_i = stamp_slot(wg);
+#define STAMP(layer, k)                                                                   \
+  do {                                                                                    \
+    if (t == 0 && stamp_i >= 0) s_stamp[layer][k] = __builtin_amdgcn_s_memrealtime();     \
+  } while (0)
+  if (t == 0)
+    for (int i = 0; i < (kLayers + 1) * kStampPoints; ++i) (&s_stamp[0][0])[i] = 0;
+#else
+#define STAMP(layer, k) \
+  do {                  \
+  } while (0)
+#endif
 
   const uint32_t seq = __hip_atomic_load(P.seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
   const int pos_raw = *P.pos;
@@ -541,6 +582,7 @@ extern "C" __global__ __launch_bounds__(256) void dec_step(StepParams P) {
     uint64_t* cur = P.words + (layer & 1) * kWParity;
     const uint64_t* prev = P.words + ((layer & 1) ^ 1) * kWParity;
     const uint32_t tag_prev_h = step_tag(seq, layer - 1, kPhH);
+    STAMP(layer, 0);
 
     // ---- A: q/k/v ----
     {
@@ -562,15 +604,20 @@ extern "C" __global__ __launch_bounds__(256) void dec_step(StepParams P) {
         u32x4 wv[8];
         norm_weights(an, gemv_col, wv);  // requested before the wait
         if (!W.poll_finish(512, tag_prev_h, vec, h_src, hp)) return;
+        STAMP(layer, 1);
         rmsnorm_lds_w(reinterpret_cast<const uint16_t*>(vec), gemv_col, wv, xr[0]);
       }
+      STAMP(layer, 13);
       uint8_t* lds = stage + wave * kGemvLds;
       q8_quad_stage<1>(buf, lds);
       __syncthreads();
+      STAMP(layer, 14);
       const float acc = q8_quad_dot<1>(lds, xr);
+      STAMP(layer, 15);
       uint64_t* dst = quad < 512 ? cur + kWQ : (quad < 768 ? cur + kWK : cur + kWV);
       put_quad<1>(dst, 0, qd, acc, step_tag(seq, layer, kPhQKV),
                [](float a, int) { return (uint32_t)f32_to_f16_bits(a); });
+      STAMP(layer, 2);
     }
 
     // ---- B: attention, B': merge ----
@@ -594,6 +641,7 @@ extern "C" __global__ __launch_bounds__(256) void dec_step(StepParams P) {
           [&] { W.poll_begin(256, qkv_src, qkv_poll); },
           [&](uint32_t (&xw)[3], uint32_t& v_new) {
             ok = W.poll_finish(256, tq, vec, qkv_src, qkv_poll);
+            STAMP(layer, 3);
             xw[0] = vec[lane];
             xw[1] = vec[64 + lane];
             xw[2] = vec[128 + lane];
@@ -610,11 +658,13 @@ extern "C" __global__ __launch_bounds__(256) void dec_step(StepParams P) {
             put_word(dst + 3 + 2 * lane, __builtin_bit_cast(uint32_t, a1), tp);
           });
       if (!ok) return;
+      STAMP(layer, 4);
       if (sg == 0) {
         // the 8 groups' partials of query heads 2g, 2g+1 (contiguous words)
         if (!W.wait(cur + kWPart + 2 * g * kAttnGroups * 130, 2 * kAttnGroups * 130,
                     step_tag(seq, layer, kPhPart), vec))
           return;
+        STAMP(layer, 5);
         if (wave < 2) {
           const int hh = wave;
           const float* pv = reinterpret_cast<const float*>(vec) + hh * kAttnGroups * 130;
@@ -639,6 +689,7 @@ extern "C" __global__ __launch_bounds__(256) void dec_step(StepParams P) {
             put_word(cur + kWAtt + r * kNAtt + (2 * g + hh) * 64 + lane, att,
                      step_tag(seq, layer, kPhAtt));
         }
+        STAMP(layer, 6);
         __syncthreads();  // vec is reused by the next wait
       }
       if (layer + 1 < kLayers) {  // the next layer's first chunk, into this wave's LDS region
@@ -666,6 +717,7 @@ extern "C" __global__ __launch_bounds__(256) void dec_step(StepParams P) {
         h_row = as_half(reinterpret_cast<const uint16_t*>(vec + 1024)[row - 8 * (wg - 64)]);
       }
       if (!W.wait(cur + kWAtt + rep * kNAtt, 1024, step_tag(seq, layer, kPhAtt), vec)) return;
+      STAMP(layer, 7);
       u32x4 xr[1][8];
       lds_x_cols<1>(reinterpret_cast<const uint16_t*>(vec) + 1024 * c, xr);
       uint8_t* lds = stage + wave * kGemvLds;
@@ -679,12 +731,13 @@ extern "C" __global__ __launch_bounds__(256) void dec_step(StepParams P) {
         acc = reduce_row16(acc);
         put_quad<kRep>(cur + kWRes, kNRes, quad, acc, step_tag(seq, layer, kPhRes),
                  [&](float a, int) { return (uint32_t)residual_f16(h_row, a); });
+        STAMP(layer, 8);
       }
     }
 
     // ---- D: gate/up + SwiGLU ----
-    if (wg < 64 || wg >= 128) {
-      const int b = 4 * (wg < 64 ? wg : wg - 64) + wave;  // 0..767
+    if (wg >= 64) {
+      const int b = 4 * (wg - 64) + wave;  // 0..767
       constexpr int64_t bpl = (int64_t)(2 * kFfn) * (kHidden / 32 * 34);
       const uint8_t* wl = P.wgu + layer * bpl;
       u32x4 bg[QuadShape<1>::LOADS], bu[QuadShape<1>::LOADS];
@@ -693,6 +746,7 @@ extern "C" __global__ __launch_bounds__(256) void dec_step(StepParams P) {
       u32x4 wv[8];
       norm_weights(P.ffn_norm + layer * kHidden, gemv_col, wv);  // requested before the wait
       if (!W.wait(cur + kWRes + rep * kNRes, 512, step_tag(seq, layer, kPhRes), vec)) return;
+      STAMP(layer, 9);
       u32x4 xr[1][8];
       rmsnorm_lds_w(reinterpret_cast<const uint16_t*>(vec), gemv_col, wv, xr[0]);
       uint8_t* lds = stage + wave * kGemvLds;
@@ -707,6 +761,7 @@ extern "C" __global__ __launch_bounds__(256) void dec_step(StepParams P) {
       if ((lane & 31) < kRep)
         put_word(cur + kWAct + (lane & 31) * kNAct + 2 * b + (lane >> 5), act | (next << 16),
                  step_tag(seq, layer, kPhAct));
+      STAMP(layer, 10);
     }
 
     // ---- E: ffn_down + residual: every workgroup takes row quad wg, wave
@@ -723,6 +778,7 @@ extern "C" __global__ __launch_bounds__(256) void dec_step(StepParams P) {
         return;
       const _Float16 r_row = as_half(reinterpret_cast<const uint16_t*>(vec + 1536)[lane >> 4]);
       if (!W.wait(cur + kWAct + rep * kNAct, 1536, step_tag(seq, layer, kPhAct), vec)) return;
+      STAMP(layer, 11);
       if (wave < 3) {
         u32x4 xr[1][8];
         lds_x_cols<1>(reinterpret_cast<const uint16_t*>(vec) + 1024 * wave, xr);
@@ -738,6 +794,7 @@ extern "C" __global__ __launch_bounds__(256) void dec_step(StepParams P) {
         acc = reduce_row16(acc);
         put_quad<kRep>(cur + kWH, kNH, quad, acc, step_tag(seq, layer, kPhH),
                  [&](float a, int) { return (uint32_t)residual_f16(r_row, a); });
+        STAMP(layer, 12);
       }
     }
   }
@@ -746,6 +803,7 @@ extern "C" __global__ __launch_bounds__(256) void dec_step(StepParams P) {
   const uint64_t* hfin = P.words + ((kLayers - 1) & 1) * kWParity + kWH + rep * kNH;
   const uint32_t tag_h = step_tag(seq, kLayers - 1, kPhH);
   const uint32_t tag_arg = step_tag(seq, kLayers, kPhArg);
+  STAMP(kLayers, 0);
   if (P.head) {
     bool ok = true;
     vocab_body_xp<VOCAB_NT_LOADS != 0, true>(
@@ -755,6 +813,7 @@ extern "C" __global__ __launch_bounds__(256) void dec_step(StepParams P) {
           u32x4 wv[8];
           norm_weights(P.output_norm, col, wv);  // requested before the wait
           ok = W.wait(hfin, 512, tag_h, vec);
+          STAMP(kLayers, 1);
           if (ok) rmsnorm_lds_w(reinterpret_cast<const uint16_t*>(vec), col, wv, xr);
           if (wg == 0 && t < 16) {
 #pragma unroll
@@ -767,12 +826,20 @@ extern "C" __global__ __launch_bounds__(256) void dec_step(StepParams P) {
           put_word(P.words + kWArg + 2 * wg + 1, (uint32_t)key, tag_arg);
         });
     if (!ok) return;
+    STAMP(kLayers, 2);
   }
+#if DEC_STEP_STAMPS
+  if (t == 0 && stamp_i >= 0 && wg != 0) {
+    for (int i = 0; i < (kLayers + 1) * kStampPoints; ++i)
+      P.stamps[stamp_i * (kLayers + 1) * kStampPoints + i] = (&s_stamp[0][0])[i];
+  }
+#endif
 
   // ---- workgroup 0: token, position, sequence number ----
   if (wg != 0) return;
   if (P.head) {
     if (!W.wait(P.words + kWArg, 2 * kStepWgs, tag_arg, vec)) return;
+    STAMP(kLayers, 3);
     uint64_t key = ((uint64_t)vec[2 * t] << 32) | vec[2 * t + 1];
     key = wave_max_u64(key);
     __shared__ uint64_t s_key[4];
@@ -795,4 +862,10 @@ extern "C" __global__ __launch_bounds__(256) void dec_step(StepParams P) {
     }
     __hip_atomic_store(P.seq, seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
+  STAMP(kLayers, 4);
+#if DEC_STEP_STAMPS
+  if (t == 0)
+    for (int i = 0; i < (kLayers + 1) * kStampPoints; ++i)
+      P.stamps[i] = (&s_stamp[0][0])[i];  // workgroup 0 is slot 0
+#endif
 }

@@ -941,6 +941,7 @@ struct StepParams {
   void* abort_word;
   void* status;
   void* on_out;
+  void* stamps;
   int32_t max_seq;
   int32_t advance;
   int32_t head;
@@ -977,6 +978,7 @@ int launch_step(const qwen3_weights* w, void* k_cache, void* v_cache, int64_t ma
   p.abort_word = mb(scratch) + kScrAbort;
   p.status = mb(scratch) + kScrStatus;
   p.on_out = mb(scratch) + kScrOn;
+  p.stamps = mb(scratch) + kScrPart;  // unused by this step unless built with timestamps
   p.max_seq = (int32_t)max_seq;
   p.advance = advance ? 1 : 0;
   p.head = head ? 1 : 0;
@@ -1420,6 +1422,7 @@ int64_t qwen3_scratch_offset(const char* name) {
   if (n == "q_roped") return (int64_t)kScrQr;
   if (n == "fn") return (int64_t)kScrFn;
   if (n == "on") return (int64_t)kScrOn;
+  if (n == "part") return (int64_t)kScrPart;
   return -1;
 }
 
