@@ -115,6 +115,57 @@ __device__ __forceinline__ void rmsnorm_lds_w(const uint16_t* __restrict__ h, Co
   rmsnorm_apply(hv, wv, xr);
 }
 
+// The loads of q8_quad_load<P> / q8_chunk_load<P> as copies from memory
+// straight into LDS (global_load_lds, 16 bytes per lane and instruction): load
+// i of lane l lands at lds + 1024 i + 16 l, the layout q8_quad_stage writes,
+// so q8_quad_lane_dot reads the staged quad from there.  No register holds the
+// data while it is in flight; `lds` must be wave-uniform.  The wave may read
+// the bytes once its vector memory counter has drained past these loads (the
+// compiler waits for that before the wave's next LDS access).  PACE > 0
+// sleeps 64 PACE cycles after each 1 KiB piece, so hundreds of workgroups
+// prefetching at once spread their requests instead of filling the memory
+// queues in one burst (which delays every hand-off in flight at that time).
+template <int P, int PACE = 0>
+__device__ __forceinline__ void q8_quad_prefetch(const uint8_t* __restrict__ w, int n_rows,
+                                                 int quad, uint8_t* lds) {
+  constexpr int ROWB = QuadShape<P>::ROWB;
+  const int lane = threadIdx.x & 63;
+  const int row0 = quad * 4;
+  int rows_here = n_rows - row0;
+  rows_here = rows_here < 4 ? rows_here : 4;
+  const int last = rows_here * (ROWB / 16) - 1;
+  const u32x4* src = reinterpret_cast<const u32x4*>(w + (size_t)row0 * ROWB);
+#pragma unroll
+  for (int i = 0; i < QuadShape<P>::LOADS; ++i) {
+    const int c = i * 64 + lane;
+    __builtin_amdgcn_global_load_lds((const GLOBAL_AS void*)(src + (c < last ? c : last)),
+                                     (__attribute__((address_space(3))) void*)(lds + 1024 * i),
+                                     16, 0, 0);
+    if constexpr (PACE > 0) __builtin_amdgcn_s_sleep(PACE);
+  }
+}
+
+template <int P, int PACE = 0>
+__device__ __forceinline__ void q8_chunk_prefetch(const uint8_t* __restrict__ w, int n_rows,
+                                                  int quad, int c, uint8_t* lds) {
+  const int lane = threadIdx.x & 63;
+  const int row0 = quad * 4;
+  int rows_here = n_rows - row0;
+  rows_here = rows_here < 4 ? rows_here : 4;
+  const int last = rows_here * 68 - 1;
+  const uint8_t* base = w + (size_t)row0 * (kChunkBytes * P) + kChunkBytes * c;
+#pragma unroll
+  for (int i = 0; i < QuadShape<1>::LOADS; ++i) {
+    int j = i * 64 + lane;
+    j = j < last ? j : last;
+    const int r = j / 68;
+    __builtin_amdgcn_global_load_lds(
+        (const GLOBAL_AS void*)(base + (size_t)r * (kChunkBytes * P) + 16 * (j - 68 * r)),
+        (__attribute__((address_space(3))) void*)(lds + 1024 * i), 16, 0, 0);
+    if constexpr (PACE > 0) __builtin_amdgcn_s_sleep(PACE);
+  }
+}
+
 // The Q8_0 GEMV lane layout: columns [64 p16, 64 p16 + 64) in 8 pieces of 8.
 __device__ __forceinline__ int gemv_col(int m) { return 64 * (threadIdx.x & 15) + 8 * m; }
 
@@ -222,6 +273,7 @@ constexpr int kKvPrefetchBytes = 8 * 1024 + 32 * 256;
 // kv + 1024 m + 16 l, its V word of row j at kv + 8192 + 256 j + 4 l.  kv is
 // the wave's kKvPrefetchBytes region; the data may be read once the wave's
 // vector memory counter has drained past these loads.
+template <int PACE = 0>
 __device__ __forceinline__ void kv_prefetch(uint8_t* kv, const uint16_t* __restrict__ k_cache,
                                             const uint16_t* __restrict__ v_cache, int g,
                                             const SplitRange& r) {
@@ -236,6 +288,7 @@ __device__ __forceinline__ void kv_prefetch(uint8_t* kv, const uint16_t* __restr
     __builtin_amdgcn_global_load_lds((const GLOBAL_AS void*)(krow + m),
                                      (__attribute__((address_space(3))) void*)(kv + 1024 * m), 16,
                                      0, 0);
+    if constexpr (PACE > 0) __builtin_amdgcn_s_sleep(PACE);
 #pragma unroll
   for (int j = 0; j < 32; ++j) {
     const int pj = r.start + j < r.last ? r.start + j : r.last;
@@ -244,6 +297,8 @@ __device__ __forceinline__ void kv_prefetch(uint8_t* kv, const uint16_t* __restr
                                     v_cache + ((size_t)pj * kKvHeads + g) * kHeadDim) +
                                 lane),
         (__attribute__((address_space(3))) void*)(kv + 8192 + 256 * j), 4, 0, 0);
+    if constexpr (PACE > 0)
+      if ((j & 3) == 3) __builtin_amdgcn_s_sleep(PACE);
   }
 }
 
@@ -451,7 +506,9 @@ __device__ __forceinline__ void attention_group(AttnLds& L, int g, int sg, int p
     accB0 *= cB;
     accB1 *= cB;
     const int n = end - c0 < 32 ? end - c0 : 32;
-#pragma unroll
+    // unrolled by 8, not 32: fully unrolled, the compiler hoists all 64
+    // weight reads from LDS and the step kernel runs out of registers
+#pragma unroll 8
     for (int j = 0; j < 32; ++j) {
       // positions past the split hold weight 0 and a clamped (valid) row,
       // selected to 0 so a non-finite value there cannot leak in

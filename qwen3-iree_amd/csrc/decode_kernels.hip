@@ -273,39 +273,54 @@ extern "C" __global__ __launch_bounds__(256) void dec_scratch_clear(uint32_t* __
 
 // ======================================================= single launch ====
 //
-// dec_step: the whole decode step in one launch of kStepWgs workgroups x 256
-// threads, all resident at once (cooperative launch).  Work moves between
-// workgroups as tagged words: a 64-bit word holds 32 bits of data (an f16 pair
-// or an f32) and a 32-bit tag naming (step, layer, phase); a producer stores
-// the word with one agent-scope atomic store, a consumer polls it with
-// agent-scope atomic loads until the tag matches.  A word is its own flag, so
-// no fence, counter or barrier is needed between workgroups, and a consumer
-// requests the weights of its next phase before it starts waiting.
+// dec_step: the whole decode step in one launch of kStepWgs = 512 workgroups
+// x 256 threads, two per CU, all resident at once (cooperative launch).  Work
+// moves between workgroups as tagged words: a 64-bit word holds 32 bits of
+// data (an f16 pair or an f32) and a 32-bit tag naming (step, layer, phase); a
+// producer stores the word with one agent-scope atomic store, a consumer polls
+// it with agent-scope atomic loads until the tag matches.  A word is its own
+// flag, so no fence, counter or barrier is needed between workgroups.
 //
-// Per layer (workgroup ranges; 4 waves each):
-//   A  all 256        qkv quads 4 wg + w: rms_norm(h) (h = the embedding row
-//                     for layer 0, else the previous layer's H words), GEMV,
-//                     rows published in pairs -> Q, K, V words
-//   B  0..63          attention for kv head wg / 8, split group wg % 8
-//                     (attention_group, q/k/v from the tagged words) -> PART
-//   B' 0,8,..,56      the split-group-0 workgroup of each kv head merges the
-//                     8 partials of its 2 query heads -> ATT words
-//   C  64..191        attn_o + residual: 2 row quads per workgroup, one
-//                     1024-column chunk per wave, summed in LDS -> RES words
-//   D  64..255        gate/up quad pairs + SwiGLU -> ACT words (not on the
-//                     attention workgroups: their merge and cache prefetch
-//                     would sit ahead of the residual poll in their load
-//                     queues and delay every workgroup's SwiGLU input)
-//   E  all 256        ffn_down + residual: row quad wg, waves 0-2 one
-//                     1024-column chunk each, summed in LDS -> H words
-// then the vocab GEMV over all workgroups (each publishes its best key as two
-// words), and workgroup 0 reduces the 256 keys: token, optional output slot,
+// Each workgroup keeps one role for the whole step: one phase per layer (or
+// two that lie far apart), so it requests the weights of its next phase
+// straight into LDS (global_load_lds) right after finishing the current one,
+// a layer (or most of one) ahead of use.  The weights have landed long before
+// the phase's input arrives, and a wave's in-order load queue holds no weight
+// load ahead of a poll whose answer is on the critical path.  Roles:
+//   AD  0..255    A: q/k/v quad 4 wg + w: rms_norm(h) (h = the embedding row
+//                 for layer 0, else the previous layer's H words), GEMV -> Q,
+//                 K, V words.  D on workgroups 0..191: gate/up quad pair
+//                 4 wg + w + SwiGLU -> ACT words.  Right after A the D weights
+//                 of this layer and the A weights of the next are requested.
+//   B   256..319  attention for kv head b / 8, split group b % 8 (b = wg -
+//                 256; attention_group, q/k/v from the tagged words) -> PART;
+//                 split group 0 then merges its kv head's 8 partials of both
+//                 query heads -> ATT words; then the next layer's first cache
+//                 chunk is requested into LDS.
+//   C   320..447  attn_o + residual: row quads 2 c, 2 c + 1 (c = wg - 320), one
+//                 1024-column chunk per wave, summed in LDS -> RES words.
+//   E   448..511  ffn_down + residual: row quad 4 e + w per wave over all 3072
+//                 columns (e = wg - 448) -> H words.
+// Every row is computed with the per-phase kernels' operations in their order
+// (same device functions), so both step modes give the same bits.  Then the
+// vocab GEMV over all 512 workgroups (each publishes its best key as two
+// words), and workgroup 0 reduces the 512 keys: token, optional output slot,
 // position advance, sequence number.  Layer-indexed words alternate between
-// two buffers by layer parity.  Every wait is bounded: on timeout a workgroup
-// sets status bit 1 and an abort word, and every waiting workgroup gives up.
+// two buffers by layer parity (a word of layer l is rewritten at layer l + 2,
+// after every reader of it has published something the writer waited for).
+// Every wait is bounded: on timeout a workgroup sets status bit 1 and an abort
+// word, and every waiting workgroup gives up.
 namespace {
 
-constexpr int kStepWgs = 256;
+constexpr int kStepWgs = 448;
+constexpr int kAdBase = 0, kDCount = 192;  // A on all 256, D on the first 192
+constexpr int kBBase = 256;                // 64 attention workgroups
+constexpr int kCBase = 320;                // 128 attn_o + ffn_down workgroups
+// The vocab GEMV runs on the first kVocabWgs workgroups.
+#ifndef DEC_VOCAB_WGS
+#define DEC_VOCAB_WGS 256
+#endif
+constexpr int kVocabWgs = DEC_VOCAB_WGS;
 // Vectors that every (or nearly every) workgroup waits for -- h, the
 // attention output, the attn_o + residual output, the SwiGLU output -- are
 // published in kRep replicas and workgroup w polls replica w % kRep: with one
@@ -449,6 +464,9 @@ struct Waiter {
       for (int k = 0; k < kMax; ++k)
         if (t + 256 * k < n && (uint32_t)(w[k] >> 32) != tag) w[k] = get_word(src(t + 256 * k));
     }
+    // every thread is past its previous reads of dst (a phase may read the
+    // last vector right up to its next wait) before any overwrites it
+    __syncthreads();
     if (ok) {
 #pragma unroll
       for (int k = 0; k < kMax; ++k)
@@ -504,18 +522,20 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
 // Timestamp build (-DDEC_STEP_STAMPS=1, for measuring where a step's time
 // goes; the product build compiles none of this): thread 0 of the workgroups
 // listed in stamp_slot reads the 100 MHz real-time counter at the phase
-// boundaries below into LDS, [layer][point] for layers 0..27 and [28][point]
-// for the vocab phase, and copies them to P.stamps[slot][29][16] at the end.
-//   per layer: 0 layer start, 1 h ready (A), 2 q/k/v published, 3 q/k/v ready
-//   (B), 4 partial published, 5 partials ready (B'), 6 attention output
-//   published, 7 attention output ready (C), 8 residual published, 9 residual
-//   ready (D), 10 SwiGLU published, 11 SwiGLU ready (E), 12 h published,
-//   13 A: x normalised, 14 A: weights staged in LDS, 15 A: row sums formed
+// boundaries below into LDS (its low 32 bits: differences stay exact for 42
+// s), [layer 0..27, or 28 for the vocab phase][point], and copies them to
+// P.stamps[slot][29][16] (u64, zero-extended) at the end.
+//   per layer: 0 layer start, 1 h ready (A), 13 x normalised (A), 2 q/k/v
+//   published, 9 residual ready (D), 10 SwiGLU published, 3 q/k/v ready (B),
+//   4 partial published, 5 partials ready (merge), 6 attention output
+//   published, 14 h rows ready (C), 7 attention output ready (C), 8 residual
+//   published, 11 SwiGLU ready (E), 12 h published
 //   vocab: 0 start, 1 h ready, 2 key published, 3 keys ready (wg 0), 4 token
 #ifndef DEC_STEP_STAMPS
 #define DEC_STEP_STAMPS 0
 #endif
-constexpr int kStampWgs[16] = {0, 1, 7, 8, 56, 63, 64, 65, 127, 128, 191, 192, 200, 224, 254, 255};
+constexpr int kStampWgs[16] = {0,   1,   100, 191, 192, 255, 256, 257,
+                               264, 319, 320, 321, 383, 384, 446, 447};
 constexpr int kStampPoints = 16;
 __device__ __forceinline__ int stamp_slot(int wg) {
 #pragma unroll
@@ -524,17 +544,62 @@ __device__ __forceinline__ int stamp_slot(int wg) {
   return -1;
 }
 
-constexpr int kGemvLds = QuadShape<3>::LDS_BYTES;  // the largest per-wave staging
-constexpr int kVecWords = 2 * kAttnGroups * 130;     // 2080: the largest polled vector
-constexpr int kStepLds = 4 * kVecWords + 4 * kGemvLds;
+constexpr int kVecWords = 2 * kAttnGroups * 130;  // 2080: the largest polled vector
+// Weight prefetches sleep 64 kPace* cycles between 1 KiB pieces, each set
+// spread over the time its role has before the weights are needed (the gate/up
+// weights are requested right after A, the next q/k/v weights right after D,
+// the ffn_down weights right after C, the next attn_o weights right after E,
+// the next cache chunk right after attention).  Unpaced bursts from hundreds of
+// workgroups fill the memory queues and delay the hand-offs in flight.
+#ifndef DEC_PACE_A
+#define DEC_PACE_A 32
+#endif
+#ifndef DEC_PACE_D
+#define DEC_PACE_D 32
+#endif
+#ifndef DEC_PACE_C
+#define DEC_PACE_C 32
+#endif
+#ifndef DEC_PACE_E
+#define DEC_PACE_E 32
+#endif
+#ifndef DEC_PACE_KV
+#define DEC_PACE_KV 0
+#endif
+constexpr int kPaceA = DEC_PACE_A, kPaceD = DEC_PACE_D, kPaceC = DEC_PACE_C, kPaceE = DEC_PACE_E,
+              kPaceKV = DEC_PACE_KV;
+
+// LDS of one workgroup, by role (a union: each workgroup uses one member).
+// Weight buffers are per wave and filled by that wave's global_load_lds.
+struct StepLdsAd {
+  uint8_t wa[4][QuadShape<1>::LDS_BYTES];     // the q/k/v quad of each wave
+  uint8_t wd[4][2][QuadShape<1>::LDS_BYTES];  // its gate quad and up quad
+};
+struct StepLdsB {
+  uint8_t kv[kAttnWaves][kKvPrefetchBytes];  // each wave's first cache chunk
+  AttnLds attn;
+};
+struct StepLdsCE {
+  uint8_t wc[4][QuadShape<1>::LDS_BYTES];     // C: each wave's chunk of its quad
+  uint8_t we[4][2][QuadShape<1>::LDS_BYTES];  // E: chunks 0, 1 (even waves) or 2 (odd)
+  float c_part[2][128];                       // C: the chunk sums of the two quads
+  float e_part[2][64];                        // E: chunk 2's lane sums of the two quads
+};
+union StepLds {
+  StepLdsAd ad;
+  StepLdsB b;
+  StepLdsCE ce;
+};
+// two workgroups per CU: 80 KiB each (the vocab phase adds 160 bytes)
+static_assert(sizeof(StepLds) + 4 * kVecWords <= 81920 - 256, "dec_step LDS");
 
 }  // namespace
 
-extern "C" __global__ __launch_bounds__(256) void dec_step(StepParams P) {
-  __shared__ __attribute__((aligned(16))) uint8_t smem[kStepLds];
+extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void dec_step(StepParams P) {
+  __shared__ __attribute__((aligned(16))) StepLds S;
+  __shared__ __attribute__((aligned(16))) uint32_t vec[kVecWords];  // polled words' data
   __shared__ int s_abort;
-  uint32_t* vec = reinterpret_cast<uint32_t*>(smem);               // polled words' data
-  uint8_t* stage = smem + 4 * kVecWords;                            // GEMV staging / attention
   const int wg = blockIdx.x;
   const int rep = wg % kRep;  // the replica this workgroup polls
   const int t = threadIdx.x;
@@ -542,14 +607,15 @@ extern "C" __global__ __launch_bounds__(256) void dec_step(StepParams P) {
   const int lane = t & 63;
   if (t == 0) s_abort = 0;
 #if DEC_STEP_STAMPS
-  __shared__ uint64_t s_stamp[kLayers + 1][kStampPoints];
+  __shared__ uint32_t s_stamp[kLayers + 1][kStampPoints];
   const int stamp_i = stamp_slot(wg);
-#define STAMP(layer, k)                                                                   \
-  do {                                                                                    \
-    if (t == 0 && stamp_i >= 0) s_stamp[layer][k] = __builtin_amdgcn_s_memrealtime();     \
-  } while (0)
   if (t == 0)
     for (int i = 0; i < (kLayers + 1) * kStampPoints; ++i) (&s_stamp[0][0])[i] = 0;
+#define STAMP(layer, k)                                                                    \
+  do {                                                                                     \
+    if (t == 0 && stamp_i >= 0)                                                            \
+      s_stamp[layer][k] = (uint32_t)__builtin_amdgcn_s_memrealtime();                       \
+  } while (0)
 #else
 #define STAMP(layer, k) \
   do {                  \
@@ -562,70 +628,89 @@ extern "C" __global__ __launch_bounds__(256) void dec_step(StepParams P) {
   tok = (tok < 0 || tok >= kVocab) ? 0 : tok;
   const uint16_t* emb = P.token_embd + (size_t)tok * kHidden;
   const Waiter W{P.abort_word, P.status, P.seq, seq, P.spin_limit, &s_abort};
-  float rope_cs[2], rope_sn[2];  // the position's RoPE angles, for every layer
-  // Attention workgroups keep the first 32 cache rows of their split for the
-  // next layer in LDS: requested (global_load_lds) as soon as the current
-  // layer's attention is done, they arrive while the workgroup works on other
-  // phases (layer 0's at the start).
-  __shared__ __attribute__((aligned(16))) uint8_t kv_lds[kAttnWaves * kKvPrefetchBytes];
-  __shared__ float e_part[3][128];  // attn_o / ffn_down: the chunks' lane sums
-  uint8_t* const kv_mine = kv_lds + wave * kKvPrefetchBytes;
   const int pos_c = pos_raw < 0 ? 0 : (pos_raw >= P.max_seq ? P.max_seq - 1 : pos_raw);
-  const SplitRange my_split = split_range((wg % kAttnGroups) * kAttnWaves + wave, pos_c);
-  if (wg < 64) {
-    kv_prefetch(kv_mine, P.k_cache, P.v_cache, wg / kAttnGroups, my_split);
-    rope_angles(pos_c, rope_cs, rope_sn);
-  }
   __syncthreads();
 
-  for (int layer = 0; layer < kLayers; ++layer) {
-    uint64_t* cur = P.words + (layer & 1) * kWParity;
-    const uint64_t* prev = P.words + ((layer & 1) ^ 1) * kWParity;
-    const uint32_t tag_prev_h = step_tag(seq, layer - 1, kPhH);
-    STAMP(layer, 0);
-
-    // ---- A: q/k/v ----
-    {
-      const int quad = 4 * wg + wave;  // 0..1023
-      const uint8_t* w = quad < 512 ? P.wq : (quad < 768 ? P.wk : P.wv);
-      const int n = quad < 512 ? 2048 : 1024;
-      const int qd = quad < 512 ? quad : (quad < 768 ? quad - 512 : quad - 768);
-      const int64_t bpl = (int64_t)n * (kHidden / 32 * 34);
-      const auto h_src = [=](int i) { return prev + kWH + rep * kNH + i; };
-      uint64_t hp[Waiter::kMax];
-      if (layer > 0) W.poll_begin(512, h_src, hp);  // ahead of the weight loads
-      u32x4 buf[QuadShape<1>::LOADS];
-      q8_quad_load<1>(w + layer * bpl, n, qd, buf);
+  if (wg < kBBase) {
+    // ================= AD: q/k/v of every layer; gate/up on 0..191 =================
+    const int quad = 4 * wg + wave;  // 0..1023: q quads, then k, then v
+    const uint8_t* wsel = quad < 512 ? P.wq : (quad < 768 ? P.wk : P.wv);
+    const int n = quad < 512 ? 2048 : 1024;
+    const int qd = quad < 512 ? quad : (quad < 768 ? quad - 512 : quad - 768);
+    const int64_t bpl = (int64_t)n * (kHidden / 32 * 34);
+    const bool has_d = wg < kDCount;
+    const int b = 4 * wg + wave;  // gate/up quad pair (has_d)
+    constexpr int64_t bpl_gu = (int64_t)(2 * kFfn) * (kHidden / 32 * 34);
+    uint8_t* const la = S.ad.wa[wave];
+    uint8_t* const lg = S.ad.wd[wave][0];
+    uint8_t* const lu = S.ad.wd[wave][1];
+    q8_quad_prefetch<1>(wsel, n, qd, la);
+    for (int layer = 0; layer < kLayers; ++layer) {
+      uint64_t* cur = P.words + (layer & 1) * kWParity;
+      const uint64_t* prev = P.words + ((layer & 1) ^ 1) * kWParity;
+      STAMP(layer, 0);
+      // ---- A ----
       u32x4 xr[1][8];
       const uint16_t* an = P.attn_norm + layer * kHidden;
       if (layer == 0) {
         rmsnorm_gemv_x<false>(emb, an, xr[0]);
       } else {
+        const auto h_src = [=](int i) { return prev + kWH + rep * kNH + i; };
+        uint64_t hp[Waiter::kMax];
+        W.poll_begin(512, h_src, hp);
         u32x4 wv[8];
         norm_weights(an, gemv_col, wv);  // requested before the wait
-        if (!W.poll_finish(512, tag_prev_h, vec, h_src, hp)) return;
+        if (!W.poll_finish(512, step_tag(seq, layer - 1, kPhH), vec, h_src, hp)) return;
         STAMP(layer, 1);
         rmsnorm_lds_w(reinterpret_cast<const uint16_t*>(vec), gemv_col, wv, xr[0]);
       }
       STAMP(layer, 13);
-      uint8_t* lds = stage + wave * kGemvLds;
-      q8_quad_stage<1>(buf, lds);
-      __syncthreads();
-      STAMP(layer, 14);
-      const float acc = q8_quad_dot<1>(lds, xr);
-      STAMP(layer, 15);
+      const float acc = q8_quad_dot<1>(la, xr);
       uint64_t* dst = quad < 512 ? cur + kWQ : (quad < 768 ? cur + kWK : cur + kWV);
       put_quad<1>(dst, 0, qd, acc, step_tag(seq, layer, kPhQKV),
-               [](float a, int) { return (uint32_t)f32_to_f16_bits(a); });
+                  [](float a, int) { return (uint32_t)f32_to_f16_bits(a); });
       STAMP(layer, 2);
+      // this layer's gate/up weights (the next layer's q/k/v weights follow D)
+      if (has_d) {
+        const uint8_t* wl = P.wgu + layer * bpl_gu;
+        q8_quad_prefetch<1, kPaceD>(wl, 2 * kFfn, b, lg);
+        q8_quad_prefetch<1, kPaceD>(wl, 2 * kFfn, kFfn / 4 + b, lu);
+      }
+      // ---- D: gate/up + SwiGLU ----
+      if (has_d) {
+        u32x4 wv[8];
+        norm_weights(P.ffn_norm + layer * kHidden, gemv_col, wv);  // requested before the wait
+        if (!W.wait(cur + kWRes + rep * kNRes, 512, step_tag(seq, layer, kPhRes), vec)) return;
+        STAMP(layer, 9);
+        u32x4 xd[1][8];
+        rmsnorm_lds_w(reinterpret_cast<const uint16_t*>(vec), gemv_col, wv, xd[0]);
+        const float ag = q8_quad_dot<1>(lg, xd);
+        const float au = q8_quad_dot<1>(lu, xd);
+        const uint32_t act = swiglu_f16(ag, au);
+        const uint32_t next = __shfl(act, (lane + 16) & 63, 64);
+        if ((lane & 31) < kRep)
+          put_word(cur + kWAct + (lane & 31) * kNAct + 2 * b + (lane >> 5), act | (next << 16),
+                   step_tag(seq, layer, kPhAct));
+        STAMP(layer, 10);
+      }
+      if (layer + 1 < kLayers) q8_quad_prefetch<1, kPaceA>(wsel + (layer + 1) * bpl, n, qd, la);
     }
-
-    // ---- B: attention, B': merge ----
-    if (wg < 64) {
-      const int g = wg / kAttnGroups;
-      const int sg = wg % kAttnGroups;
+  } else if (wg < kCBase) {
+    // ================= B: attention (+ merge on split group 0) =================
+    const int bw = wg - kBBase;
+    const int g = bw / kAttnGroups;
+    const int sg = bw % kAttnGroups;
+    uint8_t* const kv_mine = S.b.kv[wave];
+    // the first chunk of each wave's split stays in LDS: requested for layer 0
+    // now, for layer l + 1 as soon as layer l's attention (and merge) is done
+    const SplitRange my_split = split_range(sg * kAttnWaves + wave, pos_c);
+    kv_prefetch(kv_mine, P.k_cache, P.v_cache, g, my_split);
+    float rope_cs[2], rope_sn[2];  // the position's RoPE angles, for every layer
+    rope_angles(pos_c, rope_cs, rope_sn);
+    for (int layer = 0; layer < kLayers; ++layer) {
+      uint64_t* cur = P.words + (layer & 1) * kWParity;
+      STAMP(layer, 0);
       const int64_t cache_layer = (int64_t)layer * P.max_seq * (kKvHeads * kHeadDim);
-      AttnLds& L = *reinterpret_cast<AttnLds*>(stage);
       bool ok = true;
       const uint32_t tq = step_tag(seq, layer, kPhQKV);
       // q heads 2g, 2g+1 (words 128g..), k head g, v head g (words 64g..)
@@ -635,10 +720,9 @@ extern "C" __global__ __launch_bounds__(256) void dec_step(StepParams P) {
       };
       uint64_t qkv_poll[Waiter::kMax];
       attention_group(
-          L, g, sg, pos_raw, rope_cs, rope_sn, P.max_seq, P.q_norm + layer * kHeadDim,
-          P.k_norm + layer * kHeadDim,
-          P.k_cache + cache_layer, P.v_cache + cache_layer, nullptr, kv_mine,
-          [&] { W.poll_begin(256, qkv_src, qkv_poll); },
+          S.b.attn, g, sg, pos_raw, rope_cs, rope_sn, P.max_seq, P.q_norm + layer * kHeadDim,
+          P.k_norm + layer * kHeadDim, P.k_cache + cache_layer, P.v_cache + cache_layer, nullptr,
+          kv_mine, [&] { W.poll_begin(256, qkv_src, qkv_poll); },
           [&](uint32_t (&xw)[3], uint32_t& v_new) {
             ok = W.poll_finish(256, tq, vec, qkv_src, qkv_poll);
             STAMP(layer, 3);
@@ -648,14 +732,14 @@ extern "C" __global__ __launch_bounds__(256) void dec_step(StepParams P) {
             v_new = vec[192 + lane];
           },
           [&](int hh, float M, float Ls, float a0, float a1) {
-            uint64_t* dst = cur + kWPart + ((2 * g + hh) * kAttnGroups + sg) * 130;
+            uint64_t* d = cur + kWPart + ((2 * g + hh) * kAttnGroups + sg) * 130;
             const uint32_t tp = step_tag(seq, layer, kPhPart);
             if (lane == 0) {
-              put_word(dst, __builtin_bit_cast(uint32_t, M), tp);
-              put_word(dst + 1, __builtin_bit_cast(uint32_t, Ls), tp);
+              put_word(d, __builtin_bit_cast(uint32_t, M), tp);
+              put_word(d + 1, __builtin_bit_cast(uint32_t, Ls), tp);
             }
-            put_word(dst + 2 + 2 * lane, __builtin_bit_cast(uint32_t, a0), tp);
-            put_word(dst + 3 + 2 * lane, __builtin_bit_cast(uint32_t, a1), tp);
+            put_word(d + 2 + 2 * lane, __builtin_bit_cast(uint32_t, a0), tp);
+            put_word(d + 3 + 2 * lane, __builtin_bit_cast(uint32_t, a1), tp);
           });
       if (!ok) return;
       STAMP(layer, 4);
@@ -694,117 +778,107 @@ extern "C" __global__ __launch_bounds__(256) void dec_step(StepParams P) {
       }
       if (layer + 1 < kLayers) {  // the next layer's first chunk, into this wave's LDS region
         const int64_t next = (int64_t)(layer + 1) * P.max_seq * (kKvHeads * kHeadDim);
-        kv_prefetch(kv_mine, P.k_cache + next, P.v_cache + next, g, my_split);
+        kv_prefetch<kPaceKV>(kv_mine, P.k_cache + next, P.v_cache + next, g, my_split);
       }
     }
-
-    // ---- C: attn_o + residual: workgroups 64..191, row quads 2 (wg - 64)
-    // and 2 (wg - 64) + 1 (waves 0-1 and 2-3), one 1024-column chunk per wave,
-    // the two chunk sums added in LDS in the per-phase kernel's order ----
-    if (wg >= 64 && wg < 192) {
-      const int quad = 2 * (wg - 64) + (wave >> 1);  // 0..255
-      const int c = wave & 1;
-      constexpr int64_t bpl = (int64_t)kHidden * (2 * kHidden / 32 * 34);
-      u32x4 buf[QuadShape<1>::LOADS];
-      q8_chunk_load<2>(P.wo + layer * bpl, kHidden, quad, c, buf);
-      const int row = 4 * quad + (lane >> 4);
+  } else {
+    // ================= CE: attn_o + residual, then ffn_down + residual =================
+    // C: row quads 2 cw and 2 cw + 1 (waves 0-1 and 2-3), one 1024-column
+    // chunk per wave, the two chunk sums added in LDS in the per-phase
+    // kernel's order.  E: the same two quads of W_down, waves 2 qi (chunks 0
+    // and 1) and 2 qi + 1 (chunk 2), the lane sums added in chunk order; the
+    // residual of each row is the value this workgroup's C just published.
+    const int cw = wg - kCBase;  // 0..127
+    const int qi = wave >> 1;
+    const int quad = 2 * cw + qi;  // 0..255
+    const int c = wave & 1;
+    constexpr int64_t bpl_o = (int64_t)kHidden * (2 * kHidden / 32 * 34);
+    constexpr int64_t bpl_dn = (int64_t)kHidden * (kFfn / 32 * 34);
+    uint8_t* const lwc = S.ce.wc[wave];
+    uint8_t* const lwe0 = S.ce.we[wave][0];
+    uint8_t* const lwe1 = S.ce.we[wave][1];
+    auto prefetch_e = [&](int layer) {
+      const uint8_t* wl = P.wdn + layer * bpl_dn;
+      if (c == 0) {
+        q8_chunk_prefetch<3, kPaceE>(wl, kHidden, quad, 0, lwe0);
+        q8_chunk_prefetch<3, kPaceE>(wl, kHidden, quad, 1, lwe1);
+      } else {
+        q8_chunk_prefetch<3, kPaceE>(wl, kHidden, quad, 2, lwe0);
+      }
+    };
+    q8_chunk_prefetch<2>(P.wo, kHidden, quad, c, lwc);
+    prefetch_e(0);
+    const int row = 4 * quad + (lane >> 4);
+    for (int layer = 0; layer < kLayers; ++layer) {
+      uint64_t* cur = P.words + (layer & 1) * kWParity;
+      const uint64_t* prev = P.words + ((layer & 1) ^ 1) * kWParity;
+      STAMP(layer, 0);
+      // ---- C ----
       _Float16 h_row;
       if (layer == 0) {
         h_row = as_half(load_global_u16(emb + row));
       } else {
-        // this workgroup's 8 residual rows = h words [4 (wg - 64), +4)
-        if (!W.wait(prev + kWH + rep * kNH + 4 * (wg - 64), 4, tag_prev_h, vec + 1024)) return;
-        h_row = as_half(reinterpret_cast<const uint16_t*>(vec + 1024)[row - 8 * (wg - 64)]);
+        // this workgroup's 8 residual rows = h words [4 cw, +4)
+        if (!W.wait(prev + kWH + rep * kNH + 4 * cw, 4, step_tag(seq, layer - 1, kPhH),
+                    vec + 1024))
+          return;
+        STAMP(layer, 14);
+        h_row = as_half(reinterpret_cast<const uint16_t*>(vec + 1024)[row - 8 * cw]);
       }
       if (!W.wait(cur + kWAtt + rep * kNAtt, 1024, step_tag(seq, layer, kPhAtt), vec)) return;
       STAMP(layer, 7);
-      u32x4 xr[1][8];
-      lds_x_cols<1>(reinterpret_cast<const uint16_t*>(vec) + 1024 * c, xr);
-      uint8_t* lds = stage + wave * kGemvLds;
-      q8_quad_stage<1>(buf, lds);
-      e_part[wave & 2][lane + 64 * c] = q8_quad_lane_dot<1>(lds, xr);
+      {
+        u32x4 xr[1][8];
+        lds_x_cols<1>(reinterpret_cast<const uint16_t*>(vec) + 1024 * c, xr);
+        S.ce.c_part[qi][lane + 64 * c] = q8_quad_lane_dot<1>(lwc, xr);
+      }
       __syncthreads();
+      uint16_t res_row = 0;  // this row's attn_o + residual (waves with c == 0)
       if (c == 0) {
         float acc = 0.0f;
-        acc += e_part[wave][lane];
-        acc += e_part[wave][lane + 64];
+        acc += S.ce.c_part[qi][lane];
+        acc += S.ce.c_part[qi][lane + 64];
         acc = reduce_row16(acc);
+        res_row = residual_f16(h_row, acc);
         put_quad<kRep>(cur + kWRes, kNRes, quad, acc, step_tag(seq, layer, kPhRes),
-                 [&](float a, int) { return (uint32_t)residual_f16(h_row, a); });
+                       [&](float, int) { return (uint32_t)res_row; });
         STAMP(layer, 8);
       }
-    }
-
-    // ---- D: gate/up + SwiGLU ----
-    if (wg >= 64) {
-      const int b = 4 * (wg - 64) + wave;  // 0..767
-      constexpr int64_t bpl = (int64_t)(2 * kFfn) * (kHidden / 32 * 34);
-      const uint8_t* wl = P.wgu + layer * bpl;
-      u32x4 bg[QuadShape<1>::LOADS], bu[QuadShape<1>::LOADS];
-      q8_quad_load<1>(wl, 2 * kFfn, b, bg);
-      q8_quad_load<1>(wl, 2 * kFfn, kFfn / 4 + b, bu);
-      u32x4 wv[8];
-      norm_weights(P.ffn_norm + layer * kHidden, gemv_col, wv);  // requested before the wait
-      if (!W.wait(cur + kWRes + rep * kNRes, 512, step_tag(seq, layer, kPhRes), vec)) return;
-      STAMP(layer, 9);
-      u32x4 xr[1][8];
-      rmsnorm_lds_w(reinterpret_cast<const uint16_t*>(vec), gemv_col, wv, xr[0]);
-      uint8_t* lds = stage + wave * kGemvLds;
-      constexpr int LDSB = QuadShape<1>::LDS_BYTES;
-      q8_quad_stage<1>(bg, lds);
-      q8_quad_stage<1>(bu, lds + LDSB);
-      __syncthreads();
-      const float ag = q8_quad_dot<1>(lds, xr);
-      const float au = q8_quad_dot<1>(lds + LDSB, xr);
-      const uint32_t act = swiglu_f16(ag, au);
-      const uint32_t next = __shfl(act, (lane + 16) & 63, 64);
-      if ((lane & 31) < kRep)
-        put_word(cur + kWAct + (lane & 31) * kNAct + 2 * b + (lane >> 5), act | (next << 16),
-                 step_tag(seq, layer, kPhAct));
-      STAMP(layer, 10);
-    }
-
-    // ---- E: ffn_down + residual: every workgroup takes row quad wg, wave
-    // c < 3 the quad's chunk c; the chunks' lane sums meet in LDS in chunk
-    // order (the per-phase kernel's order) ----
-    {
-      const int quad = wg;
-      constexpr int64_t bpl = (int64_t)kHidden * (kFfn / 32 * 34);
-      u32x4 buf[QuadShape<1>::LOADS];
-      if (wave < 3) q8_chunk_load<3>(P.wdn + layer * bpl, kHidden, quad, wave, buf);
-      // the quad's 4 residual rows: words 2 quad, 2 quad + 1
-      if (!W.wait(cur + kWRes + rep * kNRes + 2 * quad, 2, step_tag(seq, layer, kPhRes),
-                  vec + 1536))
-        return;
-      const _Float16 r_row = as_half(reinterpret_cast<const uint16_t*>(vec + 1536)[lane >> 4]);
+      if (layer + 1 < kLayers)
+        q8_chunk_prefetch<2, kPaceC>(P.wo + (layer + 1) * bpl_o, kHidden, quad, c, lwc);
+      // ---- E ----
       if (!W.wait(cur + kWAct + rep * kNAct, 1536, step_tag(seq, layer, kPhAct), vec)) return;
       STAMP(layer, 11);
-      if (wave < 3) {
+      float e = 0.0f;
+      if (c == 0) {
         u32x4 xr[1][8];
-        lds_x_cols<1>(reinterpret_cast<const uint16_t*>(vec) + 1024 * wave, xr);
-        uint8_t* lds = stage + wave * kGemvLds;
-        q8_quad_stage<1>(buf, lds);
-        e_part[wave][lane] = q8_quad_lane_dot<1>(lds, xr);
+        lds_x_cols<1>(reinterpret_cast<const uint16_t*>(vec), xr);
+        e += q8_quad_lane_dot<1>(lwe0, xr);
+        lds_x_cols<1>(reinterpret_cast<const uint16_t*>(vec) + 1024, xr);
+        e += q8_quad_lane_dot<1>(lwe1, xr);
+      } else {
+        u32x4 xr[1][8];
+        lds_x_cols<1>(reinterpret_cast<const uint16_t*>(vec) + 2048, xr);
+        S.ce.e_part[qi][lane] = q8_quad_lane_dot<1>(lwe0, xr);
       }
       __syncthreads();
-      if (wave == 0) {
-        float acc = 0.0f;
-#pragma unroll
-        for (int c = 0; c < 3; ++c) acc += e_part[c][lane];
-        acc = reduce_row16(acc);
-        put_quad<kRep>(cur + kWH, kNH, quad, acc, step_tag(seq, layer, kPhH),
-                 [&](float a, int) { return (uint32_t)residual_f16(r_row, a); });
+      if (c == 0) {
+        e += S.ce.e_part[qi][lane];
+        e = reduce_row16(e);
+        put_quad<kRep>(cur + kWH, kNH, quad, e, step_tag(seq, layer, kPhH),
+                       [&](float a, int) { return (uint32_t)residual_f16(as_half(res_row), a); });
         STAMP(layer, 12);
       }
+      if (layer + 1 < kLayers) prefetch_e(layer + 1);
     }
   }
 
-  // ---- vocab GEMV + argmax ----
+  // ---- vocab GEMV + argmax over all workgroups ----
   const uint64_t* hfin = P.words + ((kLayers - 1) & 1) * kWParity + kWH + rep * kNH;
   const uint32_t tag_h = step_tag(seq, kLayers - 1, kPhH);
   const uint32_t tag_arg = step_tag(seq, kLayers, kPhArg);
   STAMP(kLayers, 0);
-  if (P.head) {
+  if (P.head && wg < kVocabWgs) {
     bool ok = true;
     vocab_body_xp<VOCAB_NT_LOADS != 0, true>(
         P.output_w,
@@ -824,23 +898,27 @@ extern "C" __global__ __launch_bounds__(256) void dec_step(StepParams P) {
         P.logits, kVocab, [&](uint64_t key) {
           put_word(P.words + kWArg + 2 * wg, (uint32_t)(key >> 32), tag_arg);
           put_word(P.words + kWArg + 2 * wg + 1, (uint32_t)key, tag_arg);
-        });
+        }, kVocabWgs);
     if (!ok) return;
     STAMP(kLayers, 2);
   }
+
 #if DEC_STEP_STAMPS
-  if (t == 0 && stamp_i >= 0 && wg != 0) {
+  if (t == 0 && stamp_i >= 0 && wg != 0)
     for (int i = 0; i < (kLayers + 1) * kStampPoints; ++i)
       P.stamps[stamp_i * (kLayers + 1) * kStampPoints + i] = (&s_stamp[0][0])[i];
-  }
 #endif
-
   // ---- workgroup 0: token, position, sequence number ----
   if (wg != 0) return;
   if (P.head) {
-    if (!W.wait(P.words + kWArg, 2 * kStepWgs, tag_arg, vec)) return;
+    if (!W.wait(P.words + kWArg, 2 * kVocabWgs, tag_arg, vec)) return;
     STAMP(kLayers, 3);
-    uint64_t key = ((uint64_t)vec[2 * t] << 32) | vec[2 * t + 1];
+    // keys of workgroups t and t + 256
+    uint64_t key = t < kVocabWgs ? ((uint64_t)vec[2 * t] << 32) | vec[2 * t + 1] : 0;
+    if (t + 256 < kVocabWgs) {
+      const uint64_t key2 = ((uint64_t)vec[512 + 2 * t] << 32) | vec[512 + 2 * t + 1];
+      key = key2 > key ? key2 : key;
+    }
     key = wave_max_u64(key);
     __shared__ uint64_t s_key[4];
     if (lane == 0) s_key[wave] = key;

@@ -492,10 +492,12 @@ __device__ __forceinline__ float f16_row_dot(const u32x4& w, const u32x4& xv, fl
 // atomic max over argmax_key, whose order is the same rule.
 // The workgroup's result reaches publish(key) on thread 0: key =
 // argmax_key(best) or 0 when the workgroup saw no candidate.
+// The rows are split over workgroups 0 .. groups - 1 (the whole grid unless a
+// caller runs the GEMV on only the first `groups` workgroups).
 template <bool NT, bool ARGMAX, class XLoad, class Publish>
 __device__ __forceinline__ void vocab_body_xp(const uint16_t* __restrict__ W, XLoad&& xload,
                                               uint16_t* __restrict__ logits, int n_rows,
-                                              Publish&& publish) {
+                                              Publish&& publish, int groups = -1) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int grp = lane >> 4;
@@ -504,7 +506,7 @@ __device__ __forceinline__ void vocab_body_xp(const uint16_t* __restrict__ W, XL
   // takes no rows)
   const int64_t wpb = blockDim.x >> 6;
   const int64_t gw = (int64_t)blockIdx.x * wpb + wave;
-  const int64_t tw = (int64_t)gridDim.x * wpb;
+  const int64_t tw = (int64_t)(groups > 0 ? groups : (int)gridDim.x) * wpb;
   const int64_t nbatch = ((int64_t)n_rows + 3) / 4;
   const int b_begin = wave < wpb ? (int)(gw * nbatch / tw) : 0;
   const int b_end = wave < wpb ? (int)((gw + 1) * nbatch / tw) : 0;

@@ -46,7 +46,7 @@ constexpr KindInfo kKinds[5] = {
 };
 
 constexpr int kVocabMaxWorkgroups = 8192;
-constexpr int kStepWorkgroups = 256;  // dec_step's fixed grid (one workgroup per CU)
+constexpr int kStepWorkgroups = 448;  // dec_step's fixed grid (up to two workgroups per CU)
 constexpr uint32_t kDefaultSpinLimit = 1u << 20;  // dec_step: poll rounds before a wait gives up
 constexpr int kQ8MaxWorkgroups = 65536;
 constexpr size_t kVocabWorkspaceBytes = 256;
@@ -347,8 +347,8 @@ int q8gemv_init(const char* code_object_path) {
   int cus = 0;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
     cus = 256;
-  // The single-launch step needs its 256 workgroups resident together: a
-  // cooperative launch on a device with at least 256 CUs that fits one per CU.
+  // The single-launch step needs its 448 workgroups resident together: a
+  // cooperative launch on a device whose CUs hold them all (two per CU).
   g.step_capable = false;
   if (g.dec_step) {
     int coop = 0, per_cu = 0;
@@ -906,7 +906,7 @@ constexpr size_t kScrAbort = 20;     // u32 abort word (single-launch step)
 // the attention partials once (layout in decode_kernels.hip)
 constexpr size_t kStepWordsParity = 4 * 512 + 1024 + 512 + 512 + 16 * 8 * 130 + 4 * 1024 +
                                     4 * 512 + 4 * 1536;
-constexpr size_t kStepWords = 2 * kStepWordsParity + 2 * 256;
+constexpr size_t kStepWords = 2 * kStepWordsParity + 2 * kStepWorkgroups;
 constexpr size_t kScrWords = (kScrPart + 16 * kAttnGroupsHost * 132 * 4 + 255) / 256 * 256;
 constexpr size_t kScrBytes = kScrWords + kStepWords * 8;
 

@@ -30,14 +30,14 @@ import numpy as np
 PKG = Path(__file__).resolve().parent
 REPO = PKG.parent
 
-POINTS = {0: "layer start", 1: "A: h ready", 13: "A: x normalised", 14: "A: weights staged",
-          15: "A: row sums formed", 2: "A: q/k/v published", 3: "B: q/k/v ready",
-          4: "B: partial published", 5: "B': partials ready", 6: "B': attention published",
+POINTS = {0: "layer start", 1: "A: h ready", 13: "A: x normalised", 2: "A: q/k/v published",
+          3: "B: q/k/v ready", 4: "B: partial published", 5: "merge: partials ready",
+          6: "merge: attention published", 14: "C: h rows ready",
           7: "C: attention ready", 8: "C: residual published", 9: "D: residual ready",
           10: "D: SwiGLU published", 11: "E: SwiGLU ready", 12: "E: h published"}
 VOCAB_POINTS = {0: "vocab start", 1: "vocab: h ready", 2: "vocab: key published",
                 3: "keys ready (wg 0)", 4: "token written (wg 0)"}
-STAMP_WGS = (0, 1, 7, 8, 56, 63, 64, 65, 127, 128, 191, 192, 200, 224, 254, 255)
+STAMP_WGS = (0, 1, 100, 191, 192, 255, 256, 257, 264, 319, 320, 321, 383, 384, 446, 447)
 TICK_US = 0.01  # s_memrealtime: 100 MHz
 
 
@@ -91,7 +91,10 @@ def main() -> int:
     step_us = e0.elapsed_ms(e1) * 1e3 / args.steps
     sess.check_status()
     raw = sess.scratch.download(np.uint64, 16 * 29 * 16, D.scratch_offset("part"))
-    st = raw.reshape(16, 29, 16).astype(np.int64)
+    # 32-bit clock reads: unwrap against workgroup 0's first stamp (0 = not reached)
+    lo = (raw & 0xFFFFFFFF).astype(np.int64).reshape(16, 29, 16)
+    ref = lo[0, 0, 0]
+    st = np.where(lo != 0, ref + ((lo - ref + (1 << 31)) % (1 << 32)) - (1 << 31), 0)
     t0 = st[0, 0, 0]
 
     print(f"# dec_step timeline — context {ctx}, one cooperative launch per step\n")
@@ -103,7 +106,7 @@ def main() -> int:
     layer_len = [(st[0, l + 1, 0] - st[0, l, 0]) * TICK_US for l in range(1, 27)]
     print(f"Layer length on workgroup 0: mean {statistics.mean(layer_len):.2f} us, min "
           f"{min(layer_len):.2f}, max {max(layer_len):.2f}; layers end to end "
-          f"{(st[0, 27, 12] - st[0, 0, 0]) * TICK_US if st[0, 27, 12] else float('nan'):.1f} us; "
+          f"{(max(st[:, 27, 12]) - st[0, 0, 0]) * TICK_US:.1f} us; "
           f"vocab phase on workgroup 0 {(st[0, 28, 4] - st[0, 28, 0]) * TICK_US:.1f} us.\n")
     print("| point | " + " | ".join(f"wg {w}" for w in STAMP_WGS) + " |")
     print("|---|" + "---|" * len(STAMP_WGS))
