@@ -307,9 +307,7 @@ def bench_prefill(Q, stream, args) -> dict:
     log(f"prefill of {n} tokens: {ms:.3f} ms (median {statistics.median(times):.3f}) = "
         f"{n / ms * 1e3:.0f} tok/s, {(gemm + attn) / ms / 1e9:.1f} TFLOP/s; as decode steps "
         f"{steps_ms:.1f} ms")
-    for spec in args.prefill_tiling or []:
-        rows, split = (int(x) for x in spec.split(":"))
-        D.set_prefill_tiling(rows, split)
+    def mean_ms():
         for _ in range(3):
             one()
         stream.synchronize()
@@ -317,15 +315,25 @@ def bench_prefill(Q, stream, args) -> dict:
         for _ in range(reps):
             one()
         stream.synchronize()
-        t = (time.perf_counter() - t0) * 1e3 / reps
-        log(f"  tiling gemm_rows {rows} attn_split_blocks {split}: {t:.3f} ms")
+        return (time.perf_counter() - t0) * 1e3 / reps
+
+    for spec in args.prefill_tiling or []:
+        rows, split = (int(x) for x in spec.split(":"))
+        D.set_prefill_tiling(rows, split)
+        log(f"  tiling gemm_rows {rows} attn_split_blocks {split}: {mean_ms():.3f} ms")
     D.set_prefill_tiling(0, 0)
+    # the same calls with the GEMMs forming the f16 weights from the Q8_0
+    # stacks in registers (no f16 matrices): same bits, for comparison
+    model.use_prefill_matrices(False)
+    q8_ms = mean_ms()
+    model.use_prefill_matrices(True)
+    log(f"  GEMMs over the Q8_0 stacks instead of the f16 matrices: {q8_ms:.3f} ms")
     ws.free()
     pbuf.free()
     sess.free()
     model.free()
     return {"tokens": n, "ms": round(ms, 3), "median_ms": round(statistics.median(times), 3),
-            "tok_per_s": round(n / ms * 1e3, 1),
+            "tok_per_s": round(n / ms * 1e3, 1), "q8_stacks_ms": round(q8_ms, 3),
             "gemm_flops": gemm, "attention_flops": attn,
             "TFLOPs": round((gemm + attn) / ms / 1e9, 2),
             "decode_steps_ms": round(steps_ms, 2), "speedup_vs_steps": round(steps_ms / ms, 1),

@@ -42,6 +42,12 @@ typedef struct qwen3_weights {
   const void* wdn;         /* Q8_0 [28, 3342336] */
   const void* output_norm; /* f16 [1024] */
   const void* output_w;    /* f16 [151936, 1024] (output_T.weight) */
+  /* Optional (NULL when unused): f16 copies of the six layer matrices, made
+   * from the Q8_0 stacks above by qwen3_prefill_matrices_expand (256-byte
+   * aligned, qwen3_prefill_matrices_bytes()).  When set, the prompt GEMMs of
+   * qwen3_prefill_batched / qwen3_prefill_layer read these instead of the
+   * Q8_0 stacks; the decode step never reads them. */
+  const void* prefill_f16;
 } qwen3_weights;
 
 /* KV cache: two f16 buffers [28 * max_seq, 8, 128] each (K, V), the flat
@@ -139,12 +145,30 @@ int qwen3_prefill(const qwen3_weights* w, void* k_cache, void* v_cache, int64_t 
  * reference reads f16 copies of the layer matrices for this function
  * (@model_params.attn_q_weight etc., :1132-1210), made from a Q8_0 file as
  * f16(scale * q) with the product exact (tools/convert_gguf_to_irpa.py:28-44,
- * 174-199); this one reads the same Q8_0 stacks as the decode step and forms
- * those f16 weights in registers, so prompt and decode share one set of
- * weights.  (The decode GEMVs scale each block's exact dot instead, as the
- * reference's decode kernels do; the two routes' logits differ by about 2e-3
- * relative.) */
+ * 174-199).  With w->prefill_f16 set this function reads such copies
+ * (qwen3_prefill_matrices_expand); without it, it reads the decode step's
+ * Q8_0 stacks and forms the same f16 weights in registers.  Both routes give
+ * the same bits (the same MFMA instructions on the same values in the same
+ * order); the f16 one runs no conversion in its GEMM loops.  (The decode
+ * GEMVs scale each block's exact dot instead, as the reference's decode
+ * kernels do; the two routes' logits differ by about 2e-3 relative.) */
 size_t qwen3_prefill_workspace_bytes(int32_t n_prompt);
+
+/* The f16 layer matrices of qwen3_weights.prefill_f16: bytes needed
+ * (880,803,840: 28 layers x 15,728,640 f16 weights) and their expansion from
+ * w's Q8_0 stacks into `matrices` (device memory, 256-byte aligned, at least
+ * that many bytes), enqueued on `stream`.  Each weight becomes f16(scale * q),
+ * the f16 value the reference's converter writes for it
+ * (tools/convert_gguf_to_irpa.py:28-44, 174-199).  Per layer: q, k and v rows
+ * as one [4096, 1024] matrix, attn_o [1024, 2048], gate/up [6144, 1024] with
+ * the rows in groups of 32 (16 gate rows, then the 16 up rows of the same
+ * SwiGLU outputs), ffn_down [1024, 3072].  Run it again after the Q8_0 stacks
+ * change.  No counterpart call in the reference (its converter writes the f16
+ * matrices to the parameter file). */
+size_t qwen3_prefill_matrices_bytes(void);
+int qwen3_prefill_matrices_expand(const qwen3_weights* w, void* matrices, size_t bytes,
+                                  void* stream);
+
 int qwen3_prefill_batched(const qwen3_weights* w, void* k_cache, void* v_cache, int64_t max_seq,
                           const int32_t* prompt, int32_t n_prompt, int32_t* token, int32_t* pos,
                           void* logits, int chunk_local, void* workspace, size_t workspace_bytes,
@@ -167,10 +191,13 @@ int64_t qwen3_prefill_workspace_offset(int32_t n_tokens, const char* name);
 
 /* Work division of qwen3_prefill_batched / qwen3_prefill_layer (0 = the
  * default, for either):
- * gemm_rows: token rows per workgroup of the q/k/v, attn_o and ffn_down GEMMs
- *   (gate/up always uses 64): 32 or 64; default: 32 where 64 would give
- *   fewer than 2 workgroups per CU.  Both tiles compute every output with the
- *   same operations in the same order (tested bit for bit).
+ * gemm_rows: token rows per GEMM workgroup, 32, 64 or 128.  Over the Q8_0
+ *   stacks: the q/k/v, attn_o and ffn_down GEMMs (gate/up always uses 64),
+ *   32 or 64 (128 = 64); default: 32 where 64 would give fewer than 2
+ *   workgroups per CU.  Over the f16 matrices: every GEMM, the tile of that
+ *   many rows (the next larger where the GEMM has none); default: the largest
+ *   tile whose grid gives every CU two workgroups.  Every tile computes each
+ *   output with the same operations in the same order (tested bit for bit).
  * attn_split_blocks: cache positions per attention split, in blocks of 32
  *   (>= 1; raised where the workspace's partial slots would not hold the
  *   splits); default 8.  Splits change the order of the softmax sums, within

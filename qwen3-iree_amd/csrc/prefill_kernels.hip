@@ -266,7 +266,279 @@ __device__ __forceinline__ void gemm_q8(const GemmArgs& A) {
   }
 }
 
+// ------------------------------------------------------------ f16 GEMM ----
+//
+// The same products over f16 copies of the layer matrices (pf_expand_q8: every
+// weight f16(scale * q), the value gemm_q8 forms in registers), so no
+// conversion runs in the loop.  Y[m, n] = sum_k X[m, k] W[n, k], X [M, ldx]
+// and W [N, K] both f16 with k contiguous.
+//
+// Workgroup tile (32 MS) x (32 NS), four waves 2 (m) x 2 (n) of (16 MS) x
+// (16 NS), each 16 x 16 piece one chain of v_mfma_f32_16x16x32_f16 over K in
+// order: every output sees the instructions gemm_q8 gives it, on the same
+// values in the same order, so the two GEMMs' results are the same bits.
+//
+// A stage is KS k: the tile's BM X rows and BN W rows, 2 KS bytes each,
+// copied from memory into LDS by the memory system (global_load_lds, 16 bytes
+// per lane, 1 KiB per wave instruction) into one of NBUF buffers while the
+// waves multiply another: the copies run NBUF - 1 stages ahead.  The buffers
+// are separate LDS arrays and the loop is unrolled by NBUF, so the compiler
+// sees that a stage's reads do not touch the buffers being filled and lets
+// those copies stay in flight.  Row R's 16-byte chunk c sits in slot
+// c ^ swz(R) of the row, so the 16 rows one fragment read touches (lanes with
+// the same k chunk) fall in 16 distinct 16-byte slots of 256 bytes, and any 8
+// of them that are consecutive in 8 distinct slots of 128 bytes: no bank
+// conflicts whether the LDS serves 8 or 16 lanes of a ds_read_b128 per cycle.
+
+struct GemmF16Args {
+  const uint16_t* x;  // [M, ldx] f16
+  const uint16_t* w;  // [N, K] f16
+  uint16_t* y;        // [M, ldy] f16 (output columns [0, seg_col[0]))
+  const uint16_t* r;  // residual [M, ldr] (kEpiResidual)
+  float* part;        // kEpiPartial: split s's sums at part[(s M + m) N + n]
+  int M, K;
+  int n_tiles;        // tiles of BN columns of W
+  int ldx, ldy, ldr;
+  int splits;         // kEpiPartial: K in `splits` equal ranges
+  // output columns [seg_col[0], seg_col[1]) go to y_seg[0] (ld ldy_seg[0]),
+  // columns from seg_col[1] on to y_seg[1], each counted from its first;
+  // seg_col = N when unused
+  uint16_t* y_seg[2];
+  int ldy_seg[2];
+  int seg_col[2];
+};
+
+// slot permutation of a row of C 16-byte chunks (C = 8: 128-byte rows; C >=
+// 16: rows of 256 bytes or more)
+template <int C>
+__device__ __forceinline__ int f16_swz(int row) {
+  if constexpr (C >= 16)
+    return row & 15;
+  else
+    return (row & 7) ^ ((row >> 3) & 1);
+}
+
+// vmcnt(n) with the other counters left alone (gfx9 s_waitcnt encoding)
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0f70);
+}
+
+template <int EPI, int MS, int NS, int KS, int NBUF>
+__device__ __forceinline__ void gemm_f16(const GemmF16Args& A) {
+  static_assert(EPI != kEpiSwiGLU || NS % 2 == 0, "gate/up pairs");
+  static_assert(KS == 64 || KS == 128 || KS == 256, "stage length");
+  static_assert(NBUF >= 2 && NBUF <= 4, "buffers");
+  constexpr int BM = 32 * MS, BN = 32 * NS;
+  constexpr int kRows = BM + BN;
+  constexpr int RB = 2 * KS;         // bytes of a tile row per stage
+  constexpr int C = RB / 16;         // 16-byte chunks per row
+  constexpr int RPI = 1024 / RB;     // rows per wave instruction
+  constexpr int J = kRows / RPI / 4; // copy instructions per wave per stage
+  static_assert(kRows % (4 * RPI) == 0 && BM % RPI == 0, "copy pieces");
+  static_assert(J * (NBUF - 2) < 64, "vmcnt range");
+  constexpr int kBuf = kRows * RB;
+  __shared__ __attribute__((aligned(1024))) uint8_t lds0[kBuf];
+  __shared__ __attribute__((aligned(1024))) uint8_t lds1[kBuf];
+  __shared__ __attribute__((aligned(1024))) uint8_t lds2[NBUF > 2 ? kBuf : 16];
+  __shared__ __attribute__((aligned(1024))) uint8_t lds3[NBUF > 3 ? kBuf : 16];
+  const int t = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int lane = t & 63;
+  const int g = lane >> 4;
+  const int c16 = lane & 15;
+
+  // XCD-aware tile order as in gemm_q8: the m tiles of one n tile run on one
+  // XCD one after another, so its W rows come from HBM once
+  const int mt = (A.M + BM - 1) / BM;
+  const int tiles = mt * A.n_tiles;
+  const int split = EPI == kEpiPartial ? (int)blockIdx.x / tiles : 0;
+  const int bid = (int)blockIdx.x - split * tiles;
+  const int xcd = bid & 7;
+  const int slot = bid >> 3;
+  const int n_tile = (slot / mt) * 8 + xcd;
+  const int m0 = (slot % mt) * BM;
+  const int n0 = n_tile * BN;
+  const int stages = A.K / KS / (EPI == kEpiPartial ? A.splits : 1);
+  const int k0 = split * stages * KS;
+
+  // Copy sources: instruction j of this wave fills tile rows RPI (J wave + j)
+  // .. + RPI - 1 (X rows first, then W rows); lane l writes slot l % C of row
+  // RPI (J wave + j) + l / C with the row's chunk (l % C) ^ swz(row).  X rows
+  // past M repeat row M - 1 (their products are never stored).
+  const uint8_t* src[J];
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    const int row = RPI * (J * wave + j) + lane / C;
+    const int kc = (lane % C) ^ f16_swz<C>(row);
+    if (row < BM) {
+      const int m = m0 + row < A.M ? m0 + row : A.M - 1;
+      src[j] = reinterpret_cast<const uint8_t*>(A.x + (size_t)m * A.ldx + k0) + 16 * kc;
+    } else {
+      src[j] = reinterpret_cast<const uint8_t*>(A.w + (size_t)(n0 + row - BM) * A.K + k0) + 16 * kc;
+    }
+  }
+  auto issue = [&](int s, uint8_t* buf) {
+#pragma unroll
+    for (int j = 0; j < J; ++j)
+      __builtin_amdgcn_global_load_lds((const GLOBAL_AS void*)(src[j] + RB * s),
+                                       (LDS_AS void*)(buf + 1024 * (J * wave + j)), 16, 0, 0);
+  };
+
+  const int wm = wave & 1;
+  const int wn = wave >> 1;
+  // this lane's fragment chunk of k block kb (k chunk 4 kb + g) in a 16-row
+  // group: row c16, slot (4 kb + g) ^ swz(c16)
+  const int hc = f16_swz<C>(c16);
+  f32x4 acc[MS][NS];
+#pragma unroll
+  for (int ms = 0; ms < MS; ++ms)
+#pragma unroll
+    for (int ns = 0; ns < NS; ++ns) acc[ms][ns] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+
+  auto compute = [&](const uint8_t* buf) {
+#pragma unroll
+    for (int kb = 0; kb < KS / 32; ++kb) {
+      const uint8_t* base = buf + c16 * RB + 16 * ((4 * kb + g) ^ hc);
+      f16x8 a[MS], b[NS];
+#pragma unroll
+      for (int ms = 0; ms < MS; ++ms)
+        a[ms] = *reinterpret_cast<const f16x8*>(base + (16 * MS * wm + 16 * ms) * RB);
+#pragma unroll
+      for (int ns = 0; ns < NS; ++ns)
+        b[ns] = *reinterpret_cast<const f16x8*>(base + (BM + 16 * NS * wn + 16 * ns) * RB);
+#pragma unroll
+      for (int ms = 0; ms < MS; ++ms)
+#pragma unroll
+        for (int ns = 0; ns < NS; ++ns)
+          acc[ms][ns] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[ms], b[ns], acc[ms][ns], 0, 0, 0);
+    }
+  };
+
+  // Stage s lives in buffer s % NBUF.  Before stage s: this wave's copies of
+  // stage s have landed (later stages' copies, up to NBUF - 2 of them, may
+  // still be in flight: vmcnt counts in issue order), then a barrier makes
+  // every wave's copies visible and shows that all waves are done with
+  // stage s - 1, whose buffer then receives stage s + NBUF - 1.
+  auto step = [&](int s, uint8_t* cur, uint8_t* refill) {
+    if (s + NBUF - 2 < stages)
+      wait_vm<J * (NBUF - 2)>();
+    else
+      wait_vm<0>();
+    __syncthreads();
+    if (s + NBUF - 1 < stages) issue(s + NBUF - 1, refill);
+    compute(cur);
+  };
+#pragma unroll
+  for (int i = 0; i < NBUF - 1; ++i)
+    if (i < stages) issue(i, i == 0 ? lds0 : i == 1 ? lds1 : lds2);
+  for (int s = 0; s < stages; s += NBUF) {
+    if constexpr (NBUF == 2) {
+      step(s, lds0, lds1);
+      if (s + 1 < stages) step(s + 1, lds1, lds0);
+    } else if constexpr (NBUF == 3) {
+      step(s, lds0, lds2);
+      if (s + 1 < stages) step(s + 1, lds1, lds0);
+      if (s + 2 < stages) step(s + 2, lds2, lds1);
+    } else {
+      step(s, lds0, lds3);
+      if (s + 1 < stages) step(s + 1, lds1, lds0);
+      if (s + 2 < stages) step(s + 2, lds2, lds1);
+      if (s + 3 < stages) step(s + 3, lds3, lds2);
+    }
+  }
+
+  // epilogue: lane holds rows 4 g + i, column c16 of each 16 x 16 piece
+  const int N = BN * A.n_tiles;
+  int col0 = n0 + 16 * NS * wn;
+  uint16_t* yb = A.y;
+  int ldy = A.ldy;
+  if constexpr (EPI == kEpiStore) {
+    if (n0 >= A.seg_col[0]) {
+      const int sg = n0 >= A.seg_col[1] ? 1 : 0;
+      yb = A.y_seg[sg];
+      ldy = A.ldy_seg[sg];
+      col0 -= A.seg_col[sg];
+    }
+  }
+#pragma unroll
+  for (int ms = 0; ms < MS; ++ms) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int m = m0 + 16 * MS * wm + 16 * ms + 4 * g + i;
+      if (m >= A.M) continue;
+      if constexpr (EPI == kEpiSwiGLU) {
+        // W rows come in groups of 32: 16 gate rows, then the matching 16 up
+        // rows (pf_expand_q8's gate/up order); group G feeds columns 16 G ..
+#pragma unroll
+        for (int p = 0; p < NS / 2; ++p) {
+          const int col = (col0 + 32 * p) / 2 + c16;
+          yb[(size_t)m * ldy + col] = swiglu_f16(acc[ms][2 * p][i], acc[ms][2 * p + 1][i]);
+        }
+      } else {
+#pragma unroll
+        for (int ns = 0; ns < NS; ++ns) {
+          const int col = col0 + 16 * ns + c16;
+          if constexpr (EPI == kEpiResidual)
+            yb[(size_t)m * ldy + col] =
+                residual_f16(as_half(A.r[(size_t)m * A.ldr + col]), acc[ms][ns][i]);
+          else if constexpr (EPI == kEpiPartial)
+            A.part[((size_t)split * A.M + m) * N + col] = acc[ms][ns][i];
+          else
+            yb[(size_t)m * ldy + col] = f32_to_f16_bits(acc[ms][ns][i]);
+        }
+      }
+    }
+  }
+}
+
 }  // namespace
+
+// f16 copies of Q8_0 layer matrices: dst row r' of layer l = f16(scale * q)
+// of every weight of src row r (the reference converter's f16 weights,
+// tools/convert_gguf_to_irpa.py:28-44: q exact in f16, one rounding of the
+// product; the same two operations gemm_q8 does in registers).  gu_half > 0
+// (gate/up stack: rows 0 .. gu_half - 1 gate, then as many up rows) orders the
+// rows in groups of 32, gate rows 16 G .. 16 G + 15 then up rows 16 G ..
+// 16 G + 15, the order gemm_f16's SwiGLU epilogue reads; otherwise r' = r.
+// Thread = one Q8_0 block (34 bytes -> 32 f16); grid (ceil(blocks / 256),
+// layers).
+extern "C" __global__ __launch_bounds__(256) void pf_expand_q8(
+    const uint8_t* __restrict__ src, long long src_layer_bytes, int rows, int K, int gu_half,
+    uint16_t* __restrict__ dst, long long dst_layer_elems) {
+  const int bpr = K / 32;
+  const long long blk = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (blk >= (long long)rows * bpr) return;
+  const int r = (int)(blk / bpr);
+  const int b = (int)(blk - (long long)r * bpr);
+  const uint8_t* s = src + (size_t)blockIdx.y * src_layer_bytes + (size_t)blk * 34;
+  int rd = r;
+  if (gu_half > 0) {
+    const int up = r >= gu_half ? 1 : 0;
+    const int j = r - up * gu_half;
+    rd = 32 * (j >> 4) + 16 * up + (j & 15);
+  }
+  const uint16_t* s16 = reinterpret_cast<const uint16_t*>(s);  // blocks are 2-byte aligned
+  const _Float16 sc = as_half(s16[0]);
+  const f16x2 s2 = {sc, sc};
+  u32x4 out[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    // int8 k = 8 i .. 8 i + 7
+    const uint32_t lo = (uint32_t)s16[1 + 4 * i] | ((uint32_t)s16[2 + 4 * i] << 16);
+    const uint32_t hi = (uint32_t)s16[3 + 4 * i] | ((uint32_t)s16[4 + 4 * i] << 16);
+    const uint32_t bl = lo ^ 0x80808080u, bh = hi ^ 0x80808080u;
+    const f16x2 v0 = q8x2_to_f16x2(bl, kSelLo) * s2, v1 = q8x2_to_f16x2(bl, kSelHi) * s2;
+    const f16x2 v2 = q8x2_to_f16x2(bh, kSelLo) * s2, v3 = q8x2_to_f16x2(bh, kSelHi) * s2;
+    out[i] = (u32x4){__builtin_bit_cast(uint32_t, v0), __builtin_bit_cast(uint32_t, v1),
+                     __builtin_bit_cast(uint32_t, v2), __builtin_bit_cast(uint32_t, v3)};
+  }
+  u32x4* d = reinterpret_cast<u32x4*>(dst + (size_t)blockIdx.y * dst_layer_elems +
+                                      (size_t)rd * K + 32 * b);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) d[i] = out[i];
+}
 
 // h[i] = token_embd[tokens[i]] (qwen3_full.mlir:86-94); an id outside the
 // vocabulary reads row 0, as the decode step does.
@@ -379,6 +651,31 @@ extern "C" __global__ __launch_bounds__(256) void pf_res_reduce_norm(
 extern "C" __global__ __launch_bounds__(256) void pf_gemm_q8_swiglu(GemmArgs A) {
   gemm_q8<kEpiSwiGLU, 64>(A);
 }
+
+// gemm_f16 instances: pf_gemm_f16[_epilogue]_<MS><NS>[k] covers 32 MS
+// tokens x 32 NS columns of W per workgroup; the stage length and buffer
+// count are the fastest measured for where the host uses each (cold weights,
+// 512-2048 tokens): 64 k for the 128-column tiles (two workgroups per CU);
+// 128 k for the 64 x 64 tiles of q/k/v and attn_o / ffn_down with two
+// workgroups per CU, 256 k (the "k" names: 128 KiB of LDS, one workgroup per
+// CU) where the grid covers the CUs once; the SwiGLU 64 x 64 tile keeps 64 k.
+#define PF_GEMM_F16(name, EPI, MS, NS, KS, NBUF)                          \
+  extern "C" __global__ __launch_bounds__(256) void name(GemmF16Args A) { \
+    gemm_f16<EPI, MS, NS, KS, NBUF>(A);                                   \
+  }
+PF_GEMM_F16(pf_gemm_f16_44, kEpiStore, 4, 4, 64, 2)
+PF_GEMM_F16(pf_gemm_f16_24, kEpiStore, 2, 4, 64, 2)
+PF_GEMM_F16(pf_gemm_f16_22, kEpiStore, 2, 2, 128, 2)
+PF_GEMM_F16(pf_gemm_f16_swiglu_44, kEpiSwiGLU, 4, 4, 64, 2)
+PF_GEMM_F16(pf_gemm_f16_swiglu_24, kEpiSwiGLU, 2, 4, 64, 2)
+PF_GEMM_F16(pf_gemm_f16_swiglu_22, kEpiSwiGLU, 2, 2, 64, 2)
+PF_GEMM_F16(pf_gemm_f16_res_22, kEpiResidual, 2, 2, 128, 2)
+PF_GEMM_F16(pf_gemm_f16_res_22k, kEpiResidual, 2, 2, 256, 2)
+PF_GEMM_F16(pf_gemm_f16_res_12k, kEpiResidual, 1, 2, 256, 3)
+PF_GEMM_F16(pf_gemm_f16_part_22, kEpiPartial, 2, 2, 128, 2)
+PF_GEMM_F16(pf_gemm_f16_part_22k, kEpiPartial, 2, 2, 256, 2)
+PF_GEMM_F16(pf_gemm_f16_part_12k, kEpiPartial, 1, 2, 256, 3)
+#undef PF_GEMM_F16
 
 // Token i = blockIdx.x (position start + i): per-head rms_norm with q_norm /
 // k_norm (qwen3_full.mlir:1812-1879) and RoPE (@position_components.rope,

@@ -111,7 +111,14 @@ struct State {
                 pf_gemm_part = nullptr, pf_gemm_part_m32 = nullptr, pf_res_reduce = nullptr,
                 pf_res_reduce_norm = nullptr, pf_rope = nullptr, pf_attn = nullptr, pf_attn_merge = nullptr,
                 pf_set_pos = nullptr;
-  int pf_tile_rows = 0;   // prefill GEMM token tile: 0 = by shape, 32 or 64
+  // the f16 GEMMs (pf_gemm_f16*: over the f16 layer matrices) and their
+  // expansion from Q8_0 (pf_expand_q8)
+  hipFunction_t pf_f16_44 = nullptr, pf_f16_24 = nullptr, pf_f16_22 = nullptr,
+                pf_f16_sw_44 = nullptr, pf_f16_sw_24 = nullptr, pf_f16_sw_22 = nullptr,
+                pf_f16_res_22 = nullptr, pf_f16_res_22k = nullptr, pf_f16_res_12k = nullptr,
+                pf_f16_part_22 = nullptr, pf_f16_part_22k = nullptr, pf_f16_part_12k = nullptr,
+                pf_expand = nullptr;
+  int pf_tile_rows = 0;   // prefill GEMM token tile: 0 = by shape, 32, 64 or 128
   int pf_attn_split = 0;  // prefill attention positions per split in blocks of 32: 0 = by shape
   int step_single = -1;   // single-launch decode step: -1 unknown, 0 off, 1 on
   bool step_capable = false;
@@ -332,7 +339,20 @@ int q8gemv_init(const char* code_object_path) {
                      {&g.pf_gemm_part_m32, "pf_gemm_q8_part_m32"},
                      {&g.pf_res_reduce, "pf_res_reduce"},
                      {&g.pf_res_reduce_norm, "pf_res_reduce_norm"},
-                     {&g.pf_set_pos, "pf_set_pos"}};
+                     {&g.pf_set_pos, "pf_set_pos"},
+                     {&g.pf_f16_44, "pf_gemm_f16_44"},
+                     {&g.pf_f16_24, "pf_gemm_f16_24"},
+                     {&g.pf_f16_22, "pf_gemm_f16_22"},
+                     {&g.pf_f16_sw_44, "pf_gemm_f16_swiglu_44"},
+                     {&g.pf_f16_sw_24, "pf_gemm_f16_swiglu_24"},
+                     {&g.pf_f16_sw_22, "pf_gemm_f16_swiglu_22"},
+                     {&g.pf_f16_res_22, "pf_gemm_f16_res_22"},
+                     {&g.pf_f16_res_22k, "pf_gemm_f16_res_22k"},
+                     {&g.pf_f16_res_12k, "pf_gemm_f16_res_12k"},
+                     {&g.pf_f16_part_22, "pf_gemm_f16_part_22"},
+                     {&g.pf_f16_part_22k, "pf_gemm_f16_part_22k"},
+                     {&g.pf_f16_part_12k, "pf_gemm_f16_part_12k"},
+                     {&g.pf_expand, "pf_expand_q8"}};
         bool ok = true;
         for (auto& n : names) ok = ok && hipModuleGetFunction(n.fn, pm, n.name) == hipSuccess;
         if (ok) {
@@ -389,6 +409,10 @@ void q8gemv_shutdown(void) {
   g.pf_embed = g.pf_norm = g.pf_gemm = g.pf_gemm_res = g.pf_gemm_m32 = g.pf_gemm_res_m32 =
       g.pf_gemm_swiglu = g.pf_rope = g.pf_attn = g.pf_attn_merge = g.pf_set_pos = nullptr;
   g.pf_gemm_part = g.pf_gemm_part_m32 = g.pf_res_reduce = g.pf_res_reduce_norm = nullptr;
+  g.pf_f16_44 = g.pf_f16_24 = g.pf_f16_22 = g.pf_f16_sw_44 = g.pf_f16_sw_24 = g.pf_f16_sw_22 =
+      nullptr;
+  g.pf_f16_res_22 = g.pf_f16_res_22k = g.pf_f16_res_12k = g.pf_f16_part_22 = g.pf_f16_part_22k =
+      g.pf_f16_part_12k = g.pf_expand = nullptr;
   g.vocab = g.vocab_finalize = g.ws_reset = g.copy = nullptr;
   g.ready = false;
 }
@@ -1024,6 +1048,8 @@ int validate_weights(const qwen3_weights* w) {
     if (!p) return fail(Q8_ERR_NULL_POINTER, "null weight pointer");
     if (!aligned(p, 16)) return fail(Q8_ERR_MISALIGNED, "weights must be 16-byte aligned");
   }
+  if (w->prefill_f16 && !aligned(w->prefill_f16, 256))
+    return fail(Q8_ERR_MISALIGNED, "prefill_f16 must be 256-byte aligned");
   return Q8_OK;
 }
 
@@ -1260,6 +1286,84 @@ int launch_gemm(hipFunction_t fn, hipFunction_t fn_m32, const void* x, int ldx, 
   return launch(fn, (uint32_t)grid, 256, args, st);
 }
 
+// Argument block of pf_gemm_f16* (layout shared with prefill_kernels.hip).
+struct GemmF16Args {
+  const void* x;
+  const void* w;
+  void* y;
+  const void* r;
+  float* part;
+  int M, K;
+  int n_tiles;
+  int ldx, ldy, ldr;
+  int splits;
+  void* y_seg[2];  // output columns from seg_col[0] / seg_col[1] on
+  int ldy_seg[2];
+  int seg_col[2];
+};
+
+// The f16 layer matrices (qwen3_weights.prefill_f16), f16 elements per
+// layer: q/k/v rows [4096, 1024] (q rows, then k, then v), attn_o [1024,
+// 2048], gate/up [6144, 1024] in groups of 16 gate rows + the matching 16 up
+// rows, ffn_down [1024, 3072].
+constexpr int64_t kPfF16Qkv = 0;
+constexpr int64_t kPfF16O = 4096LL * 1024;
+constexpr int64_t kPfF16Gu = kPfF16O + 1024LL * 2048;
+constexpr int64_t kPfF16Dn = kPfF16Gu + 6144LL * 1024;
+constexpr int64_t kPfF16Layer = kPfF16Dn + 1024LL * 3072;
+constexpr size_t kPfF16Bytes = (size_t)kLayers * kPfF16Layer * 2;
+
+struct F16Tile {
+  hipFunction_t fn;
+  int ms, ns;   // 32 ms token rows x 32 ns W rows per workgroup
+  int ks;       // k per stage (K per split must be a multiple)
+  int per_cu;   // chosen when the grid gives every CU at least this many workgroups
+};
+
+// One pf_gemm_f16* launch.  Tile: the first of `tiles` whose grid gives every
+// CU at least its per_cu workgroups (the last one regardless); a gemm_rows
+// setting (qwen3_set_prefill_tiling) picks the first tile of that many token
+// rows instead (the next larger where the GEMM has none).  Every tile gives
+// the same bits.
+int launch_gemm_f16(std::initializer_list<F16Tile> tiles, const void* x, int ldx, const void* wm,
+                    int K, int n_w, void* y, int ldy, const void* r, int ldr, int M,
+                    hipStream_t st, float* part = nullptr, int splits = 1,
+                    const int (*seg_col)[2] = nullptr, void* const (*y_seg)[2] = nullptr,
+                    const int (*ldy_seg)[2] = nullptr) {
+  auto grid_of = [&](const F16Tile& t) {
+    return ((int64_t)M + 32 * t.ms - 1) / (32 * t.ms) * (n_w / (32 * t.ns)) * splits;
+  };
+  const F16Tile* pick = nullptr;
+  if (g.pf_tile_rows > 0) {
+    for (const F16Tile& t : tiles)
+      if (32 * t.ms >= g.pf_tile_rows && (!pick || t.ms < pick->ms)) pick = &t;
+  } else {
+    for (const F16Tile& t : tiles)
+      if (!pick && grid_of(t) >= (int64_t)t.per_cu * g.compute_units) pick = &t;
+  }
+  if (!pick) pick = tiles.end() - 1;
+  const int bn = 32 * pick->ns;
+  // the kernel maps workgroups to n tiles in groups of 8 (one per XCD)
+  if (n_w % (8 * bn) != 0 || splits < 1 || K % (pick->ks * splits) != 0)
+    return fail(Q8_ERR_BAD_SHAPE, "prefill f16 GEMM shape N=%d K=%d splits=%d", n_w, K, splits);
+  GemmF16Args a{x, wm, y, r, part, M, K, n_w / bn, ldx, ldy, ldr, splits,
+                {nullptr, nullptr}, {0, 0}, {n_w, n_w}};
+  if (seg_col) {
+    if ((*seg_col)[0] % bn != 0 || (*seg_col)[1] % bn != 0)
+      return fail(Q8_ERR_BAD_SHAPE, "prefill f16 GEMM segments at %d, %d", (*seg_col)[0],
+                  (*seg_col)[1]);
+    for (int i = 0; i < 2; ++i) {
+      a.seg_col[i] = (*seg_col)[i];
+      a.y_seg[i] = (*y_seg)[i];
+      a.ldy_seg[i] = (*ldy_seg)[i];
+    }
+  }
+  const int64_t grid = grid_of(*pick);
+  if (grid > 0x7fffffff) return fail(Q8_ERR_BAD_SHAPE, "prefill GEMM grid too large");
+  void* args[] = {&a};
+  return launch(pick->fn, (uint32_t)grid, 256, args, st);
+}
+
 // y = r + x W^T for N = 1024 (attn_o, ffn_down).  Where 32-token tiles would
 // leave CUs idle (short prompts), K is split into equal ranges of whole stages
 // (the fewest that fill the CUs), each range's f32 sums go to `part`, and
@@ -1273,7 +1377,7 @@ int launch_gemm(hipFunction_t fn, hipFunction_t fn_m32, const void* x, int ldx, 
 int launch_gemm_res(const void* x, int ldx, const void* wl, int K, void* y, const void* r,
                     int M, void* part, size_t part_bytes, hipStream_t st,
                     const void* norm_w = nullptr, void* norm_out = nullptr,
-                    bool* normed = nullptr) {
+                    bool* normed = nullptr, const void* wf16 = nullptr) {
   if (normed) *normed = false;
   constexpr int kN = 1024;
   const int n_tiles = kN / 64;
@@ -1296,11 +1400,22 @@ int launch_gemm_res(const void* x, int ldx, const void* wl, int K, void* y, cons
   // with a norm to form, even an unsplit K goes through the f32 sums and the
   // reduce (which adds the residual exactly as the GEMM epilogue would):
   // 1024 tokens 4.24 -> 4.13 ms, 2048 tokens 7.69 -> 7.61 ms
-  if (splits == 1 && !(norm_w && g.pf_gemm_part && (size_t)M * kN * 4 <= part_bytes))
+  if (splits == 1 && !(norm_w && g.pf_gemm_part && (size_t)M * kN * 4 <= part_bytes)) {
+    if (wf16)
+      return launch_gemm_f16({{g.pf_f16_res_22, 2, 2, 128, 2}, {g.pf_f16_res_22k, 2, 2, 256, 1},
+                              {g.pf_f16_res_12k, 1, 2, 256, 0}},
+                             x, ldx, wf16, K, kN, y, kN, r, kN, M, st);
     return launch_gemm(g.pf_gemm_res, g.pf_gemm_res_m32, x, ldx, wl, K, kN, 64, y, kN, r, kN, 0,
                        M, st);
-  int rc = launch_gemm(g.pf_gemm_part, g.pf_gemm_part_m32, x, ldx, wl, K, kN, 64, nullptr, kN,
-                       nullptr, 0, 0, M, st, nullptr, static_cast<float*>(part), splits);
+  }
+  int rc = wf16 ? launch_gemm_f16({{g.pf_f16_part_22, 2, 2, 128, 2},
+                                   {g.pf_f16_part_22k, 2, 2, 256, 1},
+                                   {g.pf_f16_part_12k, 1, 2, 256, 0}},
+                                  x, ldx, wf16, K, kN, nullptr, kN, nullptr, 0, M, st,
+                                  static_cast<float*>(part), splits)
+                : launch_gemm(g.pf_gemm_part, g.pf_gemm_part_m32, x, ldx, wl, K, kN, 64, nullptr,
+                              kN, nullptr, 0, 0, M, st, nullptr, static_cast<float*>(part),
+                              splits);
   if (rc) return rc;
   const void* pp = part;
   int sp = splits, mm = M, nn = kN, ld = kN;
@@ -1339,7 +1454,19 @@ int launch_prefill_layer(const qwen3_weights* w, int layer, void* k_cache, void*
     void* args[] = {&h, &an, &xn, &n};
     if ((rc = launch(g.pf_norm, norm_grid, 256, args, st))) return rc;
   }
-  {  // q, k, v in one launch (tiles 0-31 q, 32-47 k, 48-63 v)
+  // f16 layer matrices when the caller made them, else the Q8_0 stacks
+  const uint8_t* f16l =
+      w->prefill_f16 ? cb(w->prefill_f16) + (int64_t)layer * kPfF16Layer * 2 : nullptr;
+  if (f16l) {  // q, k, v as one [4096, 1024] matrix, output columns split three ways
+    const int seg_col[2] = {2048, 3072};
+    void* const y_seg[2] = {k, v};
+    const int ldy_seg[2] = {1024, 1024};
+    if ((rc = launch_gemm_f16({{g.pf_f16_44, 4, 4, 64, 2}, {g.pf_f16_24, 2, 4, 64, 2},
+                               {g.pf_f16_22, 2, 2, 128, 0}},
+                              xn, 1024, f16l + kPfF16Qkv * 2, 1024, 4096, q, 2048, nullptr, 0, n,
+                              st, nullptr, 1, &seg_col, &y_seg, &ldy_seg)))
+      return rc;
+  } else {  // q, k, v in one launch (tiles 0-31 q, 32-47 k, 48-63 v)
     const GemmMore kv{cb(w->wk) + layer * bpl_kv, k, 1024, 1024,
                       cb(w->wv) + layer * bpl_kv, v, 1024, 1024};
     if ((rc = launch_gemm(g.pf_gemm, g.pf_gemm_m32, xn, 1024, cb(w->wq) + layer * bpl_q, 1024,
@@ -1370,17 +1497,23 @@ int launch_prefill_layer(const qwen3_weights* w, int layer, void* k_cache, void*
   const size_t part_bytes = pf_region_bytes(n, kPfTokenRegions);
   bool fn_done = false;
   if ((rc = launch_gemm_res(attn, 2048, cb(w->wo) + layer * bpl_o, 2048, h1, h, n, part,
-                            part_bytes, st, fn, fnx, &fn_done)))
+                            part_bytes, st, fn, fnx, &fn_done,
+                            f16l ? f16l + kPfF16O * 2 : nullptr)))
     return rc;
   if (!fn_done) {
     void* args[] = {&h1, &fn, &fnx, &n};
     if ((rc = launch(g.pf_norm, norm_grid, 256, args, st))) return rc;
   }
-  if ((rc = launch_gemm(g.pf_gemm_swiglu, nullptr, fnx, 1024, cb(w->wgu) + layer * bpl_gu, 1024, 3072, 32,
-                        act, 3072, nullptr, 0, 3072, n, st)))
-    return rc;
+  if (f16l)
+    rc = launch_gemm_f16({{g.pf_f16_sw_44, 4, 4, 64, 2}, {g.pf_f16_sw_24, 2, 4, 64, 2},
+                          {g.pf_f16_sw_22, 2, 2, 64, 0}},
+                         fnx, 1024, f16l + kPfF16Gu * 2, 1024, 6144, act, 3072, nullptr, 0, n, st);
+  else
+    rc = launch_gemm(g.pf_gemm_swiglu, nullptr, fnx, 1024, cb(w->wgu) + layer * bpl_gu, 1024, 3072,
+                     32, act, 3072, nullptr, 0, 3072, n, st);
+  if (rc) return rc;
   return launch_gemm_res(act, 3072, cb(w->wdn) + layer * bpl_dn, 3072, h, h1, n, part, part_bytes,
-                         st, next_norm, xn, next_xn_ready);
+                         st, next_norm, xn, next_xn_ready, f16l ? f16l + kPfF16Dn * 2 : nullptr);
 }
 
 int check_prefill_ready() {
@@ -1480,8 +1613,8 @@ int qwen3_get_step_mode(int* mode) {
 }
 
 int qwen3_set_prefill_tiling(int gemm_rows, int attn_split_blocks) {
-  if (gemm_rows != 0 && gemm_rows != 32 && gemm_rows != 64)
-    return fail(Q8_ERR_BAD_ARGUMENT, "prefill GEMM rows %d not in {0, 32, 64}", gemm_rows);
+  if (gemm_rows != 0 && gemm_rows != 32 && gemm_rows != 64 && gemm_rows != 128)
+    return fail(Q8_ERR_BAD_ARGUMENT, "prefill GEMM rows %d not in {0, 32, 64, 128}", gemm_rows);
   if (attn_split_blocks < 0)
     return fail(Q8_ERR_BAD_ARGUMENT, "attention split of %d blocks", attn_split_blocks);
   int rc = check_prefill_ready();
@@ -1672,6 +1805,43 @@ int qwen3_prefill_layer(const qwen3_weights* w, int layer, void* k_cache, void* 
 size_t qwen3_prefill_workspace_bytes(int32_t n_prompt) {
   if (n_prompt < 1 || n_prompt > kPfMaxTokens) return 0;
   return pf_workspace_bytes(n_prompt);
+}
+
+size_t qwen3_prefill_matrices_bytes(void) { return kPfF16Bytes; }
+
+int qwen3_prefill_matrices_expand(const qwen3_weights* w, void* matrices, size_t bytes,
+                                  void* stream) {
+  int rc = validate_weights(w);
+  if (rc) return rc;
+  if (!matrices) return fail(Q8_ERR_NULL_POINTER, "null matrices buffer");
+  if (!aligned(matrices, 256)) return fail(Q8_ERR_MISALIGNED, "matrices must be 256-byte aligned");
+  if (bytes < kPfF16Bytes)
+    return fail(Q8_ERR_BAD_SHAPE, "matrices buffer of %zu bytes, %zu needed", bytes, kPfF16Bytes);
+  if ((rc = check_prefill_ready())) return rc;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  // (Q8_0 stack, its rows and K, first destination row in the layer's f16 matrices)
+  struct Part {
+    const void* src;
+    int rows, K;
+    int64_t dst;
+    int gu_half;
+  } parts[] = {{w->wq, 2048, 1024, kPfF16Qkv, 0},
+               {w->wk, 1024, 1024, kPfF16Qkv + 2048LL * 1024, 0},
+               {w->wv, 1024, 1024, kPfF16Qkv + 3072LL * 1024, 0},
+               {w->wo, 1024, 2048, kPfF16O, 0},
+               {w->wgu, 6144, 1024, kPfF16Gu, 3072},
+               {w->wdn, 1024, 3072, kPfF16Dn, 0}};
+  for (const Part& p : parts) {
+    const void* src = p.src;
+    long long src_layer = (long long)p.rows * p.K / 32 * 34;
+    int rows = p.rows, K = p.K, gu = p.gu_half;
+    void* dst = mb(matrices) + p.dst * 2;
+    long long dst_layer = kPfF16Layer;
+    void* args[] = {&src, &src_layer, &rows, &K, &gu, &dst, &dst_layer};
+    const uint32_t blocks = (uint32_t)(((int64_t)rows * K / 32 + 255) / 256);
+    if ((rc = launch2(g.pf_expand, blocks, kLayers, 256, args, st))) return rc;
+  }
+  return Q8_OK;
 }
 
 int qwen3_prefill_batched(const qwen3_weights* w, void* k_cache, void* v_cache, int64_t max_seq,

@@ -102,26 +102,65 @@ def synthetic_weights(seed: int = 0, workers: int = 8) -> HostWeights:
 
 class WeightsC(ctypes.Structure):
     """struct qwen3_weights (include/qwen3_decode.h)."""
-    _fields_ = [(f, ctypes.c_void_p) for f in WEIGHT_FIELDS]
+    _fields_ = [(f, ctypes.c_void_p) for f in WEIGHT_FIELDS] + [("prefill_f16", ctypes.c_void_p)]
+
+
+def prefill_matrices_bytes() -> int:
+    """Bytes of the f16 layer matrices the prompt GEMMs can read."""
+    return int(Q.load_library().qwen3_prefill_matrices_bytes())
 
 
 class DeviceWeights:
-    """The parameters resident in device memory, one allocation each."""
+    """The parameters resident in device memory, one allocation each.
 
-    def __init__(self, host: HostWeights):
+    prefill_f16: also make the f16 copies of the layer matrices
+    (qwen3_prefill_matrices_expand, 0.88 GB) that the batched prompt path
+    then reads instead of forming them from Q8_0 in its GEMM loops."""
+
+    def __init__(self, host: HostWeights, prefill_f16: bool = True):
         host.validate()
         self.buffers = {f.name: Q.DeviceBuffer.from_array(getattr(host, f.name))
                         for f in fields(HostWeights)}
-        self.struct = WeightsC(*(self.buffers[f].ptr for f in WEIGHT_FIELDS))
+        self.struct = WeightsC(*(self.buffers[f].ptr for f in WEIGHT_FIELDS), None)
+        self.prefill_matrices: Q.DeviceBuffer | None = None
+        if prefill_f16:
+            self.expand_prefill_matrices()
+
+    def expand_prefill_matrices(self) -> None:
+        """(Re)make the f16 layer matrices from the resident Q8_0 stacks and
+        point the struct at them."""
+        if self.prefill_matrices is None:
+            self.prefill_matrices = Q.DeviceBuffer(prefill_matrices_bytes())
+        stream = Q.Stream()
+        try:
+            self.struct.prefill_f16 = None
+            Q._call("qwen3_prefill_matrices_expand", self.ref(), self.prefill_matrices.ptr,
+                    self.prefill_matrices.nbytes, stream.handle)
+            stream.synchronize()
+        finally:
+            stream.destroy()
+        self.struct.prefill_f16 = self.prefill_matrices.ptr
+
+    def use_prefill_matrices(self, on: bool) -> None:
+        """Route the prompt GEMMs through the f16 matrices (on) or the Q8_0
+        stacks (off); the matrices stay allocated."""
+        if on and self.prefill_matrices is None:
+            self.expand_prefill_matrices()
+        self.struct.prefill_f16 = self.prefill_matrices.ptr if on else None
 
     @property
     def nbytes(self) -> int:
-        return sum(b.nbytes for b in self.buffers.values())
+        n = sum(b.nbytes for b in self.buffers.values())
+        return n + (self.prefill_matrices.nbytes if self.prefill_matrices is not None else 0)
 
     def ref(self):
         return ctypes.byref(self.struct)
 
     def free(self) -> None:
+        self.struct.prefill_f16 = None
+        if self.prefill_matrices is not None:
+            self.prefill_matrices.free()
+            self.prefill_matrices = None
         for b in self.buffers.values():
             b.free()
 

@@ -165,6 +165,8 @@ _SIGNATURES = {
     "qwen3_prefill": [_P, _P, _P, _I64, _P, ctypes.c_int32, _P, _P, _P, _P],
     "qwen3_generate": [_P, _P, _P, _I64, _P, _P, ctypes.c_int32, ctypes.c_int32, _P, _P, _P, _P],
     "qwen3_prefill_workspace_bytes": [ctypes.c_int32],
+    "qwen3_prefill_matrices_bytes": [],
+    "qwen3_prefill_matrices_expand": [_P, _P, _SZ, _P],
     "qwen3_prefill_batched": [_P, _P, _P, _I64, _P, ctypes.c_int32, _P, _P, _P, _I, _P, _SZ, _P,
                               _P],
     "qwen3_prefill_layer": [_P, _I, _P, _P, _I64, ctypes.c_int32, ctypes.c_int32, _I, _P, _SZ, _P],
@@ -184,6 +186,7 @@ _RESTYPES = {
     "qwen3_scratch_status_offset": _SZ,
     "qwen3_scratch_offset": _I64,
     "qwen3_prefill_workspace_bytes": _SZ,
+    "qwen3_prefill_matrices_bytes": _SZ,
     "qwen3_prefill_workspace_offset": _I64,
 }
 
