@@ -267,6 +267,21 @@ def bench_prefill(Q, stream, args) -> dict:
                 pbuf.ptr, n, sess.token_ptr, sess.pos_ptr, logits, 0, ws.ptr, nbytes,
                 sess.scratch.ptr, Q._stream(stream))
 
+    if args.kernels_only:
+        # counter runs: three calls over the f16 matrices, then three over the
+        # Q8_0 stacks (their GEMM kernels have different names), nothing else
+        for f16 in (True, False):
+            model.use_prefill_matrices(f16)
+            for _ in range(3):
+                one()
+            stream.synchronize()
+        model.use_prefill_matrices(True)
+        ws.free()
+        pbuf.free()
+        sess.free()
+        model.free()
+        return {"tokens": n, "calls": 6, "parity_ok": True}
+
     # parity against the decode-step path on the same prompt
     one(sess.logits.ptr)
     stream.synchronize()
@@ -497,7 +512,9 @@ def main() -> int:
     ap.add_argument("--kernels-only", action="store_true",
                     help="run only the GEMV kernels (batched sweep, per-dispatch sweep, vocab, the "
                          "decode step's GEMV share) and print the line without the decode step, "
-                         "prompt, generation and CPU parts (for counter runs)")
+                         "prompt, generation and CPU parts (for counter runs); with "
+                         "--prefill-only: three untimed prompt calls over the f16 matrices and "
+                         "three over the Q8_0 stacks, no parity check")
     ap.add_argument("--generate-only", action="store_true",
                     help="run only end-to-end generation and print its JSON line")
     ap.add_argument("--step-mode", type=int, choices=(0, 1), default=None,

@@ -273,10 +273,11 @@ __device__ __forceinline__ void gemm_q8(const GemmArgs& A) {
 // conversion runs in the loop.  Y[m, n] = sum_k X[m, k] W[n, k], X [M, ldx]
 // and W [N, K] both f16 with k contiguous.
 //
-// Workgroup tile (32 MS) x (32 NS), four waves 2 (m) x 2 (n) of (16 MS) x
-// (16 NS), each 16 x 16 piece one chain of v_mfma_f32_16x16x32_f16 over K in
-// order: every output sees the instructions gemm_q8 gives it, on the same
-// values in the same order, so the two GEMMs' results are the same bits.
+// Workgroup tile (16 MS WM) x (16 NS WN), WM x WN waves (default 2 x 2) of
+// (16 MS) x (16 NS), each 16 x 16 piece one chain of v_mfma_f32_16x16x32_f16
+// over K in order: every output sees the instructions gemm_q8 gives it, on
+// the same values in the same order, so the two GEMMs' results are the same
+// bits.
 //
 // A stage is KS k: the tile's BM X rows and BN W rows, 2 KS bytes each,
 // copied from memory into LDS by the memory system (global_load_lds, 16 bytes
@@ -284,11 +285,16 @@ __device__ __forceinline__ void gemm_q8(const GemmArgs& A) {
 // waves multiply another: the copies run NBUF - 1 stages ahead.  The buffers
 // are separate LDS arrays and the loop is unrolled by NBUF, so the compiler
 // sees that a stage's reads do not touch the buffers being filled and lets
-// those copies stay in flight.  Row R's 16-byte chunk c sits in slot
-// c ^ swz(R) of the row, so the 16 rows one fragment read touches (lanes with
-// the same k chunk) fall in 16 distinct 16-byte slots of 256 bytes, and any 8
-// of them that are consecutive in 8 distinct slots of 128 bytes: no bank
-// conflicts whether the LDS serves 8 or 16 lanes of a ds_read_b128 per cycle.
+// those copies stay in flight.
+//
+// LDS layout of a stage (f16_lds_off): rows of 256 bytes or more keep row R's
+// 16-byte chunk c in slot c ^ (R & 15) of its 256-byte block, so the 16 rows
+// one fragment read touches (lanes with the same k chunk) fall in 16 distinct
+// slots; 128-byte rows go two to a 256-byte line (line L = R / 2, position
+// 8 (R & 1) + c) with position p in slot p ^ (L & 15), the same pattern over
+// the same 16 slots.  Measured with SQ_LDS_BANK_CONFLICT: both read without
+// bank conflicts, where 128-byte rows with slot c ^ ((R & 7) ^ (R >> 3 & 1))
+// took about 4 conflict cycles per ds_read_b128.
 
 struct GemmF16Args {
   const uint16_t* x;  // [M, ldx] f16
@@ -308,14 +314,17 @@ struct GemmF16Args {
   int seg_col[2];
 };
 
-// slot permutation of a row of C 16-byte chunks (C = 8: 128-byte rows; C >=
-// 16: rows of 256 bytes or more)
+// byte offset of row r's 16-byte chunk c (k 8 c .. 8 c + 7 of the stage) in
+// a stage buffer with rows of C chunks
 template <int C>
-__device__ __forceinline__ int f16_swz(int row) {
-  if constexpr (C >= 16)
-    return row & 15;
-  else
-    return (row & 7) ^ ((row >> 3) & 1);
+__device__ __forceinline__ int f16_lds_off(int r, int c) {
+  if constexpr (C >= 16) {
+    return r * 16 * C + 16 * (c ^ (r & 15));
+  } else {
+    static_assert(C == 8, "row length");
+    const int line = r >> 1;
+    return 256 * line + 16 * ((((r & 1) << 3) | c) ^ (line & 15));
+  }
 }
 
 // vmcnt(n) with the other counters left alone (gfx9 s_waitcnt encoding)
@@ -325,18 +334,19 @@ __device__ __forceinline__ void wait_vm() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0f70);
 }
 
-template <int EPI, int MS, int NS, int KS, int NBUF>
+template <int EPI, int MS, int NS, int KS, int NBUF, int WM = 2, int WN = 2>
 __device__ __forceinline__ void gemm_f16(const GemmF16Args& A) {
   static_assert(EPI != kEpiSwiGLU || NS % 2 == 0, "gate/up pairs");
   static_assert(KS == 64 || KS == 128 || KS == 256, "stage length");
   static_assert(NBUF >= 2 && NBUF <= 4, "buffers");
-  constexpr int BM = 32 * MS, BN = 32 * NS;
+  constexpr int kWaves = WM * WN;
+  constexpr int BM = 16 * MS * WM, BN = 16 * NS * WN;
   constexpr int kRows = BM + BN;
-  constexpr int RB = 2 * KS;         // bytes of a tile row per stage
-  constexpr int C = RB / 16;         // 16-byte chunks per row
-  constexpr int RPI = 1024 / RB;     // rows per wave instruction
-  constexpr int J = kRows / RPI / 4; // copy instructions per wave per stage
-  static_assert(kRows % (4 * RPI) == 0 && BM % RPI == 0, "copy pieces");
+  constexpr int RB = 2 * KS;               // bytes of a tile row per stage
+  constexpr int C = RB / 16;               // 16-byte chunks per row
+  constexpr int RPI = 1024 / RB;           // rows per wave instruction
+  constexpr int J = kRows / RPI / kWaves;  // copy instructions per wave per stage
+  static_assert(kRows % (kWaves * RPI) == 0 && BM % RPI == 0, "copy pieces");
   static_assert(J * (NBUF - 2) < 64, "vmcnt range");
   constexpr int kBuf = kRows * RB;
   __shared__ __attribute__((aligned(1024))) uint8_t lds0[kBuf];
@@ -363,15 +373,24 @@ __device__ __forceinline__ void gemm_f16(const GemmF16Args& A) {
   const int stages = A.K / KS / (EPI == kEpiPartial ? A.splits : 1);
   const int k0 = split * stages * KS;
 
-  // Copy sources: instruction j of this wave fills tile rows RPI (J wave + j)
-  // .. + RPI - 1 (X rows first, then W rows); lane l writes slot l % C of row
-  // RPI (J wave + j) + l / C with the row's chunk (l % C) ^ swz(row).  X rows
-  // past M repeat row M - 1 (their products are never stored).
+  // Copy sources: instruction j of this wave fills the 1 KiB at byte
+  // 1024 (J wave + j) of the buffer, tile rows RPI (J wave + j) .. + RPI - 1
+  // (X rows first, then W rows); lane l writes its 16 bytes at 16 l of that,
+  // so it loads the (row, chunk) f16_lds_off places there.  X rows past M
+  // repeat row M - 1 (their products are never stored).
   const uint8_t* src[J];
 #pragma unroll
   for (int j = 0; j < J; ++j) {
-    const int row = RPI * (J * wave + j) + lane / C;
-    const int kc = (lane % C) ^ f16_swz<C>(row);
+    int row, kc;
+    if constexpr (C >= 16) {
+      row = RPI * (J * wave + j) + lane / C;
+      kc = (lane % C) ^ (row & 15);
+    } else {
+      const int line = 4 * (J * wave + j) + (lane >> 4);
+      const int p = (lane & 15) ^ (line & 15);
+      row = 2 * line + (p >> 3);
+      kc = p & 7;
+    }
     if (row < BM) {
       const int m = m0 + row < A.M ? m0 + row : A.M - 1;
       src[j] = reinterpret_cast<const uint8_t*>(A.x + (size_t)m * A.ldx + k0) + 16 * kc;
@@ -386,11 +405,20 @@ __device__ __forceinline__ void gemm_f16(const GemmF16Args& A) {
                                        (LDS_AS void*)(buf + 1024 * (J * wave + j)), 16, 0, 0);
   };
 
-  const int wm = wave & 1;
-  const int wn = wave >> 1;
-  // this lane's fragment chunk of k block kb (k chunk 4 kb + g) in a 16-row
-  // group: row c16, slot (4 kb + g) ^ swz(c16)
-  const int hc = f16_swz<C>(c16);
+  const int wm = wave % WM;
+  const int wn = wave / WM;
+  // This lane's fragment chunk of k block kb (k chunk 4 kb + g) in the 16-row
+  // group at row base b (a multiple of 16) is at 16 C b + off[(b / 16) & 1][kb]:
+  // with 128-byte rows the slot key depends on bit 4 of b, which is known for
+  // every fragment at compile time (MS and NS even there).
+  static_assert(C >= 16 || (MS % 2 == 0 && NS % 2 == 0), "fragment row bases");
+  static_assert(BM % 32 == 0, "fragment row bases");
+  int off[2][KS / 32];
+#pragma unroll
+  for (int hb = 0; hb < 2; ++hb)
+#pragma unroll
+    for (int kb = 0; kb < KS / 32; ++kb)
+      off[hb][kb] = f16_lds_off<C>(16 * hb + c16, 4 * kb + g) - 16 * C * 16 * hb;
   f32x4 acc[MS][NS];
 #pragma unroll
   for (int ms = 0; ms < MS; ++ms)
@@ -400,14 +428,15 @@ __device__ __forceinline__ void gemm_f16(const GemmF16Args& A) {
   auto compute = [&](const uint8_t* buf) {
 #pragma unroll
     for (int kb = 0; kb < KS / 32; ++kb) {
-      const uint8_t* base = buf + c16 * RB + 16 * ((4 * kb + g) ^ hc);
       f16x8 a[MS], b[NS];
 #pragma unroll
       for (int ms = 0; ms < MS; ++ms)
-        a[ms] = *reinterpret_cast<const f16x8*>(base + (16 * MS * wm + 16 * ms) * RB);
+        a[ms] = *reinterpret_cast<const f16x8*>(buf + (16 * MS * wm + 16 * ms) * RB +
+                                                off[ms & 1][kb]);
 #pragma unroll
       for (int ns = 0; ns < NS; ++ns)
-        b[ns] = *reinterpret_cast<const f16x8*>(base + (BM + 16 * NS * wn + 16 * ns) * RB);
+        b[ns] = *reinterpret_cast<const f16x8*>(buf + (BM + 16 * NS * wn + 16 * ns) * RB +
+                                                off[ns & 1][kb]);
 #pragma unroll
       for (int ms = 0; ms < MS; ++ms)
 #pragma unroll
@@ -653,7 +682,7 @@ extern "C" __global__ __launch_bounds__(256) void pf_gemm_q8_swiglu(GemmArgs A) 
 }
 
 // gemm_f16 instances: pf_gemm_f16[_epilogue]_<MS><NS>[k] covers 32 MS
-// tokens x 32 NS columns of W per workgroup; the stage length and buffer
+// tokens x 32 NS columns of W per workgroup (four waves); the stage length and buffer
 // count are the fastest measured for where the host uses each (cold weights,
 // 512-2048 tokens): 64 k for the 128-column tiles (two workgroups per CU);
 // 128 k for the 64 x 64 tiles of q/k/v and attn_o / ffn_down with two
@@ -663,6 +692,12 @@ extern "C" __global__ __launch_bounds__(256) void pf_gemm_q8_swiglu(GemmArgs A) 
   extern "C" __global__ __launch_bounds__(256) void name(GemmF16Args A) { \
     gemm_f16<EPI, MS, NS, KS, NBUF>(A);                                   \
   }
+// 256 x 192 over eight waves 4 (m) x 2 (n) of 64 x 96, 112 KiB of LDS: the
+// gate/up product of 2048 tokens in one round of 256 workgroups (42.0 ->
+// 32.6 us against 128 x 128 tiles, whose 768 workgroups take 1.5 rounds)
+extern "C" __global__ __launch_bounds__(512) void pf_gemm_f16_swiglu_46w(GemmF16Args A) {
+  gemm_f16<kEpiSwiGLU, 4, 6, 64, 2, 4, 2>(A);
+}
 PF_GEMM_F16(pf_gemm_f16_44, kEpiStore, 4, 4, 64, 2)
 PF_GEMM_F16(pf_gemm_f16_24, kEpiStore, 2, 4, 64, 2)
 PF_GEMM_F16(pf_gemm_f16_22, kEpiStore, 2, 2, 128, 2)

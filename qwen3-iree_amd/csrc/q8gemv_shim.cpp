@@ -114,7 +114,8 @@ struct State {
   // the f16 GEMMs (pf_gemm_f16*: over the f16 layer matrices) and their
   // expansion from Q8_0 (pf_expand_q8)
   hipFunction_t pf_f16_44 = nullptr, pf_f16_24 = nullptr, pf_f16_22 = nullptr,
-                pf_f16_sw_44 = nullptr, pf_f16_sw_24 = nullptr, pf_f16_sw_22 = nullptr,
+                pf_f16_sw_46w = nullptr, pf_f16_sw_44 = nullptr, pf_f16_sw_24 = nullptr,
+                pf_f16_sw_22 = nullptr,
                 pf_f16_res_22 = nullptr, pf_f16_res_22k = nullptr, pf_f16_res_12k = nullptr,
                 pf_f16_part_22 = nullptr, pf_f16_part_22k = nullptr, pf_f16_part_12k = nullptr,
                 pf_expand = nullptr;
@@ -343,6 +344,7 @@ int q8gemv_init(const char* code_object_path) {
                      {&g.pf_f16_44, "pf_gemm_f16_44"},
                      {&g.pf_f16_24, "pf_gemm_f16_24"},
                      {&g.pf_f16_22, "pf_gemm_f16_22"},
+                     {&g.pf_f16_sw_46w, "pf_gemm_f16_swiglu_46w"},
                      {&g.pf_f16_sw_44, "pf_gemm_f16_swiglu_44"},
                      {&g.pf_f16_sw_24, "pf_gemm_f16_swiglu_24"},
                      {&g.pf_f16_sw_22, "pf_gemm_f16_swiglu_22"},
@@ -409,8 +411,8 @@ void q8gemv_shutdown(void) {
   g.pf_embed = g.pf_norm = g.pf_gemm = g.pf_gemm_res = g.pf_gemm_m32 = g.pf_gemm_res_m32 =
       g.pf_gemm_swiglu = g.pf_rope = g.pf_attn = g.pf_attn_merge = g.pf_set_pos = nullptr;
   g.pf_gemm_part = g.pf_gemm_part_m32 = g.pf_res_reduce = g.pf_res_reduce_norm = nullptr;
-  g.pf_f16_44 = g.pf_f16_24 = g.pf_f16_22 = g.pf_f16_sw_44 = g.pf_f16_sw_24 = g.pf_f16_sw_22 =
-      nullptr;
+  g.pf_f16_44 = g.pf_f16_24 = g.pf_f16_22 = g.pf_f16_sw_46w = g.pf_f16_sw_44 = g.pf_f16_sw_24 =
+      g.pf_f16_sw_22 = nullptr;
   g.pf_f16_res_22 = g.pf_f16_res_22k = g.pf_f16_res_12k = g.pf_f16_part_22 = g.pf_f16_part_22k =
       g.pf_f16_part_12k = g.pf_expand = nullptr;
   g.vocab = g.vocab_finalize = g.ws_reset = g.copy = nullptr;
@@ -1315,9 +1317,10 @@ constexpr size_t kPfF16Bytes = (size_t)kLayers * kPfF16Layer * 2;
 
 struct F16Tile {
   hipFunction_t fn;
-  int ms, ns;   // 32 ms token rows x 32 ns W rows per workgroup
+  int bm, bn;   // token rows x W rows per workgroup
   int ks;       // k per stage (K per split must be a multiple)
   int per_cu;   // chosen when the grid gives every CU at least this many workgroups
+  int threads = 256;
 };
 
 // One pf_gemm_f16* launch.  Tile: the first of `tiles` whose grid gives every
@@ -1331,18 +1334,18 @@ int launch_gemm_f16(std::initializer_list<F16Tile> tiles, const void* x, int ldx
                     const int (*seg_col)[2] = nullptr, void* const (*y_seg)[2] = nullptr,
                     const int (*ldy_seg)[2] = nullptr) {
   auto grid_of = [&](const F16Tile& t) {
-    return ((int64_t)M + 32 * t.ms - 1) / (32 * t.ms) * (n_w / (32 * t.ns)) * splits;
+    return ((int64_t)M + t.bm - 1) / t.bm * (n_w / t.bn) * splits;
   };
   const F16Tile* pick = nullptr;
   if (g.pf_tile_rows > 0) {
     for (const F16Tile& t : tiles)
-      if (32 * t.ms >= g.pf_tile_rows && (!pick || t.ms < pick->ms)) pick = &t;
+      if (t.bm >= g.pf_tile_rows && (!pick || t.bm < pick->bm)) pick = &t;
   } else {
     for (const F16Tile& t : tiles)
       if (!pick && grid_of(t) >= (int64_t)t.per_cu * g.compute_units) pick = &t;
   }
   if (!pick) pick = tiles.end() - 1;
-  const int bn = 32 * pick->ns;
+  const int bn = pick->bn;
   // the kernel maps workgroups to n tiles in groups of 8 (one per XCD)
   if (n_w % (8 * bn) != 0 || splits < 1 || K % (pick->ks * splits) != 0)
     return fail(Q8_ERR_BAD_SHAPE, "prefill f16 GEMM shape N=%d K=%d splits=%d", n_w, K, splits);
@@ -1361,7 +1364,7 @@ int launch_gemm_f16(std::initializer_list<F16Tile> tiles, const void* x, int ldx
   const int64_t grid = grid_of(*pick);
   if (grid > 0x7fffffff) return fail(Q8_ERR_BAD_SHAPE, "prefill GEMM grid too large");
   void* args[] = {&a};
-  return launch(pick->fn, (uint32_t)grid, 256, args, st);
+  return launch(pick->fn, (uint32_t)grid, (uint32_t)pick->threads, args, st);
 }
 
 // y = r + x W^T for N = 1024 (attn_o, ffn_down).  Where 32-token tiles would
@@ -1402,15 +1405,16 @@ int launch_gemm_res(const void* x, int ldx, const void* wl, int K, void* y, cons
   // 1024 tokens 4.24 -> 4.13 ms, 2048 tokens 7.69 -> 7.61 ms
   if (splits == 1 && !(norm_w && g.pf_gemm_part && (size_t)M * kN * 4 <= part_bytes)) {
     if (wf16)
-      return launch_gemm_f16({{g.pf_f16_res_22, 2, 2, 128, 2}, {g.pf_f16_res_22k, 2, 2, 256, 1},
-                              {g.pf_f16_res_12k, 1, 2, 256, 0}},
+      return launch_gemm_f16({{g.pf_f16_res_22, 64, 64, 128, 2},
+                              {g.pf_f16_res_22k, 64, 64, 256, 1},
+                              {g.pf_f16_res_12k, 32, 64, 256, 0}},
                              x, ldx, wf16, K, kN, y, kN, r, kN, M, st);
     return launch_gemm(g.pf_gemm_res, g.pf_gemm_res_m32, x, ldx, wl, K, kN, 64, y, kN, r, kN, 0,
                        M, st);
   }
-  int rc = wf16 ? launch_gemm_f16({{g.pf_f16_part_22, 2, 2, 128, 2},
-                                   {g.pf_f16_part_22k, 2, 2, 256, 1},
-                                   {g.pf_f16_part_12k, 1, 2, 256, 0}},
+  int rc = wf16 ? launch_gemm_f16({{g.pf_f16_part_22, 64, 64, 128, 2},
+                                   {g.pf_f16_part_22k, 64, 64, 256, 1},
+                                   {g.pf_f16_part_12k, 32, 64, 256, 0}},
                                   x, ldx, wf16, K, kN, nullptr, kN, nullptr, 0, M, st,
                                   static_cast<float*>(part), splits)
                 : launch_gemm(g.pf_gemm_part, g.pf_gemm_part_m32, x, ldx, wl, K, kN, 64, nullptr,
@@ -1461,8 +1465,8 @@ int launch_prefill_layer(const qwen3_weights* w, int layer, void* k_cache, void*
     const int seg_col[2] = {2048, 3072};
     void* const y_seg[2] = {k, v};
     const int ldy_seg[2] = {1024, 1024};
-    if ((rc = launch_gemm_f16({{g.pf_f16_44, 4, 4, 64, 2}, {g.pf_f16_24, 2, 4, 64, 2},
-                               {g.pf_f16_22, 2, 2, 128, 0}},
+    if ((rc = launch_gemm_f16({{g.pf_f16_44, 128, 128, 64, 2}, {g.pf_f16_24, 64, 128, 64, 2},
+                               {g.pf_f16_22, 64, 64, 128, 0}},
                               xn, 1024, f16l + kPfF16Qkv * 2, 1024, 4096, q, 2048, nullptr, 0, n,
                               st, nullptr, 1, &seg_col, &y_seg, &ldy_seg)))
       return rc;
@@ -1505,8 +1509,9 @@ int launch_prefill_layer(const qwen3_weights* w, int layer, void* k_cache, void*
     if ((rc = launch(g.pf_norm, norm_grid, 256, args, st))) return rc;
   }
   if (f16l)
-    rc = launch_gemm_f16({{g.pf_f16_sw_44, 4, 4, 64, 2}, {g.pf_f16_sw_24, 2, 4, 64, 2},
-                          {g.pf_f16_sw_22, 2, 2, 64, 0}},
+    rc = launch_gemm_f16({{g.pf_f16_sw_46w, 256, 192, 64, 1, 512},
+                          {g.pf_f16_sw_44, 128, 128, 64, 2}, {g.pf_f16_sw_24, 64, 128, 64, 2},
+                          {g.pf_f16_sw_22, 64, 64, 64, 0}},
                          fnx, 1024, f16l + kPfF16Gu * 2, 1024, 6144, act, 3072, nullptr, 0, n, st);
   else
     rc = launch_gemm(g.pf_gemm_swiglu, nullptr, fnx, 1024, cb(w->wgu) + layer * bpl_gu, 1024, 3072,
