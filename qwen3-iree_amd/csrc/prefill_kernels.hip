@@ -794,16 +794,23 @@ extern "C" __global__ __launch_bounds__(256) void pf_qk_rope_cache(
 // whole cache, what the decode steps of @prefill_all see) or lo = start with
 // chunk_local != 0 (this call's tokens only, as the reference's @prefill
 // attends).  Wave w takes query head 2g + (w >> 1) and tokens 32 qb + 16 (w &
-// 1) .. + 15.  Per block of 32 cache positions: the K tile ([32][128], rows
-// padded to 272 bytes) and the V tile ([32][128], rows padded to 288 bytes, read
-// back transposed) go to LDS; S = Q K^T is 8 v_mfma_f32_16x16x32_f16 per wave (exact f16
-// products, f32 sums), scaled by rsqrt(128); the causal mask and an online
-// softmax in f32 (running max m and sum l per query row, as the decode step);
-// the weights p are split into f16 hi + lo (p - hi), so P V = hi V + lo V (8 + 8
-// MFMAs) carries p to about 2^-22.  out: [n, 2048] f16 = O / l.  The softmax
-// runs in base 2: scores are scaled by rsqrt(128) log2(e), so each weight is
-// one exp2 (v_exp_f32) instead of a range-reduced exp; m is kept in those
-// units, in the partials too.
+// 1) .. + 15.  Per block of 32 cache positions the K tile ([32][128], rows
+// padded to 272 bytes) and the V tile ([32][128], rows padded to 288 bytes)
+// go to LDS, and each wave works transposed, one query per lane column:
+//   S^T = K Q^T: 8 v_mfma_f32_16x16x32_f16 (K rows as A, the wave's 16 query
+//     rows as B; exact f16 products, f32 sums), so lane (c16, grp) holds the
+//     scores of query c16 at positions 4 grp + e and 16 + 4 grp + e (e < 4);
+//   online softmax in f32 per query (running max m, the lane's share of the
+//     sum l; the max over a query's four lanes by permlane swaps), scores
+//     scaled by rsqrt(128) log2(e) so each weight is one exp2 (v_exp_f32);
+//   O^T += V^T P^T: the lane's 8 weights are the B operand as they are, with
+//     the MFMA's 32 k slots standing for positions in the order 4 grp + e,
+//     16 + 4 grp + e; V^T comes from two transposing LDS reads per 16 dims in
+//     that order.  p is split into f16 hi + lo (p - hi), O^T = V^T hi +
+//     V^T lo (8 + 8 MFMAs), carrying p to about 2^-22.
+// No weight goes through LDS.  Blocks below every query of the wave skip the
+// mask; the O rescale is skipped when no lane's max moved.  out: [n, 2048]
+// f16 = O / l.
 //
 // A query block's positions are divided into splits of split_blocks blocks of
 // 32 (prefill_split.h); grid (pairs of query block and split, 8).  A query
@@ -813,12 +820,19 @@ extern "C" __global__ __launch_bounds__(256) void pf_qk_rope_cache(
 namespace {
 constexpr float kScoreScaleLog2 = 0.0883883461356163f * 1.44269504088896341f;
 
-__device__ __forceinline__ float max_row16(float v) {
-  v = fmaxf(v, dpp<0xB1>(v));
-  v = fmaxf(v, dpp<0x4E>(v));
-  v = fmaxf(v, dpp<0x141>(v));
-  v = fmaxf(v, dpp<0x140>(v));
-  return v;
+// the max / sum of v over lanes i, i ^ 16, i ^ 32, i ^ 48 (v_permlane16_swap /
+// v_permlane32_swap hand each lane the value of its partner row)
+__device__ __forceinline__ float max_col4(float v) {
+  auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float sum_col4(float v) {
+  auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 }  // namespace
 
@@ -826,9 +840,8 @@ extern "C" __global__ __launch_bounds__(256) void pf_attention(
     const uint16_t* __restrict__ q_roped, const uint16_t* __restrict__ k_cache,
     const uint16_t* __restrict__ v_cache, int n, int start, int chunk_local, int split_blocks,
     float* __restrict__ part, uint16_t* __restrict__ out) {
-  __shared__ __attribute__((aligned(16))) _Float16 kt[32][136];      // K tile [key][dim]
-  __shared__ __attribute__((aligned(16))) _Float16 vt[32][144];      // V tile [key][dim]
-  __shared__ __attribute__((aligned(16))) _Float16 pt[4][2][16][40];  // P hi / lo [row][key]
+  __shared__ __attribute__((aligned(16))) _Float16 kt[32][136];  // K tile [key][dim]
+  __shared__ __attribute__((aligned(16))) _Float16 vt[32][144];  // V tile [key][dim]
   const int g = blockIdx.y;
   const int t = threadIdx.x;
   const int wave = t >> 6;
@@ -842,39 +855,35 @@ extern "C" __global__ __launch_bounds__(256) void pf_attention(
   const int qb = P.qb;
   const int q0 = 32 * qb + 16 * (wave & 1);  // this wave's first token
 
-  // Q rows as the MFMA A operand: row c16, dims 32 s + 8 grp .. + 7
-  f16x8 qa[4];
+  // Q rows as the MFMA B operand: column c16 (query q0 + c16), dims 32 s +
+  // 8 grp .. + 7
+  f16x8 qf[4];
   {
     const int qi = q0 + c16 < n ? q0 + c16 : n - 1;
     const _Float16* qs = reinterpret_cast<const _Float16*>(q_roped) + (size_t)qi * 2048 + head * 128;
 #pragma unroll
     for (int st = 0; st < 4; ++st)
-      qa[st] = *reinterpret_cast<const f16x8*>(qs + 32 * st + 8 * grp);
+      qf[st] = *reinterpret_cast<const f16x8*>(qs + 32 * st + 8 * grp);
   }
   const int last_tok = 32 * qb + 31 < n ? 32 * qb + 31 : n - 1;
   const int hi = start + last_tok;  // the last position any query here attends
   // this split's positions: [kb_lo, kb_hi]
   const int kb_lo = lo + 32 * split_blocks * P.s;
   const int kb_hi = hi < kb_lo + 32 * split_blocks - 1 ? hi : kb_lo + 32 * split_blocks - 1;
-  // this lane's 4 query rows (4 grp + i) and their positions
-  int qpos[4];
-  bool qok[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int tok = q0 + 4 * grp + i;
-    qok[i] = tok < n;
-    qpos[i] = start + tok;
-  }
-  float m[4], l[4];
+  // this lane's query and its position; the wave's first query position
+  const bool qok = q0 + c16 < n;
+  const int qpos = start + q0 + c16;
+  const bool wave_full = q0 + 15 < n;  // all 16 queries of the wave exist
+  float m = -__builtin_inff(), l = 0.0f;
   f32x4 o[8];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    m[i] = -__builtin_inff();
-    l[i] = 0.0f;
-  }
 #pragma unroll
   for (int d = 0; d < 8; ++d) o[d] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
   const f32x4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
+  // V^T reads: lane j of a 16-lane group addresses row vrow + j / 4, columns
+  // 16 d + 4 (j % 4) .. + 3; ds_read_b64_tr_b16 gives lane i element i % 4 of
+  // the pieces of lanes i / 4 + 4 r (r = 0..3): V[vrow + r][16 d + i]
+  const int vrow = 4 * grp + (c16 >> 2);
+  const int vcol = 4 * (c16 & 3);
 
   // thread t moves position kb + (t >> 3), dims 16 (t & 7) .. + 15 of K and V;
   // the next block's loads are in flight while the current block is used
@@ -901,7 +910,7 @@ extern "C" __global__ __launch_bounds__(256) void pf_attention(
     __syncthreads();
     if (kb + 32 <= kb_hi) load_tile(kb + 32);
 
-    // S = Q K^T for positions kb .. kb + 15 (tile 0) and kb + 16 .. kb + 31 (tile 1)
+    // S^T for positions kb .. kb + 15 (tile 0) and kb + 16 .. kb + 31 (tile 1)
     f32x4 sc[2];
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
@@ -909,87 +918,98 @@ extern "C" __global__ __launch_bounds__(256) void pf_attention(
 #pragma unroll
       for (int st = 0; st < 4; ++st) {
         const f16x8 kf = *reinterpret_cast<const f16x8*>(&kt[16 * nt + c16][32 * st + 8 * grp]);
-        sc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[st], kf, sc[nt], 0, 0, 0);
+        sc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[st], sc[nt], 0, 0, 0);
       }
     }
-    // online softmax per query row 4 grp + i (its 32 scores over the 16 lanes of the row group)
+    // s[4 nt + e]: position kb + 16 nt + 4 grp + e (a split ends on a block
+    // edge or at hi, so positions past kb_hi only appear masked)
+    float s[8];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      float sv[2];
-      bool ok[2];
+    for (int nt = 0; nt < 2; ++nt)
 #pragma unroll
-      for (int nt = 0; nt < 2; ++nt) {
-        const int kp = kb + 16 * nt + c16;
-        ok[nt] = qok[i] && kp <= qpos[i];  // a split ends on a block edge or at hi
-        sv[nt] = ok[nt] ? sc[nt][i] * kScoreScaleLog2 : -__builtin_inff();
+      for (int e = 0; e < 4; ++e) s[4 * nt + e] = sc[nt][e];
+    const bool masked = !(wave_full && kb + 31 <= start + q0);
+    if (masked) {
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int kp = kb + 16 * nt + 4 * grp + e;
+          if (!(qok && kp <= qpos)) s[4 * nt + e] = -__builtin_inff();
+        }
+    }
+    float mx = fmaxf(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])),
+                     fmaxf(fmaxf(s[4], s[5]), fmaxf(s[6], s[7])));
+    // fl(c x) is monotonic in x for c > 0: the max of the scaled scores
+    mx = max_col4(mx) * kScoreScaleLog2;
+    const float mn = fmaxf(m, mx);
+    // v_exp_f32 without the denormal-range fix-up of exp2f: a weight below
+    // 2^-126 beside the max's weight 1 changes no f32 sum
+    const float alpha = mn == -__builtin_inff() ? 1.0f : __builtin_amdgcn_exp2f(m - mn);
+    float p[8], ps = 0.0f;
+    if (masked) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        p[i] = s[i] == -__builtin_inff() ? 0.0f
+                                          : __builtin_amdgcn_exp2f(s[i] * kScoreScaleLog2 - mn);
+        ps += p[i];
       }
-      const float mx = max_row16(fmaxf(sv[0], sv[1]));
-      const float mn = fmaxf(m[i], mx);
-      const float alpha = mn == -__builtin_inff() ? 1.0f : exp2f(m[i] - mn);
-      float p[2];
+    } else {  // every score finite, mn finite
 #pragma unroll
-      for (int nt = 0; nt < 2; ++nt) p[nt] = ok[nt] ? exp2f(sv[nt] - mn) : 0.0f;
-      const float ps = reduce_row16(p[0] + p[1]);
-      l[i] = l[i] * alpha + ps;
-      m[i] = mn;
-#pragma unroll
-      for (int d = 0; d < 8; ++d) o[d][i] *= alpha;
-#pragma unroll
-      for (int nt = 0; nt < 2; ++nt) {
-        const _Float16 ph = to_f16(p[nt]);
-        const _Float16 pl = to_f16(p[nt] - (float)ph);
-        pt[wave][0][4 * grp + i][16 * nt + c16] = ph;
-        pt[wave][1][4 * grp + i][16 * nt + c16] = pl;
+      for (int i = 0; i < 8; ++i) {
+        p[i] = __builtin_amdgcn_exp2f(s[i] * kScoreScaleLog2 - mn);
+        ps += p[i];
       }
     }
-    // O += P V: A = P rows (this wave's 16 queries x 32 positions), B = V
-    // (positions x 16 dims per tile); LDS is in order within the wave.  B's
-    // lane c16 + 16 grp needs V[8 grp .. 8 grp + 7][16 d + c16]: two
-    // transposing reads (ds_read_b64_tr_b16, lane i of a 16-lane group gets
-    // element i % 4 of the 8-byte pieces addressed by lanes i / 4 + 4 r,
-    // r = 0..3), lane j of the group addressing row 8 grp + 4 h + j / 4,
-    // columns 16 d + 4 (j % 4) .. + 3, for positions 8 grp + 4 h .. + 3
-    const f16x8 ph = *reinterpret_cast<const f16x8*>(&pt[wave][0][c16][8 * grp]);
-    const f16x8 pl = *reinterpret_cast<const f16x8*>(&pt[wave][1][c16][8 * grp]);
-    const int vrow = 8 * grp + (c16 >> 2);
-    const int vcol = 4 * (c16 & 3);
+    l = l * alpha + ps;
+    m = mn;
+    if (__builtin_amdgcn_ballot_w64(alpha != 1.0f) != 0) {
+#pragma unroll
+      for (int d = 0; d < 8; ++d) o[d] *= alpha;
+    }
+    f16x8 ph, pl;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const _Float16 h = to_f16(p[i]);
+      ph[i] = h;
+      pl[i] = to_f16(p[i] - (float)h);
+    }
 #pragma unroll
     for (int d = 0; d < 8; ++d) {
       const v4i16 v0 =
           __builtin_amdgcn_ds_read_tr16_b64_v4i16((LDS_AS v4i16*)(&vt[vrow][16 * d + vcol]));
       const v4i16 v1 =
-          __builtin_amdgcn_ds_read_tr16_b64_v4i16((LDS_AS v4i16*)(&vt[vrow + 4][16 * d + vcol]));
+          __builtin_amdgcn_ds_read_tr16_b64_v4i16((LDS_AS v4i16*)(&vt[vrow + 16][16 * d + vcol]));
       const f16x8 vf = __builtin_bit_cast(
           f16x8, (v8i16){v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w});
-      o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph, vf, o[d], 0, 0, 0);
-      o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pl, vf, o[d], 0, 0, 0);
+      o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, ph, o[d], 0, 0, 0);
+      o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pl, o[d], 0, 0, 0);
     }
   }
+  // o[d][e]: dim 16 d + 4 grp + e of query q0 + c16; l over its four lanes
+  l = sum_col4(l);
 
   if (P.ns == 1) {
+    if (!qok) return;
+    uint16_t* orow = out + (size_t)(q0 + c16) * 2048 + head * 128 + 4 * grp;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int tok = q0 + 4 * grp + i;
-      if (tok >= n) continue;
-      uint16_t* orow = out + (size_t)tok * 2048 + head * 128;
-#pragma unroll
-      for (int d = 0; d < 8; ++d) orow[16 * d + c16] = f32_to_f16_bits(o[d][i] / l[i]);
+    for (int d = 0; d < 8; ++d) {
+      const uint2 v = {pack_f16x2(o[d][0] / l, o[d][1] / l), pack_f16x2(o[d][2] / l, o[d][3] / l)};
+      *reinterpret_cast<uint2*>(orow + 16 * d) = v;
     }
     return;
   }
 
-  // several splits: (m, l, O) of this split's positions to its slot, rows
-  // 16 wave + 4 grp + i; pf_attn_merge combines the slots
+  // several splits: (m, l, O) of this split's positions to its slot, row
+  // 16 wave + c16; pf_attn_merge combines the slots
   float* slot = part + ((size_t)blockIdx.x * kKvHeads + g) * kPfAttnSlotFloats;
+  const int r = 16 * wave + c16;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int r = 16 * wave + 4 * grp + i;
-#pragma unroll
-    for (int d = 0; d < 8; ++d) slot[r * kHeadDim + 16 * d + c16] = o[d][i];
-    if (c16 == 0) {
-      slot[64 * kHeadDim + r] = m[i];
-      slot[64 * kHeadDim + 64 + r] = l[i];
-    }
+  for (int d = 0; d < 8; ++d)
+    *reinterpret_cast<f32x4*>(slot + r * kHeadDim + 16 * d + 4 * grp) = o[d];
+  if (grp == 0) {
+    slot[64 * kHeadDim + r] = m;
+    slot[64 * kHeadDim + 64 + r] = l;
   }
 }
 
