@@ -794,9 +794,12 @@ extern "C" __global__ __launch_bounds__(256) void pf_qk_rope_cache(
 // whole cache, what the decode steps of @prefill_all see) or lo = start with
 // chunk_local != 0 (this call's tokens only, as the reference's @prefill
 // attends).  Wave w takes query head 2g + (w >> 1) and tokens 32 qb + 16 (w &
-// 1) .. + 15.  Per block of 32 cache positions the K tile ([32][128], rows
-// padded to 272 bytes) and the V tile ([32][128], rows padded to 288 bytes)
-// go to LDS, and each wave works transposed, one query per lane column:
+// 1) .. + 15.  Per block of 32 cache positions the K tile and the V tile
+// ([32][128] f16 each) are copied into LDS by the memory system
+// (global_load_lds, two blocks ahead, three buffers), row r's 16-byte chunk c
+// in slot c ^ (r & 15) (K) or c ^ 2 (r & 7) (V) so that the fragment reads
+// below hit distinct banks, and each wave works transposed, one query per
+// lane column:
 //   S^T = K Q^T: 8 v_mfma_f32_16x16x32_f16 (K rows as A, the wave's 16 query
 //     rows as B; exact f16 products, f32 sums), so lane (c16, grp) holds the
 //     scores of query c16 at positions 4 grp + e and 16 + 4 grp + e (e < 4);
@@ -840,8 +843,10 @@ extern "C" __global__ __launch_bounds__(256) void pf_attention(
     const uint16_t* __restrict__ q_roped, const uint16_t* __restrict__ k_cache,
     const uint16_t* __restrict__ v_cache, int n, int start, int chunk_local, int split_blocks,
     float* __restrict__ part, uint16_t* __restrict__ out) {
-  __shared__ __attribute__((aligned(16))) _Float16 kt[32][136];  // K tile [key][dim]
-  __shared__ __attribute__((aligned(16))) _Float16 vt[32][144];  // V tile [key][dim]
+  // K and V tiles of three blocks: separate arrays so the compiler sees that
+  // reading one buffer does not wait for the copies into the others
+  __shared__ __attribute__((aligned(1024))) uint8_t kt0[8192], kt1[8192], kt2[8192];
+  __shared__ __attribute__((aligned(1024))) uint8_t vt0[8192], vt1[8192], vt2[8192];
   const int g = blockIdx.y;
   const int t = threadIdx.x;
   const int wave = t >> 6;
@@ -880,35 +885,45 @@ extern "C" __global__ __launch_bounds__(256) void pf_attention(
   for (int d = 0; d < 8; ++d) o[d] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
   const f32x4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
   // V^T reads: lane j of a 16-lane group addresses row vrow + j / 4, columns
-  // 16 d + 4 (j % 4) .. + 3; ds_read_b64_tr_b16 gives lane i element i % 4 of
-  // the pieces of lanes i / 4 + 4 r (r = 0..3): V[vrow + r][16 d + i]
+  // 16 d + 4 (j % 4) .. + 3 (chunk 2 d + (j % 4) / 2, 8 (j % 2) bytes in);
+  // ds_read_b64_tr_b16 gives lane i element i % 4 of the pieces of lanes
+  // i / 4 + 4 r (r = 0..3): V[vrow + r][16 d + i]
   const int vrow = 4 * grp + (c16 >> 2);
-  const int vcol = 4 * (c16 & 3);
-
-  // thread t moves position kb + (t >> 3), dims 16 (t & 7) .. + 15 of K and V;
-  // the next block's loads are in flight while the current block is used
-  const int key = t >> 3;
-  const int dg = 16 * (t & 7);
-  u32x4 kr[2], vr[2];
-  auto load_tile = [&](int kb) {
-    const int kp = kb + key <= kb_hi ? kb + key : kb_hi;
-    const size_t row = ((size_t)kp * kKvHeads + g) * kHeadDim + dg;
-    kr[0] = load_global(reinterpret_cast<const u32x4*>(k_cache + row));
-    kr[1] = load_global(reinterpret_cast<const u32x4*>(k_cache + row + 8));
-    vr[0] = load_global(reinterpret_cast<const u32x4*>(v_cache + row));
-    vr[1] = load_global(reinterpret_cast<const u32x4*>(v_cache + row + 8));
+  auto v_off = [&](int row, int d) {
+    return 256 * row + 16 * ((2 * d + ((c16 & 3) >> 1)) ^ (2 * (row & 7))) + 8 * (c16 & 1);
   };
-  load_tile(kb_lo);
-  for (int kb = kb_lo; kb <= kb_hi; kb += 32) {
-    __syncthreads();  // every wave is done with the previous tiles
-    {
-      *reinterpret_cast<u32x4*>(&kt[key][dg]) = kr[0];
-      *reinterpret_cast<u32x4*>(&kt[key][dg + 8]) = kr[1];
-      *reinterpret_cast<u32x4*>(&vt[key][dg]) = vr[0];
-      *reinterpret_cast<u32x4*>(&vt[key][dg + 8]) = vr[1];
+
+  // Copies: wave w fills 1 KiB pieces 2 w, 2 w + 1 of each tile (rows 4 p ..
+  // 4 p + 3); lane l loads row 4 p + l / 16, the chunk whose slot is l % 16.
+  // Positions past kb_hi repeat kb_hi (only ever masked).
+  const int prow = lane >> 4;
+  auto issue = [&](int kb, uint8_t* kt, uint8_t* vt) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int pc = 2 * wave + j;
+      const int row = 4 * pc + prow;
+      const int kp = kb + row <= kb_hi ? kb + row : kb_hi;
+      const uint16_t* base = k_cache + ((size_t)kp * kKvHeads + g) * kHeadDim;
+      const size_t voff = ((size_t)kp * kKvHeads + g) * kHeadDim;
+      __builtin_amdgcn_global_load_lds(
+          (const GLOBAL_AS void*)(base + 8 * ((lane & 15) ^ (row & 15))),
+          (LDS_AS void*)(kt + 1024 * pc), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(
+          (const GLOBAL_AS void*)(v_cache + voff + 8 * ((lane & 15) ^ (2 * (row & 7)))),
+          (LDS_AS void*)(vt + 1024 * pc), 16, 0, 0);
     }
+  };
+
+  // One block: its copies landed (the next block's four copies per wave may
+  // still be in flight), a barrier (every wave's copies visible, every wave
+  // done with the previous block, whose buffers then receive block + 2).
+  auto block = [&](int kb, const uint8_t* kt, const uint8_t* vt, uint8_t* kn, uint8_t* vn) {
+    if (kb + 32 <= kb_hi)
+      wait_vm<4>();
+    else
+      wait_vm<0>();
     __syncthreads();
-    if (kb + 32 <= kb_hi) load_tile(kb + 32);
+    if (kb + 64 <= kb_hi) issue(kb + 64, kn, vn);
 
     // S^T for positions kb .. kb + 15 (tile 0) and kb + 16 .. kb + 31 (tile 1)
     f32x4 sc[2];
@@ -917,7 +932,8 @@ extern "C" __global__ __launch_bounds__(256) void pf_attention(
       sc[nt] = zero;
 #pragma unroll
       for (int st = 0; st < 4; ++st) {
-        const f16x8 kf = *reinterpret_cast<const f16x8*>(&kt[16 * nt + c16][32 * st + 8 * grp]);
+        const int row = 16 * nt + c16;
+        const f16x8 kf = *reinterpret_cast<const f16x8*>(kt + 256 * row + 16 * ((4 * st + grp) ^ c16));
         sc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[st], sc[nt], 0, 0, 0);
       }
     }
@@ -976,15 +992,26 @@ extern "C" __global__ __launch_bounds__(256) void pf_attention(
     }
 #pragma unroll
     for (int d = 0; d < 8; ++d) {
-      const v4i16 v0 =
-          __builtin_amdgcn_ds_read_tr16_b64_v4i16((LDS_AS v4i16*)(&vt[vrow][16 * d + vcol]));
-      const v4i16 v1 =
-          __builtin_amdgcn_ds_read_tr16_b64_v4i16((LDS_AS v4i16*)(&vt[vrow + 16][16 * d + vcol]));
+      const v4i16 v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (LDS_AS v4i16*)(vt + v_off(vrow, d)));
+      const v4i16 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (LDS_AS v4i16*)(vt + v_off(vrow + 16, d)));
       const f16x8 vf = __builtin_bit_cast(
           f16x8, (v8i16){v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w});
       o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, ph, o[d], 0, 0, 0);
       o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pl, o[d], 0, 0, 0);
     }
+  };
+
+  // buffer of block i: i % 3 (the loop unrolled by three)
+  issue(kb_lo, kt0, vt0);
+  if (kb_lo + 32 <= kb_hi) issue(kb_lo + 32, kt1, vt1);
+  for (int kb = kb_lo; kb <= kb_hi; kb += 96) {
+    block(kb, kt0, vt0, kt2, vt2);
+    if (kb + 32 > kb_hi) break;
+    block(kb + 32, kt1, vt1, kt0, vt0);
+    if (kb + 64 > kb_hi) break;
+    block(kb + 64, kt2, vt2, kt1, vt1);
   }
   // o[d][e]: dim 16 d + 4 grp + e of query q0 + c16; l over its four lanes
   l = sum_col4(l);
