@@ -195,9 +195,11 @@ int64_t qwen3_prefill_workspace_offset(int32_t n_tokens, const char* name);
  *   stacks: the q/k/v, attn_o and ffn_down GEMMs (gate/up always uses 64),
  *   32 or 64 (128 = 64); default: 32 where 64 would give fewer than 2
  *   workgroups per CU.  Over the f16 matrices: every GEMM, the tile of that
- *   many rows (the next larger where the GEMM has none); default: the largest
- *   tile whose grid gives every CU two workgroups.  Every tile computes each
- *   output with the same operations in the same order (tested bit for bit).
+ *   many rows (the next larger where the GEMM has none); default: per GEMM the
+ *   first of its tiles, largest first, whose grid fills the CUs with the
+ *   workgroups that tile is built to share a CU with.  Every tile computes
+ *   each output with the same operations in the same order (tested bit for
+ *   bit).
  * attn_split_blocks: cache positions per attention split, in blocks of 32
  *   (>= 1; raised where the workspace's partial slots would not hold the
  *   splits); default 8.  Splits change the order of the softmax sums, within

@@ -824,7 +824,10 @@ namespace {
 constexpr float kScoreScaleLog2 = 0.0883883461356163f * 1.44269504088896341f;
 
 // the max / sum of v over lanes i, i ^ 16, i ^ 32, i ^ 48 (v_permlane16_swap /
-// v_permlane32_swap hand each lane the value of its partner row)
+// v_permlane32_swap hand each lane the value of its partner row).  Both results
+// of each swap are used; the generated code was checked for that (a swap whose
+// second result is dropped reduces nothing), and the attention tests against
+// the oracle would fail on any lane seeing a different max.
 __device__ __forceinline__ float max_col4(float v) {
   auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
   v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
