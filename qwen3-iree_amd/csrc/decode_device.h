@@ -45,8 +45,13 @@ __device__ __forceinline__ float sum32(float v) {
   return v + __shfl_xor(v, 16, 64);
 }
 
+// f16(a) | f16(b) << 16, each rounded to nearest even (one v_cvt_pk_f16_f32);
+// the opaque copy keeps the compiler from folding a preceding multiply into a
+// single-rounding mixed-precision op, as to_f16 does
 __device__ __forceinline__ uint32_t pack_f16x2(float a, float b) {
-  return (uint32_t)f32_to_f16_bits(a) | ((uint32_t)f32_to_f16_bits(b) << 16);
+  asm volatile("" : "+v"(a), "+v"(b));
+  typedef float f32x2_t __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){a, b}, f16x2));
 }
 
 __device__ __forceinline__ _Float16 as_half(uint16_t b) { return __builtin_bit_cast(_Float16, b); }
@@ -57,26 +62,37 @@ __device__ __forceinline__ _Float16 as_half(uint16_t b) { return __builtin_bit_c
 // squares meet in a row reduction.
 __device__ __forceinline__ void rmsnorm_apply(const u32x4 (&hv)[8], const u32x4 (&wv)[8],
                                               u32x4 (&xr)[8]) {
-  float ss = 0.0f;
+  // the lane's 64 squares in 8 independent FMA chains of 8 (this sits on the
+  // critical path of every phase that starts from a freshly arrived vector:
+  // one chain of 128 dependent steps took about a microsecond), combined by a
+  // fixed tree; every kernel that normalises uses this function, so all of
+  // them round the same way
+  float s8[8];
+#pragma unroll
+  for (int c = 0; c < 8; ++c) s8[c] = 0.0f;
 #pragma unroll
   for (int m = 0; m < 8; ++m) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const f16x2 hp = as_f16x2(hv[m][j]);
       const float a = (float)hp.x, b = (float)hp.y;
-      ss = ss + a * a;
-      ss = ss + b * b;
+      s8[2 * j] = __builtin_fmaf(a, a, s8[2 * j]);
+      s8[2 * j + 1] = __builtin_fmaf(b, b, s8[2 * j + 1]);
     }
   }
+  float ss = ((s8[0] + s8[1]) + (s8[2] + s8[3])) + ((s8[4] + s8[5]) + (s8[6] + s8[7]));
   ss = reduce_row16(ss);
   const float inv = 1.0f / sqrtf(ss / 1024.0f + kEps);
+  // (h inv) w per column, each product rounded to f32 as written: fmaf with a
+  // -0 addend is exactly the product, and lets the f16 operands convert inside
+  // v_fma_mix_f32 (two instructions per column instead of five)
 #pragma unroll
   for (int m = 0; m < 8; ++m) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const f16x2 hp = as_f16x2(hv[m][j]), wp = as_f16x2(wv[m][j]);
-      const float a = ((float)hp.x * inv) * (float)wp.x;
-      const float b = ((float)hp.y * inv) * (float)wp.y;
+      const float a = __builtin_fmaf(__builtin_fmaf((float)hp.x, inv, -0.0f), (float)wp.x, -0.0f);
+      const float b = __builtin_fmaf(__builtin_fmaf((float)hp.y, inv, -0.0f), (float)wp.y, -0.0f);
       xr[m][j] = pack_f16x2(a, b);
     }
   }

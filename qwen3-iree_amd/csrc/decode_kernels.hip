@@ -656,10 +656,12 @@ void dec_step(StepParams P) {
         rmsnorm_gemv_x<false>(emb, an, xr[0]);
       } else {
         const auto h_src = [=](int i) { return prev + kWH + rep * kNH + i; };
+        // the norm weights first: the polled words come back after them (in
+        // order), so once h has arrived its norm never waits on these loads
+        u32x4 wv[8];
+        norm_weights(an, gemv_col, wv);
         uint64_t hp[Waiter::kMax];
         W.poll_begin(512, h_src, hp);
-        u32x4 wv[8];
-        norm_weights(an, gemv_col, wv);  // requested before the wait
         if (!W.poll_finish(512, step_tag(seq, layer - 1, kPhH), vec, h_src, hp)) return;
         STAMP(layer, 1);
         rmsnorm_lds_w(reinterpret_cast<const uint16_t*>(vec), gemv_col, wv, xr[0]);
