@@ -1043,19 +1043,22 @@ extern "C" __global__ __launch_bounds__(256) void pf_attention(
   }
 }
 
-// The splits of query block blockIdx.x, kv head g = blockIdx.y (nothing to do
-// for a block with one split), merged in split order with a running maximum
-// (m in base-2 units, as pf_attention keeps it):
+// The splits of query block blockIdx.x / 4, kv head g = blockIdx.y (nothing
+// to do for a block with one split), merged in split order with a running
+// maximum (m in base-2 units, as pf_attention keeps it):
 //   M' = max(M, m_s),  O' = O 2^(M - M') + O_s 2^(m_s - M'),
 //   l' = l 2^(M - M') + l_s 2^(m_s - M'),
-// out = O / l.  The partials of up to 2 splits are requested before any is
-// used.  Thread t: slot row t >> 2 (wave w = row >> 4 of pf_attention: head
-// 2g + (w >> 1), token 32 qb + 16 (w & 1) + (row & 15)), dims 32 (t & 3) ..
-// + 31.
+// out = O / l.  Four workgroups per query block, one per 32 of the 128
+// dimensions; thread t: slot row t >> 2 (wave w = row >> 4 of pf_attention:
+// head 2g + (w >> 1), token 32 qb + 16 (w & 1) + (row & 15)), dims
+// 32 (blockIdx.x % 4) + 8 (t & 3) .. + 7.  The partials of up to 8 splits are
+// requested before any is used, so a query block with many splits waits for
+// memory once per 8 splits.
 extern "C" __global__ __launch_bounds__(256) void pf_attn_merge(
     const float* __restrict__ part, int n, int start, int chunk_local, int split_blocks,
     uint16_t* __restrict__ out) {
-  const int qb = blockIdx.x;
+  const int qb = blockIdx.x >> 2;
+  const int quarter = blockIdx.x & 3;
   const int g = blockIdx.y;
   const PfSplitGeometry G = pf_split_geometry(n, start, chunk_local ? start : 0);
   const int nb = qb == G.nqb - 1 ? G.nb_last : qb + G.c;
@@ -1064,17 +1067,17 @@ extern "C" __global__ __launch_bounds__(256) void pf_attn_merge(
   const size_t first = (size_t)pf_pairs_before(G, qb, split_blocks) * kKvHeads + g;
   const int t = threadIdx.x;
   const int r = t >> 2;
-  const int d0 = 32 * (t & 3);
+  const int d0 = 32 * quarter + 8 * (t & 3);
   const int w = r >> 4;
   const int tok = 32 * qb + 16 * (w & 1) + (r & 15);
   if (tok >= n) return;
-  constexpr int kGroup = 2;
-  float M = -__builtin_inff(), L = 0.0f, acc[32];
+  constexpr int kGroup = 8;
+  float M = -__builtin_inff(), L = 0.0f, acc[8];
 #pragma unroll
-  for (int d = 0; d < 32; ++d) acc[d] = 0.0f;
+  for (int d = 0; d < 8; ++d) acc[d] = 0.0f;
   for (int s0 = 0; s0 < ns; s0 += kGroup) {
     float ms[kGroup], ls[kGroup];
-    float4 os[kGroup][8];
+    float4 os[kGroup][2];
 #pragma unroll
     for (int k = 0; k < kGroup; ++k) {
       const int s = s0 + k < ns ? s0 + k : ns - 1;
@@ -1082,8 +1085,8 @@ extern "C" __global__ __launch_bounds__(256) void pf_attn_merge(
       ms[k] = sl[64 * kHeadDim + r];
       ls[k] = sl[64 * kHeadDim + 64 + r];
       const float4* orow = reinterpret_cast<const float4*>(sl + r * kHeadDim + d0);
-#pragma unroll
-      for (int j = 0; j < 8; ++j) os[k][j] = orow[j];
+      os[k][0] = orow[0];
+      os[k][1] = orow[1];
     }
 #pragma unroll
     for (int k = 0; k < kGroup; ++k) {
@@ -1093,7 +1096,7 @@ extern "C" __global__ __launch_bounds__(256) void pf_attn_merge(
         const float b = ms[k] == -__builtin_inff() ? 0.0f : exp2f(ms[k] - mn);
         L = L * a + ls[k] * b;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
+        for (int j = 0; j < 2; ++j) {
           acc[4 * j] = acc[4 * j] * a + os[k][j].x * b;
           acc[4 * j + 1] = acc[4 * j + 1] * a + os[k][j].y * b;
           acc[4 * j + 2] = acc[4 * j + 2] * a + os[k][j].z * b;
@@ -1103,13 +1106,9 @@ extern "C" __global__ __launch_bounds__(256) void pf_attn_merge(
       }
     }
   }
-  uint32_t packed[16];
-#pragma unroll
-  for (int j = 0; j < 16; ++j) packed[j] = pack_f16x2(acc[2 * j] / L, acc[2 * j + 1] / L);
-  u32x4* dst = reinterpret_cast<u32x4*>(out + (size_t)tok * 2048 + (2 * g + (w >> 1)) * kHeadDim + d0);
-#pragma unroll
-  for (int j = 0; j < 4; ++j)
-    dst[j] = (u32x4){packed[4 * j], packed[4 * j + 1], packed[4 * j + 2], packed[4 * j + 3]};
+  const u32x4 v = {pack_f16x2(acc[0] / L, acc[1] / L), pack_f16x2(acc[2] / L, acc[3] / L),
+                   pack_f16x2(acc[4] / L, acc[5] / L), pack_f16x2(acc[6] / L, acc[7] / L)};
+  *reinterpret_cast<u32x4*>(out + (size_t)tok * 2048 + (2 * g + (w >> 1)) * kHeadDim + d0) = v;
 }
 
 // *pos = v (the position after the prompt, before the head's advance).

@@ -1493,7 +1493,7 @@ int launch_prefill_layer(const qwen3_weights* w, int layer, void* k_cache, void*
     if ((rc = launch2(g.pf_attn, (uint32_t)pairs, 8, 256, args, st))) return rc;
     if (pairs > G.nqb) {  // some query block has several splits
       void* margs[] = {&part, &nn, &start, &cl, &sb, &attn};
-      if ((rc = launch2(g.pf_attn_merge, (uint32_t)G.nqb, 8, 256, margs, st))) return rc;
+      if ((rc = launch2(g.pf_attn_merge, (uint32_t)(4 * G.nqb), 8, 256, margs, st))) return rc;
     }
   }
   // the attention partials are consumed by now: their region holds the
