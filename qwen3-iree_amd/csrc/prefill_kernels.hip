@@ -957,10 +957,13 @@ extern "C" __global__ __launch_bounds__(256) void pf_attention(
           if (!(qok && kp <= qpos)) s[4 * nt + e] = -__builtin_inff();
         }
     }
+    // scores in base-2 units (products are canonical floats, so the max below
+    // needs no NaN-quieting of its inputs)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) s[i] *= kScoreScaleLog2;
     float mx = fmaxf(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])),
                      fmaxf(fmaxf(s[4], s[5]), fmaxf(s[6], s[7])));
-    // fl(c x) is monotonic in x for c > 0: the max of the scaled scores
-    mx = max_col4(mx) * kScoreScaleLog2;
+    mx = max_col4(mx);
     const float mn = fmaxf(m, mx);
     // v_exp_f32 without the denormal-range fix-up of exp2f: a weight below
     // 2^-126 beside the max's weight 1 changes no f32 sum
@@ -969,14 +972,13 @@ extern "C" __global__ __launch_bounds__(256) void pf_attention(
     if (masked) {
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        p[i] = s[i] == -__builtin_inff() ? 0.0f
-                                          : __builtin_amdgcn_exp2f(s[i] * kScoreScaleLog2 - mn);
+        p[i] = s[i] == -__builtin_inff() ? 0.0f : __builtin_amdgcn_exp2f(s[i] - mn);
         ps += p[i];
       }
     } else {  // every score finite, mn finite
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        p[i] = __builtin_amdgcn_exp2f(s[i] * kScoreScaleLog2 - mn);
+        p[i] = __builtin_amdgcn_exp2f(s[i] - mn);
         ps += p[i];
       }
     }
@@ -986,12 +988,19 @@ extern "C" __global__ __launch_bounds__(256) void pf_attention(
 #pragma unroll
       for (int d = 0; d < 8; ++d) o[d] *= alpha;
     }
+    // hi = f16(p), lo = f16(p - hi), pairs at a time (v_cvt_pk_f16_f32); p - hi
+    // is exact in f32, so however the compiler forms lo it rounds once
     f16x8 ph, pl;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const _Float16 h = to_f16(p[i]);
-      ph[i] = h;
-      pl[i] = to_f16(p[i] - (float)h);
+    for (int i = 0; i < 8; i += 2) {
+      typedef float f32x2_t __attribute__((ext_vector_type(2)));
+      const f16x2 h2 = __builtin_convertvector((f32x2_t){p[i], p[i + 1]}, f16x2);
+      const f16x2 l2 = __builtin_convertvector(
+          (f32x2_t){p[i] - (float)h2.x, p[i + 1] - (float)h2.y}, f16x2);
+      ph[i] = h2.x;
+      ph[i + 1] = h2.y;
+      pl[i] = l2.x;
+      pl[i + 1] = l2.y;
     }
 #pragma unroll
     for (int d = 0; d < 8; ++d) {
