@@ -56,79 +56,80 @@ __device__ __forceinline__ uint32_t pack_f16x2(float a, float b) {
 
 __device__ __forceinline__ _Float16 as_half(uint16_t b) { return __builtin_bit_cast(_Float16, b); }
 
-// rms_norm (qwen3_full.mlir:134-165) of a 1024-vector for the 64 columns this
-// lane holds (hv: the values, wv: the norm weights, 8 per u32x4): the 16
-// lanes of a DPP row together hold all 1024 columns, so their partial sums of
-// squares meet in a row reduction.
+// rms_norm (qwen3_full.mlir:134-165).  Every kernel sums the 1024 squares in
+// one canonical order, a perfect binary tree over the columns in index order
+// with the leaves fl(x^2), so a vector normalized by the 16 lanes of a row
+// (rmsnorm_apply) or by a whole workgroup (rmsnorm_wg) gives the same bits.
+
+// the tree over columns 4k .. 4k + 3 (two f16 pairs): (q0 + q1) + (q2 + q3)
+__device__ __forceinline__ float sq_tree4(uint32_t lo, uint32_t hi) {
+  const f16x2 a = as_f16x2(lo), b = as_f16x2(hi);
+  const float a0 = (float)a.x, a1 = (float)a.y, b0 = (float)b.x, b1 = (float)b.y;
+  return (a0 * a0 + a1 * a1) + (b0 * b0 + b1 * b1);  // contraction is off: each term rounded
+}
+
+// x = f16((h inv) w) for an f16 pair of h and of w, packed
+__device__ __forceinline__ uint32_t norm_pair(uint32_t h2, uint32_t w2, float inv) {
+  const f16x2 hp = as_f16x2(h2), wp = as_f16x2(w2);
+  return pack_f16x2(((float)hp.x * inv) * (float)wp.x, ((float)hp.y * inv) * (float)wp.y);
+}
+
+__device__ __forceinline__ float rms_inv(float ss) { return 1.0f / sqrtf(ss / 1024.0f + kEps); }
+
+// The 64 columns this lane holds, contiguous (hv: the values, wv: the norm
+// weights, 8 per u32x4): the lane's subtree over them, then the 16 lanes of
+// its DPP row (reduce_row16 pairs lanes as a perfect tree in index order, fp
+// addition being commutative), so the row must hold the vector's columns in
+// lane order.
 __device__ __forceinline__ void rmsnorm_apply(const u32x4 (&hv)[8], const u32x4 (&wv)[8],
                                               u32x4 (&xr)[8]) {
-  // the lane's 64 squares in 8 independent FMA chains of 8 (this sits on the
-  // critical path of every phase that starts from a freshly arrived vector:
-  // one chain of 128 dependent steps took about a microsecond), combined by a
-  // fixed tree; every kernel that normalises uses this function, so all of
-  // them round the same way
-  float s8[8];
-#pragma unroll
-  for (int c = 0; c < 8; ++c) s8[c] = 0.0f;
+  float gs[16];
 #pragma unroll
   for (int m = 0; m < 8; ++m) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const f16x2 hp = as_f16x2(hv[m][j]);
-      const float a = (float)hp.x, b = (float)hp.y;
-      s8[2 * j] = __builtin_fmaf(a, a, s8[2 * j]);
-      s8[2 * j + 1] = __builtin_fmaf(b, b, s8[2 * j + 1]);
-    }
+    gs[2 * m] = sq_tree4(hv[m][0], hv[m][1]);
+    gs[2 * m + 1] = sq_tree4(hv[m][2], hv[m][3]);
   }
-  float ss = ((s8[0] + s8[1]) + (s8[2] + s8[3])) + ((s8[4] + s8[5]) + (s8[6] + s8[7]));
-  ss = reduce_row16(ss);
-  const float inv = 1.0f / sqrtf(ss / 1024.0f + kEps);
-  // (h inv) w per column, each product rounded to f32 as written: fmaf with a
-  // -0 addend is exactly the product, and lets the f16 operands convert inside
-  // v_fma_mix_f32 (two instructions per column instead of five)
 #pragma unroll
-  for (int m = 0; m < 8; ++m) {
+  for (int w = 8; w >= 1; w >>= 1)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const f16x2 hp = as_f16x2(hv[m][j]), wp = as_f16x2(wv[m][j]);
-      const float a = __builtin_fmaf(__builtin_fmaf((float)hp.x, inv, -0.0f), (float)wp.x, -0.0f);
-      const float b = __builtin_fmaf(__builtin_fmaf((float)hp.y, inv, -0.0f), (float)wp.y, -0.0f);
-      xr[m][j] = pack_f16x2(a, b);
-    }
-  }
+    for (int i = 0; i < w; ++i) gs[i] = gs[2 * i] + gs[2 * i + 1];
+  const float inv = rms_inv(reduce_row16(gs[0]));
+#pragma unroll
+  for (int m = 0; m < 8; ++m)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) xr[m][j] = norm_pair(hv[m][j], wv[m][j], inv);
 }
 
-// h from global memory (H_LDS = false) or from LDS (true); columns col(m).
-template <bool H_LDS, class ColOf>
-__device__ __forceinline__ void rmsnorm_cols(const uint16_t* __restrict__ h,
-                                             const uint16_t* __restrict__ w, ColOf col,
-                                             u32x4 (&xr)[8]) {
-  u32x4 hv[8], wv[8];
-#pragma unroll
-  for (int m = 0; m < 8; ++m) {
-    if constexpr (H_LDS) hv[m] = *reinterpret_cast<const u32x4*>(h + col(m));
-    else hv[m] = load_global(reinterpret_cast<const u32x4*>(h + col(m)));
-    wv[m] = load_global(reinterpret_cast<const u32x4*>(w + col(m)));
-  }
-  rmsnorm_apply(hv, wv, xr);
+// the sum of v over lanes i, i ^ 16, i ^ 32, i ^ 48: (r0 + r1) + (r2 + r3) for
+// the values r of the wave's four DPP rows, in every lane (v_permlane16_swap /
+// v_permlane32_swap hand each lane the value of its partner row; both results
+// of each swap are used, and fp addition is commutative)
+__device__ __forceinline__ float sum_col4(float v) {
+  auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
-// The norm weights of columns col(m), loaded ahead of the vector they scale.
-template <class ColOf>
-__device__ __forceinline__ void norm_weights(const uint16_t* __restrict__ w, ColOf col,
-                                             u32x4 (&wv)[8]) {
-#pragma unroll
-  for (int m = 0; m < 8; ++m) wv[m] = load_global(reinterpret_cast<const u32x4*>(w + col(m)));
+// rms_norm of a 1024-vector by a workgroup of 256 threads: thread t holds
+// columns 4t .. 4t + 3 (hv: their f16 values, w4: their norm weights) and gets
+// their x.  The thread's subtree, its DPP row (64 columns), the wave's four
+// rows, then the four waves' sums through red[4] in LDS.  Every thread of the
+// workgroup calls it; one barrier.  The caller keeps red from being written
+// again before every thread has read it (a barrier between two calls that
+// share it).
+__device__ __forceinline__ uint2 rmsnorm_wg(uint2 hv, uint2 w4, float* red) {
+  const int t = threadIdx.x;
+  const float v = sum_col4(reduce_row16(sq_tree4(hv.x, hv.y)));
+  if ((t & 63) == 0) red[t >> 6] = v;
+  __syncthreads();
+  const float inv = rms_inv((red[0] + red[1]) + (red[2] + red[3]));
+  return (uint2){norm_pair(hv.x, w4.x, inv), norm_pair(hv.y, w4.y, inv)};
 }
 
-// rms_norm of an f16 vector in LDS with norm weights already in registers.
-template <class ColOf>
-__device__ __forceinline__ void rmsnorm_lds_w(const uint16_t* __restrict__ h, ColOf col,
-                                              const u32x4 (&wv)[8], u32x4 (&xr)[8]) {
-  u32x4 hv[8];
-#pragma unroll
-  for (int m = 0; m < 8; ++m) hv[m] = *reinterpret_cast<const u32x4*>(h + col(m));
-  rmsnorm_apply(hv, wv, xr);
+// this thread's four norm weights for rmsnorm_wg
+__device__ __forceinline__ uint2 norm_weights4(const uint16_t* __restrict__ w) {
+  return load_global(reinterpret_cast<const uint2*>(w) + threadIdx.x);
 }
 
 // The loads of q8_quad_load<P> / q8_chunk_load<P> as copies from memory
@@ -185,11 +186,34 @@ __device__ __forceinline__ void q8_chunk_prefetch(const uint8_t* __restrict__ w,
 // The Q8_0 GEMV lane layout: columns [64 p16, 64 p16 + 64) in 8 pieces of 8.
 __device__ __forceinline__ int gemv_col(int m) { return 64 * (threadIdx.x & 15) + 8 * m; }
 
+// rms_norm of the 1024-vector h (global memory, or LDS for H_LDS) by the 16
+// lanes of each DPP row, in their GEMV columns: every row gets the whole x.
 template <bool H_LDS>
 __device__ __forceinline__ void rmsnorm_gemv_x(const uint16_t* __restrict__ h,
                                                const uint16_t* __restrict__ w, u32x4 (&xr)[8]) {
-  const int p16 = threadIdx.x & 15;
-  rmsnorm_cols<H_LDS>(h, w, [=](int m) { return 64 * p16 + 8 * m; }, xr);
+  u32x4 hv[8], wv[8];
+#pragma unroll
+  for (int m = 0; m < 8; ++m) {
+    if constexpr (H_LDS) hv[m] = *reinterpret_cast<const u32x4*>(h + gemv_col(m));
+    else hv[m] = load_global(reinterpret_cast<const u32x4*>(h + gemv_col(m)));
+    wv[m] = load_global(reinterpret_cast<const u32x4*>(w + gemv_col(m)));
+  }
+  rmsnorm_apply(hv, wv, xr);
+}
+
+// rms_norm by the workgroup (rmsnorm_wg) with x written over the 1024-vector
+// in LDS (vec: 512 words of f16 pairs, thread t's h4 the pair of words 2t,
+// 2t + 1), then this lane's GEMV columns of x read back.  Ends with the
+// barrier that makes x visible; whatever writes vec next must first wait
+// for every thread's reads.
+__device__ __forceinline__ void norm_to_vec(uint2 h4, uint2 w4, uint32_t* vec, float* red,
+                                            u32x4 (&xr)[8]) {
+  const uint2 x = rmsnorm_wg(h4, w4, red);
+  reinterpret_cast<uint2*>(vec)[threadIdx.x] = x;
+  __syncthreads();
+  const uint16_t* xs = reinterpret_cast<const uint16_t*>(vec);
+#pragma unroll
+  for (int m = 0; m < 8; ++m) xr[m] = *reinterpret_cast<const u32x4*>(xs + gemv_col(m));
 }
 
 // x for this lane's GEMV columns of chunk c, from an f16 vector in LDS.

@@ -220,15 +220,19 @@ extern "C" __global__ __launch_bounds__(256) void dec_vocab_argmax(
     const uint16_t* __restrict__ W, const uint16_t* __restrict__ h,
     const uint16_t* __restrict__ norm_w, uint16_t* __restrict__ logits, uint8_t* __restrict__ ws,
     uint16_t* __restrict__ xn) {
+  __shared__ __attribute__((aligned(16))) uint16_t xs[kHidden];
+  __shared__ float red[4];
   vocab_body_x<VOCAB_NT_LOADS != 0, true>(
       W,
       [&](int li, u32x4 (&xr)[8]) {
-        rmsnorm_cols<false>(h, norm_w, [=](int m) { return 128 * m + 8 * li; }, xr);
-        if (blockIdx.x == 0 && threadIdx.x < 16) {
+        const int t = threadIdx.x;
+        const uint2 x = rmsnorm_wg(load_global(reinterpret_cast<const uint2*>(h) + t),
+                                   norm_weights4(norm_w), red);
+        reinterpret_cast<uint2*>(xs)[t] = x;
+        if (blockIdx.x == 0) reinterpret_cast<uint2*>(xn)[t] = x;
+        __syncthreads();
 #pragma unroll
-          for (int m = 0; m < 8; ++m)
-            reinterpret_cast<u32x4*>(xn + 128 * m + 8 * li)[0] = xr[m];
-        }
+        for (int m = 0; m < 8; ++m) xr[m] = *reinterpret_cast<const u32x4*>(xs + 128 * m + 8 * li);
       },
       logits, kVocab, ws);
 }
@@ -600,6 +604,7 @@ void dec_step(StepParams P) {
   __shared__ __attribute__((aligned(16))) StepLds S;
   __shared__ __attribute__((aligned(16))) uint32_t vec[kVecWords];  // polled words' data
   __shared__ int s_abort;
+  __shared__ float s_red[4];  // rms_norm: the waves' sums
   const int wg = blockIdx.x;
   const int rep = wg % kRep;  // the replica this workgroup polls
   const int t = threadIdx.x;
@@ -652,20 +657,21 @@ void dec_step(StepParams P) {
       // ---- A ----
       u32x4 xr[1][8];
       const uint16_t* an = P.attn_norm + layer * kHidden;
+      // the norm weights first: the polled words come back after them (in
+      // order), so once h has arrived its norm never waits on these loads
+      const uint2 aw4 = norm_weights4(an);
+      uint2 h4;
       if (layer == 0) {
-        rmsnorm_gemv_x<false>(emb, an, xr[0]);
+        h4 = load_global(reinterpret_cast<const uint2*>(emb) + t);
       } else {
         const auto h_src = [=](int i) { return prev + kWH + rep * kNH + i; };
-        // the norm weights first: the polled words come back after them (in
-        // order), so once h has arrived its norm never waits on these loads
-        u32x4 wv[8];
-        norm_weights(an, gemv_col, wv);
         uint64_t hp[Waiter::kMax];
         W.poll_begin(512, h_src, hp);
         if (!W.poll_finish(512, step_tag(seq, layer - 1, kPhH), vec, h_src, hp)) return;
         STAMP(layer, 1);
-        rmsnorm_lds_w(reinterpret_cast<const uint16_t*>(vec), gemv_col, wv, xr[0]);
+        h4 = reinterpret_cast<const uint2*>(vec)[t];
       }
+      norm_to_vec(h4, aw4, vec, s_red, xr[0]);
       STAMP(layer, 13);
       const float acc = q8_quad_dot<1>(la, xr);
       uint64_t* dst = quad < 512 ? cur + kWQ : (quad < 768 ? cur + kWK : cur + kWV);
@@ -680,12 +686,11 @@ void dec_step(StepParams P) {
       }
       // ---- D: gate/up + SwiGLU ----
       if (has_d) {
-        u32x4 wv[8];
-        norm_weights(P.ffn_norm + layer * kHidden, gemv_col, wv);  // requested before the wait
+        const uint2 dw4 = norm_weights4(P.ffn_norm + layer * kHidden);  // before the wait
         if (!W.wait(cur + kWRes + rep * kNRes, 512, step_tag(seq, layer, kPhRes), vec)) return;
         STAMP(layer, 9);
         u32x4 xd[1][8];
-        rmsnorm_lds_w(reinterpret_cast<const uint16_t*>(vec), gemv_col, wv, xd[0]);
+        norm_to_vec(reinterpret_cast<const uint2*>(vec)[t], dw4, vec, s_red, xd[0]);
         const float ag = q8_quad_dot<1>(lg, xd);
         const float au = q8_quad_dot<1>(lu, xd);
         const uint32_t act = swiglu_f16(ag, au);
@@ -885,17 +890,19 @@ void dec_step(StepParams P) {
     vocab_body_xp<VOCAB_NT_LOADS != 0, true>(
         P.output_w,
         [&](int li, u32x4 (&xr)[8]) {
-          const auto col = [=](int m) { return 128 * m + 8 * li; };
-          u32x4 wv[8];
-          norm_weights(P.output_norm, col, wv);  // requested before the wait
+          const uint2 w4 = norm_weights4(P.output_norm);  // requested before the wait
           ok = W.wait(hfin, 512, tag_h, vec);
           STAMP(kLayers, 1);
-          if (ok) rmsnorm_lds_w(reinterpret_cast<const uint16_t*>(vec), col, wv, xr);
-          if (wg == 0 && t < 16) {
+          if (!ok) return;
+          uint2* v2 = reinterpret_cast<uint2*>(vec);
+          const uint2 x = rmsnorm_wg(v2[t], w4, s_red);
+          v2[t] = x;
+          if (wg == 0) reinterpret_cast<uint2*>(P.on_out)[t] = x;
+          __syncthreads();
+          const uint16_t* xs = reinterpret_cast<const uint16_t*>(vec);
 #pragma unroll
-            for (int m = 0; m < 8; ++m)
-              reinterpret_cast<u32x4*>(P.on_out + 128 * m + 8 * li)[0] = xr[m];
-          }
+          for (int m = 0; m < 8; ++m)
+            xr[m] = *reinterpret_cast<const u32x4*>(xs + 128 * m + 8 * li);
         },
         P.logits, kVocab, [&](uint64_t key) {
           put_word(P.words + kWArg + 2 * wg, (uint32_t)(key >> 32), tag_arg);

@@ -634,18 +634,19 @@ extern "C" __global__ __launch_bounds__(256) void pf_res_reduce(
 // pf_res_reduce for N = 1024 (y, r ld 1024) followed by out = rms_norm(y, w)
 // of the same row, so no separate pf_rmsnorm launch is needed.  Workgroup =
 // one row: every thread reduces 4 columns (all splits' loads issued first,
-// then added in split order, as pf_res_reduce adds them) and adds the
-// residual; the row goes through LDS to the first 16 lanes, which normalise
-// it with pf_rmsnorm's lane layout and device function.  y and out are those
-// two kernels' bits.  splits <= kPfMaxSplits.
+// then added in split order, as pf_res_reduce adds them), adds the residual
+// and normalises its columns with the workgroup (rmsnorm_wg, the same sum
+// order as pf_rmsnorm's 16 lanes).  y and out are those two kernels' bits.
+// splits <= kPfMaxSplits.
 extern "C" __global__ __launch_bounds__(256) void pf_res_reduce_norm(
     const float* __restrict__ part, int splits, int M, const uint16_t* __restrict__ r,
     uint16_t* __restrict__ y, const uint16_t* __restrict__ w, uint16_t* __restrict__ out) {
-  __shared__ __attribute__((aligned(16))) uint16_t row_h[kHidden];
+  __shared__ float red[4];
   const int m = blockIdx.x;
   const int c = 4 * threadIdx.x;
   const size_t e = (size_t)m * kHidden + c;
   const size_t plane = (size_t)M * kHidden;
+  const uint2 w4 = norm_weights4(w);
   float4 v[kPfMaxSplits];
 #pragma unroll
   for (int s = 0; s < kPfMaxSplits; ++s)
@@ -666,15 +667,7 @@ extern "C" __global__ __launch_bounds__(256) void pf_res_reduce_norm(
                       ((uint32_t)residual_f16(as_half((uint16_t)(rv.y >> 16)), a.w) << 16);
   const uint2 o = {lo, hi};
   *reinterpret_cast<uint2*>(y + e) = o;
-  *reinterpret_cast<uint2*>(row_h + c) = o;
-  __syncthreads();
-  if (threadIdx.x < 16) {
-    u32x4 xr[8];
-    rmsnorm_cols<true>(row_h, w, gemv_col, xr);
-    u32x4* xo = reinterpret_cast<u32x4*>(out + (size_t)m * kHidden + gemv_col(0));
-#pragma unroll
-    for (int k = 0; k < 8; ++k) xo[k] = xr[k];
-  }
+  *reinterpret_cast<uint2*>(out + e) = rmsnorm_wg(o, w4, red);
 }
 
 extern "C" __global__ __launch_bounds__(256) void pf_gemm_q8_swiglu(GemmArgs A) {
@@ -823,22 +816,17 @@ extern "C" __global__ __launch_bounds__(256) void pf_qk_rope_cache(
 namespace {
 constexpr float kScoreScaleLog2 = 0.0883883461356163f * 1.44269504088896341f;
 
-// the max / sum of v over lanes i, i ^ 16, i ^ 32, i ^ 48 (v_permlane16_swap /
-// v_permlane32_swap hand each lane the value of its partner row).  Both results
-// of each swap are used; the generated code was checked for that (a swap whose
-// second result is dropped reduces nothing), and the attention tests against
-// the oracle would fail on any lane seeing a different max.
+// the max of v over lanes i, i ^ 16, i ^ 32, i ^ 48 (v_permlane16_swap /
+// v_permlane32_swap hand each lane the value of its partner row; sum_col4 is
+// the sum).  Both results of each swap are used; the generated code was
+// checked for that (a swap whose second result is dropped reduces nothing),
+// and the attention tests against the oracle would fail on any lane seeing a
+// different max.
 __device__ __forceinline__ float max_col4(float v) {
   auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
   v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
   auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
   return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
-}
-__device__ __forceinline__ float sum_col4(float v) {
-  auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
-  auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 }  // namespace
 
