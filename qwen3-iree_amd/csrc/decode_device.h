@@ -25,25 +25,42 @@ constexpr float kRopeBase = 1.0e6f;       // qwen3_full.mlir:59
 // rsqrt(128) of qwen3_full.mlir:721-723, the f32 nearest 2^-3.5 (0x3DB504F3)
 constexpr float kAttnScale = 0.0883883461356163f;
 
-__device__ __forceinline__ float wave_sum(float v) {
-  v = reduce_row16(v);
-  v += __shfl_xor(v, 16, 64);
-  v += __shfl_xor(v, 32, 64);
-  return v;
+// Lane exchanges through v_permlane16_swap / v_permlane32_swap (VALU, no LDS
+// round trip).  With both operands v, permlane16_swap returns {v of rows 0, 0,
+// 2, 2; v of rows 1, 1, 3, 3} and permlane32_swap {v of lanes i & 31; v of
+// lanes 32 + (i & 31)}: every lane holds its own value and its partner's.
+__device__ __forceinline__ float sum_rows2(float v) {  // rows 2k and 2k + 1: r_2k + r_2k+1
+  auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(a[0]) + __uint_as_float(a[1]);
 }
+__device__ __forceinline__ float sum_halves(float v) {  // lanes i and i ^ 32: v_lo + v_hi
+  auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(a[0]) + __uint_as_float(a[1]);
+}
+__device__ __forceinline__ float xor32(float v) {  // the value of lane i ^ 32
+  auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float((threadIdx.x & 32) ? a[0] : a[1]);
+}
+
+// the sum of v over lanes i, i ^ 16, i ^ 32, i ^ 48: (r0 + r1) + (r2 + r3) for
+// the values r of the wave's four DPP rows, in every lane (fp addition is
+// commutative, so a lane adding its partner's value to its own or the other
+// way round gets the same bits)
+__device__ __forceinline__ float sum_col4(float v) { return sum_halves(sum_rows2(v)); }
+
+// the sum over the wave: rows in index order, (r0 + r1) + (r2 + r3)
+__device__ __forceinline__ float wave_sum(float v) { return sum_col4(reduce_row16(v)); }
 
 __device__ __forceinline__ float max32(float v) {  // over the 32 lanes of a wave half
   v = fmaxf(v, dpp<0xB1>(v));
   v = fmaxf(v, dpp<0x4E>(v));
   v = fmaxf(v, dpp<0x141>(v));
   v = fmaxf(v, dpp<0x140>(v));
-  return fmaxf(v, __shfl_xor(v, 16, 64));
+  auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
 }
 
-__device__ __forceinline__ float sum32(float v) {
-  v = reduce_row16(v);
-  return v + __shfl_xor(v, 16, 64);
-}
+__device__ __forceinline__ float sum32(float v) { return sum_rows2(reduce_row16(v)); }
 
 // f16(a) | f16(b) << 16, each rounded to nearest even (one v_cvt_pk_f16_f32);
 // the opaque copy keeps the compiler from folding a preceding multiply into a
@@ -98,17 +115,6 @@ __device__ __forceinline__ void rmsnorm_apply(const u32x4 (&hv)[8], const u32x4 
   for (int m = 0; m < 8; ++m)
 #pragma unroll
     for (int j = 0; j < 4; ++j) xr[m][j] = norm_pair(hv[m][j], wv[m][j], inv);
-}
-
-// the sum of v over lanes i, i ^ 16, i ^ 32, i ^ 48: (r0 + r1) + (r2 + r3) for
-// the values r of the wave's four DPP rows, in every lane (v_permlane16_swap /
-// v_permlane32_swap hand each lane the value of its partner row; both results
-// of each swap are used, and fp addition is commutative)
-__device__ __forceinline__ float sum_col4(float v) {
-  auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
-  auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
 // rms_norm of a 1024-vector by a workgroup of 256 threads: thread t holds
@@ -307,20 +313,22 @@ __device__ __forceinline__ SplitRange split_range(int s, int pos) {
 // row, 8 x 1 KiB) then V (32 rows x the lane's two dims, 32 x 256 B).
 constexpr int kKvPrefetchBytes = 8 * 1024 + 32 * 256;
 
-// The first chunk of a split's cache rows (the loads attention_group's step 0
-// issues) copied into LDS by the memory system (global_load_lds), so no
-// register holds them while they are in flight: lane l's K piece m lands at
-// kv + 1024 m + 16 l, its V word of row j at kv + 8192 + 256 j + 4 l.  kv is
-// the wave's kKvPrefetchBytes region; the data may be read once the wave's
-// vector memory counter has drained past these loads.
+// One chunk of a split's cache rows -- positions c0 .. c0 + 31, clamped to
+// `last` -- copied into the wave's LDS region kv by the memory system
+// (global_load_lds), so no register holds them while they are in flight: lane
+// (pl, half)'s K piece m (row c0 + pl, dims 64 half + 8 m .. + 8) lands at kv
+// + 1024 m + 16 lane, the V word of row c0 + j (dims 2 lane, 2 lane + 1) at kv
+// + 8192 + 256 j + 4 lane.  The wave may read them once its vector memory
+// counter has drained past these loads.  PACE > 0 sleeps 64 PACE cycles after
+// the K pieces and after every fourth V row.
 template <int PACE = 0>
-__device__ __forceinline__ void kv_prefetch(uint8_t* kv, const uint16_t* __restrict__ k_cache,
-                                            const uint16_t* __restrict__ v_cache, int g,
-                                            const SplitRange& r) {
+__device__ __forceinline__ void kv_stage(uint8_t* kv, const uint16_t* __restrict__ k_cache,
+                                         const uint16_t* __restrict__ v_cache, int g, int c0,
+                                         int last) {
   const int lane = threadIdx.x & 63;
   const int half = lane >> 5;
   const int pl = lane & 31;
-  const int p = r.start + pl < r.last ? r.start + pl : r.last;
+  const int p = c0 + pl < last ? c0 + pl : last;
   const u32x4* krow = reinterpret_cast<const u32x4*>(
       k_cache + ((size_t)p * kKvHeads + g) * kHeadDim + 64 * half);
 #pragma unroll
@@ -328,10 +336,10 @@ __device__ __forceinline__ void kv_prefetch(uint8_t* kv, const uint16_t* __restr
     __builtin_amdgcn_global_load_lds((const GLOBAL_AS void*)(krow + m),
                                      (__attribute__((address_space(3))) void*)(kv + 1024 * m), 16,
                                      0, 0);
-    if constexpr (PACE > 0) __builtin_amdgcn_s_sleep(PACE);
+  if constexpr (PACE > 0) __builtin_amdgcn_s_sleep(PACE);
 #pragma unroll
   for (int j = 0; j < 32; ++j) {
-    const int pj = r.start + j < r.last ? r.start + j : r.last;
+    const int pj = c0 + j < last ? c0 + j : last;
     __builtin_amdgcn_global_load_lds(
         (const GLOBAL_AS void*)(reinterpret_cast<const uint32_t*>(
                                     v_cache + ((size_t)pj * kKvHeads + g) * kHeadDim) +
@@ -342,11 +350,18 @@ __device__ __forceinline__ void kv_prefetch(uint8_t* kv, const uint16_t* __restr
   }
 }
 
+// The first chunk of split r (what attention_group reads first).
+template <int PACE = 0>
+__device__ __forceinline__ void kv_prefetch(uint8_t* kv, const uint16_t* __restrict__ k_cache,
+                                            const uint16_t* __restrict__ v_cache, int g,
+                                            const SplitRange& r) {
+  kv_stage<PACE>(kv, k_cache, v_cache, g, r.start, r.last);
+}
+
 // LDS of one attention workgroup.
 struct __attribute__((aligned(16))) AttnLds {
   uint32_t qh[2][64];  // roped q_A, q_B as f16 pairs
   uint32_t kh[64];     // roped new k as f16 pairs
-  float pbuf[kAttnWaves][2][32];
   float mrg[kAttnWaves][2][2 + kHeadDim];
 };
 
@@ -354,11 +369,11 @@ struct __attribute__((aligned(16))) AttnLds {
 // position split s = 4 sg + w of the 32 equal splits of ctx = pos + 1; the
 // four results merge in LDS into one partial per query head and group.  Per
 // wave:
-//  0. the split's first 32 cache rows (K: half a row per lane, V: the lane's
-//     two dims for each of the 32 positions) are requested before q/k/v are
-//     fetched (get_qkv), so their latency overlaps that wait and steps 1-2;
-//     with kv != null they were prefetched into LDS (kv_prefetch, this wave's
-//     region) and are read from there;
+//  0. the split's cache rows go through the wave's LDS region kv
+//     (kKvPrefetchBytes, kv_stage) 32 at a time; the first chunk is staged
+//     before q/k/v are fetched (get_qkv), so its latency overlaps that wait
+//     and steps 1-2, or was staged by the caller long before (kv_staged:
+//     kv_prefetch);
 //  1. waves 0, 1, 2 take q head 2g, q head 2g+1 and k head g: per-head
 //     rms_norm with q_norm / k_norm (qwen3_full.mlir:648-702), then RoPE
 //     (:324-454) at position pos, shared with the other waves through LDS;
@@ -370,8 +385,8 @@ struct __attribute__((aligned(16))) AttnLds {
 //     on dims [64*half, 64*half + 64) for both q heads, the halves meet in one
 //     cross-half add; s_j = (q . k_j) * rsqrt(128); online softmax; the
 //     weighted sum of v (each lane owns dims 2*lane, 2*lane+1 of both heads).
-//     The chunk count is uniform over the workgroup (splits differ by at most
-//     one position), so every wave meets every barrier;
+//     A position's weights reach the lanes holding v as lane reads, so a
+//     wave runs its chunks without waiting for the others;
 //  4. publish(hh, m, l, a0, a1) on waves 0 and 1 (query head 2g + hh): m =
 //     max over the 4 waves, l and this lane's two dims rescaled by
 //     exp(m_w - m).  An empty split (ctx < 32) contributes m = -inf, l = 0.
@@ -388,7 +403,7 @@ __device__ __forceinline__ void attention_group(AttnLds& L, int g, int sg, int p
                                                 uint16_t* __restrict__ k_cache,
                                                 uint16_t* __restrict__ v_cache,
                                                 uint16_t* __restrict__ q_roped,
-                                                const uint8_t* kv, PreQKV&& pre_qkv,
+                                                uint8_t* kv, bool kv_staged, PreQKV&& pre_qkv,
                                                 GetQKV&& get_qkv, Publish&& publish) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -412,39 +427,15 @@ __device__ __forceinline__ void attention_group(AttnLds& L, int g, int sg, int p
                         pos < split_range(sg * kAttnWaves + kAttnWaves - 1, pos).end;
   const int n_chunks = ((ctx + kAttnSplits - 1) / kAttnSplits + 31) / 32;  // workgroup-uniform
 
-  // ---- 0. first chunk of the cache ----
-  // Every lane issues every load (rows clamped into [start, end - 1], row 0
-  // for an empty split) so the compiler's waits stay exact.
+  // ---- 0. first chunk of the cache (rows clamped into [start, end - 1],
+  // row 0 for an empty split), staged into this wave's LDS region unless the
+  // caller already did (kv_prefetch) ----
   const int last = sr.last;
-  u32x4 kreg[8];
-  uint32_t vreg[32];
-  auto load_chunk = [&](int c0) {
-    const int p = c0 + pl < last ? c0 + pl : last;
-    const u32x4* krow = reinterpret_cast<const u32x4*>(
-        k_cache + ((size_t)p * kKvHeads + g) * kHeadDim + 64 * half);
-#pragma unroll
-    for (int m = 0; m < 8; ++m) kreg[m] = load_global(krow + m);
-#pragma unroll
-    for (int j = 0; j < 32; ++j) {
-      const int pj = c0 + j < last ? c0 + j : last;
-      vreg[j] = load_global(
-          reinterpret_cast<const uint32_t*>(v_cache + ((size_t)pj * kKvHeads + g) * kHeadDim) + lane);
-    }
-  };
-  if (kv == nullptr) load_chunk(start);
+  if (!kv_staged) kv_stage(kv, k_cache, v_cache, g, start, last);
   __builtin_amdgcn_sched_barrier(0);
 
   uint32_t xw[3], v_new;
   get_qkv(xw, v_new);
-  if (kv != nullptr) {  // the first chunk was prefetched into LDS (kv_prefetch)
-    // read after get_qkv's wait, when every earlier memory operation of the
-    // wave (the prefetch included) has completed
-#pragma unroll
-    for (int m = 0; m < 8; ++m) kreg[m] = *reinterpret_cast<const u32x4*>(kv + 1024 * m + 16 * lane);
-#pragma unroll
-    for (int j = 0; j < 32; ++j)
-      vreg[j] = *reinterpret_cast<const uint32_t*>(kv + 8192 + 256 * j + 4 * lane);
-  }
 
   // ---- 1. head norms + RoPE: wave t < 3 takes vector t (q head 2g, q head
   // 2g+1, k head g), lane owns dims 2*lane, 2*lane+1; RoPE's partner dims
@@ -463,7 +454,7 @@ __device__ __forceinline__ void attention_group(AttnLds& L, int g, int sg, int p
     float r2[2];
 #pragma unroll
     for (int dd = 0; dd < 2; ++dd) {
-      const float other = __shfl_xor(xs[dd], 32, 64);
+      const float other = xor32(xs[dd]);
       if (lane < 32) {
         const float u = xs[dd] * cs[dd];
         const float w2 = other * sn[dd];
@@ -498,8 +489,12 @@ __device__ __forceinline__ void attention_group(AttnLds& L, int g, int sg, int p
     const int c0 = start + 32 * c;
     const int p = c0 + pl;
     const bool valid = p < end;
+    u32x4 kreg[8];
+#pragma unroll
+    for (int mm = 0; mm < 8; ++mm)
+      kreg[mm] = *reinterpret_cast<const u32x4*>(kv + 1024 * mm + 16 * lane);
     // the row of position pos is this step's k (in LDS; the cache slot was
-    // requested before it was written): one lane takes it over
+    // staged before it was written): one lane takes it over
     if (p == pos) {
 #pragma unroll
       for (int mm = 0; mm < 8; ++mm)
@@ -521,8 +516,8 @@ __device__ __forceinline__ void attention_group(AttnLds& L, int g, int sg, int p
       }
     }
     float dA = dA0 + dA1, dB = dB0 + dB1;
-    dA = dA + __shfl_xor(dA, 32, 64);
-    dB = dB + __shfl_xor(dB, 32, 64);
+    dA = sum_halves(dA);
+    dB = sum_halves(dB);
     const float sA = valid ? dA * kAttnScale : -__builtin_inff();
     const float sB = valid ? dB * kAttnScale : -__builtin_inff();
     const float mnA = fmaxf(m, max32(sA));
@@ -536,33 +531,43 @@ __device__ __forceinline__ void attention_group(AttnLds& L, int g, int sg, int p
     lB = lB * cB + sum32(pB);
     m = mnA;
     mB = mnB;
-    if (half == 0) {
-      L.pbuf[wave][0][pl] = pA;
-      L.pbuf[wave][1][pl] = pB;
-    }
-    __syncthreads();
     accA0 *= cA;
     accA1 *= cA;
     accB0 *= cB;
     accB1 *= cB;
+    __builtin_amdgcn_sched_barrier(0);
+    // position j's weights are lane j's p (lanes j and j + 32 hold the same
+    // value), read into scalar registers four positions at a time (the
+    // scheduling fences keep the compiler from hoisting all 64 reads).
+    // With `fix`, position pos takes this step's v, and positions past the
+    // split (weight 0, a clamped valid row) take v = 0, so a non-finite value
+    // there cannot leak in; most chunks need neither (a wave-uniform branch).
     const int n = end - c0 < 32 ? end - c0 : 32;
-    // unrolled by 8, not 32: fully unrolled, the compiler hoists all 64
-    // weight reads from LDS and the step kernel runs out of registers
-#pragma unroll 8
-    for (int j = 0; j < 32; ++j) {
-      // positions past the split hold weight 0 and a clamped (valid) row,
-      // selected to 0 so a non-finite value there cannot leak in
-      const uint32_t vw = c0 + j == pos ? v_new : (j < n ? vreg[j] : 0u);
-      const f16x2 vv = as_f16x2(vw);
-      const float v0 = (float)vv.x, v1 = (float)vv.y;
-      const float wa = L.pbuf[wave][0][j], wb = L.pbuf[wave][1][j];
-      accA0 = __builtin_fmaf(wa, v0, accA0);
-      accA1 = __builtin_fmaf(wa, v1, accA1);
-      accB0 = __builtin_fmaf(wb, v0, accB0);
-      accB1 = __builtin_fmaf(wb, v1, accB1);
-    }
-    __syncthreads();
-    if (c + 1 < n_chunks) load_chunk(c0 + 32);
+    const auto weighted_v = [&](bool fix) {
+#pragma unroll
+      for (int j0 = 0; j0 < 32; j0 += 4) {
+#pragma unroll
+        for (int j = j0; j < j0 + 4; ++j) {
+          const uint32_t vs = *reinterpret_cast<const uint32_t*>(kv + 8192 + 256 * j + 4 * lane);
+          const uint32_t vw = fix ? (c0 + j == pos ? v_new : (j < n ? vs : 0u)) : vs;
+          const f16x2 vv = as_f16x2(vw);
+          const float v0 = (float)vv.x, v1 = (float)vv.y;
+          const float wa = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pA), j));
+          const float wb = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pB), j));
+          accA0 = __builtin_fmaf(wa, v0, accA0);
+          accA1 = __builtin_fmaf(wa, v1, accA1);
+          accB0 = __builtin_fmaf(wb, v0, accB0);
+          accB1 = __builtin_fmaf(wb, v1, accB1);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    };
+    if (n < 32 || (pos >= c0 && pos < c0 + 32)) weighted_v(true);
+    else weighted_v(false);
+    __builtin_amdgcn_sched_barrier(0);
+    // the next chunk into the same region: every read of this one has
+    // returned (its values were used above)
+    if (c + 1 < n_chunks) kv_stage(kv, k_cache, v_cache, g, c0 + 32, last);
   }
 
   // ---- 4. the four waves' results -> one partial per query head ----

@@ -82,6 +82,7 @@ extern "C" __global__ __launch_bounds__(256) void dec_attention(
     uint16_t* __restrict__ k_cache, uint16_t* __restrict__ v_cache, float* __restrict__ part,
     uint16_t* __restrict__ q_roped) {
   __shared__ AttnLds lds;
+  __shared__ __attribute__((aligned(16))) uint8_t kv[kAttnWaves][kKvPrefetchBytes];
   const int g = blockIdx.x / kAttnGroups;
   const int sg = blockIdx.x % kAttnGroups;
   const int lane = threadIdx.x & 63;
@@ -89,8 +90,8 @@ extern "C" __global__ __launch_bounds__(256) void dec_attention(
   float cs[2], sn[2];
   rope_angles(pos_raw < 0 ? 0 : (pos_raw >= max_seq ? max_seq - 1 : pos_raw), cs, sn);
   attention_group(
-      lds, g, sg, pos_raw, cs, sn, max_seq, qn_w, kn_w, k_cache, v_cache, q_roped, nullptr,
-      [] {},
+      lds, g, sg, pos_raw, cs, sn, max_seq, qn_w, kn_w, k_cache, v_cache, q_roped,
+      kv[threadIdx.x >> 6], false, [] {},
       [&](uint32_t (&xw)[3], uint32_t& v_new) {
         xw[0] = load_global(reinterpret_cast<const uint32_t*>(q_raw + (2 * g) * kHeadDim) + lane);
         xw[1] = load_global(reinterpret_cast<const uint32_t*>(q_raw + (2 * g + 1) * kHeadDim) + lane);
@@ -568,7 +569,7 @@ constexpr int kVecWords = 2 * kAttnGroups * 130;  // 2080: the largest polled ve
 #define DEC_PACE_E 32
 #endif
 #ifndef DEC_PACE_KV
-#define DEC_PACE_KV 0
+#define DEC_PACE_KV 8
 #endif
 constexpr int kPaceA = DEC_PACE_A, kPaceD = DEC_PACE_D, kPaceC = DEC_PACE_C, kPaceE = DEC_PACE_E,
               kPaceKV = DEC_PACE_KV;
@@ -729,7 +730,7 @@ void dec_step(StepParams P) {
       attention_group(
           S.b.attn, g, sg, pos_raw, rope_cs, rope_sn, P.max_seq, P.q_norm + layer * kHeadDim,
           P.k_norm + layer * kHeadDim, P.k_cache + cache_layer, P.v_cache + cache_layer, nullptr,
-          kv_mine, [&] { W.poll_begin(256, qkv_src, qkv_poll); },
+          kv_mine, true, [&] { W.poll_begin(256, qkv_src, qkv_poll); },
           [&](uint32_t (&xw)[3], uint32_t& v_new) {
             ok = W.poll_finish(256, tq, vec, qkv_src, qkv_poll);
             STAMP(layer, 3);

@@ -756,7 +756,7 @@ extern "C" __global__ __launch_bounds__(256) void pf_qk_rope_cache(
     float r2[2];
 #pragma unroll
     for (int dd = 0; dd < 2; ++dd) {
-      const float other = __shfl_xor(xs[dd], 32, 64);  // dim d + 64 or d - 64
+      const float other = xor32(xs[dd]);  // dim d + 64 or d - 64
       if (lane < 32) {
         const float u = xs[dd] * cs[dd];
         const float w2 = other * sn[dd];
