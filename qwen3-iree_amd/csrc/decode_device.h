@@ -536,19 +536,30 @@ __device__ __forceinline__ void attention_group(AttnLds& L, int g, int sg, int p
     accB0 *= cB;
     accB1 *= cB;
     __builtin_amdgcn_sched_barrier(0);
-    // position j's weights are lane j's p (lanes j and j + 32 hold the same
-    // value), read into scalar registers four positions at a time (the
-    // scheduling fences keep the compiler from hoisting all 64 reads).
-    // With `fix`, position pos takes this step's v, and positions past the
-    // split (weight 0, a clamped valid row) take v = 0, so a non-finite value
-    // there cannot leak in; most chunks need neither (a wave-uniform branch).
+    // Four positions at a time, the next four's v requested from LDS before
+    // this four's products: position j's weights are lane j's p (lanes j and
+    // j + 32 hold the same value), read into scalar registers (the scheduling
+    // fences keep the compiler from hoisting all 64 reads).  With `fix`,
+    // position pos takes this step's v, and positions past the split (weight
+    // 0, a clamped valid row) take v = 0, so a non-finite value there cannot
+    // leak in; most chunks need neither (a wave-uniform branch).
     const int n = end - c0 < 32 ? end - c0 : 32;
+    const auto v_word = [&](int j) {
+      return *reinterpret_cast<const uint32_t*>(kv + 8192 + 256 * j + 4 * lane);
+    };
     const auto weighted_v = [&](bool fix) {
+      uint32_t vbuf[2][4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) vbuf[0][j] = v_word(j);
 #pragma unroll
       for (int j0 = 0; j0 < 32; j0 += 4) {
+        if (j0 + 4 < 32) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) vbuf[((j0 >> 2) + 1) & 1][j] = v_word(j0 + 4 + j);
+        }
 #pragma unroll
         for (int j = j0; j < j0 + 4; ++j) {
-          const uint32_t vs = *reinterpret_cast<const uint32_t*>(kv + 8192 + 256 * j + 4 * lane);
+          const uint32_t vs = vbuf[(j0 >> 2) & 1][j - j0];
           const uint32_t vw = fix ? (c0 + j == pos ? v_new : (j < n ? vs : 0u)) : vs;
           const f16x2 vv = as_f16x2(vw);
           const float v0 = (float)vv.x, v1 = (float)vv.y;

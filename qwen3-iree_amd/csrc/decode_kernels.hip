@@ -323,7 +323,7 @@ constexpr int kBBase = 256;                // 64 attention workgroups
 constexpr int kCBase = 320;                // 128 attn_o + ffn_down workgroups
 // The vocab GEMV runs on the first kVocabWgs workgroups.
 #ifndef DEC_VOCAB_WGS
-#define DEC_VOCAB_WGS 256
+#define DEC_VOCAB_WGS 448
 #endif
 constexpr int kVocabWgs = DEC_VOCAB_WGS;
 // Vectors that every (or nearly every) workgroup waits for -- h, the
