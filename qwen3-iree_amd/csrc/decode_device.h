@@ -73,6 +73,11 @@ __device__ __forceinline__ uint32_t pack_f16x2(float a, float b) {
 
 __device__ __forceinline__ _Float16 as_half(uint16_t b) { return __builtin_bit_cast(_Float16, b); }
 
+__device__ __forceinline__ uint2 load_global(const uint2* p) {
+  const uint64_t v = *(const GLOBAL_AS uint64_t*)p;
+  return make_uint2((uint32_t)v, (uint32_t)(v >> 32));
+}
+
 // rms_norm (qwen3_full.mlir:134-165).  Every kernel sums the 1024 squares in
 // one canonical order, a perfect binary tree over the columns in index order
 // with the leaves fl(x^2), so a vector normalized by the 16 lanes of a row

@@ -66,10 +66,6 @@ __device__ __forceinline__ u32x4 load_global(const u32x4* p) {
 __device__ __forceinline__ uint32_t load_global(const uint32_t* p) {
   return *(const GLOBAL_AS uint32_t*)p;
 }
-__device__ __forceinline__ uint2 load_global(const uint2* p) {
-  const uint64_t v = *(const GLOBAL_AS uint64_t*)p;
-  return make_uint2((uint32_t)v, (uint32_t)(v >> 32));
-}
 
 __device__ __forceinline__ uint16_t load_global_u16(const uint16_t* p) {
   return *(const GLOBAL_AS uint16_t*)p;
