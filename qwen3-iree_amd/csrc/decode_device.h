@@ -286,18 +286,18 @@ __device__ __forceinline__ float merge_dim(const float (&acc)[kAttnGroups],
 // (qwen3_full.mlir:324-454): theta = pos * (1e6^(-(2i/128)) * 1), i = d mod 64.
 // They depend on the position only, so a step computes them once for all
 // layers.
+// cos and sin of the angle of frequency i (0..63) at position pos.
+__device__ __forceinline__ void rope_angle(int pos, int i, float& c, float& s) {
+  const float e = -((2.0f * (float)i) / 128.0f);
+  const float th = (float)pos * (powf(kRopeBase, e) * 1.0f);
+  c = cosf(th);
+  s = sinf(th);
+}
+
 __device__ __forceinline__ void rope_angles(int pos, float (&cs)[2], float (&sn)[2]) {
   const int lane = threadIdx.x & 63;
-  const float posf = (float)pos;
 #pragma unroll
-  for (int dd = 0; dd < 2; ++dd) {
-    const int d = 2 * lane + dd;
-    const int i = d < 64 ? d : d - 64;
-    const float e = -((2.0f * (float)i) / 128.0f);
-    const float th = posf * (powf(kRopeBase, e) * 1.0f);
-    cs[dd] = cosf(th);
-    sn[dd] = sinf(th);
-  }
+  for (int dd = 0; dd < 2; ++dd) rope_angle(pos, (2 * lane + dd) & 63, cs[dd], sn[dd]);
 }
 
 // Position range [start, end) of attention split s (of kAttnSplits) over ctx

@@ -739,8 +739,17 @@ extern "C" __global__ __launch_bounds__(256) void pf_qk_rope_cache(
         reinterpret_cast<const uint32_t*>(v + (size_t)i * 1024 + (2 * w + j) * kHeadDim) + lane);
   const f16x2 qwv = as_f16x2(load_global(reinterpret_cast<const uint32_t*>(qn_w) + lane));
   const f16x2 kwv = as_f16x2(load_global(reinterpret_cast<const uint32_t*>(kn_w) + lane));
+  // the token's 64 angles once (wave 0, one per lane), shared through LDS:
+  // the same values rope_angles gives each lane
+  __shared__ float s_cs[64], s_sn[64];
+  if (w == 0) rope_angle(pos, lane, s_cs[lane], s_sn[lane]);
+  __syncthreads();
   float cs[2], sn[2];
-  rope_angles(pos, cs, sn);
+#pragma unroll
+  for (int dd = 0; dd < 2; ++dd) {
+    cs[dd] = s_cs[(2 * lane + dd) & 63];
+    sn[dd] = s_sn[(2 * lane + dd) & 63];
+  }
   uint32_t out[kVecs];
 #pragma unroll
   for (int j = 0; j < kVecs; ++j) {
