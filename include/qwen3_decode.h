@@ -182,8 +182,9 @@ int qwen3_prefill_batched(const qwen3_weights* w, void* k_cache, void* v_cache, 
  * the workspace.  qwen3_prefill_workspace_offset(n_tokens, name) = byte
  * offset of a region ("h", "res", "xn", "q", "k", "v", "q_roped", "attn",
  * "act", "fn"; f16 rows of 1024, 1024, 1024, 2048, 1024, 1024, 2048, 2048,
- * 3072, 1024 columns; then "attn_part", the attention's split partials), -1
- * for an unknown name. */
+ * 3072, 1024 columns; then "attn_part", the attention's split partials, and
+ * "rope", f32 [n_tokens, 128]: the RoPE cosines and sines of each token's
+ * position), -1 for an unknown name. */
 int qwen3_prefill_layer(const qwen3_weights* w, int layer, void* k_cache, void* v_cache,
                         int64_t max_seq, int32_t n_tokens, int32_t start_pos, int chunk_local,
                         void* workspace, size_t workspace_bytes, void* stream);

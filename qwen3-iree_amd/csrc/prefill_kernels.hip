@@ -705,6 +705,17 @@ PF_GEMM_F16(pf_gemm_f16_part_22k, kEpiPartial, 2, 2, 256, 2)
 PF_GEMM_F16(pf_gemm_f16_part_12k, kEpiPartial, 1, 2, 256, 3)
 #undef PF_GEMM_F16
 
+// table[i] = the 64 cosines then the 64 sines of the RoPE angles at position
+// start + i (rope_angle: the decode step's values), for every layer of a
+// prompt.  One 64-lane workgroup per token.
+extern "C" __global__ __launch_bounds__(64) void pf_rope_table(int start, float* __restrict__ table) {
+  const int i = blockIdx.x, lane = threadIdx.x;
+  float c, s;
+  rope_angle(start + i, lane, c, s);
+  table[(size_t)i * 128 + lane] = c;
+  table[(size_t)i * 128 + 64 + lane] = s;
+}
+
 // Token i = blockIdx.x (position start + i): per-head rms_norm with q_norm /
 // k_norm (qwen3_full.mlir:1812-1879) and RoPE (@position_components.rope,
 // :1060-1130, the decode step's formula) -> q_roped[i] / the k cache slot,
@@ -712,12 +723,14 @@ PF_GEMM_F16(pf_gemm_f16_part_12k, kEpiPartial, 1, 2, 256, 3)
 // heads 4w .. 4w + 3, k heads 2w, 2w + 1 and v heads 2w, 2w + 1; the six
 // vectors are independent chains in the same wave.  Lane owns dims 2 lane,
 // 2 lane + 1; per vector the same operations as the decode step's attention
-// prologue.  k_cache, v_cache: the layer's base ([max_seq, 8, 128]).
+// prologue; the angles come from pf_rope_table.  k_cache, v_cache: the
+// layer's base ([max_seq, 8, 128]).
 extern "C" __global__ __launch_bounds__(256) void pf_qk_rope_cache(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ v, int start, const uint16_t* __restrict__ qn_w,
-    const uint16_t* __restrict__ kn_w, uint16_t* __restrict__ q_roped,
-    uint16_t* __restrict__ k_cache, uint16_t* __restrict__ v_cache) {
+    const uint16_t* __restrict__ kn_w, const float* __restrict__ rope,
+    uint16_t* __restrict__ q_roped, uint16_t* __restrict__ k_cache,
+    uint16_t* __restrict__ v_cache) {
   const int i = blockIdx.x;
   const int w = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
@@ -739,17 +752,12 @@ extern "C" __global__ __launch_bounds__(256) void pf_qk_rope_cache(
         reinterpret_cast<const uint32_t*>(v + (size_t)i * 1024 + (2 * w + j) * kHeadDim) + lane);
   const f16x2 qwv = as_f16x2(load_global(reinterpret_cast<const uint32_t*>(qn_w) + lane));
   const f16x2 kwv = as_f16x2(load_global(reinterpret_cast<const uint32_t*>(kn_w) + lane));
-  // the token's 64 angles once (wave 0, one per lane), shared through LDS:
-  // the same values rope_angles gives each lane
-  __shared__ float s_cs[64], s_sn[64];
-  if (w == 0) rope_angle(pos, lane, s_cs[lane], s_sn[lane]);
-  __syncthreads();
-  float cs[2], sn[2];
-#pragma unroll
-  for (int dd = 0; dd < 2; ++dd) {
-    cs[dd] = s_cs[(2 * lane + dd) & 63];
-    sn[dd] = s_sn[(2 * lane + dd) & 63];
-  }
+  // this lane's frequencies 2 lane, 2 lane + 1 (mod 64) at the token's position
+  const uint2 c2 = load_global(reinterpret_cast<const uint2*>(rope + (size_t)i * 128 + ((2 * lane) & 63)));
+  const uint2 s2 =
+      load_global(reinterpret_cast<const uint2*>(rope + (size_t)i * 128 + 64 + ((2 * lane) & 63)));
+  const float cs[2] = {__uint_as_float(c2.x), __uint_as_float(c2.y)};
+  const float sn[2] = {__uint_as_float(s2.x), __uint_as_float(s2.y)};
   uint32_t out[kVecs];
 #pragma unroll
   for (int j = 0; j < kVecs; ++j) {

@@ -109,8 +109,8 @@ struct State {
   hipFunction_t pf_embed = nullptr, pf_norm = nullptr, pf_gemm = nullptr, pf_gemm_res = nullptr,
                 pf_gemm_m32 = nullptr, pf_gemm_res_m32 = nullptr, pf_gemm_swiglu = nullptr,
                 pf_gemm_part = nullptr, pf_gemm_part_m32 = nullptr, pf_res_reduce = nullptr,
-                pf_res_reduce_norm = nullptr, pf_rope = nullptr, pf_attn = nullptr, pf_attn_merge = nullptr,
-                pf_set_pos = nullptr;
+                pf_res_reduce_norm = nullptr, pf_rope = nullptr, pf_rope_table = nullptr,
+                pf_attn = nullptr, pf_attn_merge = nullptr, pf_set_pos = nullptr;
   // the f16 GEMMs (pf_gemm_f16*: over the f16 layer matrices) and their
   // expansion from Q8_0 (pf_expand_q8)
   hipFunction_t pf_f16_44 = nullptr, pf_f16_24 = nullptr, pf_f16_22 = nullptr,
@@ -333,7 +333,7 @@ int q8gemv_init(const char* code_object_path) {
                      {&g.pf_gemm_m32, "pf_gemm_q8_m32"},
                      {&g.pf_gemm_res_m32, "pf_gemm_q8_res_m32"},
                      {&g.pf_gemm_swiglu, "pf_gemm_q8_swiglu"},
-                     {&g.pf_rope, "pf_qk_rope_cache"},
+                     {&g.pf_rope, "pf_qk_rope_cache"}, {&g.pf_rope_table, "pf_rope_table"},
                      {&g.pf_attn, "pf_attention"},
                      {&g.pf_attn_merge, "pf_attn_merge"},
                      {&g.pf_gemm_part, "pf_gemm_q8_part"},
@@ -409,7 +409,7 @@ void q8gemv_shutdown(void) {
   if (g.pf_module) (void)hipModuleUnload(g.pf_module);
   g.pf_module = nullptr;
   g.pf_embed = g.pf_norm = g.pf_gemm = g.pf_gemm_res = g.pf_gemm_m32 = g.pf_gemm_res_m32 =
-      g.pf_gemm_swiglu = g.pf_rope = g.pf_attn = g.pf_attn_merge = g.pf_set_pos = nullptr;
+      g.pf_gemm_swiglu = g.pf_rope = g.pf_rope_table = g.pf_attn = g.pf_attn_merge = g.pf_set_pos = nullptr;
   g.pf_gemm_part = g.pf_gemm_part_m32 = g.pf_res_reduce = g.pf_res_reduce_norm = nullptr;
   g.pf_f16_44 = g.pf_f16_24 = g.pf_f16_22 = g.pf_f16_sw_46w = g.pf_f16_sw_44 = g.pf_f16_sw_24 =
       g.pf_f16_sw_22 = nullptr;
@@ -1197,9 +1197,11 @@ struct GemmMore {
 // (rms_norm(h, attn_norm)), q, k, v, q_roped, attention output, SwiGLU
 // output, fn (rms_norm(h1, ffn_norm)).
 // Then the attention's split partials (f32 slots of kPfAttnSlotFloats for
-// pf_attn_pair_cap(n) pairs x 8 kv heads).
+// pf_attn_pair_cap(n) pairs x 8 kv heads), then the RoPE table (per token
+// the 64 cosines, then the 64 sines, f32).
 constexpr int kPfTokenRegions = 10;
-constexpr int kPfRegions = 11;
+constexpr int kPfRegions = 12;
+constexpr int kPfRopeRegion = 11;
 constexpr int kPfCols[kPfTokenRegions] = {1024, 1024, 1024, 2048, 1024, 1024, 2048, 2048, 3072, 1024};
 constexpr int32_t kPfMaxTokens = 1 << 20;
 
@@ -1210,6 +1212,8 @@ size_t pf_region_bytes(int32_t n, int i) {
   size_t b;
   if (i < kPfTokenRegions)
     b = (size_t)n * kPfCols[i] * 2;
+  else if (i == kPfRopeRegion)
+    b = (size_t)n * 128 * 4;
   else
     b = (size_t)pf_attn_pair_cap(n) * kKvHeads * kPfAttnSlotFloats * 4;
   return (b + 255) / 256 * 256;
@@ -1440,7 +1444,8 @@ int launch_gemm_res(const void* x, int ldx, const void* wl, int K, void* y, cons
 int launch_prefill_layer(const qwen3_weights* w, int layer, void* k_cache, void* v_cache,
                          int64_t max_seq, int32_t n, int32_t p0, int chunk_local,
                          void* const (&ws)[kPfRegions], hipStream_t st, bool xn_ready = false,
-                         const void* next_norm = nullptr, bool* next_xn_ready = nullptr) {
+                         const void* next_norm = nullptr, bool* next_xn_ready = nullptr,
+                         bool rope_ready = false) {
   const int64_t bpl_q = 2048LL * 1024 / 32 * 34, bpl_kv = 1024LL * 1024 / 32 * 34;
   const int64_t bpl_o = 1024LL * 2048 / 32 * 34, bpl_gu = 6144LL * 1024 / 32 * 34;
   const int64_t bpl_dn = 1024LL * 3072 / 32 * 34;
@@ -1451,7 +1456,7 @@ int launch_prefill_layer(const qwen3_weights* w, int layer, void* k_cache, void*
   void* kc = mb(k_cache) + (int64_t)layer * max_seq * kKvRow * 2;
   void* vc = mb(v_cache) + (int64_t)layer * max_seq * kKvRow * 2;
   void *h = ws[0], *h1 = ws[1], *xn = ws[2], *q = ws[3], *k = ws[4], *v = ws[5], *qr = ws[6],
-       *attn = ws[7], *act = ws[8], *fnx = ws[9], *part = ws[10];
+       *attn = ws[7], *act = ws[8], *fnx = ws[9], *part = ws[10], *rope = ws[kPfRopeRegion];
   const uint32_t norm_grid = (uint32_t)((n + 15) / 16);
   int rc;
   if (!xn_ready) {
@@ -1479,7 +1484,11 @@ int launch_prefill_layer(const qwen3_weights* w, int layer, void* k_cache, void*
   }
   {
     int start = p0;
-    void* args[] = {&q, &k, &v, &start, &qn, &kn, &qr, &kc, &vc};
+    if (!rope_ready) {  // the prompt positions' angles (the same for every layer)
+      void* targs[] = {&start, &rope};
+      if ((rc = launch(g.pf_rope_table, (uint32_t)n, 64, targs, st))) return rc;
+    }
+    void* args[] = {&q, &k, &v, &start, &qn, &kn, &rope, &qr, &kc, &vc};
     if ((rc = launch(g.pf_rope, (uint32_t)n, 256, args, st))) return rc;
   }
   {
@@ -1769,7 +1778,7 @@ int qwen3_generate(const qwen3_weights* w, void* k_cache, void* v_cache, int64_t
 
 int64_t qwen3_prefill_workspace_offset(int32_t n_prompt, const char* name) {
   static const char* const kNames[kPfRegions] = {"h", "res",     "xn",   "q",   "k",  "v",
-                                                 "q_roped", "attn", "act", "fn", "attn_part"};
+                                                 "q_roped", "attn", "act", "fn", "attn_part", "rope"};
   if (!name || n_prompt < 1 || n_prompt > kPfMaxTokens) return -1;
   int64_t off = 0;
   for (int i = 0; i < kPfRegions; ++i) {
@@ -1888,7 +1897,7 @@ int qwen3_prefill_batched(const qwen3_weights* w, void* k_cache, void* v_cache, 
   for (int l = 0; l < kLayers; ++l) {
     const void* next_norm = l + 1 < kLayers ? cb(w->attn_norm) + (l + 1) * 2048 : nullptr;
     if ((rc = launch_prefill_layer(w, l, k_cache, v_cache, max_seq, n_prompt, p0, chunk_local, ws,
-                                   st, xn_ready, next_norm, &xn_ready)))
+                                   st, xn_ready, next_norm, &xn_ready, l > 0)))
       return rc;
   }
   {

@@ -295,6 +295,8 @@ def test_prefill_workspace_layout(Q):
         sizes = [(name, 2 * n * cols) for name, cols in decode.PREFILL_REGIONS]
         # attention split partials: 64 x 128 + 2 x 64 f32 per (pair, kv head)
         sizes += [("attn_part", (2 * nqb + 64) * 8 * (64 * 128 + 128) * 4)]
+        # RoPE table: per token 64 cosines and 64 sines, f32
+        sizes += [("rope", n * 128 * 4)]
         spans = sorted((L.qwen3_prefill_workspace_offset(n, name.encode()),
                         L.qwen3_prefill_workspace_offset(n, name.encode()) + size)
                        for name, size in sizes)
