@@ -705,6 +705,52 @@ PF_GEMM_F16(pf_gemm_f16_part_22k, kEpiPartial, 2, 2, 256, 2)
 PF_GEMM_F16(pf_gemm_f16_part_12k, kEpiPartial, 1, 2, 256, 3)
 #undef PF_GEMM_F16
 
+// Per-head rms_norm (q_norm / k_norm, qwen3_full.mlir:648-702) and RoPE
+// (:324-454) of one head vector: lane owns dims 2 lane, 2 lane + 1 (xw, an
+// f16 pair), wv the lane's norm weights, cs / sn its two frequencies' cosines
+// and sines; the same operations as the decode step's attention prologue.
+__device__ __forceinline__ uint32_t head_norm_rope(uint32_t xw, f16x2 wv, const float (&cs)[2],
+                                                   const float (&sn)[2]) {
+  const int lane = threadIdx.x & 63;
+  const f16x2 xv = as_f16x2(xw);
+  const float a = (float)xv.x, b = (float)xv.y;
+  float ss = a * a;
+  ss = ss + b * b;
+  ss = wave_sum(ss);
+  const float r = sqrtf(ss / 128.0f + kEps);
+  float xs[2];
+  xs[0] = (float)to_f16((a / r) * (float)wv.x);
+  xs[1] = (float)to_f16((b / r) * (float)wv.y);
+  float r2[2];
+#pragma unroll
+  for (int dd = 0; dd < 2; ++dd) {
+    const float other = xor32(xs[dd]);  // dim d + 64 or d - 64
+    if (lane < 32) {
+      const float u = xs[dd] * cs[dd];
+      const float w2 = other * sn[dd];
+      r2[dd] = u - w2;
+    } else {
+      const float u = other * sn[dd];
+      const float w2 = xs[dd] * cs[dd];
+      r2[dd] = u + w2;
+    }
+  }
+  return pack_f16x2(r2[0], r2[1]);
+}
+
+// this lane's two frequencies (2 lane, 2 lane + 1, mod 64) for token m
+__device__ __forceinline__ void rope_lane(const float* __restrict__ rope, int m, float (&cs)[2],
+                                          float (&sn)[2]) {
+  const int lane = threadIdx.x & 63;
+  const uint2 c2 = load_global(reinterpret_cast<const uint2*>(rope + (size_t)m * 128 + ((2 * lane) & 63)));
+  const uint2 s2 =
+      load_global(reinterpret_cast<const uint2*>(rope + (size_t)m * 128 + 64 + ((2 * lane) & 63)));
+  cs[0] = __uint_as_float(c2.x);
+  cs[1] = __uint_as_float(c2.y);
+  sn[0] = __uint_as_float(s2.x);
+  sn[1] = __uint_as_float(s2.y);
+}
+
 // table[i] = the 64 cosines then the 64 sines of the RoPE angles at position
 // start + i (rope_angle: the decode step's values), for every layer of a
 // prompt.  One 64-lane workgroup per token.
@@ -752,40 +798,12 @@ extern "C" __global__ __launch_bounds__(256) void pf_qk_rope_cache(
         reinterpret_cast<const uint32_t*>(v + (size_t)i * 1024 + (2 * w + j) * kHeadDim) + lane);
   const f16x2 qwv = as_f16x2(load_global(reinterpret_cast<const uint32_t*>(qn_w) + lane));
   const f16x2 kwv = as_f16x2(load_global(reinterpret_cast<const uint32_t*>(kn_w) + lane));
-  // this lane's frequencies 2 lane, 2 lane + 1 (mod 64) at the token's position
-  const uint2 c2 = load_global(reinterpret_cast<const uint2*>(rope + (size_t)i * 128 + ((2 * lane) & 63)));
-  const uint2 s2 =
-      load_global(reinterpret_cast<const uint2*>(rope + (size_t)i * 128 + 64 + ((2 * lane) & 63)));
-  const float cs[2] = {__uint_as_float(c2.x), __uint_as_float(c2.y)};
-  const float sn[2] = {__uint_as_float(s2.x), __uint_as_float(s2.y)};
+  float cs[2], sn[2];
+  rope_lane(rope, i, cs, sn);  // this lane's frequencies at the token's position
   uint32_t out[kVecs];
 #pragma unroll
-  for (int j = 0; j < kVecs; ++j) {
-    const f16x2 wv = j < 4 ? qwv : kwv;
-    const float a = (float)xv[j].x, b = (float)xv[j].y;
-    float ss = a * a;
-    ss = ss + b * b;
-    ss = wave_sum(ss);
-    const float r = sqrtf(ss / 128.0f + kEps);
-    float xs[2];
-    xs[0] = (float)to_f16((a / r) * (float)wv.x);
-    xs[1] = (float)to_f16((b / r) * (float)wv.y);
-    float r2[2];
-#pragma unroll
-    for (int dd = 0; dd < 2; ++dd) {
-      const float other = xor32(xs[dd]);  // dim d + 64 or d - 64
-      if (lane < 32) {
-        const float u = xs[dd] * cs[dd];
-        const float w2 = other * sn[dd];
-        r2[dd] = u - w2;
-      } else {
-        const float u = other * sn[dd];
-        const float w2 = xs[dd] * cs[dd];
-        r2[dd] = u + w2;
-      }
-    }
-    out[j] = pack_f16x2(r2[0], r2[1]);
-  }
+  for (int j = 0; j < kVecs; ++j)
+    out[j] = head_norm_rope(__builtin_bit_cast(uint32_t, xv[j]), j < 4 ? qwv : kwv, cs, sn);
 #pragma unroll
   for (int j = 0; j < 4; ++j)
     reinterpret_cast<uint32_t*>(q_roped + (size_t)i * 2048 + (4 * w + j) * kHeadDim)[lane] = out[j];
