@@ -24,6 +24,14 @@ constexpr float kEps = 9.99999997e-7f;    // qwen3_full.mlir:63
 constexpr float kRopeBase = 1.0e6f;       // qwen3_full.mlir:59
 // rsqrt(128) of qwen3_full.mlir:721-723, the f32 nearest 2^-3.5 (0x3DB504F3)
 constexpr float kAttnScale = 0.0883883461356163f;
+// attention scores in base-2 units: s log2(e), so each weight is one exp2
+constexpr float kScoreScaleLog2 = kAttnScale * 1.44269504088896341f;
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+typedef short v8i16 __attribute__((ext_vector_type(8)));
+#define LDS_AS __attribute__((address_space(3)))
 
 // Lane exchanges through v_permlane16_swap / v_permlane32_swap (VALU, no LDS
 // round trip).  With both operands v, permlane16_swap returns {v of rows 0, 0,
@@ -48,8 +56,30 @@ __device__ __forceinline__ float xor32(float v) {  // the value of lane i ^ 32
 // way round gets the same bits)
 __device__ __forceinline__ float sum_col4(float v) { return sum_halves(sum_rows2(v)); }
 
+// vmcnt(n) with the other counters left alone (gfx9 s_waitcnt encoding)
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0f70);
+}
+// lgkmcnt(0): every LDS read of the wave has returned its data
+__device__ __forceinline__ void wait_lds() { __builtin_amdgcn_s_waitcnt(0xc07f); }
+
 // the sum over the wave: rows in index order, (r0 + r1) + (r2 + r3)
 __device__ __forceinline__ float wave_sum(float v) { return sum_col4(reduce_row16(v)); }
+
+// the max of v over lanes i, i ^ 16, i ^ 32, i ^ 48 (v_permlane16_swap /
+// v_permlane32_swap hand each lane the value of its partner row; sum_col4 is
+// the sum).  Both results of each swap are used; the generated code was
+// checked for that (a swap whose second result is dropped reduces nothing),
+// and the attention tests against the oracle would fail on any lane seeing a
+// different max.
+__device__ __forceinline__ float max_col4(float v) {
+  auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
 
 __device__ __forceinline__ float max32(float v) {  // over the 32 lanes of a wave half
   v = fmaxf(v, dpp<0xB1>(v));
@@ -257,8 +287,8 @@ __device__ __forceinline__ uint16_t residual_f16(_Float16 base, float acc) {
   return __builtin_bit_cast(uint16_t, (_Float16)(base + to_f16(acc)));
 }
 
-// Weights of the 8 split-group partials of one query head: w_g = exp(m_g -
-// max m) (0 for an empty group), L = sum_g l_g w_g, summed in group order.
+// Weights of the 8 split-group partials of one query head: w_g = 2^(m_g -
+// max m) (the maxima are in base-2 units; 0 for an empty group), L = sum_g l_g w_g, summed in group order.
 __device__ __forceinline__ void merge_weights(const float (&m)[kAttnGroups],
                                               const float (&l)[kAttnGroups],
                                               float (&w)[kAttnGroups], float& L) {
@@ -268,7 +298,7 @@ __device__ __forceinline__ void merge_weights(const float (&m)[kAttnGroups],
   L = 0.0f;
 #pragma unroll
   for (int g = 0; g < kAttnGroups; ++g) {
-    w[g] = m[g] == -__builtin_inff() ? 0.0f : expf(m[g] - M);
+    w[g] = m[g] == -__builtin_inff() ? 0.0f : exp2f(m[g] - M);
     L = L + l[g] * w[g];
   }
 }
@@ -314,22 +344,25 @@ __device__ __forceinline__ SplitRange split_range(int s, int pos) {
   return r;
 }
 
-// Bytes of one wave's prefetched first chunk: K (32 rows x this lane's half
-// row, 8 x 1 KiB) then V (32 rows x the lane's two dims, 32 x 256 B).
+// Bytes of one wave's staged chunk of 32 cache rows: K (8 KiB) then V (8 KiB).
 constexpr int kKvPrefetchBytes = 8 * 1024 + 32 * 256;
 
 // One chunk of a split's cache rows -- positions c0 .. c0 + 31, clamped to
 // `last` -- copied into the wave's LDS region kv by the memory system
-// (global_load_lds), so no register holds them while they are in flight: lane
-// (pl, half)'s K piece m (row c0 + pl, dims 64 half + 8 m .. + 8) lands at kv
-// + 1024 m + 16 lane, the V word of row c0 + j (dims 2 lane, 2 lane + 1) at kv
-// + 8192 + 256 j + 4 lane.  The wave may read them once its vector memory
-// counter has drained past these loads.  PACE > 0 sleeps 64 PACE cycles after
-// the K pieces and after every fourth V row.
+// (global_load_lds), so no register holds them while they are in flight: K
+// row r's 16-byte chunk ch (dims 8 ch .. + 7) lands at kv + 1024 (ch & 7) +
+// 512 (ch >> 3) + 16 r (lane (r, ch >> 3) loads pieces ch & 7 = 0..7), V row
+// r's chunk ch at kv + 8192 + 256 r + 16 (ch ^ 2 (r & 7)) (each lane loads the
+// four bytes that land at its slot, so the transposing reads of attention_group
+// hit distinct banks).  The K part is 8 loads per lane, the V part 32, in that
+// order; the compiler does not track these copies for the LDS reads that
+// follow, so readers wait on the vector memory counter themselves (wait_vm)
+// and let every LDS read of the region return (wait_lds) before the region
+// is staged again.  PACE > 0 sleeps 64 PACE cycles after the K pieces and
+// after every fourth V row.
 template <int PACE = 0>
-__device__ __forceinline__ void kv_stage(uint8_t* kv, const uint16_t* __restrict__ k_cache,
-                                         const uint16_t* __restrict__ v_cache, int g, int c0,
-                                         int last) {
+__device__ __forceinline__ void kv_stage_k(uint8_t* kv, const uint16_t* __restrict__ k_cache,
+                                           int g, int c0, int last) {
   const int lane = threadIdx.x & 63;
   const int half = lane >> 5;
   const int pl = lane & 31;
@@ -342,17 +375,32 @@ __device__ __forceinline__ void kv_stage(uint8_t* kv, const uint16_t* __restrict
                                      (__attribute__((address_space(3))) void*)(kv + 1024 * m), 16,
                                      0, 0);
   if constexpr (PACE > 0) __builtin_amdgcn_s_sleep(PACE);
+}
+
+template <int PACE = 0>
+__device__ __forceinline__ void kv_stage_v(uint8_t* kv, const uint16_t* __restrict__ v_cache,
+                                           int g, int c0, int last) {
+  const int lane = threadIdx.x & 63;
 #pragma unroll
   for (int j = 0; j < 32; ++j) {
     const int pj = c0 + j < last ? c0 + j : last;
+    const int word = 4 * ((lane >> 2) ^ (2 * (j & 7))) + (lane & 3);
     __builtin_amdgcn_global_load_lds(
         (const GLOBAL_AS void*)(reinterpret_cast<const uint32_t*>(
                                     v_cache + ((size_t)pj * kKvHeads + g) * kHeadDim) +
-                                lane),
+                                word),
         (__attribute__((address_space(3))) void*)(kv + 8192 + 256 * j), 4, 0, 0);
     if constexpr (PACE > 0)
       if ((j & 3) == 3) __builtin_amdgcn_s_sleep(PACE);
   }
+}
+
+template <int PACE = 0>
+__device__ __forceinline__ void kv_stage(uint8_t* kv, const uint16_t* __restrict__ k_cache,
+                                         const uint16_t* __restrict__ v_cache, int g, int c0,
+                                         int last) {
+  kv_stage_k<PACE>(kv, k_cache, g, c0, last);
+  kv_stage_v<PACE>(kv, v_cache, g, c0, last);
 }
 
 // The first chunk of split r (what attention_group reads first).
@@ -367,7 +415,7 @@ __device__ __forceinline__ void kv_prefetch(uint8_t* kv, const uint16_t* __restr
 struct __attribute__((aligned(16))) AttnLds {
   uint32_t qh[2][64];  // roped q_A, q_B as f16 pairs
   uint32_t kh[64];     // roped new k as f16 pairs
-  float mrg[kAttnWaves][2][2 + kHeadDim];
+  float mrg[kAttnWaves][2][4 + kHeadDim];  // per wave and q head: m, l, 2 pad, o[128]
 };
 
 // Attention for kv head g and split group sg: four waves, wave w taking
@@ -386,15 +434,14 @@ struct __attribute__((aligned(16))) AttnLds {
 //     2) and the raw v (wave 3) to cache slot pos (k_cache / v_cache: the
 //     layer's base; slot layout [max_seq, 8, 128]); split group 0 stores the
 //     roped q heads to q_roped when it is not null;
-//  3. chunks of 32 positions: lane (j, half) scores position j of the chunk
-//     on dims [64*half, 64*half + 64) for both q heads, the halves meet in one
-//     cross-half add; s_j = (q . k_j) * rsqrt(128); online softmax; the
-//     weighted sum of v (each lane owns dims 2*lane, 2*lane+1 of both heads).
-//     A position's weights reach the lanes holding v as lane reads, so a
-//     wave runs its chunks without waiting for the others;
+//  3. chunks of 32 positions on the matrix cores, both q heads at once as two
+//     columns of the MFMA's B operand: scores S^T = K Q^T in f32 from exact
+//     f16 products, s_j = (q . k_j) * rsqrt(128) log2(e) (base-2 units);
+//     online softmax; O^T += V^T P^T with p as f16 hi + lo.  A wave runs its
+//     chunks without waiting for the others;
 //  4. publish(hh, m, l, a0, a1) on waves 0 and 1 (query head 2g + hh): m =
-//     max over the 4 waves, l and this lane's two dims rescaled by
-//     exp(m_w - m).  An empty split (ctx < 32) contributes m = -inf, l = 0.
+//     max over the 4 waves (base 2), l and this lane's two dims rescaled by
+//     2^(m_w - m).  An empty split (ctx < 32) contributes m = -inf, l = 0.
 // get_qkv(xw, v_new) fills this lane's words (dims 2*lane, 2*lane+1) of q
 // head 2g, q head 2g+1, k head g (xw[0..2]) and v head g; every thread of the
 // workgroup calls it once, and pre_qkv() once before any load of this
@@ -486,117 +533,134 @@ __device__ __forceinline__ void attention_group(AttnLds& L, int g, int sg, int p
   }
   __syncthreads();
 
-  // ---- 3. scores, online softmax, weighted v ----
-  float m = -__builtin_inff(), l = 0.0f;  // per q head; identical in all lanes
-  float mB = -__builtin_inff(), lB = 0.0f;
-  float accA0 = 0.0f, accA1 = 0.0f, accB0 = 0.0f, accB1 = 0.0f;
+  // ---- 3. per chunk (this wave's LDS region), transposed on the matrix
+  // cores: S^T = K Q^T (K rows as A; B holds q_A and q_B as columns 0 and 1,
+  // the other 14 zero), so lane (c16, grp) has query c16's scores at chunk
+  // positions 16 nt + 4 grp + e; online softmax per query in base-2 units
+  // (running max m, the lane's share of the sum l); O^T += V^T P^T with the
+  // lane's 8 weights as B in the order 4 grp + e, 16 + 4 grp + e of the MFMA's
+  // k slots, V^T from two transposing LDS reads per 16 dims in that order, p
+  // split into f16 hi + lo (p - hi exact), carrying p to about 2^-22.  Lanes
+  // with c16 < 2 hold the results. ----
+  const int c16 = lane & 15;
+  const int grp = lane >> 4;
+  f16x8 qf[4];
+  {
+    const uint8_t* qrow = reinterpret_cast<const uint8_t*>(L.qh[c16 & 1]);
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+      const f16x8 q8 = *reinterpret_cast<const f16x8*>(qrow + 2 * (32 * st + 8 * grp));
+      qf[st] = c16 < 2 ? q8 : (f16x8){};
+    }
+  }
+  float m = -__builtin_inff(), l = 0.0f;
+  f32x4 o[8];
+#pragma unroll
+  for (int d = 0; d < 8; ++d) o[d] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+  const int vrow = 4 * grp + (c16 >> 2);
+  const auto v_off = [&](int row, int d) {
+    return 8192 + 256 * row + 16 * ((2 * d + ((c16 & 3) >> 1)) ^ (2 * (row & 7))) + 8 * (c16 & 1);
+  };
+  // Chunk c's copies: K(c) then V(c), issued as kv_stage does for c = 0 and
+  // for c > 0 as K(c) after chunk c - 1's scores and V(c) after its weighted
+  // sum; the loads of one wave return in order, so K(c) has landed once at
+  // most the 32 V(c) loads are outstanding, V(c) once at most K(c + 1)'s 8.
   for (int c = 0; c < n_chunks; ++c) {
     const int c0 = start + 32 * c;
-    const int p = c0 + pl;
-    const bool valid = p < end;
-    u32x4 kreg[8];
+    // the staged row of position pos predates this step's k and v: replace it
+    const bool has_pos = pos >= c0 && pos < c0 + 32;
+    const int rp = pos - c0;
+    wait_vm<32>();
+    if (has_pos && lane < 16)
+      *reinterpret_cast<u32x4*>(kv + 1024 * (lane & 7) + 512 * (lane >> 3) + 16 * rp) =
+          *reinterpret_cast<const u32x4*>(&L.kh[4 * lane]);
+    f32x4 sc[2];
 #pragma unroll
-    for (int mm = 0; mm < 8; ++mm)
-      kreg[mm] = *reinterpret_cast<const u32x4*>(kv + 1024 * mm + 16 * lane);
-    // the row of position pos is this step's k (in LDS; the cache slot was
-    // staged before it was written): one lane takes it over
-    if (p == pos) {
+    for (int nt = 0; nt < 2; ++nt) {
+      sc[nt] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-      for (int mm = 0; mm < 8; ++mm)
-        kreg[mm] = *reinterpret_cast<const u32x4*>(&L.kh[32 * half + 4 * mm]);
-    }
-    // two partial sums per head (dims of even / odd 8-dim groups) halve the
-    // dependent chain
-    float dA0 = 0.0f, dB0 = 0.0f, dA1 = 0.0f, dB1 = 0.0f;
-#pragma unroll
-    for (int mm = 0; mm < 8; mm += 2) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int i = 32 * half + 4 * mm + j;
-        const f16x2 k0 = as_f16x2(kreg[mm][j]), k1 = as_f16x2(kreg[mm + 1][j]);
-        dA0 = __builtin_amdgcn_fdot2(as_f16x2(L.qh[0][i]), k0, dA0, false);
-        dB0 = __builtin_amdgcn_fdot2(as_f16x2(L.qh[1][i]), k0, dB0, false);
-        dA1 = __builtin_amdgcn_fdot2(as_f16x2(L.qh[0][i + 4]), k1, dA1, false);
-        dB1 = __builtin_amdgcn_fdot2(as_f16x2(L.qh[1][i + 4]), k1, dB1, false);
+      for (int st = 0; st < 4; ++st) {
+        const int ch = 4 * st + grp;
+        const f16x8 kf = *reinterpret_cast<const f16x8*>(kv + 1024 * (ch & 7) + 512 * (ch >> 3) +
+                                                         16 * (16 * nt + c16));
+        sc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[st], sc[nt], 0, 0, 0);
       }
     }
-    float dA = dA0 + dA1, dB = dB0 + dB1;
-    dA = sum_halves(dA);
-    dB = sum_halves(dB);
-    const float sA = valid ? dA * kAttnScale : -__builtin_inff();
-    const float sB = valid ? dB * kAttnScale : -__builtin_inff();
-    const float mnA = fmaxf(m, max32(sA));
-    const float mnB = fmaxf(mB, max32(sB));
-    // mn = -inf only while the split has seen no valid position (acc, l = 0)
-    const float cA = mnA == -__builtin_inff() ? 1.0f : expf(m - mnA);
-    const float cB = mnB == -__builtin_inff() ? 1.0f : expf(mB - mnB);
-    const float pA = valid ? expf(sA - mnA) : 0.0f;
-    const float pB = valid ? expf(sB - mnB) : 0.0f;
-    l = l * cA + sum32(pA);
-    lB = lB * cB + sum32(pB);
-    m = mnA;
-    mB = mnB;
-    accA0 *= cA;
-    accA1 *= cA;
-    accB0 *= cB;
-    accB1 *= cB;
-    __builtin_amdgcn_sched_barrier(0);
-    // Four positions at a time, the next four's v requested from LDS before
-    // this four's products: position j's weights are lane j's p (lanes j and
-    // j + 32 hold the same value), read into scalar registers (the scheduling
-    // fences keep the compiler from hoisting all 64 reads).  With `fix`,
-    // position pos takes this step's v, and positions past the split (weight
-    // 0, a clamped valid row) take v = 0, so a non-finite value there cannot
-    // leak in; most chunks need neither (a wave-uniform branch).
-    const int n = end - c0 < 32 ? end - c0 : 32;
-    const auto v_word = [&](int j) {
-      return *reinterpret_cast<const uint32_t*>(kv + 8192 + 256 * j + 4 * lane);
-    };
-    const auto weighted_v = [&](bool fix) {
-      uint32_t vbuf[2][4];
+    // s[4 nt + e]: position c0 + 16 nt + 4 grp + e; past the split: -inf
+    float s[8];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) vbuf[0][j] = v_word(j);
+    for (int nt = 0; nt < 2; ++nt)
 #pragma unroll
-      for (int j0 = 0; j0 < 32; j0 += 4) {
-        if (j0 + 4 < 32) {
-#pragma unroll
-          for (int j = 0; j < 4; ++j) vbuf[((j0 >> 2) + 1) & 1][j] = v_word(j0 + 4 + j);
-        }
-#pragma unroll
-        for (int j = j0; j < j0 + 4; ++j) {
-          const uint32_t vs = vbuf[(j0 >> 2) & 1][j - j0];
-          const uint32_t vw = fix ? (c0 + j == pos ? v_new : (j < n ? vs : 0u)) : vs;
-          const f16x2 vv = as_f16x2(vw);
-          const float v0 = (float)vv.x, v1 = (float)vv.y;
-          const float wa = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pA), j));
-          const float wb = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pB), j));
-          accA0 = __builtin_fmaf(wa, v0, accA0);
-          accA1 = __builtin_fmaf(wa, v1, accA1);
-          accB0 = __builtin_fmaf(wb, v0, accB0);
-          accB1 = __builtin_fmaf(wb, v1, accB1);
-        }
-        __builtin_amdgcn_sched_barrier(0);
+      for (int e = 0; e < 4; ++e) {
+        const bool ok = c0 + 16 * nt + 4 * grp + e < end;
+        s[4 * nt + e] = ok ? sc[nt][e] * kScoreScaleLog2 : -__builtin_inff();
       }
-    };
-    if (n < 32 || (pos >= c0 && pos < c0 + 32)) weighted_v(true);
-    else weighted_v(false);
-    __builtin_amdgcn_sched_barrier(0);
-    // the next chunk into the same region: every read of this one has
-    // returned (its values were used above)
-    if (c + 1 < n_chunks) kv_stage(kv, k_cache, v_cache, g, c0 + 32, last);
+    float mx = fmaxf(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])),
+                     fmaxf(fmaxf(s[4], s[5]), fmaxf(s[6], s[7])));
+    mx = max_col4(mx);
+    const float mn = fmaxf(m, mx);
+    // mn = -inf only while the split has seen no valid position (o, l = 0)
+    const float alpha = mn == -__builtin_inff() ? 1.0f : __builtin_amdgcn_exp2f(m - mn);
+    float p[8], ps = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      p[i] = s[i] == -__builtin_inff() ? 0.0f : __builtin_amdgcn_exp2f(s[i] - mn);
+      ps += p[i];
+    }
+    l = l * alpha + ps;
+    m = mn;
+#pragma unroll
+    for (int d = 0; d < 8; ++d) o[d] *= alpha;
+    // the K region is free once its reads have returned: the next chunk's K
+    wait_lds();
+    if (c + 1 < n_chunks) {
+      kv_stage_k(kv, k_cache, g, c0 + 32, last);
+      wait_vm<8>();
+    } else {
+      wait_vm<0>();
+    }
+    if (has_pos)
+      *reinterpret_cast<uint32_t*>(kv + 8192 + 256 * rp + 16 * ((lane >> 2) ^ (2 * (rp & 7))) +
+                                   4 * (lane & 3)) = v_new;
+    f16x8 ph, pl;
+#pragma unroll
+    for (int i = 0; i < 8; i += 2) {
+      typedef float f32x2_t __attribute__((ext_vector_type(2)));
+      const f16x2 h2 = __builtin_convertvector((f32x2_t){p[i], p[i + 1]}, f16x2);
+      const f16x2 l2 = __builtin_convertvector(
+          (f32x2_t){p[i] - (float)h2.x, p[i + 1] - (float)h2.y}, f16x2);
+      ph[i] = h2.x;
+      ph[i + 1] = h2.y;
+      pl[i] = l2.x;
+      pl[i + 1] = l2.y;
+    }
+#pragma unroll
+    for (int d = 0; d < 8; ++d) {
+      const v4i16 v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((LDS_AS v4i16*)(kv + v_off(vrow, d)));
+      const v4i16 v1 =
+          __builtin_amdgcn_ds_read_tr16_b64_v4i16((LDS_AS v4i16*)(kv + v_off(vrow + 16, d)));
+      const f16x8 vf = __builtin_bit_cast(f16x8, (v8i16){v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w});
+      o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, ph, o[d], 0, 0, 0);
+      o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pl, o[d], 0, 0, 0);
+    }
+    // the V region is free once its reads have returned: the next chunk's V
+    if (c + 1 < n_chunks) {
+      wait_lds();
+      kv_stage_v(kv, v_cache, g, c0 + 32, last);
+    }
   }
+  l = sum_col4(l);
 
   // ---- 4. the four waves' results -> one partial per query head ----
-  if (lane == 0) {
-    L.mrg[wave][0][0] = m;
-    L.mrg[wave][0][1] = l;
-    L.mrg[wave][1][0] = mB;
-    L.mrg[wave][1][1] = lB;
+  if (c16 < 2) {
+    if (grp == 0) {
+      L.mrg[wave][c16][0] = m;
+      L.mrg[wave][c16][1] = l;
+    }
+#pragma unroll
+    for (int d = 0; d < 8; ++d)
+      *reinterpret_cast<f32x4*>(&L.mrg[wave][c16][4 + 16 * d + 4 * grp]) = o[d];
   }
-  L.mrg[wave][0][2 + 2 * lane] = accA0;
-  L.mrg[wave][0][3 + 2 * lane] = accA1;
-  L.mrg[wave][1][2 + 2 * lane] = accB0;
-  L.mrg[wave][1][3 + 2 * lane] = accB1;
   __syncthreads();
   if (wave < 2) {  // wave hh merges query head 2g + hh
     const int hh = wave;
@@ -607,10 +671,10 @@ __device__ __forceinline__ void attention_group(AttnLds& L, int g, int sg, int p
 #pragma unroll
     for (int w = 0; w < kAttnWaves; ++w) {
       const float mw = L.mrg[w][hh][0];
-      const float ww = mw == -__builtin_inff() ? 0.0f : expf(mw - M);
+      const float ww = mw == -__builtin_inff() ? 0.0f : exp2f(mw - M);
       Ls = Ls + L.mrg[w][hh][1] * ww;
-      a0 = a0 + L.mrg[w][hh][2 + 2 * lane] * ww;
-      a1 = a1 + L.mrg[w][hh][3 + 2 * lane] * ww;
+      a0 = a0 + L.mrg[w][hh][4 + 2 * lane] * ww;
+      a1 = a1 + L.mrg[w][hh][5 + 2 * lane] * ww;
     }
     publish(hh, M, Ls, a0, a1);
   }

@@ -110,7 +110,7 @@ extern "C" __global__ __launch_bounds__(256) void dec_attention(
 
 // attn = the merged attention output: head h, dim d =
 // sum_g w_g acc_g[d] / sum_g w_g l_g over the 8 partials g of head h, w_g =
-// exp(m_g - max m); then res = h + f16(W_o[layer] . attn)
+// 2^(m_g - max m) (m in base-2 units); then res = h + f16(W_o[layer] . attn)
 // (qwen3_full.mlir:739, 801-805).  Four waves per workgroup, one row quad
 // each; the workgroup's 256 threads merge 8 dims each into LDS while the
 // weight loads are in flight.  Workgroup 0 also stores attn.

@@ -37,12 +37,6 @@
 
 namespace {
 
-typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef short v4i16 __attribute__((ext_vector_type(4)));
-typedef short v8i16 __attribute__((ext_vector_type(8)));
-#define LDS_AS __attribute__((address_space(3)))
-
 // ---------------------------------------------------------------- GEMM ----
 //
 // Y[m, n] = sum_k X[m, k] W[n, k], W a [N, K] matrix of Q8_0 blocks (row n:
@@ -325,13 +319,6 @@ __device__ __forceinline__ int f16_lds_off(int r, int c) {
     const int line = r >> 1;
     return 256 * line + 16 * ((((r & 1) << 3) | c) ^ (line & 15));
   }
-}
-
-// vmcnt(n) with the other counters left alone (gfx9 s_waitcnt encoding)
-template <int N>
-__device__ __forceinline__ void wait_vm() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0f70);
 }
 
 template <int EPI, int MS, int NS, int KS, int NBUF, int WM = 2, int WN = 2>
@@ -848,22 +835,6 @@ extern "C" __global__ __launch_bounds__(256) void pf_qk_rope_cache(
 // block with one split writes its output directly; otherwise each split
 // leaves its partial in its slot of `part` and pf_attn_merge, launched next,
 // combines them.
-namespace {
-constexpr float kScoreScaleLog2 = 0.0883883461356163f * 1.44269504088896341f;
-
-// the max of v over lanes i, i ^ 16, i ^ 32, i ^ 48 (v_permlane16_swap /
-// v_permlane32_swap hand each lane the value of its partner row; sum_col4 is
-// the sum).  Both results of each swap are used; the generated code was
-// checked for that (a swap whose second result is dropped reduces nothing),
-// and the attention tests against the oracle would fail on any lane seeing a
-// different max.
-__device__ __forceinline__ float max_col4(float v) {
-  auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
-  auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
-}
-}  // namespace
 
 extern "C" __global__ __launch_bounds__(256) void pf_attention(
     const uint16_t* __restrict__ q_roped, const uint16_t* __restrict__ k_cache,
