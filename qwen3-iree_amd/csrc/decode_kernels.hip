@@ -597,6 +597,7 @@ union StepLds {
 };
 // two workgroups per CU: 80 KiB each (the vocab phase adds 160 bytes)
 static_assert(sizeof(StepLds) + 4 * kVecWords <= 81920 - 256, "dec_step LDS");
+static_assert(kKvHeads == 8 && kBBase % 8 == 0, "one kv head's attention workgroups per XCD (wg mod 8)");
 
 }  // namespace
 
@@ -705,9 +706,12 @@ void dec_step(StepParams P) {
     }
   } else if (wg < kCBase) {
     // ================= B: attention (+ merge on split group 0) =================
+    // kv head g's split groups, its merge (split group 0) among them, on
+    // workgroups wg = g (mod 8): the partials' hand-off stays within one XCD
+    // (one L2)
     const int bw = wg - kBBase;
-    const int g = bw / kAttnGroups;
-    const int sg = bw % kAttnGroups;
+    const int g = bw % kKvHeads;
+    const int sg = bw / kKvHeads;
     uint8_t* const kv_mine = S.b.kv[wave];
     // the first chunk of each wave's split stays in LDS: requested for layer 0
     // now, for layer l + 1 as soon as layer l's attention (and merge) is done
