@@ -818,8 +818,9 @@ extern "C" __global__ __launch_bounds__(256) void pf_qk_rope_cache(
 //   S^T = K Q^T: 8 v_mfma_f32_16x16x32_f16 (K rows as A, the wave's 16 query
 //     rows as B; exact f16 products, f32 sums), so lane (c16, grp) holds the
 //     scores of query c16 at positions 4 grp + e and 16 + 4 grp + e (e < 4);
-//   online softmax in f32 per query (running max m, the lane's share of the
-//     sum l; the max over a query's four lanes by permlane swaps), scores
+//   online softmax in f32 per query (a lagging reference maximum m, the
+//     lane's share of the sum l; the max over a query's four lanes by
+//     permlane swaps), scores
 //     scaled by rsqrt(128) log2(e) so each weight is one exp2 (v_exp_f32);
 //   O^T += V^T P^T: the lane's 8 weights are the B operand as they are, with
 //     the MFMA's 32 k slots standing for positions in the order 4 grp + e,
@@ -827,14 +828,21 @@ extern "C" __global__ __launch_bounds__(256) void pf_qk_rope_cache(
 //     that order.  p is split into f16 hi + lo (p - hi), O^T = V^T hi +
 //     V^T lo (8 + 8 MFMAs), carrying p to about 2^-22.
 // No weight goes through LDS.  Blocks below every query of the wave skip the
-// mask; the O rescale is skipped when no lane's max moved.  out: [n, 2048]
+// mask; the O rescale is skipped when no lane's reference moved.  out: [n, 2048]
 // f16 = O / l.
 //
 // A query block's positions are divided into splits of split_blocks blocks of
-// 32 (prefill_split.h); grid (pairs of query block and split, 8).  A query
+// 32 (prefill_split.h); grid 8 x (pairs of query block and split),
+// workgroup 8 pair + g: kv head g = workgroup mod 8 runs on XCD g (workgroups
+// go to the 8 XCDs in turn), so each XCD's L2 holds one head's cache rows
+// (1 MiB at 2048 positions) instead of all eight.  A query
 // block with one split writes its output directly; otherwise each split
 // leaves its partial in its slot of `part` and pf_attn_merge, launched next,
 // combines them.
+
+// How far (base-2 units) a block's maximum score may exceed the reference
+// maximum before the reference moves (the weights' range is [0, 2^kMaxLag]).
+constexpr float kMaxLag = 8.0f;
 
 extern "C" __global__ __launch_bounds__(256) void pf_attention(
     const uint16_t* __restrict__ q_roped, const uint16_t* __restrict__ k_cache,
@@ -844,7 +852,8 @@ extern "C" __global__ __launch_bounds__(256) void pf_attention(
   // reading one buffer does not wait for the copies into the others
   __shared__ __attribute__((aligned(1024))) uint8_t kt0[8192], kt1[8192], kt2[8192];
   __shared__ __attribute__((aligned(1024))) uint8_t vt0[8192], vt1[8192], vt2[8192];
-  const int g = blockIdx.y;
+  const int g = blockIdx.x & 7;
+  const int pair = blockIdx.x >> 3;
   const int t = threadIdx.x;
   const int wave = t >> 6;
   const int lane = t & 63;
@@ -853,7 +862,7 @@ extern "C" __global__ __launch_bounds__(256) void pf_attention(
   const int head = 2 * g + (wave >> 1);
   const int lo = chunk_local ? start : 0;
   const PfSplitGeometry G = pf_split_geometry(n, start, lo);
-  const PfSplitPair P = pf_split_pair(G, split_blocks, blockIdx.x);
+  const PfSplitPair P = pf_split_pair(G, split_blocks, pair);
   const int qb = P.qb;
   const int q0 = 32 * qb + 16 * (wave & 1);  // this wave's first token
 
@@ -958,10 +967,16 @@ extern "C" __global__ __launch_bounds__(256) void pf_attention(
     float mx = fmaxf(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])),
                      fmaxf(fmaxf(s[4], s[5]), fmaxf(s[6], s[7])));
     mx = max_col4(mx);
-    const float mn = fmaxf(m, mx);
+    // The reference maximum m lags: it moves to the block's maximum only when
+    // that exceeds it by more than kMaxLag (base-2 units), or on the first
+    // block with a valid score, so weights stay at most 2^kMaxLag and most
+    // blocks skip the rescale of o.  o and l share the reference, so o / l is
+    // the same quotient.
+    const bool grow = mx > m + kMaxLag;  // false while both are -inf
+    const float mn = grow ? mx : m;
     // v_exp_f32 without the denormal-range fix-up of exp2f: a weight below
-    // 2^-126 beside the max's weight 1 changes no f32 sum
-    const float alpha = mn == -__builtin_inff() ? 1.0f : __builtin_amdgcn_exp2f(m - mn);
+    // 2^-126 beside the weight 1 of the score that set m changes no f32 sum
+    const float alpha = grow && m != -__builtin_inff() ? __builtin_amdgcn_exp2f(m - mn) : 1.0f;
     float p[8], ps = 0.0f;
     if (masked) {
 #pragma unroll
@@ -969,7 +984,7 @@ extern "C" __global__ __launch_bounds__(256) void pf_attention(
         p[i] = s[i] == -__builtin_inff() ? 0.0f : __builtin_amdgcn_exp2f(s[i] - mn);
         ps += p[i];
       }
-    } else {  // every score finite, mn finite
+    } else {  // every score finite, mn finite (the block grew it if it was -inf)
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         p[i] = __builtin_amdgcn_exp2f(s[i] - mn);
@@ -1035,7 +1050,7 @@ extern "C" __global__ __launch_bounds__(256) void pf_attention(
 
   // several splits: (m, l, O) of this split's positions to its slot, row
   // 16 wave + c16; pf_attn_merge combines the slots
-  float* slot = part + ((size_t)blockIdx.x * kKvHeads + g) * kPfAttnSlotFloats;
+  float* slot = part + ((size_t)pair * kKvHeads + g) * kPfAttnSlotFloats;
   const int r = 16 * wave + c16;
 #pragma unroll
   for (int d = 0; d < 8; ++d)
@@ -1046,23 +1061,24 @@ extern "C" __global__ __launch_bounds__(256) void pf_attention(
   }
 }
 
-// The splits of query block blockIdx.x / 4, kv head g = blockIdx.y (nothing
-// to do for a block with one split), merged in split order with a running
-// maximum (m in base-2 units, as pf_attention keeps it):
+// The splits of query block blockIdx.x / 32, kv head g = blockIdx.x % 8 (on
+// the XCD whose L2 saw that head's partials written; nothing to do for a
+// block with one split), merged in split order with a running maximum (m in
+// base-2 units, as pf_attention keeps it):
 //   M' = max(M, m_s),  O' = O 2^(M - M') + O_s 2^(m_s - M'),
 //   l' = l 2^(M - M') + l_s 2^(m_s - M'),
 // out = O / l.  Four workgroups per query block, one per 32 of the 128
 // dimensions; thread t: slot row t >> 2 (wave w = row >> 4 of pf_attention:
 // head 2g + (w >> 1), token 32 qb + 16 (w & 1) + (row & 15)), dims
-// 32 (blockIdx.x % 4) + 8 (t & 3) .. + 7.  The partials of up to 8 splits are
-// requested before any is used, so a query block with many splits waits for
-// memory once per 8 splits.
+// 32 ((blockIdx.x / 8) % 4) + 8 (t & 3) .. + 7.  The partials of up to 8
+// splits are requested before any is used, so a query block with many splits
+// waits for memory once per 8 splits.
 extern "C" __global__ __launch_bounds__(256) void pf_attn_merge(
     const float* __restrict__ part, int n, int start, int chunk_local, int split_blocks,
     uint16_t* __restrict__ out) {
-  const int qb = blockIdx.x >> 2;
-  const int quarter = blockIdx.x & 3;
-  const int g = blockIdx.y;
+  const int qb = blockIdx.x >> 5;
+  const int quarter = (blockIdx.x >> 3) & 3;
+  const int g = blockIdx.x & 7;
   const PfSplitGeometry G = pf_split_geometry(n, start, chunk_local ? start : 0);
   const int nb = qb == G.nqb - 1 ? G.nb_last : qb + G.c;
   const int ns = (nb + split_blocks - 1) / split_blocks;

@@ -1499,10 +1499,11 @@ int launch_prefill_layer(const qwen3_weights* w, int layer, void* k_cache, void*
     if (pairs > pf_attn_pair_cap(n))
       return fail(Q8_ERR_BAD_SHAPE, "attention splits exceed the workspace");  // not reached
     void* args[] = {&qr, &kc, &vc, &nn, &start, &cl, &sb, &part, &attn};
-    if ((rc = launch2(g.pf_attn, (uint32_t)pairs, 8, 256, args, st))) return rc;
+    // 1-D grids, kv head = workgroup mod 8: one head per XCD
+    if ((rc = launch(g.pf_attn, (uint32_t)(8 * pairs), 256, args, st))) return rc;
     if (pairs > G.nqb) {  // some query block has several splits
       void* margs[] = {&part, &nn, &start, &cl, &sb, &attn};
-      if ((rc = launch2(g.pf_attn_merge, (uint32_t)(4 * G.nqb), 8, 256, margs, st))) return rc;
+      if ((rc = launch(g.pf_attn_merge, (uint32_t)(32 * G.nqb), 256, margs, st))) return rc;
     }
   }
   // the attention partials are consumed by now: their region holds the
