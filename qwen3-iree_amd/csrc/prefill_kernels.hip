@@ -971,41 +971,48 @@ extern "C" __global__ __launch_bounds__(256) void pf_attention(
     // that exceeds it by more than kMaxLag (base-2 units), or on the first
     // block with a valid score, so weights stay at most 2^kMaxLag and most
     // blocks skip the rescale of o.  o and l share the reference, so o / l is
-    // the same quotient.
+    // the same quotient.  alpha = 2^(m - mn) where it moves (0 from m = -inf,
+    // where o and l are still 0), else 1.
     const bool grow = mx > m + kMaxLag;  // false while both are -inf
     const float mn = grow ? mx : m;
     // v_exp_f32 without the denormal-range fix-up of exp2f: a weight below
     // 2^-126 beside the weight 1 of the score that set m changes no f32 sum
-    const float alpha = grow && m != -__builtin_inff() ? __builtin_amdgcn_exp2f(m - mn) : 1.0f;
-    float p[8], ps = 0.0f;
+    const float alpha = __builtin_amdgcn_exp2f(grow ? m - mx : 0.0f);
+    float p[8];
     if (masked) {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
+      for (int i = 0; i < 8; ++i)
         p[i] = s[i] == -__builtin_inff() ? 0.0f : __builtin_amdgcn_exp2f(s[i] - mn);
-        ps += p[i];
-      }
     } else {  // every score finite, mn finite (the block grew it if it was -inf)
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
+      for (int i = 0; i < 8; ++i)
         p[i] = __builtin_amdgcn_exp2f(s[i] - mn);
-        ps += p[i];
-      }
     }
+    float ps = p[0];
+#pragma unroll
+    for (int i = 1; i < 8; ++i) ps += p[i];
     l = l * alpha + ps;
     m = mn;
-    if (__builtin_amdgcn_ballot_w64(alpha != 1.0f) != 0) {
+    if (__builtin_amdgcn_ballot_w64(grow) != 0) {
 #pragma unroll
       for (int d = 0; d < 8; ++d) o[d] *= alpha;
     }
-    // hi = f16(p), lo = f16(p - hi), pairs at a time (v_cvt_pk_f16_f32); p - hi
-    // is exact in f32, so however the compiler forms lo it rounds once
+    // hi = f16(p) (pairs at a time, v_cvt_pk_f16_f32), lo = f16(p - hi): p -
+    // hi is exact in f32, so the fused -hi * 1 + p of v_fma_mixlo_f16 /
+    // v_fma_mixhi_f16 (hi's f16 half widened exactly, one rounding to f16 into
+    // the low / high half) gives the same pair as subtracting and converting
     f16x8 ph, pl;
 #pragma unroll
     for (int i = 0; i < 8; i += 2) {
       typedef float f32x2_t __attribute__((ext_vector_type(2)));
       const f16x2 h2 = __builtin_convertvector((f32x2_t){p[i], p[i + 1]}, f16x2);
-      const f16x2 l2 = __builtin_convertvector(
-          (f32x2_t){p[i] - (float)h2.x, p[i + 1] - (float)h2.y}, f16x2);
+      const uint32_t hb = __builtin_bit_cast(uint32_t, h2);
+      uint32_t lb;
+      asm("v_fma_mixlo_f16 %0, -%1, 1.0, %2 op_sel_hi:[1,0,0]" : "=v"(lb) : "v"(hb), "v"(p[i]));
+      asm("v_fma_mixhi_f16 %0, -%1, 1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]"
+          : "+v"(lb)
+          : "v"(hb), "v"(p[i + 1]));
+      const f16x2 l2 = __builtin_bit_cast(f16x2, lb);
       ph[i] = h2.x;
       ph[i + 1] = h2.y;
       pl[i] = l2.x;
