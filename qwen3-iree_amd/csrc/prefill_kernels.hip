@@ -690,6 +690,11 @@ PF_GEMM_F16(pf_gemm_f16_res_12k, kEpiResidual, 1, 2, 256, 3)
 PF_GEMM_F16(pf_gemm_f16_part_22, kEpiPartial, 2, 2, 128, 2)
 PF_GEMM_F16(pf_gemm_f16_part_22k, kEpiPartial, 2, 2, 256, 2)
 PF_GEMM_F16(pf_gemm_f16_part_12k, kEpiPartial, 1, 2, 256, 3)
+// 128 x 128 for attn_o / ffn_down where two K ranges of such tiles cover the
+// CUs once (about 2048 tokens): a 64 x 64 wave tile reads a quarter of the
+// LDS bytes per MFMA that the 32 x 32 of the 64 x 64 workgroup tile does
+PF_GEMM_F16(pf_gemm_f16_part_44, kEpiPartial, 4, 4, 64, 2)
+PF_GEMM_F16(pf_gemm_f16_part_44k, kEpiPartial, 4, 4, 128, 2)
 #undef PF_GEMM_F16
 
 // Per-head rms_norm (q_norm / k_norm, qwen3_full.mlir:648-702) and RoPE

@@ -118,7 +118,7 @@ struct State {
                 pf_f16_sw_22 = nullptr,
                 pf_f16_res_22 = nullptr, pf_f16_res_22k = nullptr, pf_f16_res_12k = nullptr,
                 pf_f16_part_22 = nullptr, pf_f16_part_22k = nullptr, pf_f16_part_12k = nullptr,
-                pf_expand = nullptr;
+                pf_f16_part_44 = nullptr, pf_f16_part_44k = nullptr, pf_expand = nullptr;
   int pf_tile_rows = 0;   // prefill GEMM token tile: 0 = by shape, 32, 64 or 128
   int pf_attn_split = 0;  // prefill attention positions per split in blocks of 32: 0 = by shape
   int step_single = -1;   // single-launch decode step: -1 unknown, 0 off, 1 on
@@ -354,6 +354,8 @@ int q8gemv_init(const char* code_object_path) {
                      {&g.pf_f16_part_22, "pf_gemm_f16_part_22"},
                      {&g.pf_f16_part_22k, "pf_gemm_f16_part_22k"},
                      {&g.pf_f16_part_12k, "pf_gemm_f16_part_12k"},
+                     {&g.pf_f16_part_44, "pf_gemm_f16_part_44"},
+                     {&g.pf_f16_part_44k, "pf_gemm_f16_part_44k"},
                      {&g.pf_expand, "pf_expand_q8"}};
         bool ok = true;
         for (auto& n : names) ok = ok && hipModuleGetFunction(n.fn, pm, n.name) == hipSuccess;
@@ -414,7 +416,7 @@ void q8gemv_shutdown(void) {
   g.pf_f16_44 = g.pf_f16_24 = g.pf_f16_22 = g.pf_f16_sw_46w = g.pf_f16_sw_44 = g.pf_f16_sw_24 =
       g.pf_f16_sw_22 = nullptr;
   g.pf_f16_res_22 = g.pf_f16_res_22k = g.pf_f16_res_12k = g.pf_f16_part_22 = g.pf_f16_part_22k =
-      g.pf_f16_part_12k = g.pf_expand = nullptr;
+      g.pf_f16_part_12k = g.pf_f16_part_44 = g.pf_f16_part_44k = g.pf_expand = nullptr;
   g.vocab = g.vocab_finalize = g.ws_reset = g.copy = nullptr;
   g.ready = false;
 }
@@ -1376,7 +1378,9 @@ int launch_gemm_f16(std::initializer_list<F16Tile> tiles, const void* x, int ldx
 // (the fewest that fill the CUs), each range's f32 sums go to `part`, and
 // pf_res_reduce adds them in order with the residual; where they fill the CUs
 // once but not twice (about 512-1023 tokens), K is split in two, since one
-// workgroup per CU walking all of K hides too little load latency.  The split
+// workgroup per CU walking all of K hides too little load latency; where
+// 128 x 128 tiles cover the CUs once in two K ranges but not in one (about
+// 2048-4095 tokens), K is split in two for those tiles.  The split
 // count depends on M only, so every token tile gives the same bits.  With
 // norm_w set and K split, the reduce also writes norm_out = rms_norm(y,
 // norm_w) (pf_res_reduce_norm, the bits of a separate pf_rmsnorm) and
@@ -1391,6 +1395,7 @@ int launch_gemm_res(const void* x, int ldx, const void* wl, int K, void* y, cons
   const int stages = K / 256;
   int splits = 1;
   const int64_t wgs32 = ((int64_t)M + 31) / 32 * n_tiles;
+  const int64_t wgs128 = ((int64_t)M + 127) / 128 * (kN / 128);
   if (g.pf_gemm_part && g.pf_gemm_part_m32 && g.pf_res_reduce) {
     if (wgs32 < g.compute_units) {
       splits = stages;
@@ -1400,6 +1405,8 @@ int launch_gemm_res(const void* x, int ldx, const void* wl, int K, void* y, cons
           break;
         }
     } else if (wgs32 < 2 * g.compute_units && stages % 2 == 0) {
+      splits = 2;
+    } else if (wgs128 < g.compute_units && 2 * wgs128 >= g.compute_units && stages % 2 == 0) {
       splits = 2;
     }
     if ((size_t)splits * M * kN * 4 > part_bytes) splits = 1;
@@ -1416,7 +1423,8 @@ int launch_gemm_res(const void* x, int ldx, const void* wl, int K, void* y, cons
     return launch_gemm(g.pf_gemm_res, g.pf_gemm_res_m32, x, ldx, wl, K, kN, 64, y, kN, r, kN, 0,
                        M, st);
   }
-  int rc = wf16 ? launch_gemm_f16({{g.pf_f16_part_22, 64, 64, 128, 2},
+  int rc = wf16 ? launch_gemm_f16({{g.pf_f16_part_44k, 128, 128, 128, 1},
+                                   {g.pf_f16_part_22, 64, 64, 128, 2},
                                    {g.pf_f16_part_22k, 64, 64, 256, 1},
                                    {g.pf_f16_part_12k, 32, 64, 256, 0}},
                                   x, ldx, wf16, K, kN, nullptr, kN, nullptr, 0, M, st,
