@@ -198,18 +198,21 @@ def bench_decode(Q, O, stream, args) -> dict:
         f"{tp['median_ms'] * 1e3:.1f}), {1e6 / dec_us:.0f} tok/s")
     # the same step as one cooperative launch (qwen3_set_step_mode(1)), eager
     ts = None
-    try:
-        D.set_step_mode(1)
-    except Q.Q8GemvError as e:
-        log(f"single-launch step unavailable: {e}")
+    if args.per_phase_only:
+        log("single-launch step: not measured (--per-phase-only)")
     else:
-        sess.set_state(first_token, ctx - 1)
-        one = lambda: sess.step(advance=False, logits=False)  # noqa: E731
-        warm(stream, one, 20)
-        ts = timed(Q, stream, one, reps)
-        ok1 = sess.get_state()[1] == ctx - 1 and sess.check_status() == 0
-        log(f"decode step as one cooperative launch: {ts['mean_ms'] * 1e3:.1f} us/token "
-            f"(median {ts['median_ms'] * 1e3:.1f}; status ok={ok1})")
+        try:
+            D.set_step_mode(1)
+        except Q.Q8GemvError as e:
+            log(f"single-launch step unavailable: {e}")
+        else:
+            sess.set_state(first_token, ctx - 1)
+            one = lambda: sess.step(advance=False, logits=False)  # noqa: E731
+            warm(stream, one, 20)
+            ts = timed(Q, stream, one, reps)
+            ok1 = sess.get_state()[1] == ctx - 1 and sess.check_status() == 0
+            log(f"decode step as one cooperative launch: {ts['mean_ms'] * 1e3:.1f} us/token "
+                f"(median {ts['median_ms'] * 1e3:.1f}; status ok={ok1})")
     D.set_step_mode(default_mode)
     sess.free()
     model.free()
@@ -230,6 +233,22 @@ def bench_decode(Q, O, stream, args) -> dict:
                            "kind": "port",
                            "sample": "one step of the C oracle at the same context and inputs "
                                      "(the parity check's step)"}}
+
+
+def copy_calibration(Q, stream, mib: int) -> dict | None:
+    """Five launches of the plain copy kernel (stream_copy_b128) over mib MiB: the
+    known-size reference that rocprof_summary.py scales FETCH_SIZE / WRITE_SIZE by."""
+    if mib <= 0:
+        return None
+    nbytes = mib << 20
+    src, dst = Q.DeviceBuffer(nbytes), Q.DeviceBuffer(nbytes)
+    tc = timed(Q, stream, lambda: Q.stream_copy(dst, src, nbytes, stream), 5, 1)
+    copy_ms = tc["mean_ms"]
+    log(f"copy calibration: {nbytes} B read + written in {copy_ms * 1e3:.1f} us")
+    src.free()
+    dst.free()
+    return {"bytes_read": nbytes, "bytes_written": nbytes, "us": round(copy_ms * 1e3, 2),
+            "GBps_read_plus_write": round(2 * nbytes / (copy_ms * 1e-3) / 1e9, 1)}
 
 
 def prefill_flops(n: int) -> tuple[int, int]:
@@ -536,6 +555,10 @@ def main() -> int:
                          "cache), upload it, check it bit for bit, print one JSON line")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline sample budget")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--per-phase-only", action="store_true",
+                    help="decode step: time only the per-phase launches, not the cooperative "
+                         "launch (for rocprofv3 runs: its exit path faults after cooperative "
+                         "launches, before the CSV files are written)")
     ap.add_argument("--no-graph", action="store_true",
                     help="issue the per-dispatch and decode-step chains eagerly instead of from hipGraphs")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -576,7 +599,9 @@ def run(Q, S, O, info, args) -> int:
         print(json.dumps({"gguf_ingest": bench_gguf(Q, Path(args.gguf_ingest))}), flush=True)
         return 0
     if args.decode_only:
-        print(json.dumps({"decode_step": bench_decode(Q, O, Q.Stream(), args)}), flush=True)
+        stream = Q.Stream()
+        copy_calibration(Q, stream, args.copy_calibration)
+        print(json.dumps({"decode_step": bench_decode(Q, O, stream, args)}), flush=True)
         return 0
     if args.prefill_only:
         print(json.dumps({"prefill": bench_prefill(Q, Q.Stream(), args)}), flush=True)
@@ -594,17 +619,7 @@ def run(Q, S, O, info, args) -> int:
         f"{sweep_bytes} algorithmic bytes per step")
     stream = Q.Stream()
 
-    copy_cal = None
-    if args.copy_calibration > 0:
-        nbytes = args.copy_calibration << 20
-        src, dst = Q.DeviceBuffer(nbytes), Q.DeviceBuffer(nbytes)
-        tc = timed(Q, stream, lambda: Q.stream_copy(dst, src, nbytes, stream), 5, 1)
-        copy_ms = tc["mean_ms"]
-        copy_cal = {"bytes_read": nbytes, "bytes_written": nbytes, "us": round(copy_ms * 1e3, 2),
-                    "GBps_read_plus_write": round(2 * nbytes / (copy_ms * 1e-3) / 1e9, 1)}
-        log(f"copy calibration: {nbytes} B read + written in {copy_ms * 1e3:.1f} us")
-        src.free()
-        dst.free()
+    copy_cal = copy_calibration(Q, stream, args.copy_calibration)
 
     # ------------------------------------------- headline: batched sweep
     batch = sw.batch()
