@@ -297,19 +297,20 @@ extern "C" __global__ __launch_bounds__(256) void dec_scratch_clear(uint32_t* __
 //                 K, V words.  D on workgroups 0..191: gate/up quad pair
 //                 4 wg + w + SwiGLU -> ACT words.  Right after A the D weights
 //                 of this layer and the A weights of the next are requested.
-//   B   256..319  attention for kv head b / 8, split group b % 8 (b = wg -
-//                 256; attention_group, q/k/v from the tagged words) -> PART;
-//                 split group 0 then merges its kv head's 8 partials of both
-//                 query heads -> ATT words; then the next layer's first cache
-//                 chunk is requested into LDS.
-//   C   320..447  attn_o + residual: row quads 2 c, 2 c + 1 (c = wg - 320), one
-//                 1024-column chunk per wave, summed in LDS -> RES words.
-//   E   448..511  ffn_down + residual: row quad 4 e + w per wave over all 3072
-//                 columns (e = wg - 448) -> H words.
+//   B   256..319  attention for kv head b % 8, split group b / 8 (b = wg -
+//                 256: a head's 8 groups on one XCD, wg mod 8; attention_group,
+//                 q/k/v from the tagged words) -> PART; split group 0 then
+//                 merges its kv head's 8 partials of both query heads -> ATT
+//                 words; then the next layer's first cache chunk is requested
+//                 into LDS.
+//   CE  320..447  C: attn_o + residual, row quads 2 c, 2 c + 1 (c = wg - 320),
+//                 one 1024-column chunk per wave, summed in LDS -> RES words;
+//                 then E: ffn_down + residual over the same two row quads,
+//                 the 3072 columns in three chunks over the waves -> H words.
 // Every row is computed with the per-phase kernels' operations in their order
 // (same device functions), so both step modes give the same bits.  Then the
-// vocab GEMV over all 512 workgroups (each publishes its best key as two
-// words), and workgroup 0 reduces the 512 keys: token, optional output slot,
+// vocab GEMV over all 448 workgroups (each publishes its best key as two
+// words), and workgroup 0 reduces the 448 keys: token, optional output slot,
 // position advance, sequence number.  Layer-indexed words alternate between
 // two buffers by layer parity (a word of layer l is rewritten at layer l + 2,
 // after every reader of it has published something the writer waited for).
