@@ -81,17 +81,6 @@ __device__ __forceinline__ float max_col4(float v) {
   return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 
-__device__ __forceinline__ float max32(float v) {  // over the 32 lanes of a wave half
-  v = fmaxf(v, dpp<0xB1>(v));
-  v = fmaxf(v, dpp<0x4E>(v));
-  v = fmaxf(v, dpp<0x141>(v));
-  v = fmaxf(v, dpp<0x140>(v));
-  auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  return fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
-}
-
-__device__ __forceinline__ float sum32(float v) { return sum_rows2(reduce_row16(v)); }
-
 // f16(a) | f16(b) << 16, each rounded to nearest even (one v_cvt_pk_f16_f32);
 // the opaque copy keeps the compiler from folding a preceding multiply into a
 // single-rounding mixed-precision op, as to_f16 does
