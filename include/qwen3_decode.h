@@ -218,7 +218,11 @@ int qwen3_set_prefill_tiling(int gemm_rows, int attn_split_blocks);
  * *n_generated (host) = tokens produced.  Blocks until the loop ends; fails
  * with Q8_ERR_BAD_SHAPE unless *pos + max_new <= max_seq, and with
  * Q8_ERR_STEP_ABORTED if the scratch carries status bit 1 before the loop or
- * after a batch (then *n_generated counts only the batches before). */
+ * after a batch (then *n_generated counts only the batches before).  The next
+ * batch is queued before the host checks the current one; when the current
+ * one ends the loop, *token, *pos and the status are restored to their values
+ * after it, but out_tokens slots past *n_generated may hold the queued
+ * batch's tokens. */
 int qwen3_generate(const qwen3_weights* w, void* k_cache, void* v_cache, int64_t max_seq,
                    int32_t* token, int32_t* pos, int32_t max_new, int32_t eos_id,
                    int32_t* out_tokens, int32_t* n_generated, void* scratch, void* stream);

@@ -1740,6 +1740,30 @@ int qwen3_prefill(const qwen3_weights* w, void* k_cache, void* v_cache, int64_t 
   return Q8_OK;
 }
 
+// qwen3_generate's host-visible copy of the loop state after a batch, and
+// the pinned slots and events it uses, released on every return path once
+// the stream has drained (no copy into a slot is left in flight).
+struct GenReadback {
+  int32_t token;
+  int32_t pos;
+  uint32_t status;
+  uint32_t pad;
+};
+struct GenResources {
+  hipStream_t st;
+  GenReadback* rb = nullptr;
+  hipEvent_t ev[2] = {nullptr, nullptr};
+  explicit GenResources(hipStream_t s) : st(s) {}
+  GenResources(const GenResources&) = delete;
+  GenResources& operator=(const GenResources&) = delete;
+  ~GenResources() {
+    (void)hipStreamSynchronize(st);
+    for (hipEvent_t e : ev)
+      if (e) (void)hipEventDestroy(e);
+    if (rb) (void)hipHostFree(rb);
+  }
+};
+
 int qwen3_generate(const qwen3_weights* w, void* k_cache, void* v_cache, int64_t max_seq,
                    int32_t* token, int32_t* pos, int32_t max_new, int32_t eos_id,
                    int32_t* out_tokens, int32_t* n_generated, void* scratch, void* stream) {
@@ -1757,30 +1781,77 @@ int qwen3_generate(const qwen3_weights* w, void* k_cache, void* v_cache, int64_t
   if (p0 < 0 || (int64_t)p0 + max_new > max_seq)
     return fail(Q8_ERR_BAD_SHAPE, "positions %d + %d new tokens exceed max_seq %lld", p0, max_new,
                 (long long)max_seq);
-  int32_t idx = 0;
-  while (idx < max_new) {
-    const int32_t batch = max_new - idx < kGenerateBatch ? max_new - idx : kGenerateBatch;
-    for (int32_t b = 0; b < batch; ++b) {
+  // One batch stays queued behind the one being checked, so the device does
+  // not wait for the host's check between batches: after batch k's steps, its
+  // token, position and status are copied into pinned host slot k % 2 and an
+  // event is recorded; batch k + 1 is launched before the host waits for that
+  // event.  When batch k ends the loop (its last token is EOS, or a step gave
+  // up), batch k + 1 -- already queued -- is waited for and the token,
+  // position and status are put back to their values after batch k, so
+  // everything the caller can observe is what a loop without the queued batch
+  // leaves (out_tokens slots past *n_generated aside).  Cache rows past the
+  // restored position are never read before a later step rewrites them.
+  GenResources res(st);
+  HIP_TRY(hipHostMalloc(reinterpret_cast<void**>(&res.rb), 2 * sizeof(GenReadback),
+                        hipHostMallocDefault));
+  for (hipEvent_t& e : res.ev) HIP_TRY(hipEventCreateWithFlags(&e, hipEventDisableTiming));
+  uint32_t* status = reinterpret_cast<uint32_t*>(mb(scratch) + kScrStatus);
+  auto launch_batch = [&](int32_t first, int32_t count, int slot) -> int {
+    for (int32_t b = 0; b < count; ++b) {
+      int brc;
       if (use_single()) {
-        if ((rc = launch_step(w, k_cache, v_cache, max_seq, token, token, pos, nullptr,
-                              out_tokens + idx + b, 1, 1, scratch, st)))
-          return rc;
+        if ((brc = launch_step(w, k_cache, v_cache, max_seq, token, token, pos, nullptr,
+                               out_tokens + first + b, 1, 1, scratch, st)))
+          return brc;
         continue;
       }
       void* h = nullptr;
-      if ((rc = launch_body(w, k_cache, v_cache, max_seq, token, pos, scratch, st, &h))) return rc;
-      if ((rc = launch_head(w, h, nullptr, token, pos, 1, max_seq, scratch, st,
-                            out_tokens + idx + b)))
-        return rc;
+      if ((brc = launch_body(w, k_cache, v_cache, max_seq, token, pos, scratch, st, &h))) return brc;
+      if ((brc = launch_head(w, h, nullptr, token, pos, 1, max_seq, scratch, st,
+                             out_tokens + first + b)))
+        return brc;
     }
-    idx += batch;
-    int32_t last = 0;
-    HIP_TRY(hipMemcpyAsync(&last, token, sizeof(last), hipMemcpyDeviceToHost, st));
+    GenReadback* r = &res.rb[slot];
+    HIP_TRY(hipMemcpyAsync(&r->token, token, sizeof(int32_t), hipMemcpyDeviceToHost, st));
+    HIP_TRY(hipMemcpyAsync(&r->pos, pos, sizeof(int32_t), hipMemcpyDeviceToHost, st));
+    HIP_TRY(hipMemcpyAsync(&r->status, status, sizeof(uint32_t), hipMemcpyDeviceToHost, st));
+    HIP_TRY(hipEventRecord(res.ev[slot], st));
+    return Q8_OK;
+  };
+  int32_t first = 0;
+  int32_t count = max_new < kGenerateBatch ? max_new : kGenerateBatch;
+  int slot = 0;
+  if (count > 0 && (rc = launch_batch(first, count, slot))) return rc;
+  while (count > 0) {
+    const int32_t next = first + count;
+    const int32_t next_count = max_new - next < kGenerateBatch ? max_new - next : kGenerateBatch;
+    if (next_count > 0 && (rc = launch_batch(next, next_count, 1 - slot))) return rc;
+    HIP_TRY(hipEventSynchronize(res.ev[slot]));
+    const GenReadback r = res.rb[slot];
+    const bool aborted = (r.status & 2u) != 0;
     // the batch's steps must all have completed; otherwise its tokens are not
     // valid and n_generated stays at the previous batch
-    if ((rc = check_not_aborted(scratch, st, "qwen3_generate"))) return rc;
-    *n_generated = idx;
-    if (last == eos_id) break;
+    if (!aborted) *n_generated = next;
+    if (aborted || r.token == eos_id) {
+      if (next_count > 0) {  // undo the queued batch
+        HIP_TRY(hipEventSynchronize(res.ev[1 - slot]));
+        res.rb[1 - slot] = r;
+        GenReadback* u = &res.rb[1 - slot];
+        HIP_TRY(hipMemcpyAsync(token, &u->token, sizeof(int32_t), hipMemcpyHostToDevice, st));
+        HIP_TRY(hipMemcpyAsync(pos, &u->pos, sizeof(int32_t), hipMemcpyHostToDevice, st));
+        HIP_TRY(hipMemcpyAsync(status, &u->status, sizeof(uint32_t), hipMemcpyHostToDevice, st));
+        HIP_TRY(hipStreamSynchronize(st));
+      }
+      if (aborted)
+        return fail(Q8_ERR_STEP_ABORTED,
+                    "qwen3_generate: a single-launch decode step gave up waiting for a hand-off "
+                    "(status bit 1); its outputs are invalid; qwen3_scratch_reset clears the "
+                    "scratch");
+      break;
+    }
+    first = next;
+    count = next_count;
+    slot = 1 - slot;
   }
   return Q8_OK;
 }

@@ -74,6 +74,10 @@ def test_generate_eos_after_batch(O, D, dmodel, eos_index):
     print(f"generate with eos {eos} (index {eos_index})", flush=True)
     got = sess.generate(12, eos_id=eos)
     assert got.size == n_want and got.tolist() == want[:n_want].tolist()
+    # the batch queued behind the EOS batch was undone: the state is the one
+    # the loop stopped with
+    assert sess.get_state() == (int(want[n_want - 1]), n_want)
+    assert sess.status() == 0
     sess.free()
 
 

@@ -145,3 +145,29 @@ def test_single_launch_abort_is_reported_and_recoverable(gpu, D, dmodel, single)
     toks = s.generate(4, eos_id=-1)
     assert len(toks) == 4 and s.get_state()[1] == 9 and s.check_status() == 0
     s.free()
+
+
+def test_generate_abort_undoes_the_queued_batch(gpu, D, dmodel, single):
+    """A step that gives up inside qwen3_generate (one-round poll limit, set
+    from the host; every workgroup still exits normally): the call reports
+    Q8_ERR_STEP_ABORTED with no tokens counted, and the batch queued behind
+    the failing one is undone -- token and position are those the failing
+    batch left (its aborted steps advance nothing), status bit 1 is set."""
+    Q = gpu
+    s = D.DecodeSession(dmodel, 64)
+    s.set_state(77, 5)
+    D.set_step_spin_limit(1)
+    try:
+        print("generate 8 with a one-round poll limit", flush=True)
+        with pytest.raises(Q.Q8GemvError) as e:
+            s.generate(8, eos_id=-1)
+        s.synchronize()
+    finally:
+        D.set_step_spin_limit(0)
+    assert e.value.code == Q.Q8_ERR_STEP_ABORTED
+    assert s.get_state() == (77, 5)
+    assert s.status() & 2
+    s.reset_scratch()
+    toks = s.generate(4, eos_id=-1)
+    assert len(toks) == 4 and s.get_state()[1] == 9 and s.check_status() == 0
+    s.free()
