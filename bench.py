@@ -18,7 +18,7 @@ pattern still rotates through the 28 layers).  Measured in the same run:
     gate_up, down) + vocab, stream-ordered, replayed from a hipGraph;
   * the full decode step (qwen3_decode_step: embedding, 28 layers with
     attention over a 1024-position KV cache, final norm, vocab, argmax) on
-    random-init Qwen3-0.6B weights, as one cooperative launch per step and as
+    random-init Qwen3-0.6B weights, as one launch per step (dec_step) and as
     a hipGraph of 143 per-phase launches, the token fed back on the device,
     checked against the oracle's step;
   * batched prompt ingestion (qwen3_prefill_batched) of 512 tokens, checked
@@ -196,7 +196,7 @@ def bench_decode(Q, O, stream, args) -> dict:
     log(f"decode step (context {ctx}, {3 + 5 * layers} launches"
         f"{'' if args.no_graph else ', hipGraph'}): {dec_us:.1f} us/token (median "
         f"{tp['median_ms'] * 1e3:.1f}), {1e6 / dec_us:.0f} tok/s")
-    # the same step as one cooperative launch (qwen3_set_step_mode(1)), eager
+    # the same step as one launch (qwen3_set_step_mode(1)), eager
     ts = None
     if args.per_phase_only:
         log("single-launch step: not measured (--per-phase-only)")
@@ -211,7 +211,7 @@ def bench_decode(Q, O, stream, args) -> dict:
             warm(stream, one, 20)
             ts = timed(Q, stream, one, reps)
             ok1 = sess.get_state()[1] == ctx - 1 and sess.check_status() == 0
-            log(f"decode step as one cooperative launch: {ts['mean_ms'] * 1e3:.1f} us/token "
+            log(f"decode step as one launch: {ts['mean_ms'] * 1e3:.1f} us/token "
                 f"(median {ts['median_ms'] * 1e3:.1f}; status ok={ok1})")
     D.set_step_mode(default_mode)
     sess.free()
@@ -222,7 +222,7 @@ def bench_decode(Q, O, stream, args) -> dict:
     return {"us": round(best_us, 2), "median_us": round(best["median_ms"] * 1e3, 2),
             "tok_per_s": round(1e6 / best_us, 1), "context": ctx,
             "bytes": dec_bytes, "GBps": round(best_gbs, 1), "frac": round(best_gbs / HBM_PEAK_GBS, 4),
-            "launch": "one cooperative launch per step" if ts is not None else
+            "launch": "one launch per step (dec_step)" if ts is not None else
                       ("hipGraph of 143 launches" if not args.no_graph else "143 eager launches"),
             "single_launch_us": None if ts is None else round(ts["mean_ms"] * 1e3, 2),
             "per_phase_us": round(dec_us, 2), "per_phase_median_us": round(tp["median_ms"] * 1e3, 2),
@@ -538,7 +538,7 @@ def main() -> int:
                     help="run only end-to-end generation and print its JSON line")
     ap.add_argument("--step-mode", type=int, choices=(0, 1), default=None,
                     help="decode step mode for the whole run (0: per-phase launches, 1: one "
-                         "cooperative launch; default: the library's)")
+                         "launch per step; default: the library's)")
     ap.add_argument("--prefill-only", action="store_true",
                     help="run only batched prompt ingestion and print its JSON line")
     ap.add_argument("--prefill-tokens", type=int, default=512,
@@ -556,9 +556,8 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline sample budget")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--per-phase-only", action="store_true",
-                    help="decode step: time only the per-phase launches, not the cooperative "
-                         "launch (for rocprofv3 runs: its exit path faults after cooperative "
-                         "launches, before the CSV files are written)")
+                    help="decode step: time only the per-phase launches, not the single "
+                         "launch (traces of the per-phase kernels alone)")
     ap.add_argument("--no-graph", action="store_true",
                     help="issue the per-dispatch and decode-step chains eagerly instead of from hipGraphs")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",

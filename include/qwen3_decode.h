@@ -85,9 +85,9 @@ int qwen3_decode_step(const qwen3_weights* w, void* k_cache, void* v_cache, int6
                       void* stream);
 
 /* How qwen3_decode_step, qwen3_prefill and qwen3_generate run a step:
- * mode 1 = one cooperative launch per step (dec_step: all phases in one
- * kernel, 256 resident workgroups handing activations over through tagged
- * words), the default where the device supports it; mode 0 = one launch per
+ * mode 1 = one launch per step (dec_step: all phases in one kernel, 448
+ * workgroups resident at once handing activations over through tagged
+ * words), the default where the device holds them; mode 0 = one launch per
  * phase (143 per step).  Both
  * compute every value with the same operations in the same order (tested bit
  * for bit).  Setting mode 1 on a device that cannot run it fails with

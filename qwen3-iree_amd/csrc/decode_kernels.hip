@@ -16,9 +16,10 @@
 // plus dec_embed (token row gather), dec_vocab_argmax (final rms_norm fused
 // into the vocab GEMV + argmax) and dec_finalize (token, position).
 //
-// Single launch: dec_step runs the whole step in one cooperative launch of
-// one workgroup per CU, phases handing activations over through tagged
-// 8-byte words instead of kernel boundaries (see its comment).
+// Single launch: dec_step runs the whole step in one launch of 448
+// workgroups, two per CU and all resident at once, phases handing activations
+// over through tagged 8-byte words instead of kernel boundaries (see its
+// comment).
 //
 // Numerics follow the reference op by op: f16 tensors between ops, f32 in
 // reductions and transcendental math, RNE to f16.  Normalisation multiplies by
@@ -278,8 +279,9 @@ extern "C" __global__ __launch_bounds__(256) void dec_scratch_clear(uint32_t* __
 
 // ======================================================= single launch ====
 //
-// dec_step: the whole decode step in one launch of kStepWgs = 512 workgroups
-// x 256 threads, two per CU, all resident at once (cooperative launch).  Work
+// dec_step: the whole decode step in one launch of kStepWgs = 448 workgroups
+// x 256 threads, two per CU, all resident at once (the launcher checks the
+// occupancy; there is no grid barrier, and every wait is bounded).  Work
 // moves between workgroups as tagged words: a 64-bit word holds 32 bits of
 // data (an f16 pair or an f32) and a 32-bit tag naming (step, layer, phase); a
 // producer stores the word with one agent-scope atomic store, a consumer polls

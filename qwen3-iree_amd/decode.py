@@ -166,7 +166,7 @@ class DeviceWeights:
 
 
 def step_mode() -> int:
-    """1: each step is one cooperative launch (dec_step); 0: one launch per phase."""
+    """1: each step is one launch (dec_step); 0: one launch per phase."""
     m = ctypes.c_int(0)
     Q._call("qwen3_get_step_mode", ctypes.byref(m))
     return m.value

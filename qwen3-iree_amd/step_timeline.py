@@ -97,7 +97,7 @@ def main() -> int:
     st = np.where(lo != 0, ref + ((lo - ref + (1 << 31)) % (1 << 32)) - (1 << 31), 0)
     t0 = st[0, 0, 0]
 
-    print(f"# dec_step timeline — context {ctx}, one cooperative launch per step\n")
+    print(f"# dec_step timeline — context {ctx}, one launch per step\n")
     print("Command (GPU box, repo root):\n\n    python3 qwen3-iree_amd/step_timeline.py "
           f"--context {ctx} --steps {args.steps}\n")
     print(f"Timestamp build: {step_us:.1f} us per step (mean of {args.steps}); times below are "

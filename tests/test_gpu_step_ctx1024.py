@@ -1,7 +1,7 @@
 """The full decode step at the configured context (Qwen3-0.6B, batch 1,
 context 1024: max_seq 1024, position 1023 over a seeded history in every
 layer's 1023 cached slots) against the oracle's own step, in both step modes
-(one cooperative launch; one launch per phase).  The reference's step is
+(one launch; one launch per phase).  The reference's step is
 @generate's inner loop, model/qwen3_full.mlir:1431-1526.
 
 Checks, as for the short-context steps:

@@ -1,4 +1,4 @@
-"""The single-launch decode step (qwen3_set_step_mode(1): one cooperative
+"""The single-launch decode step (qwen3_set_step_mode(1): one
 launch, phases handing activations over through tagged words) against the
 launch-per-phase step (mode 0, itself checked stage by stage against the
 oracle).  Both run the same operations in the same order, so logits, tokens,
