@@ -392,6 +392,24 @@ __device__ __forceinline__ void kv_stage(uint8_t* kv, const uint16_t* __restrict
   kv_stage_v<PACE>(kv, v_cache, g, c0, last);
 }
 
+// One chunk of a split's cache rows (positions c0 .. c0 + 31, clamped to
+// last) brought into the caches without being kept: lane l touches 4 bytes of
+// the 128-byte half row l % 2 of row l / 2, of K and then of V, by an LDS-DMA
+// into the wave's 256-byte region `sink` (never read), so no register waits
+// on the loads.
+__device__ __forceinline__ void kv_touch(uint8_t* sink, const uint16_t* __restrict__ k_cache,
+                                         const uint16_t* __restrict__ v_cache, int g, int c0,
+                                         int last) {
+  const int lane = threadIdx.x & 63;
+  const int r = lane >> 1;
+  const int p = c0 + r < last ? c0 + r : last;
+  const size_t off = ((size_t)p * kKvHeads + g) * kHeadDim + 64 * (lane & 1);
+  __builtin_amdgcn_global_load_lds((const GLOBAL_AS void*)(k_cache + off), (LDS_AS void*)sink, 4,
+                                   0, 0);
+  __builtin_amdgcn_global_load_lds((const GLOBAL_AS void*)(v_cache + off), (LDS_AS void*)sink, 4,
+                                   0, 0);
+}
+
 // The first chunk of split r (what attention_group reads first).
 template <int PACE = 0>
 __device__ __forceinline__ void kv_prefetch(uint8_t* kv, const uint16_t* __restrict__ k_cache,

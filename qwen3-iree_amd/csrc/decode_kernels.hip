@@ -582,6 +582,7 @@ constexpr int kPaceA = DEC_PACE_A, kPaceD = DEC_PACE_D, kPaceC = DEC_PACE_C, kPa
 struct StepLdsAd {
   uint8_t wa[4][QuadShape<1>::LDS_BYTES];     // the q/k/v quad of each wave
   uint8_t wd[4][2][QuadShape<1>::LDS_BYTES];  // its gate quad and up quad
+  uint8_t sink[4][256];                       // kv_touch's never-read landing area
 };
 struct StepLdsB {
   uint8_t kv[kAttnWaves][kKvPrefetchBytes];  // each wave's first cache chunk
@@ -652,6 +653,10 @@ void dec_step(StepParams P) {
     const int b = 4 * wg + wave;  // gate/up quad pair (has_d)
     constexpr int64_t bpl_gu = (int64_t)(2 * kFfn) * (kHidden / 32 * 34);
     uint8_t* const la = S.ad.wa[wave];
+    // kv_touch task of this wave: head wg mod 8, task (wg / 8) * 4 + wave of
+    // that head's 128 = split (task mod 32), chunk 1 + task / 32 (1-4)
+    const int touch_task = (wg >> 3) * 4 + wave;
+    const int n_split_chunks = ((pos_c + 1 + kAttnSplits - 1) / kAttnSplits + 31) / 32;
     uint8_t* const lg = S.ad.wd[wave][0];
     uint8_t* const lu = S.ad.wd[wave][1];
     q8_quad_prefetch<1>(wsel, n, qd, la);
@@ -683,6 +688,20 @@ void dec_step(StepParams P) {
       put_quad<1>(dst, 0, qd, acc, step_tag(seq, layer, kPhQKV),
                   [](float a, int) { return (uint32_t)f32_to_f16_bits(a); });
       STAMP(layer, 2);
+      // Splits of more than one chunk (context past 1024): this layer's cache
+      // chunks 1-4 of every split into the L2 of the XCD whose attention
+      // workgroups read them (head wg mod 8), one chunk per wave, about 2 us
+      // before the attention copies them (which then hit L2 instead of HBM):
+      // us/token at context 2048 636.6 -> 619.1, 4096 826.7 -> 761.1, 8192
+      // 1158.6 -> 1094.6, 16384 1763.7 -> 1714.0, 1024 unchanged.  Touching
+      // the later chunks too (two tasks per wave) measured slower (8192:
+      // 1123.0, 16384: 1749.1): L2 holds only so much beside the weights.
+      if (touch_task < 32 * (n_split_chunks - 1)) {
+        const SplitRange tr = split_range(touch_task & 31, pos_c);
+        kv_touch(S.ad.sink[wave], P.k_cache + (int64_t)layer * P.max_seq * (kKvHeads * kHeadDim),
+                 P.v_cache + (int64_t)layer * P.max_seq * (kKvHeads * kHeadDim), wg & 7,
+                 tr.start + 32 * (1 + (touch_task >> 5)), tr.last);
+      }
       // this layer's gate/up weights (the next layer's q/k/v weights follow D)
       if (has_d) {
         const uint8_t* wl = P.wgu + layer * bpl_gu;
