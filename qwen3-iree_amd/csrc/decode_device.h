@@ -56,15 +56,6 @@ __device__ __forceinline__ float xor32(float v) {  // the value of lane i ^ 32
 // way round gets the same bits)
 __device__ __forceinline__ float sum_col4(float v) { return sum_halves(sum_rows2(v)); }
 
-// vmcnt(n) with the other counters left alone (gfx9 s_waitcnt encoding)
-template <int N>
-__device__ __forceinline__ void wait_vm() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0f70);
-}
-// lgkmcnt(0): every LDS read of the wave has returned its data
-__device__ __forceinline__ void wait_lds() { __builtin_amdgcn_s_waitcnt(0xc07f); }
-
 // the sum over the wave: rows in index order, (r0 + r1) + (r2 + r3)
 __device__ __forceinline__ float wave_sum(float v) { return sum_col4(reduce_row16(v)); }
 

@@ -329,6 +329,19 @@ constexpr int kCBase = 320;                // 128 attn_o + ffn_down workgroups
 #define DEC_VOCAB_WGS 448
 #endif
 constexpr int kVocabWgs = DEC_VOCAB_WGS;
+// Vocab batches (4 rows) each wave stages into LDS before the last layer's h
+// arrives, on top of the two it loads into registers.
+#ifndef DEC_VOCAB_PRE
+#define DEC_VOCAB_PRE 2
+#endif
+constexpr int kVocabPre = DEC_VOCAB_PRE;
+// Workgroups 0..255 hold the first slot of every CU and finish their vocab
+// rows well before 256..447, which share CUs with them: each of their waves
+// takes kVocabHeavy16 / 16 times the rows of a later wave.
+#ifndef DEC_VOCAB_HEAVY16
+#define DEC_VOCAB_HEAVY16 24
+#endif
+constexpr int kVocabHeavy16 = DEC_VOCAB_HEAVY16;
 // Vectors that every (or nearly every) workgroup waits for -- h, the
 // attention output, the attn_o + residual output, the SwiGLU output -- are
 // published in kRep replicas and workgroup w polls replica w % kRep: with one
@@ -601,6 +614,11 @@ union StepLds {
 };
 // two workgroups per CU: 80 KiB each (the vocab phase adds 160 bytes)
 static_assert(sizeof(StepLds) + 4 * kVecWords <= 81920 - 256, "dec_step LDS");
+static_assert(sizeof(StepLds) >= 4 * kVocabPre * 8192, "vocab stage area");
+// the fewest batches a wave owns (a wave of workgroups 256 .. 447)
+static_assert(kVocab / 4 * 16 / (4 * (256 * kVocabHeavy16 + (kVocabWgs - 256) * 16)) - 1 >=
+                  kVocabPre + 2,
+              "vocab batches per wave");
 static_assert(kKvHeads == 8 && kBBase % 8 == 0, "one kv head's attention workgroups per XCD (wg mod 8)");
 
 }  // namespace
@@ -914,7 +932,13 @@ void dec_step(StepParams P) {
   STAMP(kLayers, 0);
   if (P.head && wg < kVocabWgs) {
     bool ok = true;
-    vocab_body_xp<VOCAB_NT_LOADS != 0, true>(
+    // The stage area is the role LDS: every wave is done with its role (and
+    // its DMAs into it) before any wave stages vocab rows there.
+    if constexpr (kVocabPre > 0) {
+      wait_vm<0>();
+      __syncthreads();
+    }
+    vocab_body_xp<VOCAB_NT_LOADS != 0, true, kVocabPre>(
         P.output_w,
         [&](int li, u32x4 (&xr)[8]) {
           const uint2 w4 = norm_weights4(P.output_norm);  // requested before the wait
@@ -934,7 +958,7 @@ void dec_step(StepParams P) {
         P.logits, kVocab, [&](uint64_t key) {
           put_word(P.words + kWArg + 2 * wg, (uint32_t)(key >> 32), tag_arg);
           put_word(P.words + kWArg + 2 * wg + 1, (uint32_t)key, tag_arg);
-        }, kVocabWgs);
+        }, kVocabWgs, reinterpret_cast<uint8_t*>(&S), 256, kVocabHeavy16);
     if (!ok) return;
     STAMP(kLayers, 2);
   }

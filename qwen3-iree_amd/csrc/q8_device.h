@@ -52,6 +52,15 @@ __device__ __forceinline__ f16x2 as_f16x2(uint32_t v) { return __builtin_bit_cas
 // full vmcnt(0) lgkmcnt(0) drain.
 #define GLOBAL_AS __attribute__((address_space(1)))
 
+// vmcnt(n) with the other counters left alone (gfx9 s_waitcnt encoding)
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0f70);
+}
+// lgkmcnt(0): every LDS read of the wave has returned its data
+__device__ __forceinline__ void wait_lds() { __builtin_amdgcn_s_waitcnt(0xc07f); }
+
 template <bool NT>
 __device__ __forceinline__ u32x4 load_stream(const u32x4* p) {
   const GLOBAL_AS u32x4* g = (const GLOBAL_AS u32x4*)p;
@@ -493,11 +502,25 @@ __device__ __forceinline__ float f16_row_dot(const u32x4& w, const u32x4& xv, fl
 // The workgroup's result reaches publish(key) on thread 0: key =
 // argmax_key(best) or 0 when the workgroup saw no candidate.
 // The rows are split over workgroups 0 .. groups - 1 (the whole grid unless a
-// caller runs the GEMV on only the first `groups` workgroups).
-template <bool NT, bool ARGMAX, class XLoad, class Publish>
+// caller runs the GEMV on only the first `groups` workgroups), evenly unless
+// heavy_wgs > 0: then each wave of workgroups 0 .. heavy_wgs - 1 takes
+// heavy_w16 / 16 times the share of a wave of the others (for a caller whose
+// later workgroups share their CUs with earlier, faster ones).
+//
+// PRE > 0 (for a caller whose x arrives late): the wave's last PRE batches go
+// straight into its LDS area stage + wave * PRE * 8 KiB (global_load_lds; load
+// m of batch s lands at + 8 KiB s + 1 KiB m + 16 lane) and its first two into
+// registers, all before xload, so 2 + PRE batches stream in while x is
+// awaited; the staged batches are consumed last, which keeps every group's
+// rows in increasing order.  Every wave must own at least PRE + 2 batches (the
+// caller checks its sizes), and the workgroup must not use the stage area
+// until the function returns.
+template <bool NT, bool ARGMAX, int PRE = 0, class XLoad, class Publish>
 __device__ __forceinline__ void vocab_body_xp(const uint16_t* __restrict__ W, XLoad&& xload,
                                               uint16_t* __restrict__ logits, int n_rows,
-                                              Publish&& publish, int groups = -1) {
+                                              Publish&& publish, int groups = -1,
+                                              uint8_t* stage = nullptr, int heavy_wgs = 0,
+                                              int heavy_w16 = 16) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int grp = lane >> 4;
@@ -508,8 +531,13 @@ __device__ __forceinline__ void vocab_body_xp(const uint16_t* __restrict__ W, XL
   const int64_t gw = (int64_t)blockIdx.x * wpb + wave;
   const int64_t tw = (int64_t)(groups > 0 ? groups : (int)gridDim.x) * wpb;
   const int64_t nbatch = ((int64_t)n_rows + 3) / 4;
-  const int b_begin = wave < wpb ? (int)(gw * nbatch / tw) : 0;
-  const int b_end = wave < wpb ? (int)((gw + 1) * nbatch / tw) : 0;
+  // a wave of workgroups 0 .. heavy_wgs - 1 takes heavy_w16 / 16 times the
+  // batches of any other wave
+  const int64_t hw = (int64_t)heavy_wgs * wpb;
+  auto cum = [&](int64_t w) { return w <= hw ? w * heavy_w16 : hw * heavy_w16 + (w - hw) * 16; };
+  const int64_t tot = cum(tw);
+  const int b_begin = wave < wpb ? (int)(cum(gw) * nbatch / tot) : 0;
+  const int b_end = wave < wpb ? (int)(cum(gw + 1) * nbatch / tot) : 0;
 
   const u32x4* Wv = reinterpret_cast<const u32x4*>(W);
   u32x4 xr[8];  // this lane's x columns, formed by xload below
@@ -551,24 +579,71 @@ __device__ __forceinline__ void vocab_body_xp(const uint16_t* __restrict__ W, XL
   // load inside the loop is unconditional, so the compiler can wait for
   // exactly the older set.
   u32x4 A[8], B[8];
-  load_batch(b_begin, A);
-  __builtin_amdgcn_sched_barrier(0);
-  xload(li, xr);
   const int nb = b_end - b_begin;
-  if (nb > 0) {
+  if constexpr (PRE > 0) {
+    const int nr = nb - PRE;  // batches read through registers, >= 2
+    uint8_t* ws = stage + (size_t)wave * (PRE * 8192);
+    load_batch(b_begin, A);
+    load_batch(b_begin + 1, B);
+#pragma unroll
+    for (int s = 0; s < PRE; ++s) {
+      int row = 4 * (b_begin + nr + s) + grp;
+      row = row < n_rows ? row : n_rows - 1;
+      const u32x4* p = Wv + (size_t)row * 128 + li;
+#pragma unroll
+      for (int m = 0; m < 8; ++m)
+        __builtin_amdgcn_global_load_lds((const GLOBAL_AS void*)(p + 16 * m),
+                                         (__attribute__((address_space(3))) void*)(ws + 8192 * s +
+                                                                                   1024 * m),
+                                         16, 0, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    xload(li, xr);
+    // A holds batch i, B batch i + 1 (loads in flight) at the top of each round
     int i = 0;
-    for (; i + 2 < nb; i += 2) {
-      load_batch(b_begin + i + 1, B);
+    for (; i + 3 < nr; i += 2) {
       consume(b_begin + i, A);
       load_batch(b_begin + i + 2, A);
       consume(b_begin + i + 1, B);
+      load_batch(b_begin + i + 3, B);
     }
-    if (nb - i == 2) {
-      load_batch(b_begin + i + 1, B);
+    if (nr - i == 3) {
       consume(b_begin + i, A);
+      load_batch(b_begin + i + 2, A);
       consume(b_begin + i + 1, B);
+      consume(b_begin + i + 2, A);
     } else {
       consume(b_begin + i, A);
+      consume(b_begin + i + 1, B);
+    }
+    wait_vm<0>();  // the staged batches have landed in LDS
+#pragma unroll
+    for (int s = 0; s < PRE; ++s) {
+      u32x4 w[8];
+#pragma unroll
+      for (int m = 0; m < 8; ++m)
+        w[m] = *reinterpret_cast<const u32x4*>(ws + 8192 * s + 1024 * m + 16 * lane);
+      consume(b_begin + nr + s, w);
+    }
+  } else {
+    load_batch(b_begin, A);
+    __builtin_amdgcn_sched_barrier(0);
+    xload(li, xr);
+    if (nb > 0) {
+      int i = 0;
+      for (; i + 2 < nb; i += 2) {
+        load_batch(b_begin + i + 1, B);
+        consume(b_begin + i, A);
+        load_batch(b_begin + i + 2, A);
+        consume(b_begin + i + 1, B);
+      }
+      if (nb - i == 2) {
+        load_batch(b_begin + i + 1, B);
+        consume(b_begin + i, A);
+        consume(b_begin + i + 1, B);
+      } else {
+        consume(b_begin + i, A);
+      }
     }
   }
 
