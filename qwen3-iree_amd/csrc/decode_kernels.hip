@@ -615,7 +615,9 @@ union StepLds {
 // two workgroups per CU: 80 KiB each (the vocab phase adds 160 bytes)
 static_assert(sizeof(StepLds) + 4 * kVecWords <= 81920 - 256, "dec_step LDS");
 static_assert(sizeof(StepLds) >= 4 * kVocabPre * 8192, "vocab stage area");
-// the fewest batches a wave owns (a wave of workgroups 256 .. 447)
+// the fewest batches a wave owns (a wave of workgroups 256 .. kVocabWgs - 1)
+static_assert(kVocabWgs > 256 || kVocabHeavy16 == 16,
+              "the weighted split assumes more than 256 vocab workgroups");
 static_assert(kVocab / 4 * 16 / (4 * (256 * kVocabHeavy16 + (kVocabWgs - 256) * 16)) - 1 >=
                   kVocabPre + 2,
               "vocab batches per wave");
