@@ -569,9 +569,13 @@ constexpr int kVecWords = 2 * kAttnGroups * 130;  // 2080: the largest polled ve
 // Weight prefetches sleep 64 kPace* cycles between 1 KiB pieces, each set
 // spread over the time its role has before the weights are needed (the gate/up
 // weights are requested right after A, the next q/k/v weights right after D,
-// the ffn_down weights right after C, the next attn_o weights right after E,
-// the next cache chunk right after attention).  Unpaced bursts from hundreds of
-// workgroups fill the memory queues and delay the hand-offs in flight.
+// the next attn_o weights right after C, the next ffn_down weights right after
+// E, the next cache chunk right after attention).  Unpaced bursts from
+// hundreds of workgroups fill the memory queues and delay the hand-offs in
+// flight; paced too slowly, a prefetch still being issued delays its wave's
+// next poll.  Measured at context 1024 (us/token, 539 with E at 32): A 16 / 48
+// 550 / 592, D 24 / 40 551 / 600, C 8 / 16 / 40 554 / 557 / 568, E 12-24
+// 535-536, E 48 653, the cache chunk 4 / 16 unchanged.
 #ifndef DEC_PACE_A
 #define DEC_PACE_A 32
 #endif
@@ -582,7 +586,7 @@ constexpr int kVecWords = 2 * kAttnGroups * 130;  // 2080: the largest polled ve
 #define DEC_PACE_C 32
 #endif
 #ifndef DEC_PACE_E
-#define DEC_PACE_E 32
+#define DEC_PACE_E 16
 #endif
 #ifndef DEC_PACE_KV
 #define DEC_PACE_KV 8
