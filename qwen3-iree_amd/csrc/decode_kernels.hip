@@ -575,7 +575,8 @@ constexpr int kVecWords = 2 * kAttnGroups * 130;  // 2080: the largest polled ve
 // flight; paced too slowly, a prefetch still being issued delays its wave's
 // next poll.  Measured at context 1024 (us/token, 539 with E at 32): A 16 / 48
 // 550 / 592, D 24 / 40 551 / 600, C 8 / 16 / 40 554 / 557 / 568, E 12-24
-// 535-536, E 48 653, the cache chunk 4 / 16 unchanged.
+// 535-536, E 48 653, the cache chunk 4 / 16 unchanged; with E at 16 (536):
+// A 28 / 36 539 / 552, D 28 / 36 547 / 561, C 28 / 36 539 / 554.
 #ifndef DEC_PACE_A
 #define DEC_PACE_A 32
 #endif
