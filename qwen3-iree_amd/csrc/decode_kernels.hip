@@ -547,7 +547,8 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
 // s), [layer 0..27, or 28 for the vocab phase][point], and copies them to
 // P.stamps[slot][29][16] (u64, zero-extended) at the end.
 //   per layer: 0 layer start, 1 h ready (A), 13 x normalised (A), 2 q/k/v
-//   published, 9 residual ready (D), 10 SwiGLU published, 3 q/k/v ready (B),
+//   published, 15 gate/up weights requested (D), 9 residual ready (D), 10
+//   SwiGLU published, 3 q/k/v ready (B),
 //   4 partial published, 5 partials ready (merge), 6 attention output
 //   published, 14 h rows ready (C), 7 attention output ready (C), 8 residual
 //   published, 11 SwiGLU ready (E), 12 h published
@@ -581,7 +582,7 @@ constexpr int kVecWords = 2 * kAttnGroups * 130;  // 2080: the largest polled ve
 #define DEC_PACE_A 32
 #endif
 #ifndef DEC_PACE_D
-#define DEC_PACE_D 32
+#define DEC_PACE_D 30
 #endif
 #ifndef DEC_PACE_C
 #define DEC_PACE_C 32
@@ -727,11 +728,35 @@ void dec_step(StepParams P) {
                  P.v_cache + (int64_t)layer * P.max_seq * (kKvHeads * kHeadDim), wg & 7,
                  tr.start + 32 * (1 + (touch_task >> 5)), tr.last);
       }
+      // The A-only workgroups (idle until the next layer's h) bring the
+      // gate/up quads of the 24 D workgroups on their XCD (wg mod 8) into its
+      // L2, one dword per 128-byte line into the never-read sink, while the D
+      // workgroups' own paced copies into LDS (below) follow: us/token at
+      // context 1024 535.7 -> 518.6 (with the D pace 32 -> 30; with the touch
+      // the D pace measured 20 / 24 / 26 / 28 / 32 / 36: 542 / 539 / 535 / 522
+      // / 528 / 568).
+      if (!has_d) {
+        const int k = (wg - kDCount) >> 3;  // this one's rank among the 8 on its XCD
+        const uint8_t* wl = P.wgu + layer * bpl_gu;
+        for (int i = 0; i < 6; ++i) {
+          const int tq = wave * 6 + i;  // D workgroup tq / 8 of 3, its wave, gate or up
+          const int j = (wg & 7) + 8 * (3 * k + tq / 8);
+          const int b = 4 * j + ((tq >> 1) & 3);
+          const int quad = (tq & 1) ? kFfn / 4 + b : b;
+          // a quad is 4 x 1088 = 4352 bytes: lines 0..33
+          const uint8_t* src =
+              wl + (size_t)quad * (4 * (kHidden / 32 * 34)) + 128 * (lane < 34 ? lane : 33);
+          __builtin_amdgcn_global_load_lds((const GLOBAL_AS void*)src, (LDS_AS void*)S.ad.sink[wave],
+                                           4, 0, 0);
+          __builtin_amdgcn_s_sleep(16);
+        }
+      }
       // this layer's gate/up weights (the next layer's q/k/v weights follow D)
       if (has_d) {
         const uint8_t* wl = P.wgu + layer * bpl_gu;
         q8_quad_prefetch<1, kPaceD>(wl, 2 * kFfn, b, lg);
         q8_quad_prefetch<1, kPaceD>(wl, 2 * kFfn, kFfn / 4 + b, lu);
+        STAMP(layer, 15);
       }
       // ---- D: gate/up + SwiGLU ----
       if (has_d) {

@@ -33,7 +33,8 @@ REPO = PKG.parent
 POINTS = {0: "layer start", 1: "A: h ready", 13: "A: x normalised", 2: "A: q/k/v published",
           3: "B: q/k/v ready", 4: "B: partial published", 5: "merge: partials ready",
           6: "merge: attention published", 14: "C: h rows ready",
-          7: "C: attention ready", 8: "C: residual published", 9: "D: residual ready",
+          7: "C: attention ready", 8: "C: residual published",
+          15: "D: gate/up weights requested", 9: "D: residual ready",
           10: "D: SwiGLU published", 11: "E: SwiGLU ready", 12: "E: h published"}
 VOCAB_POINTS = {0: "vocab start", 1: "vocab: h ready", 2: "vocab: key published",
                 3: "keys ready (wg 0)", 4: "token written (wg 0)"}
