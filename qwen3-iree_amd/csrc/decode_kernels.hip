@@ -577,7 +577,9 @@ constexpr int kVecWords = 2 * kAttnGroups * 130;  // 2080: the largest polled ve
 // next poll.  Measured at context 1024 (us/token, 539 with E at 32): A 16 / 48
 // 550 / 592, D 24 / 40 551 / 600, C 8 / 16 / 40 554 / 557 / 568, E 12-24
 // 535-536, E 48 653, the cache chunk 4 / 16 unchanged; with E at 16 (536):
-// A 28 / 36 539 / 552, D 28 / 36 547 / 561, C 28 / 36 539 / 554.
+// A 28 / 36 539 / 552, D 28 / 36 547 / 561, C 28 / 36 539 / 554; with the
+// gate/up touch and D at 30 (518): C 26 / 28 / 30 / 34 519 / 517 / 516 / 531,
+// E 12 / 20 518, A 30 522.
 #ifndef DEC_PACE_A
 #define DEC_PACE_A 32
 #endif
@@ -585,7 +587,7 @@ constexpr int kVecWords = 2 * kAttnGroups * 130;  // 2080: the largest polled ve
 #define DEC_PACE_D 30
 #endif
 #ifndef DEC_PACE_C
-#define DEC_PACE_C 32
+#define DEC_PACE_C 30
 #endif
 #ifndef DEC_PACE_E
 #define DEC_PACE_E 16
