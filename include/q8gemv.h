@@ -21,7 +21,14 @@
  *     gives the message for the calling thread.  Arguments are validated on
  *     the host before anything is enqueued; nothing aborts the process.
  *   - Compute entry points are safe to call from several host threads, each
- *     with its own stream, once q8gemv_init() has returned.
+ *     with its own stream, once q8gemv_init() has returned.  One exception:
+ *     f16_gemv_argmax_rows_noalloc keeps its argmax key in one array per GPU,
+ *     so its calls must not overlap on a GPU (streams not ordered with each
+ *     other, or a graph replay beside eager calls).
+ *   - Setters of tuning knobs (q8gemv_batch_set_workgroups,
+ *     vocab_set_workgroups and those of qwen3_decode.h) are process-wide and
+ *     may be called from any thread; a launch reads each knob once, so it
+ *     sees either the old or the new value.
  *   - Alignment: weights and x 16 bytes, y / logits 2 bytes, token 4 bytes,
  *     workspace 16 bytes.
  */

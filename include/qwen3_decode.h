@@ -64,11 +64,17 @@ int qwen3_scratch_reset(void* scratch, void* stream);
 /* Byte offset in the scratch of the u32 status word: bit 0 = a step asked to
  * advance past the last cache slot (the position then stays); bit 1 = a
  * single-launch step gave up waiting for a hand-off (its results are not
- * valid; never expected on a working device).  Bit 1 stays set until
- * qwen3_scratch_reset; the steps after an aborted one run normally (each
- * launch takes a fresh sequence number, so nothing the aborted step left
- * behind is mistaken for its data), but qwen3_generate and
- * qwen3_prefill_batched refuse to start on a scratch that carries it. */
+ * valid; it wrote neither token nor position); bit 2 = a single-launch step
+ * gave up and qwen3_decode_step_checked, qwen3_prefill or qwen3_generate
+ * re-ran it with the per-phase launches (the results are valid: both modes
+ * compute the same bits).  A wait gives up after the spin limit, or about a
+ * millisecond into a wait when not every workgroup of the launch has started
+ * (the grid is not resident at once, e.g. a kernel on another stream holds
+ * CUs).  Bit 1 stays set until the host clears it (qwen3_scratch_reset, or
+ * the re-run above); while it is set every single-launch step on the scratch
+ * returns at its start without touching token, position or cache, and
+ * qwen3_generate, qwen3_prefill, qwen3_decode_step_checked and
+ * qwen3_prefill_batched refuse to start. */
 size_t qwen3_scratch_status_offset(void);
 /* Synchronizes `stream`, then *status = the status word; returns
  * Q8_ERR_STEP_ABORTED if bit 1 is set, else Q8_OK. */
@@ -84,6 +90,25 @@ int qwen3_decode_step(const qwen3_weights* w, void* k_cache, void* v_cache, int6
                       int32_t* token, int32_t* pos, void* logits, int advance, void* scratch,
                       void* stream);
 
+/* qwen3_decode_step, then synchronizes `stream` and checks the status word:
+ * when the single launch gave up (bit 1), the step is run again with the
+ * per-phase launches (the same bits; bit 2 records it, see
+ * qwen3_step_fallback_count), so a successful return always means valid
+ * outputs.  Fails with Q8_ERR_STEP_ABORTED if the scratch carries bit 1
+ * before the call.  Not for graph capture (it synchronizes). */
+int qwen3_decode_step_checked(const qwen3_weights* w, void* k_cache, void* v_cache,
+                              int64_t max_seq, int32_t* token, int32_t* pos, void* logits,
+                              int advance, void* scratch, void* stream);
+
+/* Steps (process-wide, since the library was loaded) that a single launch
+ * gave up on and that were re-run with the per-phase launches. */
+int qwen3_step_fallback_count(uint64_t* count);
+
+/* Test hook: the single-launch step `after` launches from now (0 = the next;
+ * -1 cancels) gives up at its start as a wait that timed out would, so the
+ * error and fallback paths can be exercised without a hang or a fault. */
+int qwen3_debug_force_step_abort(int64_t after);
+
 /* How qwen3_decode_step, qwen3_prefill and qwen3_generate run a step:
  * mode 1 = one launch per step (dec_step: all phases in one kernel, 448
  * workgroups resident at once handing activations over through tagged
@@ -91,7 +116,13 @@ int qwen3_decode_step(const qwen3_weights* w, void* k_cache, void* v_cache, int6
  * phase (143 per step).  Both
  * compute every value with the same operations in the same order (tested bit
  * for bit).  Setting mode 1 on a device that cannot run it fails with
- * Q8_ERR_BAD_ARGUMENT.  No counterpart in the reference (IREE schedules its
+ * Q8_ERR_BAD_ARGUMENT.  Single-launch steps on different streams run one
+ * after another (the library orders each launch after the previous one on
+ * any other stream with an event), since two grids of 448 resident
+ * workgroups do not fit at once; launches recorded under graph capture are
+ * not ordered this way, so graphs holding such steps must not be replayed
+ * concurrently (a step that cannot get its grid resident gives up, see the
+ * status word).  No counterpart in the reference (IREE schedules its
  * dispatches itself). */
 int qwen3_set_step_mode(int mode);
 int qwen3_get_step_mode(int* mode);
@@ -99,7 +130,10 @@ int qwen3_get_step_mode(int* mode);
  * (0 = the default, 2^20, about a second) the workgroup gives up, sets status
  * bit 1 and makes every other waiter of the step give up too, so the launch
  * always completes.  A small limit forces that path (tests of the error
- * reporting); no counterpart in the reference. */
+ * reporting); no counterpart in the reference.
+ * This and the other setters of this header (step mode, prefill tiling) are
+ * process-wide: they take effect for launches made after they return, on
+ * every thread (a call reads each setting once). */
 int qwen3_set_step_spin_limit(uint32_t polls);
 
 /* The same step in parts, for tests and for callers that interleave work:
@@ -118,9 +152,13 @@ int qwen3_decode_head(const qwen3_weights* w, const void* h, void* logits, int32
  * (qwen3_full.mlir:1541-1561): for i in [0, n_prompt) one step at position
  * *pos with input token prompt[i] (device int32 [n_prompt]); logits are only
  * formed after the last prompt token, whose argmax goes to *token.  *pos ends
- * n_prompt slots further (not past max_seq - 1; see the status word).  Only
- * enqueues: check the status word (qwen3_check_status) before trusting the
- * token. */
+ * n_prompt slots further (not past max_seq - 1; see the status word).  In
+ * step mode 0 it only enqueues: check the status word (qwen3_check_status)
+ * before trusting the token.  In step mode 1 it synchronizes `stream` at its
+ * start and after the steps: when a single launch gave up, the steps from it
+ * on are run again with the per-phase launches (status bit 2), and it fails
+ * with Q8_ERR_STEP_ABORTED if the scratch carried bit 1 before the call or
+ * the cache filled up (bit 0) in an aborted run. */
 int qwen3_prefill(const qwen3_weights* w, void* k_cache, void* v_cache, int64_t max_seq,
                   const int32_t* prompt, int32_t n_prompt, int32_t* token, int32_t* pos,
                   void* scratch, void* stream);
@@ -217,12 +255,13 @@ int qwen3_set_prefill_tiling(int gemm_rows, int attn_split_blocks);
  * are produced, as in the reference.  The input token itself is not output.
  * *n_generated (host) = tokens produced.  Blocks until the loop ends; fails
  * with Q8_ERR_BAD_SHAPE unless *pos + max_new <= max_seq, and with
- * Q8_ERR_STEP_ABORTED if the scratch carries status bit 1 before the loop or
- * after a batch (then *n_generated counts only the batches before).  The next
- * batch is queued before the host checks the current one; when the current
- * one ends the loop, *token, *pos and the status are restored to their values
- * after it, but out_tokens slots past *n_generated may hold the queued
- * batch's tokens. */
+ * Q8_ERR_STEP_ABORTED if the scratch carries status bit 1 before the loop.
+ * When a single-launch step gives up, the batch is re-run from that step with
+ * the per-phase launches (status bit 2; the same tokens) and the loop goes on
+ * in that mode.  The next batch is queued before the host checks the current
+ * one; when the current one ends the loop, *token, *pos and the status are
+ * restored to their values after it, but out_tokens slots past *n_generated
+ * may hold the queued batch's tokens. */
 int qwen3_generate(const qwen3_weights* w, void* k_cache, void* v_cache, int64_t max_seq,
                    int32_t* token, int32_t* pos, int32_t max_new, int32_t eos_id,
                    int32_t* out_tokens, int32_t* n_generated, void* scratch, void* stream);

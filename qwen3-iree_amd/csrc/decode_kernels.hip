@@ -387,14 +387,16 @@ struct StepParams {
   int32_t* out;             // extra copy of the token, may be null
   uint64_t* words;          // kWTotal tagged words
   uint32_t* seq;            // step sequence number (persists across launches)
-  uint32_t* abort_word;
+  uint32_t* last_started;   // sequence number of the launch whose last workgroup started
   uint32_t* status;
   uint16_t* on_out;         // the final rms_norm(h, output_norm) (f16[1024])
   uint64_t* stamps;         // timestamp build only (DEC_STEP_STAMPS): per-phase clock reads
   int max_seq;
   int advance;
   int head;                 // 0: no vocab / argmax (a prompt step); pos still advances
-  uint32_t spin_limit;      // poll rounds after which a wait gives up (2^20 by default)
+  uint32_t spin_limit;      // poll rounds after which a wait gives up (2^20 by default);
+                            // 0: workgroup 0 gives up at its start (the host forcing the
+                            // abort path, for tests)
 };
 
 __device__ __forceinline__ uint32_t step_tag(uint32_t seq, int layer, int phase) {
@@ -410,9 +412,12 @@ __device__ __forceinline__ uint64_t get_word(const uint64_t* p) {
 }
 
 // *p = v unless *p already holds v or a newer sequence number (compared
-// modulo 2^32).  A workgroup that started late may have read the sequence
-// word after an abort advanced it and so run with seq + 1; the words then end
-// at the newest number any workgroup of the aborted launch used.
+// modulo 2^32).  The workgroup that gives up moves the word to its own
+// number, so the next launch tags its words with a number no word of the
+// aborted launch carries.  (A workgroup that starts after the give-up reads
+// the status word after the sequence word, in the same cache line, and the
+// status bit is set before the sequence word moves: it sees the bit and
+// returns at its start, so no workgroup runs with a newer number.)
 __device__ __forceinline__ void advance_seq_word(uint32_t* p, uint32_t v) {
   uint32_t cur = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   while ((int32_t)(v - cur) > 0 &&
@@ -421,8 +426,17 @@ __device__ __forceinline__ void advance_seq_word(uint32_t* p, uint32_t v) {
   }
 }
 
+// A wait that cannot complete: status bit 1 (sticky until the host clears
+// it) makes every other waiter stop at its next check and every later launch
+// on this scratch return at its start; then the sequence word moves to this
+// workgroup's number.
+__device__ __forceinline__ void give_up(uint32_t* status, uint32_t* seq_word, uint32_t seq) {
+  __hip_atomic_fetch_or(status, 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  advance_seq_word(seq_word, seq);
+}
+
 struct Waiter {
-  uint32_t* abort_word;
+  const uint32_t* last_started;
   uint32_t* status;
   uint32_t* seq_word;  // the step sequence number in the scratch
   uint32_t seq;
@@ -464,19 +478,21 @@ struct Waiter {
         if (t + 256 * k < n && (uint32_t)(w[k] >> 32) != tag) pending = true;
       if (!pending) break;
       ++spins;
+      // another workgroup gave up (it already moved the sequence word past
+      // this launch's number)
       if ((spins & 31u) == 0u &&
-          (int32_t)(__hip_atomic_load(abort_word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) -
-                    seq) >= 0) {  // this step (or a newer one) was aborted
+          (__hip_atomic_load(status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & 2u) != 0) {
         ok = false;
         break;
       }
+      // ~1 ms into a wait and not every workgroup of the launch has started:
+      // the grid is not resident at once (a kernel on another stream holds
+      // CUs), so the started ones could wait forever for the others
+      if ((spins & 1023u) == 0u &&
+          __hip_atomic_load(last_started, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != seq)
+        spins = spin_limit + 1u;
       if (spins > spin_limit) {
-        // Give up: report, make every other waiter of this step give up, and
-        // mark this sequence number as used, so the next launch runs with a
-        // newer one that matches neither this step's tags nor its abort word.
-        __hip_atomic_fetch_or(status, 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        advance_seq_word(abort_word, seq);
-        advance_seq_word(seq_word, seq);
+        give_up(status, seq_word, seq);
         ok = false;
         break;
       }
@@ -496,7 +512,12 @@ struct Waiter {
       *s_abort = 1;
     }
     __syncthreads();
-    return *s_abort == 0;
+    if (*s_abort != 0) {
+      // the workgroup is about to end: its LDS copies in flight land first
+      wait_vm<0>();
+      return false;
+    }
+    return true;
   }
 
   // poll_begin + poll_finish.
@@ -661,14 +682,33 @@ void dec_step(StepParams P) {
   } while (0)
 #endif
 
+  // The sequence number, then the status word (same cache line): a step of
+  // this scratch gave up (status bit 1, until the host clears it) and this
+  // launch does nothing, so a step queued behind an aborted one neither
+  // advances the position nor writes a token.  A thread that reads a number a
+  // give-up has already advanced also sees the bit (set before the number
+  // moves), so a workgroup that runs has one number in every thread.
   const uint32_t seq = __hip_atomic_load(P.seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
+  const uint32_t status_in = __hip_atomic_load(P.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __syncthreads();  // s_abort is 0 in every thread's view
+  if ((status_in & 2u) != 0u) s_abort = 1;
+  if (P.spin_limit == 0u && wg == 0 && t == 0 && (status_in & 2u) == 0u) {
+    give_up(P.status, P.seq, seq);  // the host forces a give-up
+    s_abort = 1;
+  }
+  // Workgroups start in index order: the last one marks the launch as
+  // resident (a wait that finds another number after ~1 ms knows the grid
+  // is not resident at once).
+  if (wg == kStepWgs - 1 && t == 0)
+    __hip_atomic_store(P.last_started, seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   const int pos_raw = *P.pos;
   int tok = *P.token_in;
   tok = (tok < 0 || tok >= kVocab) ? 0 : tok;
   const uint16_t* emb = P.token_embd + (size_t)tok * kHidden;
-  const Waiter W{P.abort_word, P.status, P.seq, seq, P.spin_limit, &s_abort};
+  const Waiter W{P.last_started, P.status, P.seq, seq, P.spin_limit, &s_abort};
   const int pos_c = pos_raw < 0 ? 0 : (pos_raw >= P.max_seq ? P.max_seq - 1 : pos_raw);
   __syncthreads();
+  if (s_abort) return;
 
   if (wg < kBBase) {
     // ================= AD: q/k/v of every layer; gate/up on 0..191 =================
@@ -827,7 +867,10 @@ void dec_step(StepParams P) {
             put_word(d + 2 + 2 * lane, __builtin_bit_cast(uint32_t, a0), tp);
             put_word(d + 3 + 2 * lane, __builtin_bit_cast(uint32_t, a1), tp);
           });
-      if (!ok) return;
+      if (!ok) {
+        wait_vm<0>();  // attention_group's copies after the failed wait
+        return;
+      }
       STAMP(layer, 4);
       if (sg == 0) {
         // the 8 groups' partials of query heads 2g, 2g+1 (contiguous words)
@@ -974,11 +1017,11 @@ void dec_step(StepParams P) {
     }
     vocab_body_xp<VOCAB_NT_LOADS != 0, true, kVocabPre>(
         P.output_w,
-        [&](int li, u32x4 (&xr)[8]) {
+        [&](int li, u32x4 (&xr)[8]) -> bool {
           const uint2 w4 = norm_weights4(P.output_norm);  // requested before the wait
           ok = W.wait(hfin, 512, tag_h, vec);
           STAMP(kLayers, 1);
-          if (!ok) return;
+          if (!ok) return false;  // no row is computed or stored
           uint2* v2 = reinterpret_cast<uint2*>(vec);
           const uint2 x = rmsnorm_wg(v2[t], w4, s_red);
           v2[t] = x;
@@ -988,6 +1031,7 @@ void dec_step(StepParams P) {
 #pragma unroll
           for (int m = 0; m < 8; ++m)
             xr[m] = *reinterpret_cast<const u32x4*>(xs + 128 * m + 8 * li);
+          return true;
         },
         P.logits, kVocab, [&](uint64_t key) {
           put_word(P.words + kWArg + 2 * wg, (uint32_t)(key >> 32), tag_arg);

@@ -482,6 +482,18 @@ __device__ __forceinline__ float f16_row_dot(const u32x4& w, const u32x4& xv, fl
   return acc;
 }
 
+// xload(li, xr) of vocab_body_xp; one that returns false (its input never
+// arrived) makes the function return without computing or storing a row.
+template <class XLoad>
+__device__ __forceinline__ bool vocab_xload(XLoad& xload, int li, u32x4 (&xr)[8]) {
+  if constexpr (__is_same(decltype(xload(li, xr)), bool)) {
+    return xload(li, xr);
+  } else {
+    xload(li, xr);
+    return true;
+  }
+}
+
 // f16 GEMV rows [0, n_rows) x K=1024 with a fused argmax.
 //
 // Rows are taken in batches of 4.  Within a wave, DPP row g (lanes 16g..16g+15)
@@ -598,7 +610,10 @@ __device__ __forceinline__ void vocab_body_xp(const uint16_t* __restrict__ W, XL
                                          16, 0, 0);
     }
     __builtin_amdgcn_sched_barrier(0);
-    xload(li, xr);
+    if (!vocab_xload(xload, li, xr)) {
+      wait_vm<0>();  // the staged rows land before the workgroup ends
+      return;
+    }
     // A holds batch i, B batch i + 1 (loads in flight) at the top of each round
     int i = 0;
     for (; i + 3 < nr; i += 2) {
@@ -628,7 +643,10 @@ __device__ __forceinline__ void vocab_body_xp(const uint16_t* __restrict__ W, XL
   } else {
     load_batch(b_begin, A);
     __builtin_amdgcn_sched_barrier(0);
-    xload(li, xr);
+    if (!vocab_xload(xload, li, xr)) {
+      wait_vm<0>();
+      return;
+    }
     if (nb > 0) {
       int i = 0;
       for (; i + 2 < nb; i += 2) {

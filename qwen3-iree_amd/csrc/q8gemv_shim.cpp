@@ -12,6 +12,7 @@
 #include <hip/hip_runtime_api.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -100,7 +101,10 @@ struct State {
   hipFunction_t vocab_finalize = nullptr;
   hipFunction_t ws_reset = nullptr;
   hipFunction_t copy = nullptr;
-  int batch_wgs = 0;      // 0 = default
+  // Tuning knobs: process-wide, set under mu, read without it (atomics), so a
+  // setter never races a launch on another thread; each call reads a knob
+  // once.
+  std::atomic<int> batch_wgs{0};  // 0 = default
   hipModule_t dec_module = nullptr;  // decode_gfx950.hsaco (optional)
   hipFunction_t dec_embed = nullptr, dec_qkv = nullptr, dec_attn = nullptr,
                 dec_o = nullptr, dec_gu = nullptr, dec_dn = nullptr, dec_vocab = nullptr,
@@ -119,14 +123,27 @@ struct State {
                 pf_f16_res_22 = nullptr, pf_f16_res_22k = nullptr, pf_f16_res_12k = nullptr,
                 pf_f16_part_22 = nullptr, pf_f16_part_22k = nullptr, pf_f16_part_12k = nullptr,
                 pf_f16_part_44 = nullptr, pf_f16_part_44k = nullptr, pf_expand = nullptr;
-  int pf_tile_rows = 0;   // prefill GEMM token tile: 0 = by shape, 32, 64 or 128
-  int pf_attn_split = 0;  // prefill attention positions per split in blocks of 32: 0 = by shape
-  int step_single = -1;   // single-launch decode step: -1 unknown, 0 off, 1 on
+  std::atomic<int> pf_tile_rows{0};   // prefill GEMM token tile: 0 = by shape, 32, 64 or 128
+  std::atomic<int> pf_attn_split{0};  // prefill attention positions per split in blocks of 32
+  std::atomic<int> step_single{-1};   // single-launch decode step: -1 unknown, 0 off, 1 on
   bool step_capable = false;
-  uint32_t step_spin_limit = kDefaultSpinLimit;  // poll rounds before a dec_step wait gives up
+  // poll rounds before a dec_step wait gives up
+  std::atomic<uint32_t> step_spin_limit{kDefaultSpinLimit};
+  // Single-launch steps of different streams run one after another: each
+  // needs all its workgroups resident at once, and two at a time do not fit.
+  // step_ev is recorded after every such launch (outside graph capture) and a
+  // launch on another stream first waits for it.
+  std::mutex step_mu;
+  hipEvent_t step_ev = nullptr;
+  hipStream_t step_last = nullptr;
+  // steps re-run with the per-phase launches after a single launch gave up
+  std::atomic<uint64_t> step_fallbacks{0};
+  // test hook: the single launch this many launches from now is forced to
+  // give up at its start (-1: none)
+  std::atomic<int64_t> force_abort_in{-1};
   int noalloc_rc = Q8_ERR_NOT_INITIALIZED;  // set-up status of the allocation-free entry point
   std::string noalloc_err;
-  int vocab_wgs = 0;      // 0 = default
+  std::atomic<int> vocab_wgs{0};  // 0 = default
 };
 
 State g;
@@ -221,7 +238,8 @@ int validate_gemv(const void* w_layer, int64_t n_rows, int64_t k, const void* x_
 }
 
 int vocab_grid() {
-  if (g.vocab_wgs > 0) return g.vocab_wgs;
+  const int set = g.vocab_wgs.load(std::memory_order_relaxed);
+  if (set > 0) return set;
   int wgs = 4 * cu_count();
   return wgs > kVocabMaxWorkgroups ? kVocabMaxWorkgroups : wgs;
 }
@@ -389,11 +407,12 @@ int q8gemv_init(const char* code_object_path) {
   }
   // The single launch is the default where it can run: no kernel boundaries,
   // and every workgroup requests its next weights before it waits.
-  if (g.step_single < 0) g.step_single = g.step_capable ? 1 : 0;
+  if (g.step_single.load() < 0) g.step_single = g.step_capable ? 1 : 0;
   g.module = mod;
   g.device = dev;
   g.compute_units = cus;
-  g.batch_wgs = g.vocab_wgs = 0;
+  g.batch_wgs = 0;
+  g.vocab_wgs = 0;
   g.ready = true;
   // the allocation-free entry point's scratch on this device (address and a
   // zero fill; an error here leaves that one entry point unavailable)
@@ -414,6 +433,12 @@ void q8gemv_shutdown(void) {
   g.dec_embed = g.dec_qkv = g.dec_attn = g.dec_o = g.dec_gu = g.dec_dn =
       g.dec_vocab = g.dec_final = g.dec_adv = g.dec_clear = g.dec_step = nullptr;
   g.step_capable = false;
+  {
+    std::lock_guard<std::mutex> step_lock(g.step_mu);
+    if (g.step_ev) (void)hipEventDestroy(g.step_ev);
+    g.step_ev = nullptr;
+    g.step_last = nullptr;
+  }
   if (g.pf_module) (void)hipModuleUnload(g.pf_module);
   g.pf_module = nullptr;
   g.pf_embed = g.pf_norm = g.pf_gemm = g.pf_gemm_res = g.pf_gemm_m32 = g.pf_gemm_res_m32 =
@@ -625,7 +650,8 @@ int q8gemv_batch(const void* device_table, int count, int32_t total_units, void*
   int rc = check_ready();
   if (rc) return rc;
   // default: 12 waves per CU
-  const int64_t cap = g.batch_wgs > 0 ? g.batch_wgs : 12LL * 64 / g.batch_threads * cu_count();
+  const int set_wgs = g.batch_wgs.load(std::memory_order_relaxed);
+  const int64_t cap = set_wgs > 0 ? set_wgs : 12LL * 64 / g.batch_threads * cu_count();
   const int64_t grid = total_units < cap ? total_units : cap;
   const void* t_arg = device_table;
   int c_arg = count;
@@ -720,6 +746,7 @@ int decode_dispatch_24_matmul_151936x1x1024_f16(const void* w_f16, const void* x
 int q8gemv_batch_set_workgroups(int workgroups) {
   if (workgroups < 0 || workgroups > kQ8MaxWorkgroups)
     return fail(Q8_ERR_BAD_ARGUMENT, "workgroups %d outside [0, %d]", workgroups, kQ8MaxWorkgroups);
+  std::lock_guard<std::mutex> lock(g.mu);
   g.batch_wgs = workgroups;
   return Q8_OK;
 }
@@ -728,6 +755,7 @@ int vocab_set_workgroups(int workgroups) {
   if (workgroups < 0 || workgroups > kVocabMaxWorkgroups)
     return fail(Q8_ERR_BAD_ARGUMENT, "workgroups %d outside [0, %d]", workgroups,
                 kVocabMaxWorkgroups);
+  std::lock_guard<std::mutex> lock(g.mu);
   g.vocab_wgs = workgroups;
   return Q8_OK;
 }
@@ -933,7 +961,7 @@ constexpr size_t kScrFn = kScrQr + 4096;     // f16[1024] rms_norm(res, ffn_norm
 constexpr size_t kScrOn = kScrFn + 2048;     // f16[1024] rms_norm(h, output_norm)
 constexpr size_t kScrPart = kScrOn + 2048;   // f32[16][8][132] attention partials
 constexpr size_t kScrSeq = 16;       // u32 step sequence number (single-launch step)
-constexpr size_t kScrAbort = 20;     // u32 abort word (single-launch step)
+constexpr size_t kScrStarted = 128;  // u32 the last launch whose grid was resident
 // tagged words of the single-launch step (u64; map in decode_kernels.hip)
 // the single-launch step's tagged words per layer parity: h, attention output,
 // attn_o + residual output and SwiGLU output in 4 replicas each, q/k/v and
@@ -972,7 +1000,7 @@ struct StepParams {
   int32_t* out;
   void* words;
   void* seq;
-  void* abort_word;
+  void* last_started;
   void* status;
   void* on_out;
   void* stamps;
@@ -982,7 +1010,9 @@ struct StepParams {
   uint32_t spin_limit;
 };
 
-// One single-launch decode step (dec_step).
+// One single-launch decode step (dec_step), ordered after the last one
+// launched on any other stream (see State::step_ev; not under graph capture,
+// where the caller orders its graphs).
 int launch_step(const qwen3_weights* w, void* k_cache, void* v_cache, int64_t max_seq,
                 const int32_t* token_in, int32_t* token_out, int32_t* pos, void* logits,
                 int32_t* out, int advance, int head, void* scratch, hipStream_t st) {
@@ -1009,22 +1039,45 @@ int launch_step(const qwen3_weights* w, void* k_cache, void* v_cache, int64_t ma
   p.out = out;
   p.words = mb(scratch) + kScrWords;
   p.seq = mb(scratch) + kScrSeq;
-  p.abort_word = mb(scratch) + kScrAbort;
+  p.last_started = mb(scratch) + kScrStarted;
   p.status = mb(scratch) + kScrStatus;
   p.on_out = mb(scratch) + kScrOn;
   p.stamps = mb(scratch) + kScrPart;  // unused by this step unless built with timestamps
   p.max_seq = (int32_t)max_seq;
   p.advance = advance ? 1 : 0;
   p.head = head ? 1 : 0;
-  p.spin_limit = g.step_spin_limit;
+  p.spin_limit = g.step_spin_limit.load(std::memory_order_relaxed);
+  if (g.force_abort_in.load(std::memory_order_relaxed) >= 0 && g.force_abort_in.fetch_sub(1) == 0)
+    p.spin_limit = 0;  // the test hook: workgroup 0 gives up at its start
   void* args[] = {&p};
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  HIP_TRY(hipStreamIsCapturing(st, &cs));
+  if (cs != hipStreamCaptureStatusNone) {
+    hipError_t e = hipModuleLaunchKernel(g.dec_step, kStepWorkgroups, 1, 1, 256, 1, 1, 0, st,
+                                         args, nullptr);
+    if (e != hipSuccess) return hip_fail(e, "launch of dec_step");
+    return Q8_OK;
+  }
+  std::lock_guard<std::mutex> lock(g.step_mu);
+  // The event only orders launches on this device, so it records without a
+  // system-scope fence (the default fence, an L2 writeback, measured 3 us
+  // per step; without it 1 us).
+  if (g.step_ev == nullptr)
+    HIP_TRY(hipEventCreateWithFlags(&g.step_ev, hipEventDisableTiming | hipEventDisableSystemFence));
+  else if (g.step_last != st)
+    HIP_TRY(hipStreamWaitEvent(st, g.step_ev, 0));
   hipError_t e = hipModuleLaunchKernel(g.dec_step, kStepWorkgroups, 1, 1, 256, 1, 1, 0, st, args,
                                        nullptr);
   if (e != hipSuccess) return hip_fail(e, "launch of dec_step");
+  HIP_TRY(hipEventRecord(g.step_ev, st));
+  g.step_last = st;
   return Q8_OK;
 }
 
-bool use_single() { return g.step_single == 1 && g.step_capable && g.dec_step != nullptr; }
+bool use_single() {
+  return g.step_single.load(std::memory_order_relaxed) == 1 && g.step_capable &&
+         g.dec_step != nullptr;
+}
 
 // Status bit 1 of a scratch: a single-launch step gave up waiting for a
 // hand-off (its outputs are not valid).  Reads the word on `st` (which the
@@ -1038,6 +1091,29 @@ int check_not_aborted(void* scratch, hipStream_t st, const char* when) {
     return fail(Q8_ERR_STEP_ABORTED,
                 "%s: a single-launch decode step gave up waiting for a hand-off (status bit 1); "
                 "its outputs are invalid; qwen3_scratch_reset clears the scratch", when);
+  return Q8_OK;
+}
+
+// The status word of a scratch, read on `st` after everything before it.
+int read_status(const void* scratch, hipStream_t st, uint32_t* status) {
+  *status = 0;
+  HIP_TRY(hipMemcpyAsync(status, cb(scratch) + kScrStatus, sizeof(*status), hipMemcpyDeviceToHost,
+                         st));
+  HIP_TRY(hipStreamSynchronize(st));
+  return Q8_OK;
+}
+
+// After a single-launch step gave up (status bit 1: its outputs are invalid,
+// it wrote neither token nor position, and every single launch queued behind
+// it on this scratch returned at its start): bit 1 cleared and bit 2 (a step
+// was re-run per phase) set on `st`, which is then synchronized, so the
+// caller can re-run the steps that did nothing with the per-phase launches
+// (the same bits).  Counts the fallback.
+int recover_from_abort(void* scratch, hipStream_t st, uint32_t status) {
+  const uint32_t v = (status & ~2u) | 4u;
+  HIP_TRY(hipMemcpyAsync(mb(scratch) + kScrStatus, &v, sizeof(v), hipMemcpyHostToDevice, st));
+  HIP_TRY(hipStreamSynchronize(st));
+  g.step_fallbacks.fetch_add(1);
   return Q8_OK;
 }
 
@@ -1239,7 +1315,8 @@ int32_t pf_attn_split_blocks(int32_t n, int32_t p0, int chunk_local) {
   const PfSplitGeometry G = pf_split_geometry(n, p0, chunk_local ? p0 : 0);
   const int64_t cap = pf_attn_pair_cap(n);
   const int32_t nb_max = std::max(G.nb_last, G.c + G.nqb - 2);
-  const int32_t s0 = g.pf_attn_split > 0 ? g.pf_attn_split : kPfAttnSplitDefault;
+  const int32_t set_split = g.pf_attn_split.load(std::memory_order_relaxed);
+  const int32_t s0 = set_split > 0 ? set_split : kPfAttnSplitDefault;
   int32_t lo_s = std::min(s0, nb_max), hi_s = nb_max;
   // smallest S >= lo_s whose pairs fit (at S = nb_max there are nqb pairs)
   while (lo_s < hi_s) {
@@ -1287,9 +1364,10 @@ int launch_gemm(hipFunction_t fn, hipFunction_t fn_m32, const void* x, int ldx, 
     return fail(Q8_ERR_BAD_SHAPE, "prefill GEMM shape N=%d K=%d", n_out, K);
   int rows = 64;
   if (fn_m32) {
-    if (g.pf_tile_rows == 32)
+    const int set_rows = g.pf_tile_rows.load(std::memory_order_relaxed);
+    if (set_rows == 32)
       rows = 32;
-    else if (g.pf_tile_rows == 0 && ((int64_t)M + 63) / 64 * a.n_tiles < 2LL * g.compute_units)
+    else if (set_rows == 0 && ((int64_t)M + 63) / 64 * a.n_tiles < 2LL * g.compute_units)
       rows = 32;
   }
   if (rows == 32) fn = fn_m32;
@@ -1349,9 +1427,10 @@ int launch_gemm_f16(std::initializer_list<F16Tile> tiles, const void* x, int ldx
     return ((int64_t)M + t.bm - 1) / t.bm * (n_w / t.bn) * splits;
   };
   const F16Tile* pick = nullptr;
-  if (g.pf_tile_rows > 0) {
+  const int set_rows = g.pf_tile_rows.load(std::memory_order_relaxed);
+  if (set_rows > 0) {
     for (const F16Tile& t : tiles)
-      if (t.bm >= g.pf_tile_rows && (!pick || t.bm < pick->bm)) pick = &t;
+      if (t.bm >= set_rows && (!pick || t.bm < pick->bm)) pick = &t;
   } else {
     for (const F16Tile& t : tiles)
       if (!pick && grid_of(t) >= (int64_t)t.per_cu * g.compute_units) pick = &t;
@@ -1607,12 +1686,27 @@ int qwen3_set_step_mode(int mode) {
   if (mode == 1 && !g.step_capable)
     return fail(Q8_ERR_BAD_ARGUMENT, "this device cannot run the single-launch step "
                 "(needs its 448 workgroups resident at once, two per CU)");
+  std::lock_guard<std::mutex> lock(g.mu);
   g.step_single = mode;
   return Q8_OK;
 }
 
 int qwen3_set_step_spin_limit(uint32_t polls) {
+  std::lock_guard<std::mutex> lock(g.mu);
   g.step_spin_limit = polls == 0 ? kDefaultSpinLimit : polls;
+  return Q8_OK;
+}
+
+int qwen3_step_fallback_count(uint64_t* count) {
+  if (!count) return fail(Q8_ERR_NULL_POINTER, "null count");
+  *count = g.step_fallbacks.load();
+  return Q8_OK;
+}
+
+int qwen3_debug_force_step_abort(int64_t after) {
+  if (after < -1) return fail(Q8_ERR_BAD_ARGUMENT, "after %lld < -1", (long long)after);
+  std::lock_guard<std::mutex> lock(g.mu);
+  g.force_abort_in = after;
   return Q8_OK;
 }
 
@@ -1648,6 +1742,7 @@ int qwen3_set_prefill_tiling(int gemm_rows, int attn_split_blocks) {
     return fail(Q8_ERR_BAD_ARGUMENT, "attention split of %d blocks", attn_split_blocks);
   int rc = check_prefill_ready();
   if (rc) return rc;
+  std::lock_guard<std::mutex> lock(g.mu);
   g.pf_tile_rows = gemm_rows;
   g.pf_attn_split = attn_split_blocks;
   return Q8_OK;
@@ -1710,6 +1805,32 @@ int qwen3_decode_step(const qwen3_weights* w, void* k_cache, void* v_cache, int6
   return launch_head(w, h, logits, token, pos, advance, max_seq, scratch, st);
 }
 
+int qwen3_decode_step_checked(const qwen3_weights* w, void* k_cache, void* v_cache,
+                              int64_t max_seq, int32_t* token, int32_t* pos, void* logits,
+                              int advance, void* scratch, void* stream) {
+  int rc = validate_step_args(w, k_cache, v_cache, max_seq, token, pos, scratch);
+  if (rc) return rc;
+  if (logits && !aligned(logits, 2)) return fail(Q8_ERR_MISALIGNED, "logits 2-byte alignment");
+  if ((rc = check_decode_ready())) return rc;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if ((rc = check_not_aborted(scratch, st, "before qwen3_decode_step_checked"))) return rc;
+  if (use_single()) {
+    if ((rc = launch_step(w, k_cache, v_cache, max_seq, token, token, pos, logits, nullptr,
+                          advance, 1, scratch, st)))
+      return rc;
+    uint32_t status = 0;
+    if ((rc = read_status(scratch, st, &status))) return rc;
+    if ((status & 2u) == 0) return Q8_OK;
+    // the launch gave up (token and position untouched): the same step per phase
+    if ((rc = recover_from_abort(scratch, st, status))) return rc;
+  }
+  void* h = nullptr;
+  if ((rc = launch_body(w, k_cache, v_cache, max_seq, token, pos, scratch, st, &h))) return rc;
+  if ((rc = launch_head(w, h, logits, token, pos, advance, max_seq, scratch, st))) return rc;
+  HIP_TRY(hipStreamSynchronize(st));
+  return Q8_OK;
+}
+
 int qwen3_prefill(const qwen3_weights* w, void* k_cache, void* v_cache, int64_t max_seq,
                   const int32_t* prompt, int32_t n_prompt, int32_t* token, int32_t* pos,
                   void* scratch, void* stream) {
@@ -1723,16 +1844,34 @@ int qwen3_prefill(const qwen3_weights* w, void* k_cache, void* v_cache, int64_t 
   hipStream_t st = static_cast<hipStream_t>(stream);
   void* status = mb(scratch) + kScrStatus;
   int ms = (int)max_seq;
+  int32_t i0 = 0;  // the first prompt token the per-phase launches take
   if (use_single()) {
+    // the position before and after, so a step that gave up can be resumed
+    int32_t p0 = 0, p1 = 0;
+    HIP_TRY(hipMemcpyAsync(&p0, pos, sizeof(p0), hipMemcpyDeviceToHost, st));
+    if ((rc = check_not_aborted(scratch, st, "before qwen3_prefill"))) return rc;
     for (int32_t i = 0; i < n_prompt; ++i) {
       const bool last = i + 1 == n_prompt;
       if ((rc = launch_step(w, k_cache, v_cache, max_seq, prompt + i, token, pos, nullptr, nullptr,
                             1, last ? 1 : 0, scratch, st)))
         return rc;
     }
-    return Q8_OK;
+    HIP_TRY(hipMemcpyAsync(&p1, pos, sizeof(p1), hipMemcpyDeviceToHost, st));
+    uint32_t sw = 0;
+    if ((rc = read_status(scratch, st, &sw))) return rc;
+    if ((sw & 2u) == 0) return Q8_OK;
+    // Each completed step moved the position by one; the step that gave up
+    // and those behind it did nothing.  With the cache full (bit 0) the
+    // position no longer counts the steps, and nothing is re-run.
+    if ((sw & 1u) != 0 || p1 < p0 || p1 - p0 >= n_prompt)
+      return fail(Q8_ERR_STEP_ABORTED,
+                  "qwen3_prefill: a single-launch step gave up waiting for a hand-off (status bit "
+                  "1) and the position cannot tell which steps completed; qwen3_scratch_reset "
+                  "clears the scratch");
+    if ((rc = recover_from_abort(scratch, st, sw))) return rc;
+    i0 = p1 - p0;
   }
-  for (int32_t i = 0; i < n_prompt; ++i) {
+  for (int32_t i = i0; i < n_prompt; ++i) {
     void* h = nullptr;
     if ((rc = launch_body(w, k_cache, v_cache, max_seq, prompt + i, pos, scratch, st, &h)))
       return rc;
@@ -1802,10 +1941,14 @@ int qwen3_generate(const qwen3_weights* w, void* k_cache, void* v_cache, int64_t
                         hipHostMallocDefault));
   for (hipEvent_t& e : res.ev) HIP_TRY(hipEventCreateWithFlags(&e, hipEventDisableTiming));
   uint32_t* status = reinterpret_cast<uint32_t*>(mb(scratch) + kScrStatus);
-  auto launch_batch = [&](int32_t first, int32_t count, int slot) -> int {
-    for (int32_t b = 0; b < count; ++b) {
+  // the step mode, once for the call; per-phase for the rest of it after a
+  // single launch gave up
+  bool single = use_single();
+  // steps first + from .. first + count - 1 of a batch (from = 0: all)
+  auto launch_batch = [&](int32_t first, int32_t count, int slot, int32_t from) -> int {
+    for (int32_t b = from; b < count; ++b) {
       int brc;
-      if (use_single()) {
+      if (single) {
         if ((brc = launch_step(w, k_cache, v_cache, max_seq, token, token, pos, nullptr,
                                out_tokens + first + b, 1, 1, scratch, st)))
           return brc;
@@ -1827,14 +1970,28 @@ int qwen3_generate(const qwen3_weights* w, void* k_cache, void* v_cache, int64_t
   int32_t first = 0;
   int32_t count = max_new < kGenerateBatch ? max_new : kGenerateBatch;
   int slot = 0;
-  if (count > 0 && (rc = launch_batch(first, count, slot))) return rc;
+  if (count > 0 && (rc = launch_batch(first, count, slot, 0))) return rc;
   while (count > 0) {
     const int32_t next = first + count;
     const int32_t next_count = max_new - next < kGenerateBatch ? max_new - next : kGenerateBatch;
-    if (next_count > 0 && (rc = launch_batch(next, next_count, 1 - slot))) return rc;
+    if (next_count > 0 && (rc = launch_batch(next, next_count, 1 - slot, 0))) return rc;
     HIP_TRY(hipEventSynchronize(res.ev[slot]));
     const GenReadback r = res.rb[slot];
-    const bool aborted = (r.status & 2u) != 0;
+    bool aborted = (r.status & 2u) != 0;
+    if (aborted && single) {
+      // A single launch of this batch gave up: it and every single launch
+      // behind it (the rest of the batch, the queued batch) returned at their
+      // start, so the position counts the steps that completed.  Re-run this
+      // batch from there per phase (the same bits) and check it again.
+      if (next_count > 0) HIP_TRY(hipEventSynchronize(res.ev[1 - slot]));
+      const int32_t done = r.pos - p0;
+      if (done >= first && done < next) {
+        if ((rc = recover_from_abort(scratch, st, r.status))) return rc;
+        single = false;
+        if ((rc = launch_batch(first, count, slot, done - first))) return rc;
+        continue;  // the next batch is queued again at the top
+      }
+    }
     // the batch's steps must all have completed; otherwise its tokens are not
     // valid and n_generated stays at the previous batch
     if (!aborted) *n_generated = next;

@@ -182,6 +182,20 @@ def set_step_spin_limit(polls: int = 0) -> None:
     Q._call("qwen3_set_step_spin_limit", int(polls))
 
 
+def step_fallback_count() -> int:
+    """Steps (process-wide) that a single launch gave up on and that were re-run
+    with the per-phase launches."""
+    n = ctypes.c_uint64(0)
+    Q._call("qwen3_step_fallback_count", ctypes.byref(n))
+    return int(n.value)
+
+
+def force_step_abort(after: int = 0) -> None:
+    """Test hook: the single-launch step `after` launches from now gives up at
+    its start (-1 cancels)."""
+    Q._call("qwen3_debug_force_step_abort", int(after))
+
+
 def set_prefill_tiling(gemm_rows: int = 0, attn_split_blocks: int = 0) -> None:
     """Work division of the batched prompt path (0 = by shape): token rows per
     GEMM workgroup (32 or 64) and cache positions per attention split in
@@ -262,6 +276,15 @@ class DecodeSession:
     def step(self, advance: bool = True, logits: bool = True) -> None:
         Q._call("qwen3_decode_step", self.model.ref(), self.k_cache.ptr, self.v_cache.ptr,
                 self.max_seq, self.token_ptr, self.pos_ptr,
+                self.logits.ptr if logits else None, int(bool(advance)), self.scratch.ptr,
+                Q._stream(self.stream))
+
+    def step_checked(self, advance: bool = True, logits: bool = True) -> None:
+        """One step, synchronized and checked: a single launch that gave up is
+        re-run with the per-phase launches (status bit 2), so the outputs are
+        valid on return."""
+        Q._call("qwen3_decode_step_checked", self.model.ref(), self.k_cache.ptr,
+                self.v_cache.ptr, self.max_seq, self.token_ptr, self.pos_ptr,
                 self.logits.ptr if logits else None, int(bool(advance)), self.scratch.ptr,
                 Q._stream(self.stream))
 

@@ -159,6 +159,9 @@ _SIGNATURES = {
     "qwen3_scratch_status_offset": [],
     "qwen3_scratch_offset": [ctypes.c_char_p],
     "qwen3_decode_step": [_P, _P, _P, _I64, _P, _P, _P, _I, _P, _P],
+    "qwen3_decode_step_checked": [_P, _P, _P, _I64, _P, _P, _P, _I, _P, _P],
+    "qwen3_step_fallback_count": [_P],
+    "qwen3_debug_force_step_abort": [_I64],
     "qwen3_decode_embed": [_P, _P, _P, _P],
     "qwen3_decode_layer": [_P, _I, _P, _P, _I64, _P, _P, _P, _P, _P],
     "qwen3_decode_head": [_P, _P, _P, _P, _P, _I, _I64, _P, _P],

@@ -58,6 +58,9 @@ def main() -> int:
                                  formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--context", type=int, default=1024)
     ap.add_argument("--steps", type=int, default=20, help="stamped steps (the last one is read)")
+    ap.add_argument("--prebuilt", type=Path, default=None,
+                    help="directory holding an already built timestamp build of the three code "
+                         "objects (instead of building one)")
     args = ap.parse_args()
 
     sys.path.insert(0, str(REPO))
@@ -67,9 +70,12 @@ def main() -> int:
     from qwen3_iree_amd import decode as D
     from qwen3_iree_amd import q8gemv as Q
 
-    with tempfile.TemporaryDirectory() as td:
-        co = build_stamped(Path(td))
-        Q.init(co)
+    if args.prebuilt is not None:
+        Q.init(str(args.prebuilt / "q8gemv_gfx950.hsaco"))
+    else:
+        with tempfile.TemporaryDirectory() as td:
+            co = build_stamped(Path(td))
+            Q.init(co)
     D.set_step_mode(1)
     ctx = args.context
     model = D.DeviceWeights(D.synthetic_weights(seed=20261201, workers=16))

@@ -153,6 +153,51 @@ def test_workspace_size_and_tuning_roundtrip(Q):
     Q.set_vocab_workgroups(0)
 
 
+def test_tuning_knobs_from_two_threads_while_calls_validate(Q):
+    """Setters of the process-wide knobs on one thread while another thread
+    makes calls that are validated and rejected before any device work (the
+    calls release the GIL, so the two really overlap): every call returns its
+    status, and the knobs end with a value one of the setters wrote."""
+    import threading
+
+    L = Q.load_library()
+    errors = []
+    stop = threading.Event()
+
+    def setters():
+        try:
+            for i in range(4000):
+                assert L.q8gemv_batch_set_workgroups(64 * (i % 4)) == 0
+                assert L.vocab_set_workgroups(256 * (1 + i % 3)) == 0
+                assert L.qwen3_set_step_spin_limit(i % 5) == 0
+        except AssertionError as e:  # pragma: no cover - reported below
+            errors.append(e)
+        finally:
+            stop.set()
+
+    def callers():
+        n = 0
+        while not stop.is_set() or n < 1000:
+            if L.q8gemv(7, A16, 0, A16, A16, None) != 2:
+                errors.append("q8gemv kind 7")
+            if L.vocab_gemv_argmax(A16 + 2, A16, None, A16, A16, None) != 5:
+                errors.append("vocab misaligned")
+            if L.qwen3_step_fallback_count(None) != 3:
+                errors.append("fallback count null")
+            n += 1
+
+    threads = [threading.Thread(target=setters), threading.Thread(target=callers)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join(timeout=120)
+    assert not errors, errors[:3]
+    assert Q.get_vocab_workgroups() == 256 * (1 + 3999 % 3)  # the last value set
+    Q.set_batch_workgroups(0)
+    Q.set_vocab_workgroups(0)
+    assert L.qwen3_set_step_spin_limit(0) == 0
+
+
 def test_code_object_targets_gfx950_and_has_every_kernel():
     co = REPO / "qwen3-iree_amd" / "lib" / "q8gemv_gfx950.hsaco"
     data = co.read_bytes()
@@ -324,6 +369,12 @@ def test_prefill_workspace_layout(Q):
     (lambda L, w: L.qwen3_decode_step(w, A16, A16, 8, A16 + 2, A16, None, 1, A16, None), 5),
     (lambda L, w: L.qwen3_decode_head(w, A16, A16 + 1, A16, A16, 1, 8, A16, None), 5),
     (lambda L, w: L.qwen3_decode_embed(w, None, A16, None), 3),
+    (lambda L, w: L.qwen3_decode_step_checked(w, A16, A16, 8, None, A16, None, 1, A16, None), 3),
+    (lambda L, w: L.qwen3_decode_step_checked(w, A16, A16, 0, A16, A16, None, 1, A16, None), 6),
+    (lambda L, w: L.qwen3_decode_step_checked(w, A16, A16, 8, A16, A16, A16 + 1, 1, A16, None),
+     5),
+    (lambda L, w: L.qwen3_step_fallback_count(None), 3),
+    (lambda L, w: L.qwen3_debug_force_step_abort(-2), 9),
     (lambda L, w: L.qwen3_scratch_reset(A16 + 16, None), 5),
     # prompt ingestion and the generation loop
     (lambda L, w: L.qwen3_prefill(w, A16, A16, 8, None, 3, A16, A16, A16, None), 3),

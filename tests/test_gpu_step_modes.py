@@ -104,10 +104,11 @@ def test_single_launch_repeated_steps_keep_sequence(D, dmodel, single):
 def test_single_launch_abort_is_reported_and_recoverable(gpu, D, dmodel, single):
     """A poll limit of one round makes the step's bounded waits give up (the
     host forces the condition; every workgroup still exits normally): status
-    bit 1 is set, the position is not advanced, qwen3_check_status and
-    qwen3_generate report Q8_ERR_STEP_ABORTED, the next step on the same
-    scratch runs normally with a fresh sequence number (the bits of a fresh
-    session's step), and a scratch reset clears the status."""
+    bit 1 is set and the position is not advanced; qwen3_check_status,
+    qwen3_decode_step_checked and qwen3_generate report Q8_ERR_STEP_ABORTED;
+    a step launched on the scratch while bit 1 is set does nothing (token and
+    position stay); a scratch reset clears the status and the step then gives
+    the bits of a fresh session's step."""
     Q = gpu
     ref = D.DecodeSession(dmodel, 64)
     ref.set_state(77, 5)
@@ -125,49 +126,69 @@ def test_single_launch_abort_is_reported_and_recoverable(gpu, D, dmodel, single)
     finally:
         D.set_step_spin_limit(0)
     assert s.status() & 2
-    assert s.get_state()[1] == 5
+    assert s.get_state() == (77, 5)
     with pytest.raises(Q.Q8GemvError) as e:
         s.check_status()
+    assert e.value.code == Q.Q8_ERR_STEP_ABORTED
+    with pytest.raises(Q.Q8GemvError) as e:
+        s.step_checked()
     assert e.value.code == Q.Q8_ERR_STEP_ABORTED
     with pytest.raises(Q.Q8GemvError) as e:
         s.generate(4, eos_id=-1)
     assert e.value.code == Q.Q8_ERR_STEP_ABORTED
 
-    s.set_state(77, 5)
-    print("step after the aborted one", flush=True)
-    s.step(advance=False, logits=True)
-    assert s.get_state() == want_state
-    assert np.array_equal(s.read_logits().view(np.uint16), want_logits.view(np.uint16))
+    print("steps behind the aborted one", flush=True)
+    for _ in range(3):
+        s.step(advance=True, logits=True)
+    s.synchronize()
+    assert s.get_state() == (77, 5)
     assert s.status() & 2  # sticky until the scratch is reset
 
     s.reset_scratch()
     assert s.check_status() == 0
+    s.step(advance=False, logits=True)
+    assert s.get_state() == want_state
+    assert np.array_equal(s.read_logits().view(np.uint16), want_logits.view(np.uint16))
     toks = s.generate(4, eos_id=-1)
     assert len(toks) == 4 and s.get_state()[1] == 9 and s.check_status() == 0
     s.free()
 
 
-def test_generate_abort_undoes_the_queued_batch(gpu, D, dmodel, single):
-    """A step that gives up inside qwen3_generate (one-round poll limit, set
-    from the host; every workgroup still exits normally): the call reports
-    Q8_ERR_STEP_ABORTED with no tokens counted, and the batch queued behind
-    the failing one is undone -- token and position are those the failing
-    batch left (its aborted steps advance nothing), status bit 1 is set."""
-    Q = gpu
+def per_phase_generate(D, dmodel, token, pos, n, max_seq=64):
+    before = D.step_mode()
+    D.set_step_mode(0)
+    try:
+        s = D.DecodeSession(dmodel, max_seq)
+        s.set_state(token, pos)
+        toks = s.generate(n, eos_id=-1)
+        out = (toks.tolist(), s.get_state(), s.status())
+        s.free()
+    finally:
+        D.set_step_mode(before)
+    return out
+
+
+def test_generate_falls_back_when_every_launch_gives_up(gpu, D, dmodel, single):
+    """A one-round poll limit (set from the host; every workgroup still exits
+    normally) makes the first single launch give up: qwen3_generate re-runs
+    the batch from that step with the per-phase launches and finishes the
+    loop in that mode, returning the per-phase loop's tokens and state with
+    status bit 2 (fallback) instead of bit 1."""
+    want_toks, want_state, _ = per_phase_generate(D, dmodel, 77, 5, 8)
     s = D.DecodeSession(dmodel, 64)
     s.set_state(77, 5)
+    n0 = D.step_fallback_count()
     D.set_step_spin_limit(1)
     try:
         print("generate 8 with a one-round poll limit", flush=True)
-        with pytest.raises(Q.Q8GemvError) as e:
-            s.generate(8, eos_id=-1)
+        toks = s.generate(8, eos_id=-1)
         s.synchronize()
     finally:
         D.set_step_spin_limit(0)
-    assert e.value.code == Q.Q8_ERR_STEP_ABORTED
-    assert s.get_state() == (77, 5)
-    assert s.status() & 2
-    s.reset_scratch()
-    toks = s.generate(4, eos_id=-1)
-    assert len(toks) == 4 and s.get_state()[1] == 9 and s.check_status() == 0
+    assert toks.tolist() == want_toks
+    assert s.get_state() == want_state
+    st = s.check_status()
+    assert st & 4 and not st & 2
+    assert D.step_fallback_count() == n0 + 1
     s.free()
+
