@@ -84,20 +84,21 @@ def profiled_traffic(name: str, grid_threads: int) -> dict:
     """HBM bytes per dispatch of kernel `name` at this grid from the committed
     rocprofv3 counter summary (FETCH_SIZE + WRITE_SIZE, each scaled by what it
     reads for a copy kernel of known size), with whether the summary was taken
-    on the device sources of this tree."""
+    on the machine code of that kernel in this tree (per-kernel digest of the
+    built code object: edits to other kernels leave it valid)."""
     from qwen3_iree_amd import build as B
 
-    out = {"bytes": None, "source_digest": None, "stale": None}
+    out = {"bytes": None, "code_digest": None, "stale": None}
     path = REPO / "profiles" / "traffic.json"
     if not path.exists():
         return out
     rep = json.loads(path.read_text())
-    out["source_digest"] = rep.get("source_digest")
-    out["stale"] = rep.get("source_digest") != B.source_digest()
     for k in rep.get("kernels", []):
         if k.get("name") == name and k.get("grid") == grid_threads and k.get("hbm_bytes"):
             out["bytes"] = int(k["hbm_bytes"])
             out["profiled_mean_us"] = round(float(k["mean_us"]), 3)
+            out["code_digest"] = k.get("code_digest")
+            out["stale"] = k.get("code_digest") != B.kernel_digest(name)
     return out
 
 
@@ -134,6 +135,74 @@ def timed(Q, stream, fn, reps: int, blocks: int = TIMING_BLOCKS) -> dict:
         e.destroy()
     return {"mean_ms": total / reps, "median_ms": statistics.median(per), "min_ms": min(per),
             "max_ms": max(per), "reps": reps, "blocks": blocks}
+
+
+SCRUB_BYTES = 1 << 30  # per scrub: 1 GiB read, 4x the 256 MB MALL
+
+
+def bound_launch_us(Q, stream, fn, n: int, scrub=None) -> list[float]:
+    """Per-launch times of the kernel fn() launches (HIP events bound to that
+    launch, q8rt_time_next_launch), n launches with the stream drained between
+    them; with scrub = (src, dst, bytes), each launch follows a copy of that
+    many bytes (read only, so no dirty line is left for the kernel to write
+    back), which leaves nothing of the kernel's inputs in the MALL."""
+    e0, e1 = Q.Event(), Q.Event()
+    out = []
+    for _ in range(n):
+        if scrub is not None:
+            Q.stream_read(scrub[0], scrub[1], stream)
+        Q.time_next_launch(e0, e1)
+        fn()
+        e1.synchronize()
+        out.append(e0.elapsed_ms(e1) * 1e3)
+    e0.destroy()
+    e1.destroy()
+    return out
+
+
+def scrub_ab(Q, stream, fn, scrub, n: int = 30) -> dict:
+    """The kernel launched by fn() timed alone, A: right after its previous
+    launch (the access pattern the benchmark times), B: after a scrub copy,
+    both with the same per-launch events.  B / A > 1 would mean part of A's
+    bytes came from the memory-side cache (MALL) rather than HBM."""
+    warm(stream, fn, 3)
+    a = bound_launch_us(Q, stream, fn, n)
+    b = bound_launch_us(Q, stream, fn, n, scrub)
+    ma, mb = statistics.median(a), statistics.median(b)
+    return {"unscrubbed_us": round(ma, 2), "scrubbed_us": round(mb, 2),
+            "ratio": round(mb / ma, 4), "launches": n, "scrub_bytes": scrub[1],
+            "method": "median of per-launch HIP events bound to the kernel (hipExtModuleLaunchKernel); "
+                      f"B launches each follow a read of {scrub[1] >> 20} MiB (4x the 256 MB MALL, "
+                      "no writes)"}
+
+
+def calibration(Q) -> dict:
+    """The two measurements the single-launch step's design rests on: what a
+    launch of its grid costs (ordinary vs cooperative, empty kernel of the same
+    shape and LDS), and what a tagged-word hand-off costs (one producer to one
+    consumer, and 128 producers to 192 consumers with 4 replicas: the attn_o
+    output feeding the gate/up workgroups)."""
+    out = {"launch_cost_us": {}, "handoff_us": {}}
+    for coop in (False, True):
+        out["launch_cost_us"]["cooperative" if coop else "ordinary"] = round(
+            Q.launch_cost(448, 256, 79360, 2000, cooperative=coop), 2)
+    for name, (p, c, n, rep) in {"one_to_one_512_words": (1, 1, 512, 1),
+                                 "128_to_192_512_words_4_replicas": (128, 192, 512, 4)}.items():
+        lat, failed = Q.handoff_latency(p, c, n, rep, rounds=100)
+        ok = lat[np.isfinite(lat)]
+        out["handoff_us"][name] = {
+            "median": round(float(np.median(ok)), 3) if ok.size else None,
+            "p10": round(float(np.percentile(ok, 10)), 3) if ok.size else None,
+            "p90": round(float(np.percentile(ok, 90)), 3) if ok.size else None,
+            "max": round(float(ok.max()), 3) if ok.size else None,
+            "samples": int(ok.size), "failed": failed,
+            "first_consumer_median": round(float(np.median(np.where(np.isfinite(lat), lat, np.inf)
+                                                          .min(axis=1))), 3) if ok.size else None}
+    log(f"calibration: launch of the 448 x 256 grid {out['launch_cost_us']['ordinary']} us "
+        f"(cooperative {out['launch_cost_us']['cooperative']} us); hand-off 1 -> 1 median "
+        f"{out['handoff_us']['one_to_one_512_words']['median']} us, 128 -> 192 median "
+        f"{out['handoff_us']['128_to_192_512_words_4_replicas']['median']} us")
+    return out
 
 
 def bench_decode(Q, O, stream, args) -> dict:
@@ -216,6 +285,7 @@ def bench_decode(Q, O, stream, args) -> dict:
     D.set_step_mode(default_mode)
     sess.free()
     model.free()
+    cal = calibration(Q)
     best = ts if ts is not None else tp
     best_us = best["mean_ms"] * 1e3
     best_gbs = dec_bytes / best_us / 1e3
@@ -229,6 +299,7 @@ def bench_decode(Q, O, stream, args) -> dict:
             "per_phase_launches": 3 + 5 * layers,
             "per_phase_launch": "eager" if args.no_graph else "hipGraph", "steps_timed": reps,
             "token": step_tok, "oracle_token": ref_tok, "parity_ok": bool(step_ok),
+            "calibration": cal,
             "cpu_oracle": {"us": round(cpu_step_us, 1), "threads": O.num_threads(),
                            "kind": "port",
                            "sample": "one step of the C oracle at the same context and inputs "
@@ -534,6 +605,12 @@ def main() -> int:
                          "prompt, generation and CPU parts (for counter runs); with "
                          "--prefill-only: three untimed prompt calls over the f16 matrices and "
                          "three over the Q8_0 stacks, no parity check")
+    ap.add_argument("--scrub-only", action="store_true",
+                    help="run only the MALL-scrub A/B of the batched sweep kernel and the vocab "
+                         "kernel (per-launch events; for kernel traces of both cases) and print "
+                         "its JSON line")
+    ap.add_argument("--scrub-launches", type=int, default=30,
+                    help="launches per case of the MALL-scrub A/B")
     ap.add_argument("--generate-only", action="store_true",
                     help="run only end-to-end generation and print its JSON line")
     ap.add_argument("--step-mode", type=int, choices=(0, 1), default=None,
@@ -633,6 +710,34 @@ def run(Q, S, O, info, args) -> int:
         f"{th['median_ms'] * 1e3:.2f}, after {warm_calls} warm-up launches), {value:.1f} GB/s "
         f"({100 * value / HBM_PEAK_GBS:.1f}% of peak); host wall {wall_s:.3f}s")
 
+    # the same kernel after a MALL scrub (A/B with per-launch events)
+    scrub = (Q.DeviceBuffer(SCRUB_BYTES), SCRUB_BYTES)
+    scrub[0].fill(0)
+    sweep_scrub = scrub_ab(Q, stream, launch, scrub, args.scrub_launches)
+    log(f"batched sweep kernel alone: {sweep_scrub['unscrubbed_us']} us, after a MALL scrub "
+        f"{sweep_scrub['scrubbed_us']} us (ratio {sweep_scrub['ratio']})")
+
+    if args.scrub_only:
+        from qwen3_iree_amd import weights as Wt
+
+        batch.free()
+        sw.free()
+        Wv = Wt.synthetic_f16_matrix(Q.VOCAB_ROWS, Q.HIDDEN, seed=SEED, tensor=24, workers=16)
+        wv_dev = Q.DeviceBuffer.from_array(Wv)
+        xv_dev = Q.DeviceBuffer.from_array(Wt.synthetic_x(Q.HIDDEN, SEED, index=9999))
+        logits_dev, tok_dev = Q.DeviceBuffer(2 * Q.VOCAB_ROWS), Q.DeviceBuffer(16)
+        ws = Q.DeviceBuffer(Q.vocab_workspace_bytes())
+        Q.vocab_workspace_reset(ws, stream)
+        vocab_scrub = scrub_ab(Q, stream, lambda: Q.vocab_gemv_argmax(
+            wv_dev, xv_dev, logits_dev, tok_dev, ws, stream), scrub, args.scrub_launches)
+        log(f"vocab GEMV kernel alone: {vocab_scrub['unscrubbed_us']} us, after a MALL scrub "
+            f"{vocab_scrub['scrubbed_us']} us (ratio {vocab_scrub['ratio']})")
+        for b in (wv_dev, xv_dev, logits_dev, tok_dev, ws, scrub[0]):
+            b.free()
+        print(json.dumps({"scrub_ab": {"q8gemv_batch_k": sweep_scrub,
+                                       "vocab_gemv_argmax_k1024": vocab_scrub}}), flush=True)
+        return 0
+
     # parity of every sweep output (the last timed launch wrote them)
     fails = floor = 0
     for layer, d in sw.order:
@@ -647,8 +752,8 @@ def run(Q, S, O, info, args) -> int:
     batch_grid = min(batch.total_units, 12 * info["compute_units"]) * 64
     traffic = profiled_traffic("q8gemv_batch_k", batch_grid)
     if traffic["stale"]:
-        log("profiles/traffic.json was taken on other device sources (digest "
-            f"{traffic['source_digest']}): its traffic figure does not describe this build")
+        log("profiles/traffic.json was taken on another build of q8gemv_batch_k (digest "
+            f"{traffic['code_digest']}): its traffic figure does not describe this build")
     headline = {
         "metric": METRIC,
         "value": round(value, 2),
@@ -688,9 +793,11 @@ def run(Q, S, O, info, args) -> int:
             "traffic": traffic["bytes"],
             "traffic_source": "profiles/traffic.json: rocprofv3 FETCH_SIZE + WRITE_SIZE per dispatch, "
                               "each scaled by its reading for the plain copy kernel of known size",
-            "traffic_source_digest": traffic["source_digest"],
+            "traffic_code_digest": traffic["code_digest"],
             "traffic_stale": traffic["stale"],
             "profiled_mean_us": traffic.get("profiled_mean_us"),
+            "scrubbed_us": sweep_scrub["scrubbed_us"],
+            "scrub_ab": sweep_scrub,
         },
         "parity_ok": fails == 0,
         "copy_calibration": copy_cal,
@@ -699,6 +806,7 @@ def run(Q, S, O, info, args) -> int:
     if args.sweep_only:
         print(json.dumps(headline), flush=True)
         sw.free()
+        scrub[0].free()
         return 0
 
     # ------------------------------- the same sweep as 140 dispatches
@@ -713,6 +821,20 @@ def run(Q, S, O, info, args) -> int:
     chain_gbs = sweep_bytes / (chain_ms * 1e-3) / 1e9
     log(f"per-dispatch sweep (140 launches{'' if args.no_graph else ', hipGraph'}): "
         f"{chain_ms * 1e3:.1f} us (median {tc['median_ms'] * 1e3:.1f}), {chain_gbs:.1f} GB/s")
+    # its floor: 140 stream-ordered empty launches the same way (one workgroup each)
+    def record_empty():
+        for _ in range(len(sw.order)):
+            Q.stream_copy(None, None, 0, stream)
+
+    if args.no_graph:
+        floor_fn = record_empty
+    else:
+        fgraph = Q.Graph(stream, record_empty)
+        floor_fn = lambda: fgraph.launch(stream)  # noqa: E731
+    warm(stream, floor_fn, 3)
+    tf = timed(Q, stream, floor_fn, max(10, args.steps // 4))
+    floor_us = tf["mean_ms"] * 1e3
+    log(f"  its floor, 140 empty launches the same way: {floor_us:.1f} us")
 
     # ------------------------------------------------------------- vocab
     from qwen3_iree_amd import weights as Wt
@@ -740,6 +862,9 @@ def run(Q, S, O, info, args) -> int:
     log(f"vocab GEMV + argmax: {v_ms * 1e3:.2f} us/op (median {tv['median_ms'] * 1e3:.2f}), "
         f"{v_gbs:.0f} GB/s, token {token} (argmax of own logits {own}, {rep_v['fail']} failing "
         f"logits)")
+    vocab_scrub = scrub_ab(Q, stream, vocab_fn, scrub, args.scrub_launches)
+    log(f"vocab GEMV kernel alone: {vocab_scrub['unscrubbed_us']} us, after a MALL scrub "
+        f"{vocab_scrub['scrubbed_us']} us (ratio {vocab_scrub['ratio']})")
 
     # ---------------------------------------- GEMV share of a decode step
     # Separate K and V weights (the attn_kv stack above serves as K).
@@ -768,17 +893,21 @@ def run(Q, S, O, info, args) -> int:
     decode_bytes = (sum(S.algorithmic_bytes(d) for d in Q.LAYER_ORDER) * layers + vocab_bytes)
     log(f"decode-step GEMVs (28 x [q8gemv_qkv, o, gate_up, down] + vocab, 114 dispatches): "
         f"{decode_gemv_us:.1f} us, {decode_bytes / decode_gemv_us / 1e3:.0f} GB/s")
-    for b in (wv_dev, xv_dev, logits_dev, tok_dev, ws, v_dev, *step_y.values()):
+    for b in (wv_dev, xv_dev, logits_dev, tok_dev, ws, v_dev, *step_y.values(), scrub[0]):
         b.free()
     kernels = {
         "per_dispatch_sweep": {"us": round(chain_ms * 1e3, 1),
                                "median_us": round(tc["median_ms"] * 1e3, 1),
                                "GBps": round(chain_gbs, 1),
                                "frac": round(chain_gbs / HBM_PEAK_GBS, 4), "dispatches": 140,
-                               "launch": "eager" if args.no_graph else "hipGraph"},
+                               "launch": "eager" if args.no_graph else "hipGraph",
+                               "floor_us": round(floor_us, 1),
+                               "floor": "140 empty launches (one workgroup each), stream-ordered "
+                                        "the same way"},
         "vocab": {"us": round(v_ms * 1e3, 2), "median_us": round(tv["median_ms"] * 1e3, 2),
                   "GBps": round(v_gbs, 1), "frac": round(v_gbs / HBM_PEAK_GBS, 4),
-                  "bytes": vocab_bytes, "token": token, "parity_ok": rep_v["fail"] == 0 and token == own},
+                  "bytes": vocab_bytes, "token": token, "parity_ok": rep_v["fail"] == 0 and token == own,
+                  "scrub_ab": vocab_scrub},
         "decode_step_gemv": {"us": round(decode_gemv_us, 2), "bytes": decode_bytes,
                              "GBps": round(decode_bytes / decode_gemv_us / 1e3, 1),
                              "dispatches": 4 * layers + 2,

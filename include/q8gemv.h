@@ -272,10 +272,39 @@ int q8rt_graph_destroy(void* graph_exec);
  * bytes % 16 == 0; bytes = 0 launches one empty workgroup).  A kernel of known
  * traffic for calibrating HBM byte counters and dispatch overhead. */
 int q8rt_stream_copy(void* dst, const void* src, size_t bytes, void* stream);
+/* Reads `bytes` at src (16-byte aligned, bytes % 16 == 0) with a plain
+ * streaming kernel and writes nothing (in practice: a word of src only if the
+ * XOR of a thread's reads equals a fixed 32-bit value).  Reading more than the
+ * 256 MB memory-side cache (MALL) holds evicts it without leaving dirty lines
+ * that a following kernel would pay to write back. */
+int q8rt_stream_read(const void* src, size_t bytes, void* stream);
 /* The calling thread's next kernel launch through this library records
  * `start` / `stop` around that kernel alone (hipExtModuleLaunchKernel
  * events), for per-kernel timing.  One-shot. */
 int q8rt_time_next_launch(void* start_event, void* stop_event);
+
+/* ---- measurement tools (allocate their own buffers and synchronize the
+ * device; not compute entry points) ---- */
+/* Mean time per launch of an empty kernel of `workgroups` x `threads` with
+ * `lds_bytes` of LDS each, `launches` of them back to back on a fresh stream,
+ * as ordinary launches or (cooperative != 0) cooperative ones: the launch
+ * cost the single-launch decode step's grid (448 x 256, 79,360 LDS bytes)
+ * pays per step. */
+int q8rt_launch_cost(int cooperative, int workgroups, int threads, size_t lds_bytes,
+                     int launches, float* us_per_launch);
+/* Latency of the single-launch decode step's hand-off (tagged 8-byte words,
+ * agent-scope atomic stores and polls): `producers` workgroups each store
+ * n_words / producers words of a vector into each of `replicas` copies, all
+ * at the same clock tick; `consumers` further workgroups each poll one copy
+ * (consumer c: copy c % replicas) until every word carries the round's tag.
+ * latency_us[r * consumers + c] (host, rounds x consumers) = when consumer c
+ * held the whole vector in round r minus when the last producer's stores were
+ * issued, from the 100 MHz device clock (10 ns ticks; a consumer can see
+ * the words a few ticks before the last producer's clock read), NaN (and
+ * counted in *failed) where a bounded wait gave up.  n_words % producers == 0, producers + consumers <=
+ * 512, rounds <= 255; rounds are 20 us apart. */
+int q8rt_handoff_latency(int producers, int consumers, int n_words, int replicas, int rounds,
+                         float* latency_us, int* failed);
 
 #ifdef __cplusplus
 }

@@ -114,6 +114,44 @@ def source_digest(code_object: str = "q8gemv") -> str:
     return h.hexdigest()[:16]
 
 
+def kernel_digest(name: str, code_object: Path = CODE_OBJECT) -> str | None:
+    """sha256 (16 hex digits) of one kernel's machine code and its kernel
+    descriptor (`name` and `name.kd` in the code object's ELF symbol table,
+    the descriptor without its bytes 16-23: the offset to the code, which
+    moves when other kernels change): the build a profile of that kernel
+    belongs to, unchanged by edits to other kernels of the same sources.
+    None if the kernel is absent."""
+    import hashlib
+    import struct
+
+    data = Path(code_object).read_bytes()
+    if data[:4] != b"\x7fELF" or data[4] != 2:
+        return None
+    shoff, = struct.unpack_from("<Q", data, 0x28)
+    shentsize, shnum = struct.unpack_from("<HH", data, 0x3A)
+    secs = [struct.unpack_from("<IIQQQQIIQQ", data, shoff + i * shentsize) for i in range(shnum)]
+    h = hashlib.sha256()
+    found = False
+    for sec in secs:
+        if sec[1] != 2:  # SHT_SYMTAB
+            continue
+        strtab = secs[sec[6]]
+        for off in range(sec[4], sec[4] + sec[5], 24):
+            st_name, _info, _other, shndx, value, size = struct.unpack_from("<IBBHQQ", data, off)
+            end = data.index(b"\0", strtab[4] + st_name)
+            sym = data[strtab[4] + st_name:end].decode()
+            if sym in (name, name + ".kd") and size and shndx < len(secs):
+                tgt = secs[shndx]
+                start = tgt[4] + (value - tgt[3])
+                body = bytearray(data[start:start + size])
+                if sym.endswith(".kd") and len(body) >= 24:
+                    body[16:24] = bytes(8)  # kernel_code_entry_byte_offset
+                h.update(sym.encode())
+                h.update(bytes(body))
+                found = found or sym == name
+    return h.hexdigest()[:16] if found else None
+
+
 def build_all() -> tuple[Path, Path, Path, Path]:
     return build_code_object(), build_decode_object(), build_prefill_object(), build_shim()
 

@@ -33,17 +33,25 @@ __device__ __forceinline__ f16x2 q8x2_to_f16x2(uint32_t biased, uint32_t sel) {
 
 __device__ __forceinline__ f16x2 as_f16x2(uint32_t v) { return __builtin_bit_cast(f16x2, v); }
 
-// Load flavour of the weight streams (read once per launch): the Q8_0 kernels
-// use nontemporal loads (global_load ... nt), the vocab kernel plain loads,
-// each the faster of the two on MI355X.
+// Load flavour of the weight streams (read once per launch): nontemporal
+// loads (global_load ... nt) for the Q8_0 and the vocab matrices.  Plain loads
+// let the memory-side cache (MALL, 256 MB) keep part of a matrix from one
+// launch to the next: measured on MI355X, the vocab kernel with plain loads
+// ran 48.3 us back to back but 56.5 us after a 1 GiB read evicted the MALL,
+// with nontemporal loads 50.5 and 51.8 us; the decode step 518.5 -> 513.9 us.
 #ifndef Q8_NT_LOADS
 #define Q8_NT_LOADS 1
 #endif
 #ifndef Q8_X_REUSE
 #define Q8_X_REUSE 1
 #endif
+// Register sets of units a wave of the batched launch keeps in flight (2 or
+// 3; three measured 1-2 % slower, warm and after a MALL eviction).
+#ifndef Q8_SEG_SETS
+#define Q8_SEG_SETS 2
+#endif
 #ifndef VOCAB_NT_LOADS
-#define VOCAB_NT_LOADS 0
+#define VOCAB_NT_LOADS 1
 #endif
 
 // Pointers read from a batch table are generic; accessing them through the
@@ -265,6 +273,36 @@ __device__ __forceinline__ void q8_segment(const Q8Seg& s, int u_begin, int u_en
   };
 
   const int n = u_end - u_begin;
+#if Q8_SEG_SETS == 3
+  // Three register sets: two units in flight while one is computed.  Loads
+  // past the segment's last unit re-read that unit (the same lines this wave
+  // just requested), so every load in the loop is unconditional.
+  int loaded = 0;
+  auto load_ring = [&](u32x4 (&dst)[kUnitLoads]) {
+    unit_load(s, lq, lc, pm, dst);
+    if (++loaded < n && ++lc == s.p) {
+      lc = 0;
+      ++lq;
+    }
+  };
+  u32x4 A[kUnitLoads], B[kUnitLoads], C[kUnitLoads];
+  load_ring(A);
+  const u32x4* xg = reinterpret_cast<const u32x4*>(s.x);
+  u32x4* xl4 = reinterpret_cast<u32x4*>(xl);
+  for (int t = lane; t < 128 * s.p; t += 64) xl4[t] = load_global(xg + t);
+  load_ring(B);
+  int i = 0;
+  for (; i + 3 <= n; i += 3) {
+    load_ring(C);
+    compute(A);
+    load_ring(A);
+    compute(B);
+    load_ring(B);
+    compute(C);
+  }
+  if (n - i >= 1) compute(A);
+  if (n - i >= 2) compute(B);
+#else
   u32x4 A[kUnitLoads], B[kUnitLoads];
   load_next(A);
   const u32x4* xg = reinterpret_cast<const u32x4*>(s.x);
@@ -284,6 +322,7 @@ __device__ __forceinline__ void q8_segment(const Q8Seg& s, int u_begin, int u_en
   } else {
     compute(A);
   }
+#endif
 }
 
 // Single GEMV: one wave per row quad, the latency-bound shape of a lone

@@ -112,6 +112,122 @@ extern "C" __global__ __launch_bounds__(256) void stream_copy_b128(const u32x4* 
     dst[i] = src[i];
 }
 
+// Plain device read of n16 16-byte words (grid-stride), writing nothing
+// unless the words' XOR happens to equal `never` (the caller passes a value
+// it is not): evicts the memory-side cache (MALL) without leaving dirty lines
+// behind, unlike a copy, whose written lines a later kernel would have to
+// write back.
+extern "C" __global__ __launch_bounds__(256) void stream_read_b128(const u32x4* __restrict__ src,
+                                                                   uint32_t* __restrict__ sink,
+                                                                   int64_t n16, uint32_t never) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  uint32_t acc = 0;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += stride) {
+    const u32x4 v = load_global(src + i);
+    acc ^= v[0] ^ v[1] ^ v[2] ^ v[3];
+  }
+  if (acc == never) sink[threadIdx.x] = acc;
+}
+
+// ------------------------------------------------- calibration kernels ----
+//
+// Measurements the single-launch decode step's design rests on, made by the
+// library itself so a benchmark can record them beside the step.
+
+// An empty kernel: the launch cost of a grid shape (its LDS comes from the
+// launch's dynamic size, so a shape can hold as many workgroups per CU as
+// the decode step does).
+extern "C" __global__ void calib_empty() {}
+
+// Arguments of calib_handoff.
+struct HandoffArgs {
+  uint64_t* words;       // replicas x n_words tagged words, then the start word
+  uint32_t* pub;         // [rounds][producers]: clock when each producer's stores were issued
+  uint32_t* recv;        // [rounds][consumers]: clock when each consumer had the whole vector
+  int producers, consumers, n_words, replicas, rounds;
+  uint32_t seq;          // distinguishes calls (tags are seq << 8 | round + 1)
+  uint32_t period;       // clock ticks between rounds
+  uint32_t spin_limit;   // poll rounds before a wait gives up (then its clock reads stay 0)
+};
+
+__device__ __forceinline__ uint32_t realtime() {
+  return (uint32_t)__builtin_amdgcn_s_memrealtime();  // 100 MHz, the same counter on every CU
+}
+
+// The latency of a tagged-word hand-off (the exchange of the single-launch
+// decode step: 8-byte words = 32 data bits + a 32-bit tag, agent-scope
+// relaxed atomic stores and polling loads).  Workgroups 0 .. producers - 1
+// each own n_words / producers words of a vector, stored in every replica;
+// workgroup producers + c polls replica c % replicas until every word carries
+// the round's tag.  Round r starts for all producers at the same clock value
+// (T0 + r * period, T0 published once by workgroup 0), so recv - max(pub) of a
+// round is the hand-off's latency from the last producer's store to a
+// consumer holding the vector.  Every wait is bounded; one that gives up
+// leaves its clock reads 0.
+extern "C" __global__ __launch_bounds__(256) void calib_handoff(HandoffArgs a) {
+  const int wg = blockIdx.x;
+  const int t = threadIdx.x;
+  __shared__ uint32_t s_t0;
+  __shared__ int s_ok;
+  uint64_t* start = a.words + (size_t)a.replicas * a.n_words;
+  const uint32_t tag0 = a.seq << 8;
+  if (t == 0) {
+    s_ok = 1;
+    if (wg == 0)
+      __hip_atomic_store(start, ((uint64_t)tag0 << 32) | (realtime() + 2000u), __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+    uint64_t w = __hip_atomic_load(start, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (uint32_t spins = 0; (uint32_t)(w >> 32) != tag0; ++spins) {
+      if (spins > a.spin_limit) {
+        s_ok = 0;
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+      w = __hip_atomic_load(start, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    s_t0 = (uint32_t)w;
+  }
+  __syncthreads();
+  if (!s_ok) return;
+  const uint32_t t0 = s_t0;
+  const int per = a.n_words / a.producers;
+  for (int r = 0; r < a.rounds; ++r) {
+    const uint32_t tag = tag0 | (uint32_t)(r + 1);
+    if (wg < a.producers) {
+      if (t == 0)
+        while ((int32_t)(realtime() - (t0 + (uint32_t)r * a.period)) < 0) __builtin_amdgcn_s_sleep(2);
+      __syncthreads();
+      for (int i = t; i < per * a.replicas; i += 256) {
+        const int rep = i / per;
+        const int k = wg * per + i % per;
+        __hip_atomic_store(a.words + (size_t)rep * a.n_words + k, ((uint64_t)tag << 32) | (uint32_t)k,
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      __syncthreads();
+      if (t == 0) a.pub[r * a.producers + wg] = realtime();
+    } else if (wg < a.producers + a.consumers) {
+      const int c = wg - a.producers;
+      const uint64_t* src = a.words + (size_t)(c % a.replicas) * a.n_words;
+      bool ok = true;
+      for (int i = t; i < a.n_words && ok; i += 256) {
+        uint64_t w = __hip_atomic_load(src + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        for (uint32_t spins = 0; (uint32_t)(w >> 32) != tag; ++spins) {
+          if (spins > a.spin_limit) {
+            ok = false;
+            break;
+          }
+          __builtin_amdgcn_s_sleep(1);
+          w = __hip_atomic_load(src + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+      }
+      if (!ok) s_ok = 0;
+      __syncthreads();
+      if (t == 0) a.recv[r * a.consumers + c] = s_ok ? realtime() : 0u;
+      if (!s_ok) return;
+    }
+  }
+}
+
 // ------------------------------------------------ IREE HAL binding ABI ----
 //
 // The same kernels under the reference's executable export names and binding

@@ -16,9 +16,11 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <limits>
 #include <mutex>
 #include <string>
 #include <utility>
+#include <vector>
 
 // hipExtModuleLaunchKernel lives in hip/hip_ext.h, which pulls in the device
 // headers; its C declaration is all the shim needs.
@@ -101,6 +103,7 @@ struct State {
   hipFunction_t vocab_finalize = nullptr;
   hipFunction_t ws_reset = nullptr;
   hipFunction_t copy = nullptr;
+  hipFunction_t calib_empty = nullptr, calib_handoff = nullptr, read = nullptr;
   // Tuning knobs: process-wide, set under mu, read without it (atomics), so a
   // setter never races a launch on another thread; each call reads a knob
   // once.
@@ -284,6 +287,9 @@ int q8gemv_init(const char* code_object_path) {
   if (e == hipSuccess) e = hipModuleGetFunction(&g.vocab_finalize, mod, "vocab_argmax_finalize");
   if (e == hipSuccess) e = hipModuleGetFunction(&g.ws_reset, mod, "vocab_workspace_reset");
   if (e == hipSuccess) e = hipModuleGetFunction(&g.copy, mod, "stream_copy_b128");
+  if (e == hipSuccess) e = hipModuleGetFunction(&g.read, mod, "stream_read_b128");
+  if (e == hipSuccess) e = hipModuleGetFunction(&g.calib_empty, mod, "calib_empty");
+  if (e == hipSuccess) e = hipModuleGetFunction(&g.calib_handoff, mod, "calib_handoff");
   if (e != hipSuccess) {
     (void)hipModuleUnload(mod);
     return fail(Q8_ERR_CODE_OBJECT, "vocab / copy kernels missing from %s", path.c_str());
@@ -449,6 +455,7 @@ void q8gemv_shutdown(void) {
   g.pf_f16_res_22 = g.pf_f16_res_22k = g.pf_f16_res_12k = g.pf_f16_part_22 = g.pf_f16_part_22k =
       g.pf_f16_part_12k = g.pf_f16_part_44 = g.pf_f16_part_44k = g.pf_expand = nullptr;
   g.vocab = g.vocab_finalize = g.ws_reset = g.copy = nullptr;
+  g.calib_empty = g.calib_handoff = g.read = nullptr;
   g.ready = false;
 }
 
@@ -924,9 +931,144 @@ int q8rt_stream_copy(void* dst, const void* src, size_t bytes, void* stream) {
   return launch(g.copy, (uint32_t)grid, 256, args, static_cast<hipStream_t>(stream));
 }
 
+int q8rt_stream_read(const void* src, size_t bytes, void* stream) {
+  if (!src && bytes) return fail(Q8_ERR_NULL_POINTER, "null src");
+  if (bytes % 16 || !aligned(src, 16))
+    return fail(Q8_ERR_MISALIGNED, "read needs a 16-byte aligned pointer and size");
+  int rc = check_ready();
+  if (rc) return rc;
+  int64_t n16 = (int64_t)(bytes / 16);
+  int64_t grid = (n16 + 255) / 256;
+  if (grid > 8192) grid = 8192;
+  if (grid < 1) grid = 1;
+  const void* s_arg = src;
+  void* sink = const_cast<void*>(src);  // written only if a thread's XOR equals `never`
+  uint32_t never = 0x9e3779b9u;
+  void* args[] = {&s_arg, &sink, &n16, &never};
+  return launch(g.read, (uint32_t)grid, 256, args, static_cast<hipStream_t>(stream));
+}
+
 int q8rt_time_next_launch(void* start_event, void* stop_event) {
   t_start = static_cast<hipEvent_t>(start_event);
   t_stop = static_cast<hipEvent_t>(stop_event);
+  return Q8_OK;
+}
+
+}  // extern "C"
+
+namespace {
+
+// A stream, two events and device buffers for a measurement, released on
+// every return path (after the stream has drained).
+struct CalibScope {
+  hipStream_t st = nullptr;
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  void* buf[3] = {nullptr, nullptr, nullptr};
+  ~CalibScope() {
+    if (st) (void)hipStreamSynchronize(st);
+    for (void* b : buf)
+      if (b) (void)hipFree(b);
+    if (e0) (void)hipEventDestroy(e0);
+    if (e1) (void)hipEventDestroy(e1);
+    if (st) (void)hipStreamDestroy(st);
+  }
+};
+
+}  // namespace
+
+extern "C" {
+
+int q8rt_launch_cost(int cooperative, int workgroups, int threads, size_t lds_bytes,
+                     int launches, float* us_per_launch) {
+  if (!us_per_launch) return fail(Q8_ERR_NULL_POINTER, "null output");
+  if (workgroups < 1 || workgroups > 65536 || threads < 1 || threads > 1024 ||
+      lds_bytes > 160 * 1024 || launches < 1 || launches > 100000)
+    return fail(Q8_ERR_BAD_ARGUMENT, "launch shape %d x %d, %zu LDS bytes, %d launches",
+                workgroups, threads, lds_bytes, launches);
+  int rc = check_ready();
+  if (rc) return rc;
+  CalibScope c;
+  HIP_TRY(hipStreamCreate(&c.st));
+  HIP_TRY(hipEventCreate(&c.e0));
+  HIP_TRY(hipEventCreate(&c.e1));
+  auto one = [&]() -> hipError_t {
+    if (cooperative)
+      return hipModuleLaunchCooperativeKernel(g.calib_empty, workgroups, 1, 1, threads, 1, 1,
+                                              (unsigned)lds_bytes, c.st, nullptr);
+    return hipModuleLaunchKernel(g.calib_empty, workgroups, 1, 1, threads, 1, 1,
+                                 (unsigned)lds_bytes, c.st, nullptr, nullptr);
+  };
+  for (int i = 0; i < 16; ++i) HIP_TRY(one());  // warm-up
+  HIP_TRY(hipEventRecord(c.e0, c.st));
+  for (int i = 0; i < launches; ++i) HIP_TRY(one());
+  HIP_TRY(hipEventRecord(c.e1, c.st));
+  HIP_TRY(hipEventSynchronize(c.e1));
+  float ms = 0.0f;
+  HIP_TRY(hipEventElapsedTime(&ms, c.e0, c.e1));
+  *us_per_launch = ms * 1e3f / (float)launches;
+  return Q8_OK;
+}
+
+// Mirrors HandoffArgs in q8gemv_kernels.hip.
+struct HandoffArgsHost {
+  void* words;
+  void* pub;
+  void* recv;
+  int32_t producers, consumers, n_words, replicas, rounds;
+  uint32_t seq, period, spin_limit;
+};
+
+int q8rt_handoff_latency(int producers, int consumers, int n_words, int replicas, int rounds,
+                         float* latency_us, int* failed) {
+  if (!latency_us || !failed) return fail(Q8_ERR_NULL_POINTER, "null output");
+  if (producers < 1 || consumers < 1 || producers + consumers > 512 || n_words < 1 ||
+      n_words > 4096 || n_words % producers != 0 || replicas < 1 || replicas > 16 ||
+      rounds < 1 || rounds > 255)
+    return fail(Q8_ERR_BAD_ARGUMENT,
+                "hand-off of %d words (%d replicas) from %d to %d workgroups over %d rounds",
+                n_words, replicas, producers, consumers, rounds);
+  int rc = check_ready();
+  if (rc) return rc;
+  static std::atomic<uint32_t> calls{0};
+  CalibScope c;
+  HIP_TRY(hipStreamCreate(&c.st));
+  const size_t wbytes = ((size_t)replicas * n_words + 1) * 8;
+  HIP_TRY(hipMalloc(&c.buf[0], wbytes));
+  HIP_TRY(hipMalloc(&c.buf[1], (size_t)rounds * producers * 4));
+  HIP_TRY(hipMalloc(&c.buf[2], (size_t)rounds * consumers * 4));
+  HIP_TRY(hipMemsetAsync(c.buf[0], 0, wbytes, c.st));
+  HIP_TRY(hipMemsetAsync(c.buf[1], 0, (size_t)rounds * producers * 4, c.st));
+  HIP_TRY(hipMemsetAsync(c.buf[2], 0, (size_t)rounds * consumers * 4, c.st));
+  HandoffArgsHost a{c.buf[0], c.buf[1], c.buf[2], producers, consumers, n_words, replicas, rounds,
+                    1u + (calls.fetch_add(1) & 0xffffu), 2000u /* 20 us */, 1u << 16};
+  void* args[] = {&a};
+  HIP_TRY(hipModuleLaunchKernel(g.calib_handoff, producers + consumers, 1, 1, 256, 1, 1, 0, c.st,
+                                args, nullptr));
+  std::vector<uint32_t> pub((size_t)rounds * producers), recv((size_t)rounds * consumers);
+  HIP_TRY(hipMemcpyAsync(pub.data(), c.buf[1], pub.size() * 4, hipMemcpyDeviceToHost, c.st));
+  HIP_TRY(hipMemcpyAsync(recv.data(), c.buf[2], recv.size() * 4, hipMemcpyDeviceToHost, c.st));
+  HIP_TRY(hipStreamSynchronize(c.st));
+  int bad = 0;
+  for (int r = 0; r < rounds; ++r) {
+    uint32_t last = 0;
+    bool have = true;
+    for (int p = 0; p < producers; ++p) {
+      const uint32_t v = pub[(size_t)r * producers + p];
+      if (v == 0) have = false;
+      if (p == 0 || (int32_t)(v - last) > 0) last = v;
+    }
+    for (int q = 0; q < consumers; ++q) {
+      const uint32_t v = recv[(size_t)r * consumers + q];
+      float& out = latency_us[(size_t)r * consumers + q];
+      if (!have || v == 0) {
+        out = std::numeric_limits<float>::quiet_NaN();
+        ++bad;
+      } else {
+        out = (float)(int32_t)(v - last) * 0.01f;  // 10 ns ticks
+      }
+    }
+  }
+  *failed = bad;
   return Q8_OK;
 }
 

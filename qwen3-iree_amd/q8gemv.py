@@ -153,6 +153,9 @@ _SIGNATURES = {
     "q8rt_graph_destroy": [_P],
     "q8rt_time_next_launch": [_P, _P],
     "q8rt_stream_copy": [_P, _P, _SZ, _P],
+    "q8rt_stream_read": [_P, _SZ, _P],
+    "q8rt_launch_cost": [_I, _I, _I, _SZ, _I, _P],
+    "q8rt_handoff_latency": [_I, _I, _I, _I, _I, _P, _P],
     # include/qwen3_decode.h
     "qwen3_scratch_bytes": [],
     "qwen3_scratch_reset": [_P, _P],
@@ -427,8 +430,32 @@ def stream_copy(dst, src, nbytes: int, stream=None) -> None:
     _call("q8rt_stream_copy", _ptr(dst), _ptr(src), int(nbytes), _stream(stream))
 
 
+def stream_read(src, nbytes: int, stream=None) -> None:
+    _call("q8rt_stream_read", _ptr(src), int(nbytes), _stream(stream))
+
+
 def time_next_launch(start: Event, stop: Event) -> None:
     _call("q8rt_time_next_launch", start.handle, stop.handle)
+
+
+def launch_cost(workgroups: int, threads: int, lds_bytes: int, launches: int = 2000,
+                cooperative: bool = False) -> float:
+    """Mean us per back-to-back launch of an empty kernel of that shape."""
+    us = ctypes.c_float(0.0)
+    _call("q8rt_launch_cost", int(bool(cooperative)), int(workgroups), int(threads),
+          int(lds_bytes), int(launches), ctypes.byref(us))
+    return float(us.value)
+
+
+def handoff_latency(producers: int, consumers: int, n_words: int, replicas: int = 1,
+                    rounds: int = 50) -> tuple[np.ndarray, int]:
+    """Tagged-word hand-off latencies in us, [rounds, consumers] (NaN where a
+    bounded wait gave up), and the count of those."""
+    out = np.zeros(rounds * consumers, np.float32)
+    failed = ctypes.c_int(0)
+    _call("q8rt_handoff_latency", int(producers), int(consumers), int(n_words), int(replicas),
+          int(rounds), out.ctypes.data, ctypes.byref(failed))
+    return out.reshape(rounds, consumers), int(failed.value)
 
 
 # ------------------------------------------------------------- operators ----

@@ -8,6 +8,10 @@ Inputs (directories written by `rocprofv3 -f csv -d DIR -o bench ...`):
   --write DIR   a --pmc WRITE_SIZE run         (bench_counter_collection.csv)
   --copy-bytes N  bytes the calibration copy kernel (stream_copy_b128) read
                 and wrote in those runs (bench.py --copy-calibration MIB)
+  --split-after NAME  report a kernel's dispatches that directly follow a
+                dispatch of NAME on the same queue as a row of their own
+                ("kernel (after NAME)"), e.g. the launches of bench.py
+                --scrub-only that follow its stream_read_b128 scrub
 
 HBM traffic per dispatch = FETCH_SIZE * (N / FETCH_SIZE of the copy kernel)
 + WRITE_SIZE * (N / WRITE_SIZE of the copy kernel): each counter is scaled by
@@ -15,7 +19,9 @@ what it reads for a copy of known size.  Kernels are grouped by name and grid
 size (one launch shape = one row).
 
 Writes the markdown report to stdout and, with --json PATH, the per-kernel
-traffic figures as JSON.
+traffic figures as JSON, each with the digest of the kernel's machine code in
+the code objects of this tree (build.kernel_digest): a figure describes a
+build whose kernel has that digest.
 """
 from __future__ import annotations
 
@@ -32,10 +38,17 @@ def _rows(path: Path):
         yield from csv.DictReader(f)
 
 
-def kernel_durations(trace_dir: Path) -> dict:
+def kernel_durations(trace_dir: Path, split_after: str | None = None) -> dict:
     out = defaultdict(list)
-    for r in _rows(trace_dir / "bench_kernel_trace.csv"):
-        key = (r["Kernel_Name"], int(r["Grid_Size_X"]))
+    rows = sorted(_rows(trace_dir / "bench_kernel_trace.csv"),
+                  key=lambda r: (r["Queue_Id"], int(r["Start_Timestamp"])))
+    prev = {}
+    for r in rows:
+        name = r["Kernel_Name"]
+        if split_after and prev.get(r["Queue_Id"]) == split_after and name != split_after:
+            name = f"{name} (after {split_after})"
+        prev[r["Queue_Id"]] = r["Kernel_Name"]
+        key = (name, int(r["Grid_Size_X"]))
         out[key].append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
     return out
 
@@ -56,10 +69,11 @@ def main() -> int:
     ap.add_argument("--write", type=Path)
     ap.add_argument("--copy-bytes", type=int, default=0)
     ap.add_argument("--kernels", nargs="*", default=None, help="only these kernel names")
+    ap.add_argument("--split-after", default=None, metavar="NAME")
     ap.add_argument("--json", type=Path)
     args = ap.parse_args()
 
-    durs = kernel_durations(args.trace)
+    durs = kernel_durations(args.trace, args.split_after)
     fetch = counter_values(args.fetch, "FETCH_SIZE") if args.fetch else {}
     write = counter_values(args.write, "WRITE_SIZE") if args.write else {}
 
@@ -70,16 +84,23 @@ def main() -> int:
         return args.copy_bytes / 1024.0 / statistics.mean(copy)
 
     fs, ws = scale(fetch), scale(write)
-    from build import source_digest  # the package directory is this script's
+    import build as B  # the package directory is this script's
 
-    digest = source_digest()
+    digest = B.source_digest()
+
+    def code_digest(name: str) -> str | None:
+        for co in (B.CODE_OBJECT, B.DECODE_OBJECT, B.PREFILL_OBJECT):
+            if co.exists() and (d := B.kernel_digest(name, co)) is not None:
+                return d
+        return None
+
     print("| kernel | grid (threads) | dispatches | mean us | median us | min us |"
           " FETCH_SIZE KiB | WRITE_SIZE KiB | HBM bytes / dispatch |")
     print("|---|---|---|---|---|---|---|---|---|")
     report = {"source_digest": digest, "fetch_scale": fs, "write_scale": ws, "kernels": []}
     for key in sorted(durs, key=lambda k: -sum(durs[k])):
         name, grid = key
-        if args.kernels and name not in args.kernels:
+        if args.kernels and name.split(" (after ")[0] not in args.kernels:
             continue
         d = durs[key]
         f = statistics.mean(fetch[key]) if fetch.get(key) else None
@@ -93,7 +114,8 @@ def main() -> int:
         report["kernels"].append({"name": name, "grid": grid, "dispatches": len(d),
                                   "mean_us": statistics.mean(d),
                                   "median_us": statistics.median(d), "fetch_kib": f,
-                                  "write_kib": w, "hbm_bytes": traffic})
+                                  "write_kib": w, "hbm_bytes": traffic,
+                                  "code_digest": code_digest(name.split(" (after ")[0])})
     print()
     print(f"FETCH_SIZE scale (copy kernel): {fs}; WRITE_SIZE scale: {ws}")
     print(f"Sources of the q8gemv code object (csrc/q8gemv_kernels.hip, csrc/q8_device.h) "

@@ -104,6 +104,15 @@ def test_dispatch_table_mirrors_reference_exports(Q):
     (lambda L: L.q8gemv_qkv(A16, A16, A16 + 4, 0, A16, A16, A16, A16, None), 5),
     (lambda L: L.q8gemv_qkv(A16, A16, A16, 0, A16, A16, A16 + 1, A16, None), 5),
     (lambda L: L.q8gemv_desc_for_kind(0, A16, 28, A16, A16, A16), 4),
+    # measurement tools
+    (lambda L: L.q8rt_launch_cost(0, 448, 256, 79360, 10, None), 3),
+    (lambda L: L.q8rt_launch_cost(0, 0, 256, 0, 10, A16), 9),
+    (lambda L: L.q8rt_launch_cost(0, 448, 2048, 0, 10, A16), 9),
+    (lambda L: L.q8rt_launch_cost(1, 448, 256, 200 * 1024, 10, A16), 9),
+    (lambda L: L.q8rt_handoff_latency(1, 1, 512, 1, 10, None, A16), 3),
+    (lambda L: L.q8rt_handoff_latency(3, 1, 512, 1, 10, A16, A16), 9),
+    (lambda L: L.q8rt_handoff_latency(128, 400, 512, 4, 10, A16, A16), 9),
+    (lambda L: L.q8rt_handoff_latency(1, 1, 512, 1, 300, A16, A16), 9),
 ])
 def test_argument_validation_before_any_device_work(Q, call, code):
     lib = Q.load_library()
