@@ -630,6 +630,9 @@ def main() -> int:
                     help="only measure GGUF ingestion: write the synthetic model as a Q8_0 GGUF "
                          "under DIR, read it back into the device layout (cold, then warm page "
                          "cache), upload it, check it bit for bit, print one JSON line")
+    ap.add_argument("--copies", type=int, default=3,
+                    help="identical weight copies the sweep and vocab steps take in turn (the "
+                         "MALL holds none of a copy by its next turn)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline sample budget")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--per-phase-only", action="store_true",
@@ -688,29 +691,46 @@ def run(Q, S, O, info, args) -> int:
 
     # ---------------------------------------------------------------- inputs
     t0 = time.time()
-    sw = S.build(SEED)
+    sw = S.build(SEED, copies=args.copies)
     layers = S.LAYERS
     sweep_bytes = sw.bytes_per_step
-    log(f"sweep inputs ready in {time.time() - t0:.1f}s: {sw.weight_bytes} weight bytes, "
-        f"{sweep_bytes} algorithmic bytes per step")
+    log(f"sweep inputs ready in {time.time() - t0:.1f}s: {sw.weight_bytes} weight bytes "
+        f"(x {sw.n_copies} copies), {sweep_bytes} algorithmic bytes per step")
     stream = Q.Stream()
 
     copy_cal = copy_calibration(Q, stream, args.copy_calibration)
 
     # ------------------------------------------- headline: batched sweep
-    batch = sw.batch()
-    launch = lambda: batch.launch(stream)  # noqa: E731
+    # Step i reads weight copy i mod copies: the MALL (256 MB) cannot hold a
+    # copy until its next turn, (copies - 1) x 437 MB later.
+    batches = [sw.batch(c) for c in range(sw.n_copies)]
+    turn = [0]
+
+    def launch():
+        batches[turn[0] % len(batches)].launch(stream)
+        turn[0] += 1
+
     warm_calls = warm(stream, launch, args.warmup)
     t_wall = time.perf_counter()
     th = timed(Q, stream, launch, args.steps)
     wall_s = time.perf_counter() - t_wall
     ms_per_step = th["mean_ms"]
     value = sweep_bytes / (ms_per_step * 1e-3) / 1e9
-    log(f"batched sweep: {ms_per_step * 1e3:.2f} us/step (median of {th['blocks']} blocks "
-        f"{th['median_ms'] * 1e3:.2f}, after {warm_calls} warm-up launches), {value:.1f} GB/s "
-        f"({100 * value / HBM_PEAK_GBS:.1f}% of peak); host wall {wall_s:.3f}s")
+    log(f"batched sweep ({sw.n_copies} weight copies in turn): {ms_per_step * 1e3:.2f} us/step "
+        f"(median of {th['blocks']} blocks {th['median_ms'] * 1e3:.2f}, after {warm_calls} "
+        f"warm-up launches), {value:.1f} GB/s ({100 * value / HBM_PEAK_GBS:.1f}% of peak); host "
+        f"wall {wall_s:.3f}s")
+    # the same launches always on one copy (each step re-reads what the last
+    # one read, 437 MB earlier): what the memory-side cache adds
+    batch = batches[0]
+    one_copy = lambda: batch.launch(stream)  # noqa: E731
+    warm(stream, one_copy, 10)
+    t1 = timed(Q, stream, one_copy, max(50, args.steps // 4))
+    log(f"  the same on one copy: {t1['mean_ms'] * 1e3:.2f} us/step "
+        f"({sweep_bytes / t1['mean_ms'] / 1e6:.1f} GB/s)")
 
-    # the same kernel after a MALL scrub (A/B with per-launch events)
+    # the kernel alone after a MALL scrub (A/B with per-launch events)
+    launch = one_copy
     scrub = (Q.DeviceBuffer(SCRUB_BYTES), SCRUB_BYTES)
     scrub[0].fill(0)
     sweep_scrub = scrub_ab(Q, stream, launch, scrub, args.scrub_launches)
@@ -720,7 +740,8 @@ def run(Q, S, O, info, args) -> int:
     if args.scrub_only:
         from qwen3_iree_amd import weights as Wt
 
-        batch.free()
+        for b in batches:
+            b.free()
         sw.free()
         Wv = Wt.synthetic_f16_matrix(Q.VOCAB_ROWS, Q.HIDDEN, seed=SEED, tensor=24, workers=16)
         wv_dev = Q.DeviceBuffer.from_array(Wv)
@@ -749,7 +770,7 @@ def run(Q, S, O, info, args) -> int:
         floor += rep["on_floor"]
     log(f"parity: {fails} failing outputs of {sw.outputs} ({floor} on the noise floor)")
 
-    batch_grid = min(batch.total_units, 12 * info["compute_units"]) * 64
+    batch_grid = min(batch.total_units, 10 * info["compute_units"]) * 64
     traffic = profiled_traffic("q8gemv_batch_k", batch_grid)
     if traffic["stale"]:
         log("profiles/traffic.json was taken on another build of q8gemv_batch_k (digest "
@@ -769,7 +790,10 @@ def run(Q, S, O, info, args) -> int:
         "data": "synthetic (seeded N(0,0.02) weights quantized to Q8_0, N(0,1) f16 x)",
         "config": {
             "workload": "28-layer stacked cold-cache Q8_0 GEMV sweep: per layer attn_q, attn_kv, "
-                        "attn_o, gate_up, ffn_dn (140 GEMVs), one batched launch per step",
+                        "attn_o, gate_up, ffn_dn (140 GEMVs), one batched launch per step; "
+                        f"steps take {sw.n_copies} identical weight copies in turn, so no step "
+                        "finds its weights in the 256 MB MALL",
+            "weight_copies": sw.n_copies,
             "layers": layers,
             "gemvs_per_step": len(sw.order),
             "weight_bytes": sw.weight_bytes,
@@ -798,11 +822,14 @@ def run(Q, S, O, info, args) -> int:
             "profiled_mean_us": traffic.get("profiled_mean_us"),
             "scrubbed_us": sweep_scrub["scrubbed_us"],
             "scrub_ab": sweep_scrub,
+            "one_copy_us": round(t1["mean_ms"] * 1e3, 2),
+            "one_copy_frac": round(sweep_bytes / t1["mean_ms"] / 1e6 / HBM_PEAK_GBS, 4),
         },
         "parity_ok": fails == 0,
         "copy_calibration": copy_cal,
     }
-    batch.free()
+    for b in batches:
+        b.free()
     if args.sweep_only:
         print(json.dumps(headline), flush=True)
         sw.free()
@@ -810,11 +837,19 @@ def run(Q, S, O, info, args) -> int:
         return 0
 
     # ------------------------------- the same sweep as 140 dispatches
+    # (the weight copies in turn, as above)
+    chain_turn = [0]
     if args.no_graph:
-        chain_fn = lambda: sw.record_dispatches(stream)  # noqa: E731
+        def chain_fn():
+            sw.record_dispatches(stream, chain_turn[0] % sw.n_copies)
+            chain_turn[0] += 1
     else:
-        graph = Q.Graph(stream, lambda: sw.record_dispatches(stream))
-        chain_fn = lambda: graph.launch(stream)  # noqa: E731
+        graphs = [Q.Graph(stream, lambda c=c: sw.record_dispatches(stream, c))
+                  for c in range(sw.n_copies)]
+
+        def chain_fn():
+            graphs[chain_turn[0] % len(graphs)].launch(stream)
+            chain_turn[0] += 1
     warm(stream, chain_fn, 3)
     tc = timed(Q, stream, chain_fn, max(10, args.steps // 4))
     chain_ms = tc["mean_ms"]
@@ -842,7 +877,8 @@ def run(Q, S, O, info, args) -> int:
     t0 = time.time()
     Wv = Wt.synthetic_f16_matrix(Q.VOCAB_ROWS, Q.HIDDEN, seed=SEED, tensor=24, workers=16)
     xv = Wt.synthetic_x(Q.HIDDEN, SEED, index=9999)
-    wv_dev = Q.DeviceBuffer.from_array(Wv)
+    wv_devs = [Q.DeviceBuffer.from_array(Wv) for _ in range(args.copies)]  # identical copies
+    wv_dev = wv_devs[0]
     xv_dev = Q.DeviceBuffer.from_array(xv)
     logits_dev = Q.DeviceBuffer(2 * Q.VOCAB_ROWS)
     tok_dev = Q.DeviceBuffer(16)
@@ -851,17 +887,26 @@ def run(Q, S, O, info, args) -> int:
     log(f"vocab inputs ready in {time.time() - t0:.1f}s")
     vocab_bytes = Q.VOCAB.bytes_per_layer + 2 * Q.HIDDEN + 2 * Q.VOCAB_ROWS + 4
     vocab_fn = lambda: Q.vocab_gemv_argmax(wv_dev, xv_dev, logits_dev, tok_dev, ws, stream)  # noqa: E731
+    vturn = [0]
+
+    def vocab_turns():  # the copies in turn, as the sweep
+        Q.vocab_gemv_argmax(wv_devs[vturn[0] % len(wv_devs)], xv_dev, logits_dev, tok_dev, ws,
+                            stream)
+        vturn[0] += 1
+
+    warm(stream, vocab_turns, 5)
+    tv = timed(Q, stream, vocab_turns, 200)
     warm(stream, vocab_fn, 5)
-    tv = timed(Q, stream, vocab_fn, 200)
+    tv1 = timed(Q, stream, vocab_fn, 100)
     v_ms = tv["mean_ms"]
     v_gbs = vocab_bytes / (v_ms * 1e-3) / 1e9
     token = int(tok_dev.download(np.int32, 1)[0])
     logits = logits_dev.download(np.float16, Q.VOCAB_ROWS)
     rep_v = O.gemv_tolerance_report(logits, O.f16_gemv(Wv, xv), O.f16_gemv_f64(Wv, xv)[1])
     own = O.argmax_tiled(logits)
-    log(f"vocab GEMV + argmax: {v_ms * 1e3:.2f} us/op (median {tv['median_ms'] * 1e3:.2f}), "
-        f"{v_gbs:.0f} GB/s, token {token} (argmax of own logits {own}, {rep_v['fail']} failing "
-        f"logits)")
+    log(f"vocab GEMV + argmax ({len(wv_devs)} matrix copies in turn): {v_ms * 1e3:.2f} us/op "
+        f"(median {tv['median_ms'] * 1e3:.2f}), {v_gbs:.0f} GB/s, token {token} (argmax of own "
+        f"logits {own}, {rep_v['fail']} failing logits); one copy {tv1['mean_ms'] * 1e3:.2f} us")
     vocab_scrub = scrub_ab(Q, stream, vocab_fn, scrub, args.scrub_launches)
     log(f"vocab GEMV kernel alone: {vocab_scrub['unscrubbed_us']} us, after a MALL scrub "
         f"{vocab_scrub['scrubbed_us']} us (ratio {vocab_scrub['ratio']})")
@@ -893,7 +938,7 @@ def run(Q, S, O, info, args) -> int:
     decode_bytes = (sum(S.algorithmic_bytes(d) for d in Q.LAYER_ORDER) * layers + vocab_bytes)
     log(f"decode-step GEMVs (28 x [q8gemv_qkv, o, gate_up, down] + vocab, 114 dispatches): "
         f"{decode_gemv_us:.1f} us, {decode_bytes / decode_gemv_us / 1e3:.0f} GB/s")
-    for b in (wv_dev, xv_dev, logits_dev, tok_dev, ws, v_dev, *step_y.values(), scrub[0]):
+    for b in (*wv_devs, xv_dev, logits_dev, tok_dev, ws, v_dev, *step_y.values(), scrub[0]):
         b.free()
     kernels = {
         "per_dispatch_sweep": {"us": round(chain_ms * 1e3, 1),
@@ -907,6 +952,7 @@ def run(Q, S, O, info, args) -> int:
         "vocab": {"us": round(v_ms * 1e3, 2), "median_us": round(tv["median_ms"] * 1e3, 2),
                   "GBps": round(v_gbs, 1), "frac": round(v_gbs / HBM_PEAK_GBS, 4),
                   "bytes": vocab_bytes, "token": token, "parity_ok": rep_v["fail"] == 0 and token == own,
+                  "weight_copies": len(wv_devs), "one_copy_us": round(tv1["mean_ms"] * 1e3, 2),
                   "scrub_ab": vocab_scrub},
         "decode_step_gemv": {"us": round(decode_gemv_us, 2), "bytes": decode_bytes,
                              "GBps": round(decode_bytes / decode_gemv_us / 1e3, 1),

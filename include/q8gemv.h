@@ -233,11 +233,11 @@ int q8gemv_hal_dispatch_grid(int ordinal, const void* binding0, const void* bind
 /* ---- launch-shape tuning (no reference counterpart) ---- */
 
 /* Upper bound on the workgroups (one wave each) of a batched Q8_0 launch;
- * 0 = default (12 per compute unit).  A launch never uses more workgroups than
+ * 0 = default (10 per compute unit).  A launch never uses more workgroups than
  * it has work units.  (A single GEMV always runs one wave per row quad.) */
 int q8gemv_batch_set_workgroups(int workgroups);
 /* Workgroups (256 threads) of the vocab kernel, 1..8192; 0 = default
- * (4 per compute unit). */
+ * (1 per compute unit). */
 int vocab_set_workgroups(int workgroups);
 int vocab_get_workgroups(int* workgroups);
 

@@ -5,6 +5,12 @@ Five stacked weight sets [28, BPL] (attn_q, attn_kv, attn_o, gate_up, ffn_dn;
 GEMVs in that order (the per-layer dispatch order of model/qwen3_full.mlir:
 751-864, one attn_kv for k and v), 140 GEMVs, each with its own f16 x and y.
 Built once here so the benchmark and the parity tests use the same table.
+
+With copies > 1 the weights are uploaded that many times (byte-identical, the
+same x and y): a benchmark that takes the copies in turn reads each byte again
+only after (copies - 1) x 437 MB of other weights, so the memory-side cache
+(MALL, 256 MB) holds none of it -- a sweep from HBM, whatever the cache's
+replacement policy.
 """
 from __future__ import annotations
 
@@ -33,6 +39,7 @@ class Sweep:
     dev_x: dict             # (layer, kind) -> DeviceBuffer
     dev_y: dict             # (layer, kind) -> DeviceBuffer (f16 [N])
     order: list = field(default_factory=list)  # [(layer, Dispatch)] in sweep order
+    copies: list = field(default_factory=list)  # dev_w of copies 1.. (kind -> DeviceBuffer)
 
     @property
     def weight_bytes(self) -> int:
@@ -46,29 +53,40 @@ class Sweep:
     def outputs(self) -> int:
         return sum(d.n for _, d in self.order)
 
-    def descs(self) -> list:
-        return [Q.desc_for_kind(d.kind, self.dev_w[d.kind], layer, self.dev_x[(layer, d.kind)],
+    @property
+    def n_copies(self) -> int:
+        return 1 + len(self.copies)
+
+    def weights(self, copy: int = 0) -> dict:
+        return self.dev_w if copy == 0 else self.copies[copy - 1]
+
+    def descs(self, copy: int = 0) -> list:
+        w = self.weights(copy)
+        return [Q.desc_for_kind(d.kind, w[d.kind], layer, self.dev_x[(layer, d.kind)],
                                 self.dev_y[(layer, d.kind)]) for layer, d in self.order]
 
-    def batch(self) -> "Q.Q8Batch":
+    def batch(self, copy: int = 0) -> "Q.Q8Batch":
         """The whole sweep as one batched launch (entries in sweep order)."""
-        return Q.Q8Batch(self.descs())
+        return Q.Q8Batch(self.descs(copy))
 
-    def record_dispatches(self, stream=None) -> None:
+    def record_dispatches(self, stream=None, copy: int = 0) -> None:
         """The sweep as 140 stream-ordered dispatches of the per-GEMV entry."""
+        w = self.weights(copy)
         for layer, d in self.order:
-            Q.q8gemv(d.kind, self.dev_w[d.kind], layer, self.dev_x[(layer, d.kind)],
+            Q.q8gemv(d.kind, w[d.kind], layer, self.dev_x[(layer, d.kind)],
                      self.dev_y[(layer, d.kind)], stream)
 
     def free(self) -> None:
-        for b in (*self.dev_w.values(), *self.dev_x.values(), *self.dev_y.values()):
+        for b in (*self.dev_w.values(), *self.dev_x.values(), *self.dev_y.values(),
+                  *(b for c in self.copies for b in c.values())):
             b.free()
 
 
-def build(seed: int, workers: int = 16) -> Sweep:
+def build(seed: int, workers: int = 16, copies: int = 1) -> Sweep:
     """Seeded sweep inputs resident on the device: W_kind ~ N(0, 0.02)
     quantised by the reference quantizer (one stream per (seed, kind, layer)),
-    x = f16(N(0, 1)) with index layer * 8 + kind."""
+    x = f16(N(0, 1)) with index layer * 8 + kind; the weights in `copies`
+    identical device copies."""
     host_w, dev_w = {}, {}
     for d in KINDS:
         host = Wt.synthetic_q8_stack(d.n, d.k, LAYERS, seed=seed, tensor=d.kind, workers=workers)
@@ -82,4 +100,5 @@ def build(seed: int, workers: int = 16) -> Sweep:
             dev_x[(layer, d.kind)] = Q.DeviceBuffer.from_array(x)
             dev_y[(layer, d.kind)] = Q.DeviceBuffer(2 * d.n)
     order = [(layer, d) for layer in range(LAYERS) for d in KINDS]
-    return Sweep(seed, host_w, dev_w, host_x, dev_x, dev_y, order)
+    more = [{k: Q.DeviceBuffer.from_array(host_w[k]) for k in host_w} for _ in range(copies - 1)]
+    return Sweep(seed, host_w, dev_w, host_x, dev_x, dev_y, order, more)
