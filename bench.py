@@ -64,6 +64,13 @@ MIN_WARM_MS = 200.0
 TIMING_BLOCKS = 10
 EOS_TOKEN = 151645   # scripts/benchmark.py:21
 MAX_NEW_TOKENS = 128  # scripts/benchmark.py:22
+IM_START = 151644     # <|im_start|>; <|im_end|> is EOS_TOKEN
+# Lengths of the ten chat prompts of scripts/benchmark.py:8-19 under its template
+# `<|im_start|>user\n{text}<|im_end|>\n<|im_start|>assistant\n` (:53): 8 template
+# tokens + the text's.  No tokenizer files exist here, so the text counts are
+# estimates (one token per word, digit and punctuation mark), and the token ids
+# are synthetic.
+REFERENCE_PROMPT_TOKENS = (9, 15, 10, 15, 15, 15, 16, 18, 20, 22)
 
 
 def log(msg: str) -> None:
@@ -285,7 +292,7 @@ def bench_decode(Q, O, stream, args) -> dict:
     D.set_step_mode(default_mode)
     sess.free()
     model.free()
-    cal = calibration(Q)
+    cal = None if args.no_calibration else calibration(Q)
     best = ts if ts is not None else tp
     best_us = best["mean_ms"] * 1e3
     best_gbs = dec_bytes / best_us / 1e3
@@ -504,10 +511,58 @@ def bench_generate(Q, stream, args) -> dict:
             f"-> {rec['tok_per_s']:.0f} tok/s ({n_out} tokens before EOS), token loop "
             f"{rec['loop_ms_per_token']:.4f} ms/token, parity {rec['parity_ok']}")
         out[name] = rec
+    out["reference_protocol"] = reference_protocol(D, model, stream, rng)
     model.free()
     out["reference_published"] = {"tok_per_s": 25.52, "where": "Jetson AGX Orin, "
                                   "benchmark.json:71-72 (other hardware)"}
     return out
+
+
+def reference_protocol(D, model, stream, rng) -> dict:
+    """The reference's end-to-end protocol (scripts/benchmark.py:52-81,
+    137-155, 203-214): ten chat prompts, one timed `run` each (wall time of
+    the call: prompt ingestion + up to 128 tokens with the EOS check every 4),
+    tok/s per prompt = tokens before EOS / that time, then the mean and the
+    population standard deviation; the record repeats the reference's JSON
+    schema {variant: {tps, mean, std, prompts}}.  The prompts are synthetic
+    ids in the chat template's shape (im_start, 2 role tokens, the text,
+    im_end, newline, im_start, 2 role tokens) at the lengths of
+    REFERENCE_PROMPT_TOKENS.  Parity: each timed run gives the tokens of an
+    untimed run of the same prompt made before it."""
+    prompts = []
+    for n in REFERENCE_PROMPT_TOKENS:
+        ids = rng.integers(0, D.VOCAB - 2, n).astype(np.int32)
+        ids[0] = IM_START
+        ids[n - 5] = EOS_TOKEN   # <|im_end|> closes the user turn
+        ids[n - 3] = IM_START
+        prompts.append(ids)
+    want = [D.run(model, p, MAX_NEW_TOKENS, EOS_TOKEN, stream) for p in prompts]
+    t_end = time.perf_counter() + MIN_WARM_MS / 1e3
+    while time.perf_counter() < t_end:
+        D.run(model, prompts[0], MAX_NEW_TOKENS, EOS_TOKEN, stream)
+    tps, ms, outs, ok = [], [], [], True
+    for p, w in zip(prompts, want):
+        t0 = time.perf_counter()
+        got = D.run(model, p, MAX_NEW_TOKENS, EOS_TOKEN, stream)
+        dt = time.perf_counter() - t0
+        toks = got.tolist()
+        n_out = toks.index(EOS_TOKEN) if EOS_TOKEN in toks else len(toks)
+        ok = ok and toks == w.tolist()
+        tps.append(n_out / dt)
+        ms.append(round(dt * 1e3, 3))
+        outs.append(n_out)
+    mean, std = float(np.mean(tps)), float(np.std(tps))
+    log(f"generate (reference protocol, 10 chat prompts of {min(REFERENCE_PROMPT_TOKENS)}-"
+        f"{max(REFERENCE_PROMPT_TOKENS)} tokens + {MAX_NEW_TOKENS}): {mean:.1f} +- {std:.1f} "
+        f"tok/s, parity {ok}")
+    return {"mi355x_hip": {"tps": [round(t, 2) for t in tps], "mean": round(mean, 2),
+                           "std": round(std, 2),
+                           "prompts": [f"synthetic chat prompt, {n} tokens"
+                                       for n in REFERENCE_PROMPT_TOKENS]},
+            "prompt_tokens": list(REFERENCE_PROMPT_TOKENS), "tokens_out": outs, "run_ms": ms,
+            "warm_up_ms": MIN_WARM_MS, "parity_ok": bool(ok),
+            "reference_published": {"mean": 25.52, "std": 1.72,
+                                    "where": "Jetson AGX Orin, benchmark.json:71-72"}}
 
 
 def bench_gguf(Q, tmpdir: Path) -> dict:
@@ -638,6 +693,9 @@ def main() -> int:
     ap.add_argument("--per-phase-only", action="store_true",
                     help="decode step: time only the per-phase launches, not the single "
                          "launch (traces of the per-phase kernels alone)")
+    ap.add_argument("--no-calibration", action="store_true",
+                    help="decode step: skip the launch-cost and hand-off measurements (their "
+                         "cooperative launches are kept out of profiler runs)")
     ap.add_argument("--no-graph", action="store_true",
                     help="issue the per-dispatch and decode-step chains eagerly instead of from hipGraphs")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",

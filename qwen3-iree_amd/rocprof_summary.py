@@ -78,9 +78,12 @@ def main() -> int:
     write = counter_values(args.write, "WRITE_SIZE") if args.write else {}
 
     def scale(values: dict) -> float | None:
-        copy = [v for (name, _), vs in values.items() if name == "stream_copy_b128" for v in vs]
-        if not copy or not args.copy_bytes:
+        # the calibration copy: the stream_copy_b128 launches of the largest grid
+        # (bench.py also launches it empty, one workgroup, to time dispatches)
+        grids = [g for (name, g) in values if name == "stream_copy_b128"]
+        if not grids or not args.copy_bytes:
             return None
+        copy = values[("stream_copy_b128", max(grids))]
         return args.copy_bytes / 1024.0 / statistics.mean(copy)
 
     fs, ws = scale(fetch), scale(write)
