@@ -445,7 +445,11 @@ struct __attribute__((aligned(16))) AttnLds {
 // workgroup calls it once, and pre_qkv() once before any load of this
 // function (where get_qkv's requests can start early).
 // cs, sn: rope_angles of the clamped position.
-template <class PreQKV, class GetQKV, class Publish>
+// stamp(k) marks points 16-20 for a timestamp build (NoStamp: nothing).
+struct NoStamp {
+  __device__ void operator()(int) const {}
+};
+template <class PreQKV, class GetQKV, class Publish, class Stamp = NoStamp>
 __device__ __forceinline__ void attention_group(AttnLds& L, int g, int sg, int pos_raw,
                                                 const float (&cs)[2], const float (&sn)[2],
                                                 int max_seq, const uint16_t* __restrict__ qn_w,
@@ -454,7 +458,8 @@ __device__ __forceinline__ void attention_group(AttnLds& L, int g, int sg, int p
                                                 uint16_t* __restrict__ v_cache,
                                                 uint16_t* __restrict__ q_roped,
                                                 uint8_t* kv, bool kv_staged, PreQKV&& pre_qkv,
-                                                GetQKV&& get_qkv, Publish&& publish) {
+                                                GetQKV&& get_qkv, Publish&& publish,
+                                                Stamp stamp = Stamp()) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int s = sg * kAttnWaves + wave;
@@ -529,6 +534,7 @@ __device__ __forceinline__ void attention_group(AttnLds& L, int g, int sg, int p
   } else if (owns_pos) {
     reinterpret_cast<uint32_t*>(v_cache + ((size_t)pos * kKvHeads + g) * kHeadDim)[lane] = v_new;
   }
+  stamp(16);
   __syncthreads();
 
   // ---- 3. per chunk (this wave's LDS region), transposed on the matrix
@@ -584,6 +590,7 @@ __device__ __forceinline__ void attention_group(AttnLds& L, int g, int sg, int p
         sc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[st], sc[nt], 0, 0, 0);
       }
     }
+    stamp(17);
     // s[4 nt + e]: position c0 + 16 nt + 4 grp + e; past the split: -inf
     float s[8];
 #pragma unroll
@@ -609,6 +616,7 @@ __device__ __forceinline__ void attention_group(AttnLds& L, int g, int sg, int p
     m = mn;
 #pragma unroll
     for (int d = 0; d < 8; ++d) o[d] *= alpha;
+    stamp(18);
     // the K region is free once its reads have returned: the next chunk's K
     wait_lds();
     if (c + 1 < n_chunks) {
@@ -647,6 +655,7 @@ __device__ __forceinline__ void attention_group(AttnLds& L, int g, int sg, int p
       kv_stage_v(kv, v_cache, g, c0 + 32, last);
     }
   }
+  stamp(19);
   l = sum_col4(l);
 
   // ---- 4. the four waves' results -> one partial per query head ----
@@ -660,6 +669,7 @@ __device__ __forceinline__ void attention_group(AttnLds& L, int g, int sg, int p
       *reinterpret_cast<f32x4*>(&L.mrg[wave][c16][4 + 16 * d + 4 * grp]) = o[d];
   }
   __syncthreads();
+  stamp(20);
   if (wave < 2) {  // wave hh merges query head 2g + hh
     const int hh = wave;
     float M = -__builtin_inff();

@@ -390,7 +390,7 @@ struct StepParams {
   uint32_t* last_started;   // sequence number of the launch whose last workgroup started
   uint32_t* status;
   uint16_t* on_out;         // the final rms_norm(h, output_norm) (f16[1024])
-  uint64_t* stamps;         // timestamp build only (DEC_STEP_STAMPS): per-phase clock reads
+  uint32_t* stamps;         // timestamp build only (DEC_STEP_STAMPS): per-phase clock reads
   int max_seq;
   int advance;
   int head;                 // 0: no vocab / argmax (a prompt step); pos still advances
@@ -566,11 +566,13 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
 // listed in stamp_slot reads the 100 MHz real-time counter at the phase
 // boundaries below into LDS (its low 32 bits: differences stay exact for 42
 // s), [layer 0..27, or 28 for the vocab phase][point], and copies them to
-// P.stamps[slot][29][16] (u64, zero-extended) at the end.
+// P.stamps[slot][29][21] (u32) at the end.
 //   per layer: 0 layer start, 1 h ready (A), 13 x normalised (A), 2 q/k/v
 //   published, 15 gate/up weights requested (D), 9 residual ready (D), 10
-//   SwiGLU published, 3 q/k/v ready (B),
-//   4 partial published, 5 partials ready (merge), 6 attention output
+//   SwiGLU published, 3 q/k/v ready (B), inside B's attention_group: 16
+//   head norms + RoPE done, 17 score MFMAs issued, 18 softmax done, 19
+//   chunk loop done, 20 the four waves' results in LDS (after the
+//   barrier), then 4 partial published, 5 partials ready (merge), 6 attention output
 //   published, 14 h rows ready (C), 7 attention output ready (C), 8 residual
 //   published, 11 SwiGLU ready (E), 12 h published
 //   vocab: 0 start, 1 h ready, 2 key published, 3 keys ready (wg 0), 4 token
@@ -579,7 +581,7 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
 #endif
 constexpr int kStampWgs[16] = {0,   1,   100, 191, 192, 255, 256, 257,
                                264, 319, 320, 321, 383, 384, 446, 447};
-constexpr int kStampPoints = 16;
+constexpr int kStampPoints = 21;
 __device__ __forceinline__ int stamp_slot(int wg) {
 #pragma unroll
   for (int i = 0; i < 16; ++i)
@@ -866,7 +868,18 @@ void dec_step(StepParams P) {
             }
             put_word(d + 2 + 2 * lane, __builtin_bit_cast(uint32_t, a0), tp);
             put_word(d + 3 + 2 * lane, __builtin_bit_cast(uint32_t, a1), tp);
-          });
+          },
+#if DEC_STEP_STAMPS
+          // the timestamp build's points inside the attention (kept in place)
+          [&](int k) {
+            __builtin_amdgcn_sched_barrier(0);
+            STAMP(layer, k);
+            __builtin_amdgcn_sched_barrier(0);
+          }
+#else
+          NoStamp()
+#endif
+      );
       if (!ok) {
         wait_vm<0>();  // attention_group's copies after the failed wait
         return;

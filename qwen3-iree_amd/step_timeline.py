@@ -31,7 +31,9 @@ PKG = Path(__file__).resolve().parent
 REPO = PKG.parent
 
 POINTS = {0: "layer start", 1: "A: h ready", 13: "A: x normalised", 2: "A: q/k/v published",
-          3: "B: q/k/v ready", 4: "B: partial published", 5: "merge: partials ready",
+          3: "B: q/k/v ready", 16: "B: head norms + RoPE done", 17: "B: score MFMAs issued",
+          18: "B: softmax done", 19: "B: chunk loop done", 20: "B: four waves merged in LDS",
+          4: "B: partial published", 5: "merge: partials ready",
           6: "merge: attention published", 14: "C: h rows ready",
           7: "C: attention ready", 8: "C: residual published",
           15: "D: gate/up weights requested", 9: "D: residual ready",
@@ -40,6 +42,7 @@ VOCAB_POINTS = {0: "vocab start", 1: "vocab: h ready", 2: "vocab: key published"
                 3: "keys ready (wg 0)", 4: "token written (wg 0)"}
 STAMP_WGS = (0, 1, 100, 191, 192, 255, 256, 257, 264, 319, 320, 321, 383, 384, 446, 447)
 TICK_US = 0.01  # s_memrealtime: 100 MHz
+N_POINTS = 21    # kStampPoints
 
 
 def build_stamped(dst: Path) -> Path:
@@ -97,9 +100,9 @@ def main() -> int:
     e1.synchronize()
     step_us = e0.elapsed_ms(e1) * 1e3 / args.steps
     sess.check_status()
-    raw = sess.scratch.download(np.uint64, 16 * 29 * 16, D.scratch_offset("part"))
+    raw = sess.scratch.download(np.uint32, 16 * 29 * N_POINTS, D.scratch_offset("part"))
     # 32-bit clock reads: unwrap against workgroup 0's first stamp (0 = not reached)
-    lo = (raw & 0xFFFFFFFF).astype(np.int64).reshape(16, 29, 16)
+    lo = raw.astype(np.int64).reshape(16, 29, N_POINTS)
     ref = lo[0, 0, 0]
     st = np.where(lo != 0, ref + ((lo - ref + (1 << 31)) % (1 << 32)) - (1 << 31), 0)
     t0 = st[0, 0, 0]
