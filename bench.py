@@ -928,6 +928,36 @@ def run(Q, S, O, info, args) -> int:
     tf = timed(Q, stream, floor_fn, max(10, args.steps // 4))
     floor_us = tf["mean_ms"] * 1e3
     log(f"  its floor, 140 empty launches the same way: {floor_us:.1f} us")
+    # the same 140 GEMVs through the reference's HAL binding ABI (the kernels an
+    # IREE executable substitution would launch), outputs checked against the
+    # C-ABI dispatches' bit for bit
+    hal_binds = sw.hal_bindings()
+    hal_turn = [0]
+    if args.no_graph:
+        def hal_fn():
+            sw.record_hal_dispatches(hal_binds, stream, hal_turn[0] % sw.n_copies)
+            hal_turn[0] += 1
+    else:
+        hgraphs = [Q.Graph(stream, lambda c=c: sw.record_hal_dispatches(hal_binds, stream, c))
+                   for c in range(sw.n_copies)]
+
+        def hal_fn():
+            hgraphs[hal_turn[0] % len(hgraphs)].launch(stream)
+            hal_turn[0] += 1
+    warm(stream, hal_fn, 3)
+    th = timed(Q, stream, hal_fn, max(10, args.steps // 4))
+    hal_us = th["mean_ms"] * 1e3
+    sw.record_dispatches(stream)
+    stream.synchronize()
+    hal_same = all(np.array_equal(
+        b2.download(np.uint16, d.n, y_off),
+        sw.dev_y[(layer, d.kind)].download(np.uint16, d.n))
+        for (layer, d), (_, b2, y_off) in ((k, hal_binds[(k[0], k[1].kind)]) for k in sw.order))
+    log(f"  through the HAL binding ABI (q8gemv_hal_dispatch): {hal_us:.1f} us, outputs "
+        f"identical to the C ABI's: {hal_same}")
+    for b1, b2, _ in hal_binds.values():
+        b1.free()
+        b2.free()
 
     # ------------------------------------------------------------- vocab
     from qwen3_iree_amd import weights as Wt
@@ -1005,6 +1035,8 @@ def run(Q, S, O, info, args) -> int:
                                "frac": round(chain_gbs / HBM_PEAK_GBS, 4), "dispatches": 140,
                                "launch": "eager" if args.no_graph else "hipGraph",
                                "floor_us": round(floor_us, 1),
+                               "hal_abi_us": round(hal_us, 1),
+                               "hal_abi_parity_ok": bool(hal_same),
                                "floor": "140 empty launches (one workgroup each), stream-ordered "
                                         "the same way"},
         "vocab": {"us": round(v_ms * 1e3, 2), "median_us": round(tv["median_ms"] * 1e3, 2),
@@ -1032,7 +1064,7 @@ def run(Q, S, O, info, args) -> int:
     gen_ok = all(v.get("parity_ok", True) for v in gen.values() if isinstance(v, dict))
 
     parity_ok = (fails == 0 and rep_v["fail"] == 0 and token == own and dec["parity_ok"]
-                 and pre["parity_ok"] and gen_ok)
+                 and pre["parity_ok"] and gen_ok and hal_same)
 
     # ------------------------------------------------------ CPU baseline
     cpu = None if args.no_cpu else cpu_baseline(O, sw, args)

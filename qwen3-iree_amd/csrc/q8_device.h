@@ -69,6 +69,18 @@ __device__ __forceinline__ void wait_vm() {
 // lgkmcnt(0): every LDS read of the wave has returned its data
 __device__ __forceinline__ void wait_lds() { __builtin_amdgcn_s_waitcnt(0xc07f); }
 
+// The launch's workgroup size and count in x, from the hidden kernel
+// arguments (code object v5: block counts at bytes 0, 4, 8, group sizes as
+// u16 at 12, 14, 16), with scalar loads.  blockDim.x compiles to a 16-bit
+// vector load (it allows for a partial last workgroup, which these launches
+// never have) whose wait would come before a kernel's first weight loads.
+__device__ __forceinline__ uint32_t launch_wg_size() {
+  return reinterpret_cast<const uint32_t*>(__builtin_amdgcn_implicitarg_ptr())[3] & 0xffffu;
+}
+__device__ __forceinline__ uint32_t launch_wgs() {
+  return reinterpret_cast<const uint32_t*>(__builtin_amdgcn_implicitarg_ptr())[0];
+}
+
 template <bool NT>
 __device__ __forceinline__ u32x4 load_stream(const u32x4* p) {
   const GLOBAL_AS u32x4* g = (const GLOBAL_AS u32x4*)p;
@@ -578,9 +590,9 @@ __device__ __forceinline__ void vocab_body_xp(const uint16_t* __restrict__ W, XL
   const int li = lane & 15;
   // full waves of the grid (a partial last wave of an odd-sized workgroup
   // takes no rows)
-  const int64_t wpb = blockDim.x >> 6;
+  const int64_t wpb = launch_wg_size() >> 6;
   const int64_t gw = (int64_t)blockIdx.x * wpb + wave;
-  const int64_t tw = (int64_t)(groups > 0 ? groups : (int)gridDim.x) * wpb;
+  const int64_t tw = (int64_t)(groups > 0 ? groups : (int)launch_wgs()) * wpb;
   const int64_t nbatch = ((int64_t)n_rows + 3) / 4;
   // a wave of workgroups 0 .. heavy_wgs - 1 takes heavy_w16 / 16 times the
   // batches of any other wave

@@ -247,17 +247,17 @@ extern "C" __global__ __launch_bounds__(256) void calib_handoff(HandoffArgs a) {
 // on the workgroup only), so the barriers inside q8_quad_core match; a wave
 // without a quad in the last round recomputes the last quad and stores
 // nothing.
+// waves: full waves per workgroup; wgs: workgroups of the launch.
 template <int P>
 __device__ __forceinline__ void hal_q8_quads(const uint8_t* __restrict__ w,
                                              const uint16_t* __restrict__ x,
                                              uint16_t* __restrict__ y, int n_rows,
-                                             uint8_t* __restrict__ lds) {
-  const int waves = (int)(blockDim.x >> 6);
+                                             uint8_t* __restrict__ lds, int waves, int wgs) {
   if (waves == 0) return;
   const int wave = threadIdx.x >> 6;
   const int nq = (n_rows + 3) / 4;
   uint8_t* mine = lds + wave * QuadShape<P>::LDS_BYTES;
-  const int step = (int)gridDim.x * waves;
+  const int step = wgs * waves;
   for (int base = (int)blockIdx.x * waves; base < nq; base += step) {
     const int quad = base + wave;
     const bool store = wave < waves && quad < nq;
@@ -275,8 +275,12 @@ __device__ __forceinline__ void hal_q8_quads(const uint8_t* __restrict__ w,
       char* __restrict__ b2, uint32_t c0, uint32_t c1) {                                      \
     __shared__ __attribute__((aligned(16))) uint8_t lds[4 * QuadShape<P>::LDS_BYTES];         \
     const uint64_t layer = (uint64_t)c0 | ((uint64_t)c1 << 32);                               \
-    hal_q8_quads<P>(q8_stacked + layer * (BPL), reinterpret_cast<const uint16_t*>(b1 + (X_OFF)), \
-                    reinterpret_cast<uint16_t*>(b2 + (Y_OFF)), N, lds);                       \
+    const uint8_t* w = q8_stacked + layer * (BPL);                                            \
+    const int waves = (int)(launch_wg_size() >> 6), wgs = (int)launch_wgs();                  \
+    /* every argument is loaded before the first branch (one scalar round trip) */            \
+    asm volatile("" ::"s"(w), "s"(b1), "s"(b2), "s"(waves), "s"(wgs));                        \
+    hal_q8_quads<P>(w, reinterpret_cast<const uint16_t*>(b1 + (X_OFF)),                       \
+                    reinterpret_cast<uint16_t*>(b2 + (Y_OFF)), N, lds, waves, wgs);           \
   }
 
 HAL_Q8_DISPATCH(decode_dispatch_3_matmul_2048x1x1024_f16, 1, 2048, 2228224ULL, 2112, 4160)
@@ -290,8 +294,11 @@ extern "C" __global__ __launch_bounds__(256) void decode_dispatch_4_matmul_1024x
     uint32_t c0, uint32_t c1, uint32_t c2) {
   __shared__ __attribute__((aligned(16))) uint8_t lds[4 * QuadShape<1>::LDS_BYTES];
   const uint64_t layer = (uint64_t)c1 | ((uint64_t)c2 << 32);
-  hal_q8_quads<1>(q8_stacked + layer * 1114112ULL, reinterpret_cast<const uint16_t*>(b1 + 2112),
-                  reinterpret_cast<uint16_t*>(b2 + (int)c0), 1024, lds);
+  const uint8_t* w = q8_stacked + layer * 1114112ULL;
+  uint16_t* y = reinterpret_cast<uint16_t*>(b2 + (int)c0);
+  const int waves = (int)(launch_wg_size() >> 6), wgs = (int)launch_wgs();
+  asm volatile("" ::"s"(w), "s"(b1), "s"(y), "s"(waves), "s"(wgs));  // as in HAL_Q8_DISPATCH
+  hal_q8_quads<1>(w, reinterpret_cast<const uint16_t*>(b1 + 2112), y, 1024, lds, waves, wgs);
 }
 
 // dispatch_24 takes the output byte offset as c0 (logits only; the reference
@@ -300,7 +307,7 @@ extern "C" __global__ __launch_bounds__(256) void decode_dispatch_4_matmul_1024x
 extern "C" __global__ __launch_bounds__(256) void decode_dispatch_24_matmul_151936x1x1024_f16(
     const uint16_t* __restrict__ weight, const char* __restrict__ b1, char* __restrict__ b2,
     uint32_t c0) {
-  if ((blockDim.x >> 6) == 0) return;
+  if ((launch_wg_size() >> 6) == 0) return;
   vocab_body<VOCAB_NT_LOADS != 0, false>(weight, reinterpret_cast<const uint16_t*>(b1 + 64),
                                          reinterpret_cast<uint16_t*>(b2 + (int)c0), 151936,
                                          nullptr);

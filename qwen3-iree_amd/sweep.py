@@ -24,6 +24,14 @@ from . import weights as Wt
 LAYERS = Q.NUM_LAYERS
 KINDS = Q.Q8_KINDS  # per layer: q, kv, o, gate_up, dn
 
+# The reference's baked-in byte offsets of x in binding 1 and y in binding 2
+# per ordinal (kernels/cuda/dispatch_3.cu:19-21, dispatch_4.cu:19-22,
+# dispatch_12.cu:19-21, dispatch_18.cu:19-21, dispatch_20.cu:19-21); dispatch
+# 4 takes its output offset as push constant c0 (HAL_Y_OFF4 here).
+HAL_OFFSETS = {3: (2112, 4160), 4: (2112, None), 12: (12352, 2048), 18: (64, 6144),
+               20: (18432, 0)}
+HAL_Y_OFF4 = 8194
+
 
 def algorithmic_bytes(d) -> int:
     """Weights + x + y of one GEMV, each byte counted once."""
@@ -75,6 +83,31 @@ class Sweep:
         for layer, d in self.order:
             Q.q8gemv(d.kind, w[d.kind], layer, self.dev_x[(layer, d.kind)],
                      self.dev_y[(layer, d.kind)], stream)
+
+    def hal_bindings(self) -> dict:
+        """(layer, kind) -> (binding 1 with x at the reference's offset, binding
+        2 with room for y at its offset, y's byte offset): the buffers an IREE
+        executable substitution would bind."""
+        out = {}
+        for layer, d in self.order:
+            x_off, y_off = HAL_OFFSETS[d.ordinal]
+            if y_off is None:
+                y_off = HAL_Y_OFF4
+            b1 = np.zeros(x_off + 2 * d.k + 64, np.uint8)
+            b1[x_off:x_off + 2 * d.k] = self.host_x[(layer, d.kind)].view(np.uint8)
+            out[(layer, d.kind)] = (Q.DeviceBuffer.from_array(b1),
+                                    Q.DeviceBuffer(y_off + 2 * d.n + 64), y_off)
+        return out
+
+    def record_hal_dispatches(self, binds: dict, stream=None, copy: int = 0) -> None:
+        """The sweep as 140 stream-ordered launches of the reference-named
+        kernels through the HAL binding ABI (q8gemv_hal_dispatch), at this
+        build's stub shape."""
+        w = self.weights(copy)
+        for layer, d in self.order:
+            b1, b2, y_off = binds[(layer, d.kind)]
+            consts = [layer, 0] if d.ordinal != 4 else [y_off, layer, 0]
+            Q.hal_dispatch(d.ordinal, w[d.kind], b1, b2, consts, stream)
 
     def free(self) -> None:
         for b in (*self.dev_w.values(), *self.dev_x.values(), *self.dev_y.values(),
