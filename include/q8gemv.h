@@ -206,6 +206,16 @@ int f16_gemv_argmax_rows(const void* w_f16, int64_t n_rows, const void* x_f16,
 int f16_gemv_argmax_rows_noalloc(const void* w_f16, int64_t n_rows, const void* x_f16,
                                  void* logits_f16, int32_t* token, void* stream);
 
+/* Argmax of n f16 values already in memory (logits of an earlier launch,
+ * such as decode_dispatch_24_matmul_151936x1x1024_f16 through the HAL ABI,
+ * which writes logits only): the reference's tiled argmax as its own pass
+ * (model/qwen3_full.mlir:1469-1511) -- the lowest index of the maximal value,
+ * NaN never winning, -1 if no value wins.  Same workspace rule as
+ * vocab_gemv_argmax (256 bytes, zero between calls; the call leaves it
+ * zero).  n in [1, 2^31), values 16-byte aligned. */
+int f16_argmax(const void* values_f16, int64_t n, int32_t* token, void* workspace,
+               void* stream);
+
 /* ---- the reference's own binding ABI ----
  *
  * The code object also exports the six kernels under the reference's

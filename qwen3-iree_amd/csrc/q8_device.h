@@ -54,6 +54,33 @@ __device__ __forceinline__ f16x2 as_f16x2(uint32_t v) { return __builtin_bit_cas
 #define VOCAB_NT_LOADS 1
 #endif
 
+// Ablation builds (qwen3-iree_amd/ablation.py) replace one design choice of
+// the batched Q8_0 GEMV and of the vocab GEMV with a plain alternative that
+// computes the same outputs, so what each choice is worth can be measured;
+// the product build takes every default.
+//   Q8_LOAD_BYTES 16 | 8 | 4: each lane's 16 bytes of a weight piece read as
+//     one 128-bit load, or as two 64-bit / four 32-bit loads
+//   Q8_X_LDS 1 | 0: x staged once per workgroup in LDS, or read by the wave
+//     from global memory for every unit
+//   Q8_DEQUANT_PACKED 1 | 0: int8 pairs made f16 pairs in registers and
+//     multiplied by v_dot2, or every int8 converted to f32 and multiplied by
+//     f32(x) (same exact products, summed one by one)
+//   Q8_REDUCE_DPP 1 | 0: 16-lane row sums by DPP, or by ds_bpermute shuffles
+//     through the LDS crossbar (same pairs, same bits)
+#ifndef Q8_LOAD_BYTES
+#define Q8_LOAD_BYTES 16
+#endif
+#ifndef Q8_X_LDS
+#define Q8_X_LDS 1
+#endif
+#ifndef Q8_DEQUANT_PACKED
+#define Q8_DEQUANT_PACKED 1
+#endif
+#ifndef Q8_REDUCE_DPP
+#define Q8_REDUCE_DPP 1
+#endif
+static_assert(Q8_LOAD_BYTES == 16 || Q8_LOAD_BYTES == 8 || Q8_LOAD_BYTES == 4, "load width");
+
 // Pointers read from a batch table are generic; accessing them through the
 // global address space keeps the loads global_load (counted by vmcnt alone)
 // rather than flat_load, whose completion the compiler can only await with a
@@ -86,6 +113,44 @@ __device__ __forceinline__ u32x4 load_stream(const u32x4* p) {
   const GLOBAL_AS u32x4* g = (const GLOBAL_AS u32x4*)p;
   if constexpr (NT) return __builtin_nontemporal_load(g);
   else return *g;
+}
+
+// A weight stream's 16 bytes per lane, as Q8_LOAD_BYTES wide loads.
+template <bool NT>
+__device__ __forceinline__ u32x4 load_weights16(const u32x4* p) {
+  if constexpr (Q8_LOAD_BYTES == 16) {
+    return load_stream<NT>(p);
+  } else {
+    // the next part's offset is hidden from the compiler, which would
+    // otherwise merge the parts back into one 128-bit load
+    int k = 1;
+    asm volatile("" : "+v"(k));
+    if constexpr (Q8_LOAD_BYTES == 8) {
+      typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+      const GLOBAL_AS u32x2* g = (const GLOBAL_AS u32x2*)p;
+      u32x2 a, b;
+      if constexpr (NT) {
+        a = __builtin_nontemporal_load(g);
+        b = __builtin_nontemporal_load(g + k);
+      } else {
+        a = g[0];
+        b = g[k];
+      }
+      return (u32x4){a.x, a.y, b.x, b.y};
+    } else {
+      const GLOBAL_AS uint32_t* g = (const GLOBAL_AS uint32_t*)p;
+      u32x4 v;
+      if constexpr (NT) {
+        v.x = __builtin_nontemporal_load(g);
+        v.y = __builtin_nontemporal_load(g + k);
+        v.z = __builtin_nontemporal_load(g + 2 * k);
+        v.w = __builtin_nontemporal_load(g + 3 * k);
+      } else {
+        v = (u32x4){g[0], g[k], g[2 * k], g[3 * k]};
+      }
+      return v;
+    }
+  }
 }
 
 __device__ __forceinline__ u32x4 load_global(const u32x4* p) {
@@ -131,10 +196,20 @@ __device__ __forceinline__ float dpp(float v) {
 // Sum over the 16 lanes of a DPP row; every lane of the row ends with the same
 // value (each step adds a lane and its mirror partner, a symmetric pairing).
 __device__ __forceinline__ float reduce_row16(float v) {
+#if Q8_REDUCE_DPP
   v += dpp<0xB1>(v);   // quad_perm [1,0,3,2]
   v += dpp<0x4E>(v);   // quad_perm [2,3,0,1]
   v += dpp<0x141>(v);  // row_half_mirror
   v += dpp<0x140>(v);  // row_mirror
+#else
+  // the same pairs through ds_bpermute (lane ^ 1, ^ 2; then the quads and
+  // half rows pair as the mirrors pair them)
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int d = 1; d < 16; d <<= 1)
+    v += __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(4 * (lane ^ d),
+                                                                __builtin_bit_cast(int, v)));
+#endif
   return v;
 }
 
@@ -145,6 +220,23 @@ __device__ __forceinline__ float reduce_row16(float v) {
 // Returns fma(f32(scale1), dot1, f32(scale0)*dot0) with each dot an f32 sum
 // of exact int8*f16 products.
 __device__ __forceinline__ float q8_pair_dot(const uint32_t (&d)[17], const u32x4 (&xr)[8]) {
+#if !Q8_DEQUANT_PACKED
+  // every int8 sign-extended, converted to f32 and multiplied by f32(x)
+  float dots[2] = {0.0f, 0.0f};
+#pragma unroll
+  for (int blk = 0; blk < 2; ++blk)
+#pragma unroll
+    for (int j = 0; j < 32; ++j) {
+      const int byte = 34 * blk + 2 + j;
+      const int q = (int)(int8_t)(uint8_t)(d[byte >> 2] >> (8 * (byte & 3)));
+      const uint32_t xw = xr[4 * blk + (j >> 3)][(j >> 1) & 3];
+      const float xv = (float)as_f16x2(xw)[j & 1];
+      dots[blk] = __builtin_fmaf((float)q, xv, dots[blk]);
+    }
+  const float s0 = f16_bits_to_f32(d[0] & 0xffffu);
+  const float s1 = f16_bits_to_f32(d[8] >> 16);
+  return __builtin_fmaf(s1, dots[1], s0 * dots[0]);
+#else
   uint32_t e[17];
 #pragma unroll
   for (int m = 0; m < 17; ++m) e[m] = d[m] ^ 0x80808080u;  // q -> q+128 per byte
@@ -161,6 +253,7 @@ __device__ __forceinline__ float q8_pair_dot(const uint32_t (&d)[17], const u32x
   const float s0 = f16_bits_to_f32(d[0] & 0xffffu);
   const float s1 = f16_bits_to_f32(d[8] >> 16);
   return __builtin_fmaf(s1, dot1, s0 * dot0);
+#endif
 }
 
 // ---------------------------------------------------------- Q8_0 GEMV ------
@@ -225,7 +318,7 @@ __device__ __forceinline__ void unit_load(const Q8Seg& s, int quad, int c, const
   for (int i = 0; i < kUnitLoads; ++i) {
     int row = quad * 4 + pm.row[i];
     row = row < s.n_rows ? row : s.n_rows - 1;  // ragged last quad: re-read a valid row
-    buf[i] = load_stream<Q8_NT_LOADS>(
+    buf[i] = load_weights16<Q8_NT_LOADS>(
         reinterpret_cast<const u32x4*>(base + (size_t)row * rowb + pm.off[i]));
   }
 }
@@ -265,9 +358,15 @@ __device__ __forceinline__ void q8_segment(const Q8Seg& s, int u_begin, int u_en
 #pragma unroll
     for (int m = 0; m < 17; ++m) d[m] = pp[m];
     if (cc != xr_c || !Q8_X_REUSE) {
+#if Q8_X_LDS
       const u32x4* xs = reinterpret_cast<const u32x4*>(xl + 1024 * cc + 64 * p16);
 #pragma unroll
       for (int m = 0; m < 8; ++m) xr[m] = xs[m];
+#else
+      const u32x4* xs = reinterpret_cast<const u32x4*>(s.x + 1024 * cc + 64 * p16);
+#pragma unroll
+      for (int m = 0; m < 8; ++m) xr[m] = load_global(xs + m);
+#endif
       xr_c = cc;
     }
     acc += q8_pair_dot(d, xr);
@@ -301,7 +400,8 @@ __device__ __forceinline__ void q8_segment(const Q8Seg& s, int u_begin, int u_en
   load_ring(A);
   const u32x4* xg = reinterpret_cast<const u32x4*>(s.x);
   u32x4* xl4 = reinterpret_cast<u32x4*>(xl);
-  for (int t = lane; t < 128 * s.p; t += 64) xl4[t] = load_global(xg + t);
+  if (Q8_X_LDS)
+    for (int t = lane; t < 128 * s.p; t += 64) xl4[t] = load_global(xg + t);
   load_ring(B);
   int i = 0;
   for (; i + 3 <= n; i += 3) {
@@ -319,7 +419,8 @@ __device__ __forceinline__ void q8_segment(const Q8Seg& s, int u_begin, int u_en
   load_next(A);
   const u32x4* xg = reinterpret_cast<const u32x4*>(s.x);
   u32x4* xl4 = reinterpret_cast<u32x4*>(xl);
-  for (int t = lane; t < 128 * s.p; t += 64) xl4[t] = load_global(xg + t);
+  if (Q8_X_LDS)
+    for (int t = lane; t < 128 * s.p; t += 64) xl4[t] = load_global(xg + t);
   int i = 0;
   for (; i + 2 < n; i += 2) {
     load_next(B);
@@ -609,7 +710,7 @@ __device__ __forceinline__ void vocab_body_xp(const uint16_t* __restrict__ W, XL
     row = row < n_rows ? row : n_rows - 1;  // only the grid's last batch can be short
     const u32x4* p = Wv + (size_t)row * 128 + li;
 #pragma unroll
-    for (int m = 0; m < 8; ++m) dst[m] = load_stream<NT>(p + 16 * m);
+    for (int m = 0; m < 8; ++m) dst[m] = load_weights16<NT>(p + 16 * m);
   };
 
   float best_v = -__builtin_inff();

@@ -94,6 +94,55 @@ extern "C" __global__ void vocab_argmax_finalize(uint64_t* __restrict__ ws,
   }
 }
 
+// Argmax of an f16 vector on its own (logits written by an earlier launch,
+// e.g. decode_dispatch_24): the tiled argmax as a separate pass, as the
+// reference runs it after the vocab matmul (model/qwen3_full.mlir:1469-1511).
+// Thread t of workgroup b takes the 8-element pieces b * 256 + t, stepping by
+// the grid's thread count, in increasing order, so a strictly-greater update
+// keeps its first maximum; keys (argmax_key: value, then the lower index)
+// meet in a wave max, then in the same 64-bit atomic max on ws[0] as the
+// fused vocab kernel's, which vocab_argmax_finalize turns into the token.
+// NaN never wins; -1 when nothing does.
+extern "C" __global__ __launch_bounds__(256) void argmax_f16_k(const uint16_t* __restrict__ v,
+                                                              int n, uint64_t* __restrict__ ws) {
+  const int t = threadIdx.x;
+  const int64_t stride = (int64_t)launch_wgs() * 256;
+  float bv = -__builtin_inff();
+  int bi = -1;
+  for (int64_t p = (int64_t)blockIdx.x * 256 + t; 8 * p < n; p += stride) {
+    const int i0 = (int)(8 * p);
+    if (i0 + 8 <= n) {
+      const u32x4 w = load_global(reinterpret_cast<const u32x4*>(v) + p);
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const float x = (float)as_f16x2(w[k >> 1])[k & 1];
+        if (x > bv) {
+          bv = x;
+          bi = i0 + k;
+        }
+      }
+    } else {
+      for (int i = i0; i < n; ++i) {
+        const float x = f16_bits_to_f32(v[i]);
+        if (x > bv) {
+          bv = x;
+          bi = i;
+        }
+      }
+    }
+  }
+  uint64_t key = bi >= 0 ? argmax_key(bv, bi) : (uint64_t)0;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const uint32_t lo = __shfl_xor((uint32_t)key, d, 64);
+    const uint32_t hi = __shfl_xor((uint32_t)(key >> 32), d, 64);
+    const uint64_t o = ((uint64_t)hi << 32) | lo;
+    key = o > key ? o : key;
+  }
+  if ((t & 63) == 0 && key != 0)
+    __hip_atomic_fetch_max(ws, key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // Zeroes the 256-byte workspace (graph-capture safe: a kernel, not a memset
 // node): the argmax key and, in a decode scratch, the status word and the
 // attention merge counters.

@@ -102,6 +102,7 @@ struct State {
   hipFunction_t hal[6] = {};  // IREE HAL-ABI kernels, in kHalDispatches order
   hipFunction_t vocab = nullptr;
   hipFunction_t vocab_finalize = nullptr;
+  hipFunction_t argmax = nullptr;  // argmax_f16_k
   hipFunction_t ws_reset = nullptr;
   hipFunction_t copy = nullptr;
   hipFunction_t calib_empty = nullptr, calib_handoff = nullptr, read = nullptr;
@@ -288,6 +289,7 @@ int q8gemv_init(const char* code_object_path) {
   }
   e = hipModuleGetFunction(&g.vocab, mod, "vocab_gemv_argmax_k1024");
   if (e == hipSuccess) e = hipModuleGetFunction(&g.vocab_finalize, mod, "vocab_argmax_finalize");
+  if (e == hipSuccess) e = hipModuleGetFunction(&g.argmax, mod, "argmax_f16_k");
   if (e == hipSuccess) e = hipModuleGetFunction(&g.ws_reset, mod, "vocab_workspace_reset");
   if (e == hipSuccess) e = hipModuleGetFunction(&g.copy, mod, "stream_copy_b128");
   if (e == hipSuccess) e = hipModuleGetFunction(&g.read, mod, "stream_read_b128");
@@ -457,7 +459,7 @@ void q8gemv_shutdown(void) {
       g.pf_f16_sw_22 = nullptr;
   g.pf_f16_res_22 = g.pf_f16_res_22k = g.pf_f16_res_12k = g.pf_f16_part_22 = g.pf_f16_part_22k =
       g.pf_f16_part_12k = g.pf_f16_part_44 = g.pf_f16_part_44k = g.pf_expand = nullptr;
-  g.vocab = g.vocab_finalize = g.ws_reset = g.copy = nullptr;
+  g.vocab = g.vocab_finalize = g.argmax = g.ws_reset = g.copy = nullptr;
   g.calib_empty = g.calib_handoff = g.read = nullptr;
   g.ready = false;
 }
@@ -753,6 +755,31 @@ int decode_dispatch_24_matmul_151936x1x1024_f16(const void* w_f16, const void* x
                                                 void* logits_f16, int32_t* token,
                                                 void* workspace, void* stream) {
   return vocab_gemv_argmax(w_f16, x_f16, logits_f16, token, workspace, stream);
+}
+
+int f16_argmax(const void* values_f16, int64_t n, int32_t* token, void* workspace,
+               void* stream) {
+  if (!values_f16 || !token || !workspace)
+    return fail(Q8_ERR_NULL_POINTER, "null values, token or workspace");
+  if (n < 1 || n >= (1LL << 31)) return fail(Q8_ERR_BAD_SHAPE, "n=%lld outside [1, 2^31)", (long long)n);
+  if (!aligned(values_f16, 16)) return fail(Q8_ERR_MISALIGNED, "values not 16-byte aligned");
+  if (!aligned(token, 4)) return fail(Q8_ERR_MISALIGNED, "token not 4-byte aligned");
+  if (!aligned(workspace, 16)) return fail(Q8_ERR_MISALIGNED, "workspace not 16-byte aligned");
+  int rc = check_ready();
+  if (rc) return rc;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const void* v_arg = values_f16;
+  int n_arg = (int)n;
+  void* ws_arg = workspace;
+  int32_t* t_arg = token;
+  // one workgroup per 2048 values (8 per thread), at most one per compute unit
+  const int64_t want = (n + 2047) / 2048;
+  const uint32_t grid = (uint32_t)(want < cu_count() ? want : cu_count());
+  void* args[] = {&v_arg, &n_arg, &ws_arg};
+  rc = launch(g.argmax, grid, 256, args, s);
+  if (rc) return rc;
+  void* fargs[] = {&ws_arg, &t_arg};
+  return launch(g.vocab_finalize, 1, 64, fargs, s);
 }
 
 int q8gemv_batch_set_workgroups(int workgroups) {

@@ -119,6 +119,7 @@ _SIGNATURES = {
     "decode_dispatch_24_matmul_151936x1x1024_f16": [_P, _P, _P, _P, _P, _P],
     "f16_gemv_argmax_rows": [_P, _I64, _P, _P, _P, _P, _P],
     "f16_gemv_argmax_rows_noalloc": [_P, _I64, _P, _P, _P, _P],
+    "f16_argmax": [_P, _I64, _P, _P, _P],
     "q8gemv_qkv": [_P, _P, _P, _I64, _P, _P, _P, _P, _P],
     "q8gemv_hal_dispatch": [_I, _P, _P, _P, _P, _I, _P],
     "q8gemv_hal_dispatch_grid": [_I, _P, _P, _P, _P, _I, ctypes.c_uint32, ctypes.c_uint32, _P],
@@ -536,6 +537,12 @@ def vocab_gemv_argmax(w, x, logits, token, workspace, stream=None) -> None:
 def f16_gemv_argmax_rows(w, n_rows: int, x, logits, token, workspace, stream=None) -> None:
     _call("f16_gemv_argmax_rows", _ptr(w), int(n_rows), _ptr(x), _ptr(logits), _ptr(token),
           _ptr(workspace), _stream(stream))
+
+
+def f16_argmax(values, n: int, token, workspace, stream=None) -> None:
+    """Argmax of n f16 values already in device memory (the tiled argmax as
+    its own pass; same workspace rule as vocab_gemv_argmax)."""
+    _call("f16_argmax", _ptr(values), int(n), _ptr(token), _ptr(workspace), _stream(stream))
 
 
 def f16_gemv_argmax_rows_noalloc(w, n_rows: int, x, logits, token, stream=None) -> None:

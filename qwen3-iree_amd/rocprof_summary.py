@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Summarise rocprofv3 CSV output of bench.py into a short markdown report.
 
-Inputs (directories written by `rocprofv3 -f csv -d DIR -o bench ...`):
+Inputs (directories written by `rocprofv3 -f csv -d DIR -o NAME ...`, any NAME):
   --trace DIR   a --kernel-trace --stats run  (bench_kernel_stats.csv,
                 bench_kernel_trace.csv)
   --fetch DIR   a --pmc FETCH_SIZE run         (bench_counter_collection.csv)
@@ -33,6 +33,14 @@ from collections import defaultdict
 from pathlib import Path
 
 
+def _one(d: Path, suffix: str) -> Path:
+    """The one `<NAME>_<suffix>` file rocprofv3 wrote into d."""
+    found = sorted(d.glob(f"*_{suffix}"))
+    if len(found) != 1:
+        raise SystemExit(f"expected one *_{suffix} in {d}, found {len(found)}")
+    return found[0]
+
+
 def _rows(path: Path):
     with open(path, newline="") as f:
         yield from csv.DictReader(f)
@@ -40,7 +48,7 @@ def _rows(path: Path):
 
 def kernel_durations(trace_dir: Path, split_after: str | None = None) -> dict:
     out = defaultdict(list)
-    rows = sorted(_rows(trace_dir / "bench_kernel_trace.csv"),
+    rows = sorted(_rows(_one(trace_dir, "kernel_trace.csv")),
                   key=lambda r: (r["Queue_Id"], int(r["Start_Timestamp"])))
     prev = {}
     for r in rows:
@@ -55,7 +63,7 @@ def kernel_durations(trace_dir: Path, split_after: str | None = None) -> dict:
 
 def counter_values(pmc_dir: Path, counter: str) -> dict:
     out = defaultdict(list)
-    for r in _rows(pmc_dir / "bench_counter_collection.csv"):
+    for r in _rows(_one(pmc_dir, "counter_collection.csv")):
         if r["Counter_Name"] != counter:
             continue
         out[(r["Kernel_Name"], int(r["Grid_Size"]))].append(float(r["Counter_Value"]))
