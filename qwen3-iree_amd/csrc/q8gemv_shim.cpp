@@ -1480,9 +1480,11 @@ size_t pf_region_bytes(int32_t n, int i) {
 // Positions per attention split, in blocks of 32.  A query block's positions
 // are walked one block after another, so without splits the longest query
 // block sets the time; each split costs a partial written and merged.  8
-// blocks (256 positions) measured best for 512- and 2048-token prompts from
-// position 0 (sweep of 1 .. 24 and unsplit).  Raised where the partial slots
-// would not hold the splits.
+// blocks (256 positions) measured best for 512-token prompts from position 0
+// (sweep of 1 .. 24 and unsplit).  Raised where the partial slots would not
+// hold the splits: 13 blocks for 2048 tokens from position 0, where slots
+// for splits of 8 / 6 / 4 blocks measured slower (attention + merge 55.1 /
+// 61.1 / 70.4 us per layer against 51.2).
 constexpr int32_t kPfAttnSplitDefault = 8;
 
 int32_t pf_attn_split_blocks(int32_t n, int32_t p0, int chunk_local) {
