@@ -982,16 +982,14 @@ extern "C" __global__ __launch_bounds__(256) void pf_attention(
     // v_exp_f32 without the denormal-range fix-up of exp2f: a weight below
     // 2^-126 beside the weight 1 of the score that set m changes no f32 sum
     const float alpha = __builtin_amdgcn_exp2f(grow ? m - mx : 0.0f);
+    // A masked score is -inf and its weight 2^(-inf - mn) = 0 while mn is
+    // finite; mn is -inf only while every score of the query so far is
+    // masked, where the reference 0 gives those weights 2^-inf = 0 as well
+    // (instead of 2^NaN).  One form for masked and unmasked blocks.
+    const float mref = mn == -__builtin_inff() ? 0.0f : mn;
     float p[8];
-    if (masked) {
 #pragma unroll
-      for (int i = 0; i < 8; ++i)
-        p[i] = s[i] == -__builtin_inff() ? 0.0f : __builtin_amdgcn_exp2f(s[i] - mn);
-    } else {  // every score finite, mn finite (the block grew it if it was -inf)
-#pragma unroll
-      for (int i = 0; i < 8; ++i)
-        p[i] = __builtin_amdgcn_exp2f(s[i] - mn);
-    }
+    for (int i = 0; i < 8; ++i) p[i] = __builtin_amdgcn_exp2f(s[i] - mref);
     float ps = p[0];
 #pragma unroll
     for (int i = 1; i < 8; ++i) ps += p[i];
