@@ -928,6 +928,12 @@ def run(Q, S, O, info, args) -> int:
     tf = timed(Q, stream, floor_fn, max(10, args.steps // 4))
     floor_us = tf["mean_ms"] * 1e3
     log(f"  its floor, 140 empty launches the same way: {floor_us:.1f} us")
+    # and what each dispatch must wait for before its first weight bytes: one
+    # dependent load from HBM (lines evicted from L2 and the MALL first)
+    mem = Q.memory_latency(4096)
+    bound_us = floor_us + len(sw.order) * mem["hbm_ns"] * 1e-3 + sw.bytes_per_step / HBM_PEAK_GBS / 1e3
+    log(f"  dependent load: HBM {mem['hbm_ns']:.0f} ns, MALL {mem['mall_ns']:.0f} ns, L2 "
+        f"{mem['l2_ns']:.0f} ns; floor + 140 HBM loads + bytes at 8 TB/s = {bound_us:.1f} us")
     # the same 140 GEMVs through the reference's HAL binding ABI (the kernels an
     # IREE executable substitution would launch), outputs checked against the
     # C-ABI dispatches' bit for bit
@@ -1038,7 +1044,11 @@ def run(Q, S, O, info, args) -> int:
                                "hal_abi_us": round(hal_us, 1),
                                "hal_abi_parity_ok": bool(hal_same),
                                "floor": "140 empty launches (one workgroup each), stream-ordered "
-                                        "the same way"},
+                                        "the same way",
+                               "memory_latency": mem,
+                               "bound_us": round(bound_us, 1),
+                               "bound": "floor_us + 140 x memory_latency.hbm_ns (each dispatch's "
+                                        "first weight bytes) + the sweep's bytes at 8 TB/s"},
         "vocab": {"us": round(v_ms * 1e3, 2), "median_us": round(tv["median_ms"] * 1e3, 2),
                   "GBps": round(v_gbs, 1), "frac": round(v_gbs / HBM_PEAK_GBS, 4),
                   "bytes": vocab_bytes, "token": token, "parity_ok": rep_v["fail"] == 0 and token == own,

@@ -315,6 +315,16 @@ int q8rt_launch_cost(int cooperative, int workgroups, int threads, size_t lds_by
  * 512, rounds <= 255; rounds are 20 us apart. */
 int q8rt_handoff_latency(int producers, int consumers, int n_words, int replicas, int rounds,
                          float* latency_us, int* failed);
+/* Load-to-use latency of one lane's dependent loads (a pointer chase through
+ * `hops` distinct 128-byte lines of a 64 MiB buffer, 16 <= hops <= 65536):
+ * ns_per_load[0] with every line in HBM only (a 1 GiB read first evicts L2
+ * and the 256 MB memory-side cache), [1] from the memory-side cache (the same
+ * lines chased again from another XCD, whose L2 never held them), [2] from
+ * the chasing XCD's own L2 (the same lines at once again); NaN where a pass
+ * could not be placed.  xcds[0], xcds[1]: the XCD ids of the two chasing
+ * workgroups.  The single-dispatch GEMVs wait for their first weight bytes
+ * about [0] after their start. */
+int q8rt_memory_latency(int hops, float* ns_per_load, int* xcds);
 
 #ifdef __cplusplus
 }

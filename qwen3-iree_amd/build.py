@@ -32,6 +32,10 @@ HIPCC_FLAGS = [
     "-std=c++17",
     # no packed-FP32 instructions anywhere in the device code
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # kernel arguments preloaded into SGPRs at dispatch, so a kernel's first
+    # address does not wait for a kernarg load (the code object keeps a
+    # prologue that loads them where the firmware does not preload)
+    "-mllvm", "-amdgpu-kernarg-preload-count=16",
     "--genco",
     "--no-gpu-bundle-output",
 ]

@@ -277,6 +277,36 @@ extern "C" __global__ __launch_bounds__(256) void calib_handoff(HandoffArgs a) {
   }
 }
 
+// Load-to-use latency of one lane's dependent loads: the lane follows the
+// cycle next[] (u32 indices into next, each a different 128-byte line of a
+// region of mask + 1 words) for `hops` steps, reading the 100 MHz clock before
+// and after, `passes` times over the same cycle (the first pass finds lines
+// wherever a previous kernel left them, a later one in this XCD's L2).  The
+// workgroup whose XCD id (HW_REG_XCC_ID) is `xcd` runs the chase (xcd < 0:
+// workgroup 0); every workgroup records its XCD id in xcd_of[blockIdx.x].
+// ticks[p] = clock ticks of pass p (0 where no workgroup ran); ticks[passes] =
+// the XCD that ran, ticks[passes + 1] = the last index (keeps the loads live).
+extern "C" __global__ __launch_bounds__(64) void calib_chase(const uint32_t* __restrict__ next,
+                                                             uint32_t mask, int hops, int passes,
+                                                             int xcd, uint32_t* __restrict__ ticks,
+                                                             uint32_t* __restrict__ xcd_of) {
+  if (threadIdx.x != 0) return;
+  uint32_t my;
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID, 0, 4)" : "=s"(my));
+  xcd_of[blockIdx.x] = my;
+  if (xcd < 0 ? blockIdx.x != 0 : (int)my != xcd) return;
+  uint32_t i = 0;
+  for (int p = 0; p < passes; ++p) {
+    const uint32_t t0 = realtime();
+    for (int h = 0; h < hops; ++h) i = next[i] & mask;
+    // the clock is read once the last load's value is in a register
+    asm volatile("" : "+v"(i) : : "memory");
+    ticks[p] = realtime() - t0;
+  }
+  ticks[passes] = my;
+  ticks[passes + 1] = i;
+}
+
 // ------------------------------------------------ IREE HAL binding ABI ----
 //
 // The same kernels under the reference's executable export names and binding

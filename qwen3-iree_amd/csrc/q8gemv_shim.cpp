@@ -105,7 +105,8 @@ struct State {
   hipFunction_t argmax = nullptr;  // argmax_f16_k
   hipFunction_t ws_reset = nullptr;
   hipFunction_t copy = nullptr;
-  hipFunction_t calib_empty = nullptr, calib_handoff = nullptr, read = nullptr;
+  hipFunction_t calib_empty = nullptr, calib_handoff = nullptr, calib_chase = nullptr,
+                read = nullptr;
   // Tuning knobs: process-wide, set under mu, read without it (atomics), so a
   // setter never races a launch on another thread; each call reads a knob
   // once.
@@ -295,6 +296,7 @@ int q8gemv_init(const char* code_object_path) {
   if (e == hipSuccess) e = hipModuleGetFunction(&g.read, mod, "stream_read_b128");
   if (e == hipSuccess) e = hipModuleGetFunction(&g.calib_empty, mod, "calib_empty");
   if (e == hipSuccess) e = hipModuleGetFunction(&g.calib_handoff, mod, "calib_handoff");
+  if (e == hipSuccess) e = hipModuleGetFunction(&g.calib_chase, mod, "calib_chase");
   if (e != hipSuccess) {
     (void)hipModuleUnload(mod);
     return fail(Q8_ERR_CODE_OBJECT, "vocab / copy kernels missing from %s", path.c_str());
@@ -460,7 +462,7 @@ void q8gemv_shutdown(void) {
   g.pf_f16_res_22 = g.pf_f16_res_22k = g.pf_f16_res_12k = g.pf_f16_part_22 = g.pf_f16_part_22k =
       g.pf_f16_part_12k = g.pf_f16_part_44 = g.pf_f16_part_44k = g.pf_expand = nullptr;
   g.vocab = g.vocab_finalize = g.argmax = g.ws_reset = g.copy = nullptr;
-  g.calib_empty = g.calib_handoff = g.read = nullptr;
+  g.calib_empty = g.calib_handoff = g.calib_chase = g.read = nullptr;
   g.ready = false;
 }
 
@@ -1101,6 +1103,71 @@ int q8rt_handoff_latency(int producers, int consumers, int n_words, int replicas
     }
   }
   *failed = bad;
+  return Q8_OK;
+}
+
+int q8rt_memory_latency(int hops, float* ns_per_load, int* xcds) {
+  if (!ns_per_load || !xcds) return fail(Q8_ERR_NULL_POINTER, "null output");
+  if (hops < 16 || hops > 65536)
+    return fail(Q8_ERR_BAD_ARGUMENT, "%d hops outside [16, 65536]", hops);
+  int rc = check_ready();
+  if (rc) return rc;
+  // A cycle through `hops` distinct 128-byte lines of a 64 MiB region, in a
+  // fixed pseudo-random order starting (and ending) at line 0.
+  constexpr uint32_t kWords = 16u << 20;  // 64 MiB of u32
+  constexpr uint32_t kLines = kWords / 32;
+  constexpr size_t kScrub = (size_t)1 << 30;
+  std::vector<uint32_t> line(kLines);
+  for (uint32_t i = 0; i < kLines; ++i) line[i] = i;
+  uint64_t st = 0x9e3779b97f4a7c15ull;
+  for (uint32_t i = kLines - 1; i > 1; --i) {  // shuffle lines 1.. (line 0 starts the cycle)
+    st = st * 6364136223846793005ull + 1442695040888963407ull;
+    const uint32_t j = 1 + (uint32_t)((st >> 33) % i);
+    std::swap(line[i], line[j]);
+  }
+  std::vector<uint32_t> next(kWords, 0u);
+  for (int h = 0; h < hops; ++h) next[(size_t)line[h] * 32] = line[(h + 1) % hops] * 32;
+  CalibScope c;
+  HIP_TRY(hipStreamCreate(&c.st));
+  HIP_TRY(hipMalloc(&c.buf[0], (size_t)kWords * 4));
+  HIP_TRY(hipMalloc(&c.buf[1], kScrub));
+  HIP_TRY(hipMalloc(&c.buf[2], 64 * 4));  // ticks [0, 8), XCD ids [16, 24)
+  HIP_TRY(hipMemcpyAsync(c.buf[0], next.data(), (size_t)kWords * 4, hipMemcpyHostToDevice, c.st));
+  HIP_TRY(hipMemsetAsync(c.buf[1], 0, kScrub, c.st));
+  uint32_t* ticks = static_cast<uint32_t*>(c.buf[2]);
+  uint32_t host[24];
+  auto chase = [&](int passes, int xcd) -> int {
+    HIP_TRY(hipMemsetAsync(c.buf[2], 0xff, 64 * 4, c.st));
+    const void* n_arg = c.buf[0];
+    uint32_t mask = kWords - 1;
+    int h_arg = hops, p_arg = passes, x_arg = xcd;
+    uint32_t* t_arg = ticks;
+    uint32_t* x_out = ticks + 16;
+    void* args[] = {&n_arg, &mask, &h_arg, &p_arg, &x_arg, &t_arg, &x_out};
+    // one workgroup per XCD (workgroups go to the XCDs in turn)
+    HIP_TRY(hipModuleLaunchKernel(g.calib_chase, 8, 1, 1, 64, 1, 1, 0, c.st, args, nullptr));
+    HIP_TRY(hipMemcpyAsync(host, c.buf[2], sizeof(host), hipMemcpyDeviceToHost, c.st));
+    HIP_TRY(hipStreamSynchronize(c.st));
+    return Q8_OK;
+  };
+  const float nan = std::numeric_limits<float>::quiet_NaN();
+  auto per_load = [&](uint32_t t) { return t == 0xffffffffu ? nan : (float)t * 10.0f / hops; };
+  // 1 GiB read (4x the memory-side cache): neither L2 nor the MALL holds a
+  // line of the cycle; then pass 1 from HBM, pass 2 from this XCD's L2
+  if ((rc = q8rt_stream_read(c.buf[1], kScrub, c.st))) return rc;
+  if ((rc = chase(2, -1))) return rc;
+  ns_per_load[0] = per_load(host[0]);
+  ns_per_load[2] = per_load(host[1]);
+  const int x0 = host[2] == 0xffffffffu ? -1 : (int)host[2];
+  xcds[0] = x0;
+  // the same lines from another XCD, whose L2 never saw them: the MALL
+  ns_per_load[1] = nan;
+  xcds[1] = -1;
+  if (x0 >= 0) {
+    if ((rc = chase(1, (x0 + 1) % 8))) return rc;
+    ns_per_load[1] = per_load(host[0]);
+    xcds[1] = host[1] == 0xffffffffu ? -1 : (int)host[1];
+  }
   return Q8_OK;
 }
 

@@ -157,6 +157,7 @@ _SIGNATURES = {
     "q8rt_stream_read": [_P, _SZ, _P],
     "q8rt_launch_cost": [_I, _I, _I, _SZ, _I, _P],
     "q8rt_handoff_latency": [_I, _I, _I, _I, _I, _P, _P],
+    "q8rt_memory_latency": [_I, _P, _P],
     # include/qwen3_decode.h
     "qwen3_scratch_bytes": [],
     "qwen3_scratch_reset": [_P, _P],
@@ -457,6 +458,16 @@ def handoff_latency(producers: int, consumers: int, n_words: int, replicas: int 
     _call("q8rt_handoff_latency", int(producers), int(consumers), int(n_words), int(replicas),
           int(rounds), out.ctypes.data, ctypes.byref(failed))
     return out.reshape(rounds, consumers), int(failed.value)
+
+
+def memory_latency(hops: int = 4096) -> dict:
+    """ns per dependent load from HBM, from the memory-side cache (MALL) and
+    from L2, and the XCDs that chased (q8rt_memory_latency)."""
+    ns = np.zeros(3, np.float32)
+    xcds = np.zeros(2, np.int32)
+    _call("q8rt_memory_latency", int(hops), ns.ctypes.data, xcds.ctypes.data)
+    return {"hbm_ns": float(ns[0]), "mall_ns": float(ns[1]), "l2_ns": float(ns[2]),
+            "xcds": [int(xcds[0]), int(xcds[1])], "hops": int(hops)}
 
 
 # ------------------------------------------------------------- operators ----

@@ -113,6 +113,9 @@ def test_dispatch_table_mirrors_reference_exports(Q):
     (lambda L: L.q8rt_handoff_latency(3, 1, 512, 1, 10, A16, A16), 9),
     (lambda L: L.q8rt_handoff_latency(128, 400, 512, 4, 10, A16, A16), 9),
     (lambda L: L.q8rt_handoff_latency(1, 1, 512, 1, 300, A16, A16), 9),
+    (lambda L: L.q8rt_memory_latency(4096, None, A16), 3),
+    (lambda L: L.q8rt_memory_latency(8, A16, A16), 9),
+    (lambda L: L.q8rt_memory_latency(1 << 17, A16, A16), 9),
 ])
 def test_argument_validation_before_any_device_work(Q, call, code):
     lib = Q.load_library()

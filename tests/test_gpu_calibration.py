@@ -1,5 +1,5 @@
 """The measurement tools behind the single-launch decode step's design
-(q8rt_launch_cost, q8rt_handoff_latency): they run to completion on the
+(q8rt_launch_cost, q8rt_handoff_latency, q8rt_memory_latency): they run to completion on the
 device and return physically sensible figures.  (The figures themselves are
 recorded by bench.py; the tests only bound them loosely.)"""
 from __future__ import annotations
@@ -33,3 +33,15 @@ def test_handoff_latency(gpu, producers, consumers, n_words, replicas):
     # (up to the clock's 10 ns tick), and no hand-off takes anywhere near the
     # 20 us between rounds
     assert lat.min() >= -0.05 and np.median(lat) < 15.0
+
+
+def test_memory_latency_by_level(gpu):
+    Q = gpu
+    r = Q.memory_latency(2048)
+    print(f"dependent load: HBM {r['hbm_ns']:.0f} ns, MALL {r['mall_ns']:.0f} ns, "
+          f"L2 {r['l2_ns']:.0f} ns (XCDs {r['xcds']})", flush=True)
+    assert 0 <= r["xcds"][0] < 8 and r["xcds"][1] == (r["xcds"][0] + 1) % 8
+    for k in ("hbm_ns", "mall_ns", "l2_ns"):
+        assert np.isfinite(r[k]) and 20.0 < r[k] < 20000.0, (k, r[k])
+    # a line from this XCD's L2 comes back sooner than one from the memory side
+    assert r["l2_ns"] < r["mall_ns"] and r["l2_ns"] < r["hbm_ns"]
