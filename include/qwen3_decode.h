@@ -241,7 +241,8 @@ int64_t qwen3_prefill_workspace_offset(int32_t n_tokens, const char* name);
  *   bit).
  * attn_split_blocks: cache positions per attention split, in blocks of 32
  *   (>= 1; raised where the workspace's partial slots would not hold the
- *   splits); default 8.  Splits change the order of the softmax sums, within
+ *   splits); default a third of the longest query block's positions, at
+ *   least 8 blocks.  Splits change the order of the softmax sums, within
  *   the attention tolerance.
  * Fails with Q8_ERR_BAD_ARGUMENT for other values.  No counterpart in the
  * reference (IREE tiles its dispatches at compile time). */

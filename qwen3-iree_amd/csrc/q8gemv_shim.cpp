@@ -1546,12 +1546,12 @@ size_t pf_region_bytes(int32_t n, int i) {
 
 // Positions per attention split, in blocks of 32.  A query block's positions
 // are walked one block after another, so without splits the longest query
-// block sets the time; each split costs a partial written and merged.  8
-// blocks (256 positions) measured best for 512-token prompts from position 0
-// (sweep of 1 .. 24 and unsplit).  Raised where the partial slots would not
-// hold the splits: 13 blocks for 2048 tokens from position 0, where slots
-// for splits of 8 / 6 / 4 blocks measured slower (attention + merge 55.1 /
-// 61.1 / 70.4 us per layer against 51.2).
+// block sets the time; each split costs a partial written and merged.  The
+// default is a third of the longest query block, at least 8 blocks: 8 (256
+// positions) measured best for 512-token prompts from position 0 (sweep of
+// 1 .. 24 and unsplit), 11 for 1024 tokens (3.218 ms against 3.249-3.317 for
+// 8-43) and 22 for 2048 (4.853 ms against 4.881-5.017 for 8-43).  Raised
+// where the partial slots would not hold the splits (4096 tokens: 32).
 constexpr int32_t kPfAttnSplitDefault = 8;
 
 int32_t pf_attn_split_blocks(int32_t n, int32_t p0, int chunk_local) {
@@ -1559,7 +1559,8 @@ int32_t pf_attn_split_blocks(int32_t n, int32_t p0, int chunk_local) {
   const int64_t cap = pf_attn_pair_cap(n);
   const int32_t nb_max = std::max(G.nb_last, G.c + G.nqb - 2);
   const int32_t set_split = g.pf_attn_split.load(std::memory_order_relaxed);
-  const int32_t s0 = set_split > 0 ? set_split : kPfAttnSplitDefault;
+  const int32_t s0 =
+      set_split > 0 ? set_split : std::max(kPfAttnSplitDefault, (nb_max + 2) / 3);
   int32_t lo_s = std::min(s0, nb_max), hi_s = nb_max;
   // smallest S >= lo_s whose pairs fit (at S = nb_max there are nqb pairs)
   while (lo_s < hi_s) {
