@@ -330,11 +330,13 @@ constexpr int kKvPrefetchBytes = 8 * 1024 + 32 * 256;
 // One chunk of a split's cache rows -- positions c0 .. c0 + 31, clamped to
 // `last` -- copied into the wave's LDS region kv by the memory system
 // (global_load_lds), so no register holds them while they are in flight: K
-// row r's 16-byte chunk ch (dims 8 ch .. + 7) lands at kv + 1024 (ch & 7) +
-// 512 (ch >> 3) + 16 r (lane (r, ch >> 3) loads pieces ch & 7 = 0..7), V row
-// r's chunk ch at kv + 8192 + 256 r + 16 (ch ^ 2 (r & 7)) (so the transposing
-// reads of attention_group hit distinct banks: the lane whose 16 bytes land in
-// slot j of row r loads chunk j ^ 2 (r & 7), four rows per load).  The K part
+// row r's 16-byte chunk ch (dims 8 ch .. + 7) lands at kv + 256 r + 16 (ch ^
+// (r & 15)), V row r's chunk ch at kv + 8192 + 256 r + 16 (ch ^ 2 (r & 7)) (so
+// the score reads and the transposing reads of attention_group hit distinct
+// banks): each load covers four whole rows, the lane whose 16 bytes land in
+// slot j of row r loading chunk j ^ (r & 15) (K) or j ^ 2 (r & 7) (V).  (K used
+// to land at kv + 1024 (ch & 7) + 512 (ch >> 3) + 16 r, each load taking 16
+// bytes of every row: 64 lines per load, each touched by all eight.)  The K part
 // is 8 loads per lane, the V part 8, in that order; the compiler does not
 // track these copies for the LDS reads that follow, so readers wait on the
 // vector memory counter themselves (wait_vm) and let every LDS read of the
@@ -346,16 +348,17 @@ template <int PACE = 0>
 __device__ __forceinline__ void kv_stage_k(uint8_t* kv, const uint16_t* __restrict__ k_cache,
                                            int g, int c0, int last) {
   const int lane = threadIdx.x & 63;
-  const int half = lane >> 5;
-  const int pl = lane & 31;
-  const int p = c0 + pl < last ? c0 + pl : last;
-  const u32x4* krow = reinterpret_cast<const u32x4*>(
-      k_cache + ((size_t)p * kKvHeads + g) * kHeadDim + 64 * half);
 #pragma unroll
-  for (int m = 0; m < 8; ++m)
-    __builtin_amdgcn_global_load_lds((const GLOBAL_AS void*)(krow + m),
-                                     (__attribute__((address_space(3))) void*)(kv + 1024 * m), 16,
-                                     0, 0);
+  for (int i = 0; i < 8; ++i) {
+    const int r = 4 * i + (lane >> 4);  // this lane's row; its 16 bytes land in slot lane % 16
+    const int pr = c0 + r < last ? c0 + r : last;
+    const int ch = (lane & 15) ^ (r & 15);
+    __builtin_amdgcn_global_load_lds(
+        (const GLOBAL_AS void*)(reinterpret_cast<const u32x4*>(
+                                    k_cache + ((size_t)pr * kKvHeads + g) * kHeadDim) +
+                                ch),
+        (__attribute__((address_space(3))) void*)(kv + 1024 * i), 16, 0, 0);
+  }
   if constexpr (PACE > 0) __builtin_amdgcn_s_sleep(PACE);
 }
 
@@ -465,8 +468,6 @@ __device__ __forceinline__ void attention_group(AttnLds& L, int g, int sg, int p
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int s = sg * kAttnWaves + wave;
-  const int half = lane >> 5;
-  const int pl = lane & 31;
 
   pre_qkv();  // a wait's first round goes out ahead of this function's loads
   uint32_t nwv[3];
@@ -567,39 +568,18 @@ __device__ __forceinline__ void attention_group(AttnLds& L, int g, int sg, int p
   const auto v_off = [&](int row, int d) {
     return 8192 + 256 * row + 16 * ((2 * d + ((c16 & 3) >> 1)) ^ (2 * (row & 7))) + 8 * (c16 & 1);
   };
-  // Chunk 0 comes into the region as kv_stage copies it.  For every later
-  // chunk c + 1, its K rows come into registers while chunk c is computed
-  // (eight 16-byte loads per lane: row pl's dims 64 half .. + 63) and are
-  // stored into the region, in the layout kv_stage_k gives them, once chunk
-  // c's reads have returned; then its V rows are copied in (kv_stage_v) and
-  // chunk c + 2's K loads go out.  K has a whole chunk's compute to arrive in
-  // (a copy into the region could only start after chunk c's scores), V chunk
-  // c + 1's scores and softmax.  Only where the bytes travel changes: every
-  // value read from the region is the same.  A wave's loads return in order,
-  // so V(c) has landed once at most chunk c + 1's 8 K loads are outstanding.
-  u32x4 kreg[8];
-  const auto load_k = [&](int c0n) {
-    const int p = c0n + pl < last ? c0n + pl : last;
-    const u32x4* krow = reinterpret_cast<const u32x4*>(
-        k_cache + ((size_t)p * kKvHeads + g) * kHeadDim + 64 * half);
-#pragma unroll
-    for (int mm = 0; mm < 8; ++mm) kreg[mm] = load_global(krow + mm);
-  };
-  if (n_chunks > 1) load_k(start + 32);
+  // Chunk c's copies: K(c) then V(c), issued as kv_stage does for c = 0 and
+  // for c > 0 as K(c) after chunk c - 1's scores and V(c) after its weighted
+  // sum; the loads of one wave return in order, so K(c) has landed once at
+  // most the 8 V(c) loads are outstanding, V(c) once at most K(c + 1)'s 8.
   for (int c = 0; c < n_chunks; ++c) {
     const int c0 = start + 32 * c;
     // the staged row of position pos predates this step's k and v: replace it
     const bool has_pos = pos >= c0 && pos < c0 + 32;
     const int rp = pos - c0;
-    // K(0): its copies went out before V(0)'s 8 and chunk 1's 8 K loads; a
-    // later chunk's K was stored by this wave (its LDS accesses are
-    // performed in order)
-    if (c == 0) {
-      if (n_chunks > 1) wait_vm<16>();
-      else wait_vm<8>();
-    }
+    wait_vm<8>();
     if (has_pos && lane < 16)
-      *reinterpret_cast<u32x4*>(kv + 1024 * (lane & 7) + 512 * (lane >> 3) + 16 * rp) =
+      *reinterpret_cast<u32x4*>(kv + 256 * rp + 16 * (lane ^ (rp & 15))) =
           *reinterpret_cast<const u32x4*>(&L.kh[4 * lane]);
     f32x4 sc[2];
 #pragma unroll
@@ -608,8 +588,8 @@ __device__ __forceinline__ void attention_group(AttnLds& L, int g, int sg, int p
 #pragma unroll
       for (int st = 0; st < 4; ++st) {
         const int ch = 4 * st + grp;
-        const f16x8 kf = *reinterpret_cast<const f16x8*>(kv + 1024 * (ch & 7) + 512 * (ch >> 3) +
-                                                         16 * (16 * nt + c16));
+        const int kr = 16 * nt + c16;
+        const f16x8 kf = *reinterpret_cast<const f16x8*>(kv + 256 * kr + 16 * (ch ^ (kr & 15)));
         sc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[st], sc[nt], 0, 0, 0);
       }
     }
@@ -640,8 +620,14 @@ __device__ __forceinline__ void attention_group(AttnLds& L, int g, int sg, int p
 #pragma unroll
     for (int d = 0; d < 8; ++d) o[d] *= alpha;
     stamp(18);
-    if (c + 1 < n_chunks) wait_vm<8>();
-    else wait_vm<0>();
+    // the K region is free once its reads have returned: the next chunk's K
+    wait_lds();
+    if (c + 1 < n_chunks) {
+      kv_stage_k(kv, k_cache, g, c0 + 32, last);
+      wait_vm<8>();
+    } else {
+      wait_vm<0>();
+    }
     if (has_pos)
       *reinterpret_cast<uint32_t*>(kv + 8192 + 256 * rp + 16 * ((lane >> 2) ^ (2 * (rp & 7))) +
                                    4 * (lane & 3)) = v_new;
@@ -666,15 +652,10 @@ __device__ __forceinline__ void attention_group(AttnLds& L, int g, int sg, int p
       o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, ph, o[d], 0, 0, 0);
       o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pl, o[d], 0, 0, 0);
     }
-    // the region is free once chunk c's reads have returned: chunk c + 1's K
-    // from the registers, its V by copies, then chunk c + 2's K loads
+    // the V region is free once its reads have returned: the next chunk's V
     if (c + 1 < n_chunks) {
       wait_lds();
-#pragma unroll
-      for (int mm = 0; mm < 8; ++mm)
-        *reinterpret_cast<u32x4*>(kv + 1024 * mm + 16 * lane) = kreg[mm];
       kv_stage_v(kv, v_cache, g, c0 + 32, last);
-      if (c + 2 < n_chunks) load_k(start + 32 * (c + 2));
     }
   }
   stamp(19);
