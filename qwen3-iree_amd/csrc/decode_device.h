@@ -569,8 +569,8 @@ __device__ __forceinline__ void attention_group(AttnLds& L, int g, int sg, int p
     return 8192 + 256 * row + 16 * ((2 * d + ((c16 & 3) >> 1)) ^ (2 * (row & 7))) + 8 * (c16 & 1);
   };
   // Chunk c's copies: K(c) then V(c), issued as kv_stage does for c = 0 and
-  // for c > 0 as K(c) after chunk c - 1's scores and V(c) after its weighted
-  // sum; the loads of one wave return in order, so K(c) has landed once at
+  // for c > 0 as K(c) after chunk c - 1's score reads and V(c) after its V^T
+  // reads; the loads of one wave return in order, so K(c) has landed once at
   // most the 8 V(c) loads are outstanding, V(c) once at most K(c + 1)'s 8.
   for (int c = 0; c < n_chunks; ++c) {
     const int c0 = start + 32 * c;
@@ -594,6 +594,11 @@ __device__ __forceinline__ void attention_group(AttnLds& L, int g, int sg, int p
       }
     }
     stamp(17);
+    // the K region is free once the score reads have returned (every MFMA
+    // above waited for its fragment): the next chunk's K goes out now, under
+    // the softmax and the weighted sum
+    wait_lds();
+    if (c + 1 < n_chunks) kv_stage_k(kv, k_cache, g, c0 + 32, last);
     // s[4 nt + e]: position c0 + 16 nt + 4 grp + e; past the split: -inf
     float s[8];
 #pragma unroll
@@ -620,14 +625,9 @@ __device__ __forceinline__ void attention_group(AttnLds& L, int g, int sg, int p
 #pragma unroll
     for (int d = 0; d < 8; ++d) o[d] *= alpha;
     stamp(18);
-    // the K region is free once its reads have returned: the next chunk's K
-    wait_lds();
-    if (c + 1 < n_chunks) {
-      kv_stage_k(kv, k_cache, g, c0 + 32, last);
-      wait_vm<8>();
-    } else {
-      wait_vm<0>();
-    }
+    // V(c) has landed: only K(c + 1)'s 8 copies, issued after it, may be out
+    if (c + 1 < n_chunks) wait_vm<8>();
+    else wait_vm<0>();
     if (has_pos)
       *reinterpret_cast<uint32_t*>(kv + 8192 + 256 * rp + 16 * ((lane >> 2) ^ (2 * (rp & 7))) +
                                    4 * (lane & 3)) = v_new;
@@ -643,19 +643,22 @@ __device__ __forceinline__ void attention_group(AttnLds& L, int g, int sg, int p
       pl[i] = l2.x;
       pl[i + 1] = l2.y;
     }
+    // every V^T fragment of the chunk first; once they have returned the
+    // region is free and the next chunk's V goes out under the weighted sum
+    f16x8 vfs[8];
 #pragma unroll
     for (int d = 0; d < 8; ++d) {
       const v4i16 v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((LDS_AS v4i16*)(kv + v_off(vrow, d)));
       const v4i16 v1 =
           __builtin_amdgcn_ds_read_tr16_b64_v4i16((LDS_AS v4i16*)(kv + v_off(vrow + 16, d)));
-      const f16x8 vf = __builtin_bit_cast(f16x8, (v8i16){v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w});
-      o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, ph, o[d], 0, 0, 0);
-      o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pl, o[d], 0, 0, 0);
+      vfs[d] = __builtin_bit_cast(f16x8, (v8i16){v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w});
     }
-    // the V region is free once its reads have returned: the next chunk's V
-    if (c + 1 < n_chunks) {
-      wait_lds();
-      kv_stage_v(kv, v_cache, g, c0 + 32, last);
+    wait_lds();
+    if (c + 1 < n_chunks) kv_stage_v(kv, v_cache, g, c0 + 32, last);
+#pragma unroll
+    for (int d = 0; d < 8; ++d) {
+      o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vfs[d], ph, o[d], 0, 0, 0);
+      o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vfs[d], pl, o[d], 0, 0, 0);
     }
   }
   stamp(19);
