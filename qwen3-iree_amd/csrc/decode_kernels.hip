@@ -602,7 +602,10 @@ constexpr int kVecWords = 2 * kAttnGroups * 130;  // 2080: the largest polled ve
 // 535-536, E 48 653, the cache chunk 4 / 16 unchanged; with E at 16 (536):
 // A 28 / 36 539 / 552, D 28 / 36 547 / 561, C 28 / 36 539 / 554; with the
 // gate/up touch and D at 30 (518): C 26 / 28 / 30 / 34 519 / 517 / 516 / 531,
-// E 12 / 20 518, A 30 522.
+// E 12 / 20 518, A 30 522.  Again with the cache rows copied whole and the
+// kernel arguments preloaded (508.5 / 511.4 as below): D 26 / 34 526.8 /
+// 542.6, A 28 / 36 515.1 / 524.4, C 26 / 34 515.3 / 529.5, E 12 / 20 512.2 /
+// 510.9.
 #ifndef DEC_PACE_A
 #define DEC_PACE_A 32
 #endif
